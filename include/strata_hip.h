@@ -1,0 +1,194 @@
+/* strata_hip: MI355X (gfx950) backend for RustingStrata's quantized-matmul hot path, as a C ABI.
+ *
+ * Each entry point is one method of the reference's `Backend` trait (src/backend.rs:98-443) on the hot path, with
+ * the trait's argument meaning: device addresses as uint64_t, strides in floats unless named otherwise, ops queued
+ * in order on the context's one stream, host copies synchronous. Every function returns 0 on success and -1 on
+ * error; the message is then in strata_last_error() (per thread). As in the reference, an op that rejects its
+ * arguments (unsupported type or shape) returns the error without launching anything.
+ *
+ * Weight type ids are the GGUF ids of `GgmlType::from_u32` (src/quant/mod.rs:15-19): Q8_0 8, Q2_K 10, Q3_K 11,
+ * Q4_K 12, Q5_K 13, Q6_K 14, IQ2_XXS 16, IQ3_S 21, IQ4_XS 23. Weights are the raw GGUF block bytes, rows of
+ * `cols` values, row r at ptr + r * row_bytes (src/weights.rs:11-37), no repacking at upload. */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct strata_ctx strata_ctx;
+
+/* GpuTensor (src/backend.rs:32-45): `rows` x `cols` of type `ty` from device address `ptr`. */
+typedef struct {
+    int32_t ty;
+    int32_t reserved;
+    uint64_t rows;
+    uint64_t cols;
+    uint64_t ptr;
+} strata_tensor;
+
+/* Activation numerics. STRATA_NUM_Q8K quantizes x as the reference CPU path does (quantize_q8k,
+ * src/cpu_moe.rs:28-46: one scale per 256 values, -127 / the signed value of largest magnitude, ties to even), so
+ * results match cpu_moe::matvec to accumulation order; it is what the reference GPU does under
+ * STRATA_LLAMA_NUMERICS (src/cuda/kernels.cu:619-651). STRATA_NUM_Q8_32 is the reference GPU default (one scale
+ * per 32 values, max / 127; src/cuda/kernels.cu:640-660). Both write the quant_xq layout. */
+enum { STRATA_NUM_Q8K = 0, STRATA_NUM_Q8_32 = 1 };
+
+/* `gemm` act flags (src/backend.rs:187-191, SAME_X at src/backend.rs:91). */
+enum { STRATA_ACT_STORE = 0, STRATA_ACT_SWIGLU = 1, STRATA_ACT_ADD = 2, STRATA_SAME_X = 4 };
+
+/* ---- context, memory and queue: backend::open and the memory methods of Backend ---- */
+
+/* backend::open (src/backend.rs:60-75) -> cuda::Gpu::new (src/cuda/mod.rs:464-526): bind GPU `device`, create the
+ * context's stream and scratch. */
+int strata_open(int device, strata_ctx** out);
+void strata_close(strata_ctx* ctx);
+/* Message of the last failed call on this thread ("" if none). */
+const char* strata_last_error(void);
+/* Backend::device (src/backend.rs:102). */
+int strata_device_name(strata_ctx* ctx, char* buf, size_t len);
+/* Activation numerics for every later op (default STRATA_NUM_Q8K). */
+int strata_set_numerics(strata_ctx* ctx, int mode);
+int strata_get_numerics(strata_ctx* ctx);
+/* Backend::alloc (src/backend.rs:108): zeroed, at least 1 byte, 256-byte aligned. */
+int strata_alloc(strata_ctx* ctx, size_t bytes, uint64_t* addr);
+/* Dropping the last Buf clone (src/backend.rs:18-30). */
+int strata_free(strata_ctx* ctx, uint64_t addr);
+/* Backend::htod / dtoh / dtod (src/backend.rs:109-111): synchronous; the device range must lie inside one
+ * allocation of this context (the reference bounds-checks against the Buf, src/cuda/mod.rs:789,816,825). */
+int strata_htod(strata_ctx* ctx, const void* src, uint64_t dst, size_t bytes);
+int strata_dtoh(strata_ctx* ctx, uint64_t src, void* dst, size_t bytes);
+int strata_dtod(strata_ctx* ctx, uint64_t src, uint64_t dst, size_t bytes);
+/* Backend::memset (src/backend.rs:113): zero `bytes` from dst, queued. */
+int strata_memset(strata_ctx* ctx, uint64_t dst, size_t bytes);
+/* Backend::mem_info (src/backend.rs:115). */
+int strata_mem_info(strata_ctx* ctx, size_t* free_bytes, size_t* total_bytes);
+/* Backend::sync (src/backend.rs:117). */
+int strata_sync(strata_ctx* ctx);
+/* The context's HIP stream (a hipStream_t), for callers that order their own work against it. */
+void* strata_stream(strata_ctx* ctx);
+
+/* ---- dequant and activation quantization ---- */
+
+/* Backend::dequant (src/backend.rs:227-228): out = the first `rows` rows of w as f32, bit-identical to
+ * quant::dequant_row (src/quant/mod.rs:65-91). */
+int strata_dequant(strata_ctx* ctx, const strata_tensor* w, uint64_t rows, uint64_t out);
+/* Backend::quant_xq (src/backend.rs:229-231): nt rows of n floats (row t at x + 4 t x_stride bytes) into nt * n
+ * int8 then nt * n / 32 f32 scales (one per 32 values), nt * (n + n / 8) bytes, under the context's numerics.
+ * n must be a multiple of 32. */
+int strata_quant_xq(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t n, uint64_t nt, uint64_t out);
+
+/* ---- decode GEMV ---- */
+
+/* Backend::gemv (src/backend.rs:199): y = W x over all rows. cols must be a multiple of 256 (of 32 for Q8_0),
+ * as Gpu::gemv_cols requires (src/cuda/mod.rs:567-571). */
+int strata_gemv(strata_ctx* ctx, const strata_tensor* w, uint64_t x, uint64_t y);
+/* Backend::gemvn (src/backend.rs:202): y[t] = W x[t] for t < nt (1..4), each weight block read once; bit-equal
+ * to strata_gemv per input. */
+int strata_gemvn(strata_ctx* ctx, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t y,
+                 uint64_t y_stride, uint64_t nt);
+/* Backend::gemvq (src/backend.rs:204): strata_gemvn reading x pre-quantized by strata_quant_xq at xq (0 =
+ * quantize x itself). */
+int strata_gemvq(strata_ctx* ctx, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t xq, uint64_t y,
+                 uint64_t y_stride, uint64_t nt);
+/* Backend::gemvq2 (src/backend.rs:206-209): gemvq of a into ya and of b into yb on the same x, one launch when the
+ * types and column counts agree (src/cuda/mod.rs:936-944). */
+int strata_gemvq2(strata_ctx* ctx, const strata_tensor* a, const strata_tensor* b, uint64_t x, uint64_t x_stride,
+                  uint64_t xq, uint64_t ya, uint64_t yb, uint64_t nt);
+/* Backend::moe_gemv (src/backend.rs:223-226): for j < k with ids[j] >= 0, y[j] (rows floats at y + 4 j rows bytes)
+ * = W_j x[j / xg], W_j the rows x cols matrix of type ty at w + ids[j] * stride bytes; slots with ids[j] < 0 are
+ * left untouched. has_pair: also the matrices at byte offset w2 into outputs at byte offset y2 (the paired gate/up
+ * launch). xq != 0: x pre-quantized by strata_quant_xq (k / xg rows), read in place of x. */
+int strata_moe_gemv(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
+                    uint64_t ids, uint64_t k, uint64_t x, uint64_t x_stride, uint64_t xg, uint64_t y,
+                    int has_pair, int64_t w2, int64_t y2, uint64_t xq);
+
+/* ---- MoE routing and combine ---- */
+
+/* Backend::router_topk (src/backend.rs:411-412; kernel src/cuda/kernels.cu:2633-2686): for each of t tokens, softmax
+ * (or sigmoid) over n logits, the k largest (ties to the lower index, ops::top_k src/ops.rs:102-107), weights
+ * renormalised by 1 / max(sum, 6.1035e-5) times extra_scale (when not 0). ids / wts: rows of k. n <= 512,
+ * k <= 32, else an error (src/cuda/mod.rs:1214-1218). */
+int strata_router_topk(strata_ctx* ctx, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t ids,
+                       uint64_t wts, uint64_t t, int sigmoid);
+/* Backend::moe_route with mb = 0 (src/backend.rs:413-417, moe_mailbox_optional 424; kernel
+ * src/cuda/kernels.cu:2693-2723): router_topk, then slots[j] = table[ids[j]] (-1: not resident) and wh[j] =
+ * wts[j] on a hit, else 0. */
+int strata_moe_route(strata_ctx* ctx, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t table,
+                     uint64_t ids, uint64_t wts, uint64_t slots, uint64_t wh, uint64_t t, int sigmoid);
+/* Backend::swiglu_q (src/backend.rs:313-318; kernel src/cuda/kernels.cu:1826-1839): silu(g) * u over `rows` rows
+ * of n floats, quantized into xq as strata_quant_xq does; g is left as is. *ret = xq (the address the following
+ * GEMV reads). */
+int strata_swiglu_q(strata_ctx* ctx, uint64_t g, uint64_t u, uint64_t n, uint64_t rows, uint64_t xq, uint64_t* ret);
+/* Backend::moe_combine with mb = 0 (src/backend.rs:418-419; kernel src/cuda/kernels.cu:2742-2773): per token,
+ * x += sum_{j<k, w[j] != 0} w[j] ye[j] (+ sigmoid(sg) sh, or + sh when sg is 0; sh 0 = no shared expert). */
+int strata_moe_combine(strata_ctx* ctx, uint64_t x, uint64_t ye, uint64_t w, uint64_t k, uint64_t sh, uint64_t sg,
+                       uint64_t n, uint64_t t);
+/* Backend::moe_down_combine with mb = 0 (src/backend.rs:436-442): moe_gemv of the down experts (k slots per token,
+ * x = h rows of cols, pre-quantized at xq when not 0) into ye, then moe_combine of ye into x with weights wh. */
+int strata_moe_down_combine(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
+                            uint64_t slots, uint64_t k, uint64_t h, uint64_t ye, uint64_t xq, uint64_t x, uint64_t wh,
+                            uint64_t sh, uint64_t sg, uint64_t t);
+/* Backend::moe_combine_seq (src/backend.rs:356; kernel src/cuda/kernels.cu:2776-2785): x[t] += sum_{j<k}
+ * wts[t, j] ye[inv[t, j]] (+ sigmoid(sg[t]) sh[t], or + sh[t] when sg is 0; sh 0 = none), j in order. */
+int strata_moe_combine_seq(strata_ctx* ctx, uint64_t x, uint64_t ye, uint64_t wts, uint64_t inv, uint64_t k,
+                           uint64_t sh, uint64_t sg, uint64_t n, uint64_t t);
+
+/* ---- prefill grouped GEMM ---- */
+
+/* The host half of GpuModel's prefill MoE block moved onto the device (src/gpu_model/prefill.rs:554-575 and the
+ * tile builder 618-642): sorts the (token, j) pairs by expert stably, writes off[n_expert + 1] (exclusive prefix counts),
+ * xrow[t * k] (token of each sorted slot), inv[t * k] (slot of pair t * k + j), and for each of the n_mats
+ * matrices m a tile list of 16-byte tiles [w_m(e), m0 | cnt << 32] (chunks of at most 128 slots per expert,
+ * experts ascending, w_m(e) = bases[m] + e * strides[m]) at tiles + m * max_tiles * 16. The tile count is written
+ * to *n_tiles_dev (device int32). max_tiles must be at least t * k / 128 + n_expert. No host synchronisation:
+ * pass the same max_tiles and n_tiles_dev to strata_gemm_grouped. An id outside 0..n_expert is replaced by no
+ * tile, counted in err_dev (device int32, may be 0), and the caller checks it after a sync (the reference fails the
+ * prefill there, src/gpu_model/prefill.rs:557-560). */
+int strata_moe_sort(strata_ctx* ctx, uint64_t ids, uint64_t t, uint64_t k, uint64_t n_expert, uint64_t off,
+                    uint64_t xrow, uint64_t inv, uint64_t n_mats, const uint64_t* bases, const uint64_t* strides,
+                    uint64_t tiles, uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t err_dev);
+/* Backend::gemm (src/backend.rs:187-191): for each tile [w, m0 | cnt << 32] of the device tile list, positions
+ * m0 .. m0 + cnt get y[m, 0..rows] (op) W x[xrow[m]] (x row m when xrow is 0), W the rows x cols matrix of type ty
+ * at w. act: STRATA_ACT_STORE, STRATA_ACT_SWIGLU (y = silu(y) * result), STRATA_ACT_ADD, | STRATA_SAME_X (x is
+ * unchanged since the previous gemm that read it: its int8 copy is reused). n_x: rows of x the tiles read. cols
+ * must be a multiple of 256 (the reference needs 64, src/cuda/mod.rs:584; every hot-path shape is a multiple of
+ * 256). */
+int strata_gemm(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t n_tiles, uint64_t x,
+                uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y, uint64_t y_stride, int act);
+/* strata_gemm with the tile count read on the device from n_tiles_dev (at most max_tiles), as strata_moe_sort
+ * leaves it: no host round trip between routing and the expert GEMMs. */
+int strata_gemm_grouped(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t max_tiles,
+                        uint64_t n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y,
+                        uint64_t y_stride, int act);
+/* Backend::gemm_dense (src/backend.rs:196): y[m] (op) W x[m] for m < n, one matrix (tiles of 128 positions,
+ * src/cuda/mod.rs:908-910). */
+int strata_gemm_dense(strata_ctx* ctx, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride, uint64_t y,
+                      uint64_t y_stride, int act);
+/* Backend::int8_gemm (src/backend.rs:192-194): 1 if gemm of type ty runs on int8 matrix cores (every supported
+ * type does here), 0 for an unsupported type. */
+int strata_int8_gemm(strata_ctx* ctx, int ty);
+/* Backend::prequant_gemm_x (src/backend.rs:197): quantize x (n rows) ahead, for a later gemm with STRATA_SAME_X. */
+int strata_prequant_gemm_x(strata_ctx* ctx, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride);
+
+/* ---- weight quantizers (host) ----
+ * The reference has none for these types (src/quant/mod.rs:1-2 only dequantizes). These make GGUF-valid blocks
+ * from f32 rows, for synthetic weights: rows of `cols` values (a multiple of 256; 32 for Q8_0) into rows *
+ * row_bytes bytes. Any valid packing serves: parity is checked on the bytes, whatever produced them. Supports
+ * Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K and IQ4_XS. Threads over rows. */
+int strata_quantize_rows(int ty, const float* src, uint64_t rows, uint64_t cols, uint8_t* dst);
+/* Bytes of one row of `cols` values of type ty (GgmlType::row_bytes, src/quant/mod.rs:47); 0 if unsupported. */
+uint64_t strata_row_bytes(int ty, uint64_t cols);
+
+/* ---- measurement (no counterpart in the reference: its harness times with CUDA events, tests/kernels.rs:270-331) */
+
+/* A HIP event recorded on the context's stream; elapsed milliseconds between two recorded events. */
+int strata_event_create(strata_ctx* ctx, void** ev);
+int strata_event_record(strata_ctx* ctx, void* ev);
+int strata_event_elapsed(void* start, void* end, float* ms);
+int strata_event_destroy(void* ev);
+
+#ifdef __cplusplus
+}
+#endif

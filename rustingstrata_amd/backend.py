@@ -1,0 +1,316 @@
+"""Host side of the MI355X backend: the reference's `Backend` trait (src/backend.rs:98-443) for the quantized-matmul
+hot path, over the C ABI of libstrata_hip.so (include/strata_hip.h).
+
+Method names, argument meaning and error behaviour follow the trait: device addresses are ints, strides are in
+floats, ops queue in order on one stream, host copies are synchronous, and an op that rejects its arguments raises
+StrataError (the trait's `Err`) without launching anything. `Buf` and `GpuTensor` mirror src/backend.rs:18-45.
+
+The library must be built (rustingstrata_amd/build.py); nothing here falls back to another implementation.
+"""
+import ctypes
+import os
+import weakref
+
+import numpy as np
+
+from . import ggml
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstrata_hip.so")
+NUM_Q8K, NUM_Q8_32 = 0, 1
+ACT_STORE, ACT_SWIGLU, ACT_ADD, SAME_X = 0, 1, 2, 4
+GEMM_BM = 128  # positions per tile (src/backend.rs:16)
+
+
+class StrataError(RuntimeError):
+    """An op refused its arguments or a HIP call failed (the trait's anyhow::Error)."""
+
+
+class _Tensor(ctypes.Structure):
+    _fields_ = [("ty", ctypes.c_int32), ("reserved", ctypes.c_int32), ("rows", ctypes.c_uint64),
+                ("cols", ctypes.c_uint64), ("ptr", ctypes.c_uint64)]
+
+
+U64, I64, I32, F32, P = ctypes.c_uint64, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_void_p
+TP = ctypes.POINTER(_Tensor)
+CTX = ctypes.c_void_p
+
+# name -> argument types (every function returns int status unless listed in _RESTYPES)
+SIGNATURES = {
+    "strata_open": [I32, ctypes.POINTER(CTX)],
+    "strata_close": [CTX],
+    "strata_last_error": [],
+    "strata_device_name": [CTX, ctypes.c_char_p, ctypes.c_size_t],
+    "strata_set_numerics": [CTX, I32],
+    "strata_get_numerics": [CTX],
+    "strata_alloc": [CTX, ctypes.c_size_t, ctypes.POINTER(U64)],
+    "strata_free": [CTX, U64],
+    "strata_htod": [CTX, P, U64, ctypes.c_size_t],
+    "strata_dtoh": [CTX, U64, P, ctypes.c_size_t],
+    "strata_dtod": [CTX, U64, U64, ctypes.c_size_t],
+    "strata_memset": [CTX, U64, ctypes.c_size_t],
+    "strata_mem_info": [CTX, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
+    "strata_sync": [CTX],
+    "strata_stream": [CTX],
+    "strata_dequant": [CTX, TP, U64, U64],
+    "strata_quant_xq": [CTX, U64, U64, U64, U64, U64],
+    "strata_gemv": [CTX, TP, U64, U64],
+    "strata_gemvn": [CTX, TP, U64, U64, U64, U64, U64],
+    "strata_gemvq": [CTX, TP, U64, U64, U64, U64, U64, U64],
+    "strata_gemvq2": [CTX, TP, TP, U64, U64, U64, U64, U64, U64],
+    "strata_moe_gemv": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32, I64, I64, U64],
+    "strata_router_topk": [CTX, U64, U64, U64, F32, U64, U64, U64, I32],
+    "strata_moe_route": [CTX, U64, U64, U64, F32, U64, U64, U64, U64, U64, U64, I32],
+    "strata_swiglu_q": [CTX, U64, U64, U64, U64, U64, ctypes.POINTER(U64)],
+    "strata_moe_combine": [CTX, U64, U64, U64, U64, U64, U64, U64, U64],
+    "strata_moe_down_combine": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64],
+    "strata_moe_combine_seq": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64],
+    "strata_moe_sort": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.POINTER(U64), ctypes.POINTER(U64),
+                        U64, U64, U64, U64],
+    "strata_gemm": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32],
+    "strata_gemm_grouped": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32],
+    "strata_gemm_dense": [CTX, TP, U64, U64, U64, U64, U64, I32],
+    "strata_int8_gemm": [CTX, I32],
+    "strata_prequant_gemm_x": [CTX, TP, U64, U64, U64],
+    "strata_quantize_rows": [I32, P, U64, U64, P],
+    "strata_row_bytes": [I32, U64],
+    "strata_event_create": [CTX, ctypes.POINTER(P)],
+    "strata_event_record": [CTX, P],
+    "strata_event_elapsed": [P, P, ctypes.POINTER(F32)],
+    "strata_event_destroy": [P],
+}
+_RESTYPES = {"strata_close": None, "strata_last_error": ctypes.c_char_p, "strata_stream": P, "strata_row_bytes": U64}
+
+_lib = None
+
+
+def lib():
+    """The loaded library. Raises if it is not built: there is no fallback path."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise StrataError(f"{LIB_PATH} is not built: run rustingstrata_amd/build.py (or __graft_entry__.build())")
+        l = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            f = getattr(l, name)
+            f.argtypes = args
+            f.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = l
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise StrataError(lib().strata_last_error().decode())
+
+
+def quantize_rows(ty, w):
+    """f32 rows -> GGUF blocks of type ty (uint8 [rows, row_bytes]) with the library's host quantizer."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    out = np.empty((rows, ggml.row_bytes(ty, cols)), dtype=np.uint8)
+    if lib().strata_quantize_rows(ty, w.ctypes.data, rows, cols, out.ctypes.data) != 0:
+        raise StrataError(f"no host quantizer for {ggml.name(ty)} with {cols} columns")
+    return out
+
+
+class Buf:
+    """`len` bytes of device memory at `addr`, freed when the last reference drops (src/backend.rs:18-30)."""
+
+    def __init__(self, backend, addr, length):
+        self.addr, self.len = addr, length
+        self._fin = weakref.finalize(self, HipBackend._free_addr, backend._ctx_ref, addr)
+
+    def __int__(self):
+        return self.addr
+
+
+class GpuTensor:
+    """`rows` x `cols` of type `ty` from device address `ptr` (src/backend.rs:32-45); keeps its Buf alive."""
+
+    def __init__(self, ty, rows, cols, buf, offset=0):
+        self.ty, self.rows, self.cols, self.buf = ty, rows, cols, buf
+        self.ptr = int(buf) + offset
+
+    def bytes(self):
+        return ggml.row_bytes(self.ty, self.cols) * self.rows
+
+    def _c(self):
+        return ctypes.byref(_Tensor(self.ty, 0, self.rows, self.cols, self.ptr))
+
+
+class _CtxRef:
+    def __init__(self, ctx):
+        self.ctx = ctx
+
+
+class HipBackend:
+    """The MI355X backend (the counterpart of cuda::Gpu, src/cuda/mod.rs)."""
+
+    name = "hip"
+
+    def __init__(self, device=0, numerics=NUM_Q8K):
+        l = lib()
+        ctx = CTX()
+        _check(l.strata_open(device, ctypes.byref(ctx)))
+        self._ctx = ctx
+        self._ctx_ref = _CtxRef(ctx)
+        self._fin = weakref.finalize(self, HipBackend._close, self._ctx_ref)
+        self.set_numerics(numerics)
+
+    @staticmethod
+    def _close(ref):
+        if ref.ctx is not None:
+            lib().strata_close(ref.ctx)
+            ref.ctx = None
+
+    @staticmethod
+    def _free_addr(ref, addr):
+        if ref.ctx is not None:
+            lib().strata_free(ref.ctx, addr)
+
+    def close(self):
+        self._fin()
+
+    # ---- context ----
+    def device(self):
+        buf = ctypes.create_string_buffer(256)
+        _check(lib().strata_device_name(self._ctx, buf, 256))
+        return buf.value.decode()
+
+    def set_numerics(self, mode):
+        _check(lib().strata_set_numerics(self._ctx, mode))
+
+    def numerics(self):
+        return lib().strata_get_numerics(self._ctx)
+
+    # ---- memory (src/backend.rs:108-117) ----
+    def alloc(self, nbytes):
+        a = U64()
+        _check(lib().strata_alloc(self._ctx, nbytes, ctypes.byref(a)))
+        return Buf(self, a.value, max(nbytes, 1))
+
+    def htod(self, src, dst, off=0):
+        src = np.ascontiguousarray(src)
+        _check(lib().strata_htod(self._ctx, src.ctypes.data, int(dst) + off, src.nbytes))
+
+    def dtoh(self, src, off, dst):
+        assert dst.flags["C_CONTIGUOUS"]
+        _check(lib().strata_dtoh(self._ctx, int(src) + off, dst.ctypes.data, dst.nbytes))
+
+    def dtod(self, src, src_off, dst, dst_off, nbytes):
+        _check(lib().strata_dtod(self._ctx, int(src) + src_off, int(dst) + dst_off, nbytes))
+
+    def memset(self, dst, nbytes=None):
+        _check(lib().strata_memset(self._ctx, int(dst), dst.len if nbytes is None else nbytes))
+
+    def mem_info(self):
+        f, t = ctypes.c_size_t(), ctypes.c_size_t()
+        _check(lib().strata_mem_info(self._ctx, ctypes.byref(f), ctypes.byref(t)))
+        return f.value, t.value
+
+    def sync(self):
+        _check(lib().strata_sync(self._ctx))
+
+    # typed helpers (`put` / `get`, src/backend.rs:447-462)
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        b = self.alloc(arr.nbytes)
+        self.htod(arr, b)
+        return b
+
+    def get(self, buf, dtype, n, at=0):
+        out = np.empty(n, dtype=dtype)
+        self.dtoh(buf, at * np.dtype(dtype).itemsize, out)
+        return out
+
+    def upload_tensor(self, ty, blocks):
+        """Backend::upload_raw (src/backend.rs:179-183): raw block bytes [rows, row_bytes] as a GpuTensor."""
+        rows = blocks.shape[0]
+        cols = blocks.shape[1] // ggml.block_bytes(ty) * ggml.block_elems(ty)
+        return GpuTensor(ty, rows, cols, self.upload(blocks))
+
+    # ---- ops ----
+    def dequant(self, w, rows, out):
+        _check(lib().strata_dequant(self._ctx, w._c(), rows, int(out)))
+
+    def quant_xq(self, x, x_stride, n, nt, out):
+        _check(lib().strata_quant_xq(self._ctx, int(x), x_stride, n, nt, int(out)))
+
+    def gemv(self, w, x, y):
+        _check(lib().strata_gemv(self._ctx, w._c(), int(x), int(y)))
+
+    def gemvn(self, w, x, x_stride, y, y_stride, nt):
+        _check(lib().strata_gemvn(self._ctx, w._c(), int(x), x_stride, int(y), y_stride, nt))
+
+    def gemvq(self, w, x, x_stride, xq, y, y_stride, nt):
+        _check(lib().strata_gemvq(self._ctx, w._c(), int(x), x_stride, int(xq), int(y), y_stride, nt))
+
+    def gemvq2(self, a, b, x, x_stride, xq, ya, yb, nt):
+        _check(lib().strata_gemvq2(self._ctx, a._c(), b._c(), int(x), x_stride, int(xq), int(ya), int(yb), nt))
+
+    def moe_gemv(self, ty, rows, cols, w, stride, ids, k, x, x_stride, xg, y, pair=None, xq=0):
+        has, w2, y2 = (1, pair[0], pair[1]) if pair is not None else (0, 0, 0)
+        _check(lib().strata_moe_gemv(self._ctx, ty, rows, cols, int(w), stride, int(ids), k, int(x), x_stride, xg,
+                                     int(y), has, w2, y2, int(xq)))
+
+    def router_topk(self, p, n, k, extra_scale, ids, wts, t, sigmoid=False):
+        _check(lib().strata_router_topk(self._ctx, int(p), n, k, extra_scale, int(ids), int(wts), t, int(sigmoid)))
+
+    def moe_route(self, p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid=False):
+        _check(lib().strata_moe_route(self._ctx, int(p), n, k, extra_scale, int(table), int(ids), int(wts),
+                                      int(slots), int(wh), t, int(sigmoid)))
+
+    def swiglu_q(self, g, u, n, rows, xq):
+        r = U64()
+        _check(lib().strata_swiglu_q(self._ctx, int(g), int(u), n, rows, int(xq), ctypes.byref(r)))
+        return r.value
+
+    def moe_combine(self, x, ye, w, k, sh, sg, n, t):
+        _check(lib().strata_moe_combine(self._ctx, int(x), int(ye), int(w), k, int(sh), int(sg), n, t))
+
+    def moe_down_combine(self, ty, rows, cols, w, stride, slots, k, h, ye, xq, x, wh, sh, sg, t):
+        _check(lib().strata_moe_down_combine(self._ctx, ty, rows, cols, int(w), stride, int(slots), k, int(h),
+                                             int(ye), int(xq), int(x), int(wh), int(sh), int(sg), t))
+
+    def moe_combine_seq(self, x, ye, wts, inv, k, sh, sg, n, t):
+        _check(lib().strata_moe_combine_seq(self._ctx, int(x), int(ye), int(wts), int(inv), k, int(sh), int(sg), n, t))
+
+    def moe_sort(self, ids, t, k, n_expert, off, xrow, inv, mats, tiles, max_tiles, n_tiles_dev, err_dev=0):
+        """Device counting sort of the (token, j) pairs by expert + tile lists; mats = [(base, stride), ...]."""
+        n = len(mats)
+        bases = (U64 * max(n, 1))(*[m[0] for m in mats])
+        strides = (U64 * max(n, 1))(*[m[1] for m in mats])
+        _check(lib().strata_moe_sort(self._ctx, int(ids), t, k, n_expert, int(off), int(xrow), int(inv), n, bases,
+                                     strides, int(tiles), max_tiles, int(n_tiles_dev), int(err_dev)))
+
+    def gemm(self, ty, rows, cols, tiles, n_tiles, x, x_stride, n_x, xrow, y, y_stride, act):
+        _check(lib().strata_gemm(self._ctx, ty, rows, cols, int(tiles), n_tiles, int(x), x_stride, n_x, int(xrow),
+                                 int(y), y_stride, act))
+
+    def gemm_grouped(self, ty, rows, cols, tiles, max_tiles, n_tiles_dev, x, x_stride, n_x, xrow, y, y_stride, act):
+        _check(lib().strata_gemm_grouped(self._ctx, ty, rows, cols, int(tiles), max_tiles, int(n_tiles_dev), int(x),
+                                         x_stride, n_x, int(xrow), int(y), y_stride, act))
+
+    def gemm_dense(self, w, n, x, x_stride, y, y_stride, act):
+        _check(lib().strata_gemm_dense(self._ctx, w._c(), n, int(x), x_stride, int(y), y_stride, act))
+
+    def int8_gemm(self, ty):
+        return bool(lib().strata_int8_gemm(self._ctx, ty))
+
+    def prequant_gemm_x(self, w, n, x, x_stride):
+        _check(lib().strata_prequant_gemm_x(self._ctx, w._c(), n, int(x), x_stride))
+
+    # ---- timing on the backend's stream ----
+    def event(self):
+        e = P()
+        _check(lib().strata_event_create(self._ctx, ctypes.byref(e)))
+        return e
+
+    def record(self, e):
+        _check(lib().strata_event_record(self._ctx, e))
+
+    @staticmethod
+    def elapsed_ms(e0, e1):
+        ms = F32()
+        _check(lib().strata_event_elapsed(e0, e1, ctypes.byref(ms)))
+        return ms.value

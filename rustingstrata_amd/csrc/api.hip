@@ -1,0 +1,536 @@
+// The C ABI (include/strata_hip.h): context, memory, argument checks, and the launch sequences of the hot-path
+// Backend methods (src/backend.rs:98-443, CUDA implementation src/cuda/mod.rs:748-1242).
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "kernels.h"
+#include "moe.h"
+#include "gemm.h"
+#include "../../include/strata_hip.h"
+
+using namespace strata;
+
+namespace strata {
+
+static thread_local std::string g_err;
+
+int set_error(const std::string& msg) {
+    g_err = msg;
+    return -1;
+}
+int hip_error(hipError_t e, const char* what) {
+    return set_error(std::string("HIP error ") + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ") in " + what);
+}
+const char* type_name(int ty) {
+    switch (ty) {
+    case Q8_0: return "Q8_0";
+    case Q2_K: return "Q2_K";
+    case Q3_K: return "Q3_K";
+    case Q4_K: return "Q4_K";
+    case Q5_K: return "Q5_K";
+    case Q6_K: return "Q6_K";
+    case IQ2_XXS: return "IQ2_XXS";
+    case IQ3_S: return "IQ3_S";
+    case IQ4_XS: return "IQ4_XS";
+    }
+    return "unknown";
+}
+
+// Device scratch that grows on demand. Growing waits for the stream first: queued kernels may still read it.
+struct Scratch {
+    void* p = nullptr;
+    size_t n = 0;
+    hipError_t need(size_t bytes, hipStream_t s) {
+        if (bytes <= n) return hipSuccess;
+        if (p) {
+            hipError_t e = hipStreamSynchronize(s);
+            if (e != hipSuccess) return e;
+            hipFree(p);
+            p = nullptr;
+            n = 0;
+        }
+        size_t want = std::max(bytes, (size_t)1 << 20);
+        hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess) return e;
+        n = want;
+        return hipSuccess;
+    }
+    void release() {
+        if (p) hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+};
+
+}  // namespace strata
+
+struct strata_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int numerics = STRATA_NUM_Q8K;
+    std::mutex mu;
+    std::map<uint64_t, size_t> allocs;  // start -> bytes
+    Scratch xq;                          // quantized x of GEMV calls that pass none
+    Scratch gx;                          // quantized x of the GEMM (kept for SAME_X)
+    uint64_t gx_key[4] = {0, 0, 0, 0};   // x, x_stride, n_x, cols of gx's contents (all 0: none)
+    Scratch misc;
+};
+
+namespace {
+
+int check_ctx(strata_ctx* c) {
+    if (!c) return set_error("null strata context");
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return hip_error(e, "hipSetDevice");
+    return 0;
+}
+
+// The allocation of this context holding [a, a + n).
+bool in_alloc(strata_ctx* c, uint64_t a, size_t n) {
+    std::lock_guard<std::mutex> g(c->mu);
+    auto it = c->allocs.upper_bound(a);
+    if (it == c->allocs.begin()) return false;
+    --it;
+    return a >= it->first && a + n <= it->first + it->second && a + n >= a;
+}
+
+int check_type(int ty) {
+    if (!supported(ty))
+        return set_error("unsupported quant type (ggml type id " + std::to_string(ty) +
+                         "); this backend decodes Q8_0 Q2_K Q3_K Q4_K Q5_K Q6_K IQ2_XXS IQ3_S IQ4_XS");
+    return 0;
+}
+
+// Gpu::gemv_cols (src/cuda/mod.rs:567-571), with this backend's requirement of whole 256-value super-blocks for the
+// K and IQ types (the reference's `_p` kernels cover partial ones; no hot-path shape has them).
+int check_gemv_cols(int ty, uint64_t cols) {
+    uint64_t b = ty == Q8_0 ? 32 : 256;
+    if (cols == 0 || cols % b)
+        return set_error(std::string(type_name(ty)) + " tensor with " + std::to_string(cols) +
+                         " columns: GEMV needs a multiple of " + std::to_string(b));
+    if (row_bytes(ty, cols) > gemv_max_row_bytes())
+        return set_error(std::string(type_name(ty)) + " tensor with " + std::to_string(cols) +
+                         " columns: a row exceeds the GEMV tile (" + std::to_string(gemv_max_row_bytes()) + " bytes)");
+    if (cols > 16384)
+        return set_error("GEMV with " + std::to_string(cols) + " columns: at most 16384");
+    return 0;
+}
+
+// Weight address alignment the decoders assume (super-block start alignment mod 16).
+int check_align(int ty, uint64_t addr, const char* what) {
+    uint64_t a = ty == Q4_K || ty == Q5_K ? 16 : ty == IQ4_XS ? 8 : ty == Q2_K ? 4 : 2;
+    if (addr % a)
+        return set_error(std::string(what) + ": " + type_name(ty) + " weights at a " + std::to_string(addr % a) +
+                         "-misaligned address (need " + std::to_string(a) + "-byte alignment)");
+    return 0;
+}
+
+// Quantize x (nt rows, x_stride apart) into the context's GEMV scratch; returns the scratch address.
+int quant_into_scratch(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t n, uint64_t nt, uint64_t* out) {
+    STRATA_HIP(c->xq.need(xq_bytes(n, nt), c->stream));
+    STRATA_HIP(launch_quant_xq((const float*)x, x_stride, (int)n, (int)nt, (int8_t*)c->xq.p, c->numerics, c->stream));
+    *out = (uint64_t)c->xq.p;
+    return 0;
+}
+
+int check_tensor(const strata_tensor* w, const char* what) {
+    if (!w) return set_error(std::string(what) + ": null tensor");
+    if (check_type(w->ty)) return -1;
+    if (!w->ptr && w->rows) return set_error(std::string(what) + ": null weight address");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* strata_last_error(void) { return g_err.c_str(); }
+
+int strata_open(int device, strata_ctx** out) {
+    if (!out) return set_error("strata_open: null out");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return hip_error(e, "hipGetDeviceCount");
+    if (device < 0 || device >= n) return set_error("strata_open: GPU " + std::to_string(device) + " of " + std::to_string(n));
+    STRATA_HIP(hipSetDevice(device));
+    strata_ctx* c = new strata_ctx();
+    c->device = device;
+    e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) { delete c; return hip_error(e, "hipStreamCreate"); }
+    *out = c;
+    return 0;
+}
+
+void strata_close(strata_ctx* c) {
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    for (auto& kv : c->allocs) hipFree((void*)kv.first);
+    c->xq.release();
+    c->gx.release();
+    c->misc.release();
+    hipStreamDestroy(c->stream);
+    delete c;
+}
+
+int strata_device_name(strata_ctx* c, char* buf, size_t len) {
+    if (check_ctx(c)) return -1;
+    hipDeviceProp_t p;
+    STRATA_HIP(hipGetDeviceProperties(&p, c->device));
+    if (buf && len) {
+        std::snprintf(buf, len, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    }
+    return 0;
+}
+
+int strata_set_numerics(strata_ctx* c, int mode) {
+    if (!c) return set_error("null strata context");
+    if (mode != STRATA_NUM_Q8K && mode != STRATA_NUM_Q8_32) return set_error("strata_set_numerics: mode " + std::to_string(mode));
+    c->numerics = mode;
+    c->gx_key[0] = c->gx_key[1] = c->gx_key[2] = c->gx_key[3] = 0;
+    return 0;
+}
+int strata_get_numerics(strata_ctx* c) { return c ? c->numerics : -1; }
+
+int strata_alloc(strata_ctx* c, size_t bytes, uint64_t* addr) {
+    if (check_ctx(c)) return -1;
+    if (!addr) return set_error("strata_alloc: null out");
+    size_t n = std::max(bytes, (size_t)1);
+    void* p = nullptr;
+    STRATA_HIP(hipMalloc(&p, (n + 255) & ~(size_t)255));
+    hipError_t e = hipMemsetAsync(p, 0, n, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) { hipFree(p); return hip_error(e, "zeroing a new buffer"); }
+    {
+        std::lock_guard<std::mutex> g(c->mu);
+        c->allocs[(uint64_t)p] = n;
+    }
+    *addr = (uint64_t)p;
+    return 0;
+}
+
+int strata_free(strata_ctx* c, uint64_t addr) {
+    if (check_ctx(c)) return -1;
+    {
+        std::lock_guard<std::mutex> g(c->mu);
+        auto it = c->allocs.find(addr);
+        if (it == c->allocs.end()) return set_error("strata_free: not an allocation of this context");
+        c->allocs.erase(it);
+    }
+    STRATA_HIP(hipStreamSynchronize(c->stream));
+    STRATA_HIP(hipFree((void*)addr));
+    return 0;
+}
+
+int strata_htod(strata_ctx* c, const void* src, uint64_t dst, size_t bytes) {
+    if (check_ctx(c)) return -1;
+    if (!bytes) return 0;
+    if (!in_alloc(c, dst, bytes)) return set_error("htod: " + std::to_string(bytes) + " bytes outside the destination buffer");
+    STRATA_HIP(hipMemcpyAsync((void*)dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    STRATA_HIP(hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int strata_dtoh(strata_ctx* c, uint64_t src, void* dst, size_t bytes) {
+    if (check_ctx(c)) return -1;
+    if (!bytes) return 0;
+    if (!in_alloc(c, src, bytes)) return set_error("dtoh: " + std::to_string(bytes) + " bytes outside the source buffer");
+    STRATA_HIP(hipMemcpyAsync(dst, (const void*)src, bytes, hipMemcpyDeviceToHost, c->stream));
+    STRATA_HIP(hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+int strata_dtod(strata_ctx* c, uint64_t src, uint64_t dst, size_t bytes) {
+    if (check_ctx(c)) return -1;
+    if (!bytes) return 0;
+    if (!in_alloc(c, src, bytes) || !in_alloc(c, dst, bytes)) return set_error("dtod: range outside its buffer");
+    STRATA_HIP(hipMemcpyAsync((void*)dst, (const void*)src, bytes, hipMemcpyDeviceToDevice, c->stream));
+    return 0;
+}
+
+int strata_memset(strata_ctx* c, uint64_t dst, size_t bytes) {
+    if (check_ctx(c)) return -1;
+    if (!bytes) return 0;
+    if (!in_alloc(c, dst, bytes)) return set_error("memset: range outside its buffer");
+    STRATA_HIP(hipMemsetAsync((void*)dst, 0, bytes, c->stream));
+    return 0;
+}
+
+int strata_mem_info(strata_ctx* c, size_t* free_bytes, size_t* total_bytes) {
+    if (check_ctx(c)) return -1;
+    size_t f = 0, t = 0;
+    STRATA_HIP(hipMemGetInfo(&f, &t));
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return 0;
+}
+
+int strata_sync(strata_ctx* c) {
+    if (check_ctx(c)) return -1;
+    STRATA_HIP(hipStreamSynchronize(c->stream));
+    return 0;
+}
+
+void* strata_stream(strata_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+int strata_dequant(strata_ctx* c, const strata_tensor* w, uint64_t rows, uint64_t out) {
+    if (check_ctx(c) || check_tensor(w, "dequant")) return -1;
+    if (rows > w->rows) return set_error("dequant: " + std::to_string(rows) + " rows of a " + std::to_string(w->rows) + "-row tensor");
+    uint64_t b = w->ty == Q8_0 ? 32 : 256;
+    if (w->cols % b) return set_error(std::string(type_name(w->ty)) + " tensor with " + std::to_string(w->cols) + " columns: dequant needs a multiple of " + std::to_string(b));
+    STRATA_HIP(launch_dequant(w->ty, (const uint8_t*)w->ptr, rows, w->cols, (float*)out, c->stream));
+    return 0;
+}
+
+int strata_quant_xq(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t n, uint64_t nt, uint64_t out) {
+    if (check_ctx(c)) return -1;
+    if (n % 32) return set_error("quant_xq: " + std::to_string(n) + " values (a multiple of 32)");
+    if (n > (1u << 30) || nt > 65535) return set_error("quant_xq: too large");
+    STRATA_HIP(launch_quant_xq((const float*)x, x_stride, (int)n, (int)nt, (int8_t*)out, c->numerics, c->stream));
+    return 0;
+}
+
+int strata_gemvq(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t xq, uint64_t y,
+                 uint64_t y_stride, uint64_t nt) {
+    if (check_ctx(c) || check_tensor(w, "gemv")) return -1;
+    if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
+    if (check_gemv_cols(w->ty, w->cols) || check_align(w->ty, w->ptr, "gemv")) return -1;
+    if (w->rows == 0) return 0;
+    if (w->rows > (1u << 30)) return set_error("gemv: too many rows");
+    if (!xq && quant_into_scratch(c, x, x_stride, w->cols, nt, &xq)) return -1;
+    GemvLaunch g;
+    g.ty = w->ty; g.w = (const uint8_t*)w->ptr; g.rows = (int)w->rows; g.cols = (int)w->cols;
+    g.nt = (int)nt; g.xq = (const int8_t*)xq; g.n_xrows = (int)nt; g.y = (float*)y; g.y_stride = (int)y_stride;
+    STRATA_HIP(launch_gemv(g, c->stream));
+    return 0;
+}
+
+int strata_gemv(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t y) {
+    return strata_gemvq(c, w, x, 0, 0, y, 0, 1);
+}
+
+int strata_gemvn(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t y, uint64_t y_stride,
+                 uint64_t nt) {
+    return strata_gemvq(c, w, x, x_stride, 0, y, y_stride, nt);
+}
+
+int strata_gemvq2(strata_ctx* c, const strata_tensor* a, const strata_tensor* b, uint64_t x, uint64_t x_stride,
+                  uint64_t xq, uint64_t ya, uint64_t yb, uint64_t nt) {
+    if (check_ctx(c) || check_tensor(a, "gemvq2") || check_tensor(b, "gemvq2")) return -1;
+    // Different shapes or types: two launches (src/cuda/mod.rs:937-940).
+    if (a->ty != b->ty || a->cols != b->cols) {
+        if (strata_gemvq(c, a, x, x_stride, xq, ya, a->rows, nt)) return -1;
+        return strata_gemvq(c, b, x, x_stride, xq, yb, b->rows, nt);
+    }
+    if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
+    if (check_gemv_cols(a->ty, a->cols) || check_align(a->ty, a->ptr, "gemvq2") || check_align(b->ty, b->ptr, "gemvq2")) return -1;
+    if (!xq && quant_into_scratch(c, x, x_stride, a->cols, nt, &xq)) return -1;
+    GemvLaunch g;
+    g.ty = a->ty; g.w = (const uint8_t*)a->ptr; g.rows = (int)a->rows; g.cols = (int)a->cols;
+    g.nt = (int)nt; g.xq = (const int8_t*)xq; g.n_xrows = (int)nt; g.y = (float*)ya; g.y_stride = (int)a->rows;
+    g.pair = true; g.w2 = (int64_t)(b->ptr - a->ptr); g.y2 = (int64_t)(yb - ya); g.rows2 = (int)b->rows;
+    // The second matrix's outputs are token-strided by its own row count; one stride serves both only when equal.
+    if (nt > 1 && a->rows != b->rows) {
+        if (strata_gemvq(c, a, x, x_stride, xq, ya, a->rows, nt)) return -1;
+        return strata_gemvq(c, b, x, x_stride, xq, yb, b->rows, nt);
+    }
+    STRATA_HIP(launch_gemv(g, c->stream));
+    return 0;
+}
+
+int strata_moe_gemv(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride, uint64_t ids,
+                    uint64_t k, uint64_t x, uint64_t x_stride, uint64_t xg, uint64_t y, int has_pair, int64_t w2,
+                    int64_t y2, uint64_t xq) {
+    if (check_ctx(c) || check_type(ty)) return -1;
+    if (check_gemv_cols(ty, cols) || check_align(ty, w, "moe_gemv")) return -1;
+    if (check_align(ty, stride, "moe_gemv stride") || (has_pair && check_align(ty, (uint64_t)w2, "moe_gemv pair offset"))) return -1;
+    if (xg < 1 || k % xg) return set_error("moe_gemv: " + std::to_string(k) + " slots in groups of " + std::to_string(xg));
+    if (k == 0 || rows == 0) return 0;
+    if (k > 65535) return set_error("moe_gemv: too many slots");
+    if (!xq && quant_into_scratch(c, x, x_stride, cols, k / xg, &xq)) return -1;
+    GemvLaunch g;
+    g.ty = ty; g.w = (const uint8_t*)w; g.rows = (int)rows; g.cols = (int)cols; g.nt = 1;
+    g.xq = (const int8_t*)xq; g.n_xrows = (int)(k / xg); g.y = (float*)y; g.y_stride = 0;
+    g.ids = (const int*)ids; g.k = (int)k; g.xg = (int)xg; g.stride = (int64_t)stride;
+    g.pair = has_pair != 0; g.w2 = w2; g.y2 = y2; g.rows2 = (int)rows;
+    STRATA_HIP(launch_gemv(g, c->stream));
+    return 0;
+}
+
+int strata_router_topk(strata_ctx* c, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t ids,
+                       uint64_t wts, uint64_t t, int sigmoid) {
+    if (check_ctx(c)) return -1;
+    if (n > 512 || k > 32 || k > n || k == 0) return set_error("router_topk: " + std::to_string(n) + " experts, top " + std::to_string(k));
+    if (!t) return 0;
+    STRATA_HIP(launch_route((const float*)p, (int)n, (int)k, extra_scale, nullptr, (int*)ids, (float*)wts, nullptr,
+                            nullptr, (int)t, sigmoid, c->stream));
+    return 0;
+}
+
+int strata_moe_route(strata_ctx* c, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t table, uint64_t ids,
+                     uint64_t wts, uint64_t slots, uint64_t wh, uint64_t t, int sigmoid) {
+    if (check_ctx(c)) return -1;
+    if (n > 512 || k > 32 || k > n || k == 0) return set_error("moe_route: " + std::to_string(n) + " experts, top " + std::to_string(k));
+    if (!table || !slots || !wh) return set_error("moe_route: null table, slots or wh");
+    if (!t) return 0;
+    STRATA_HIP(launch_route((const float*)p, (int)n, (int)k, extra_scale, (const int*)table, (int*)ids, (float*)wts,
+                            (int*)slots, (float*)wh, (int)t, sigmoid, c->stream));
+    return 0;
+}
+
+int strata_swiglu_q(strata_ctx* c, uint64_t g, uint64_t u, uint64_t n, uint64_t rows, uint64_t xq, uint64_t* ret) {
+    if (check_ctx(c)) return -1;
+    if (n % 32) return set_error("swiglu_q: " + std::to_string(n) + " values (a multiple of 32)");
+    if (!xq) return set_error("swiglu_q: null xq");
+    STRATA_HIP(launch_swiglu_q((const float*)g, (const float*)u, (int)n, (int)rows, (int8_t*)xq, c->numerics, c->stream));
+    if (ret) *ret = xq;
+    return 0;
+}
+
+int strata_moe_combine(strata_ctx* c, uint64_t x, uint64_t ye, uint64_t w, uint64_t k, uint64_t sh, uint64_t sg,
+                       uint64_t n, uint64_t t) {
+    if (check_ctx(c)) return -1;
+    if (!n || !t) return 0;
+    STRATA_HIP(launch_combine((float*)x, (const float*)ye, (const float*)w, (int)k, (const float*)sh, (const float*)sg,
+                              (int)n, (int)t, c->stream));
+    return 0;
+}
+
+int strata_moe_down_combine(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
+                            uint64_t slots, uint64_t k, uint64_t h, uint64_t ye, uint64_t xq, uint64_t x, uint64_t wh,
+                            uint64_t sh, uint64_t sg, uint64_t t) {
+    if (strata_moe_gemv(c, ty, rows, cols, w, stride, slots, t * k, h, cols, 1, ye, 0, 0, 0, xq)) return -1;
+    return strata_moe_combine(c, x, ye, wh, k, sh, sg, rows, t);
+}
+
+int strata_moe_combine_seq(strata_ctx* c, uint64_t x, uint64_t ye, uint64_t wts, uint64_t inv, uint64_t k, uint64_t sh,
+                           uint64_t sg, uint64_t n, uint64_t t) {
+    if (check_ctx(c)) return -1;
+    if (!n || !t) return 0;
+    STRATA_HIP(launch_combine_seq((float*)x, (const float*)ye, (const float*)wts, (const int*)inv, (int)k,
+                                  (const float*)sh, (const float*)sg, (int)n, (int)t, c->stream));
+    return 0;
+}
+
+int strata_moe_sort(strata_ctx* c, uint64_t ids, uint64_t t, uint64_t k, uint64_t n_expert, uint64_t off,
+                    uint64_t xrow, uint64_t inv, uint64_t n_mats, const uint64_t* bases, const uint64_t* strides,
+                    uint64_t tiles, uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t err_dev) {
+    if (check_ctx(c)) return -1;
+    if (n_expert == 0 || n_expert > 512) return set_error("moe_sort: " + std::to_string(n_expert) + " experts (1 to 512)");
+    if (n_mats > 3 || (n_mats && (!bases || !strides))) return set_error("moe_sort: at most 3 matrices, with bases and strides");
+    if (t * k > (1u << 30)) return set_error("moe_sort: too many pairs");
+    if (max_tiles < (t * k) / 128 + n_expert) return set_error("moe_sort: max_tiles " + std::to_string(max_tiles) + " < pairs / 128 + experts");
+    SortLaunch s;
+    s.ids = (const int*)ids; s.t = (int)t; s.k = (int)k; s.n_expert = (int)n_expert;
+    s.off = (int*)off; s.xrow = (int*)xrow; s.inv = (int*)inv;
+    s.n_mats = (int)n_mats;
+    for (uint64_t m = 0; m < n_mats; m++) { s.bases[m] = bases[m]; s.strides[m] = strides[m]; }
+    s.tiles = (uint64_t*)tiles; s.max_tiles = (int)max_tiles; s.n_tiles = (int*)n_tiles_dev; s.err = (int*)err_dev;
+    STRATA_HIP(c->misc.need(sort_scratch_bytes((int)n_expert), c->stream));
+    s.scratch = (int*)c->misc.p;
+    STRATA_HIP(launch_sort(s, c->stream));
+    return 0;
+}
+
+// GEMM X quantization, cached for SAME_X (Gpu::q8_x, src/cuda/mod.rs:626-636).
+static int gemm_x(strata_ctx* c, uint64_t cols, uint64_t n_x, uint64_t x, uint64_t x_stride, int same, uint64_t* out) {
+    uint64_t key[4] = {x, x_stride, n_x, cols};
+    bool hit = same && std::equal(key, key + 4, c->gx_key);
+    if (!hit) {
+        c->gx_key[0] = c->gx_key[1] = c->gx_key[2] = c->gx_key[3] = 0;
+        STRATA_HIP(c->gx.need(gemm_x_bytes(cols, n_x), c->stream));
+        STRATA_HIP(launch_gemm_quant_x((const float*)x, x_stride, (int)cols, (int)n_x, (uint8_t*)c->gx.p, c->numerics, c->stream));
+        std::copy(key, key + 4, c->gx_key);
+    }
+    *out = (uint64_t)c->gx.p;
+    return 0;
+}
+
+static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t n_tiles,
+                       const int* n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y,
+                       uint64_t y_stride, int act, const uint8_t* dense_w, uint64_t dense_n) {
+    if (check_ctx(c) || check_type(ty)) return -1;
+    if (cols == 0 || cols % 256)
+        return set_error(std::string(type_name(ty)) + " matrix with " + std::to_string(cols) + " columns: GEMM needs a multiple of 256");
+    int op = act & ~STRATA_SAME_X;
+    if (op < 0 || op > 2) return set_error("gemm: act " + std::to_string(act));
+    if (dense_w && check_align(ty, (uint64_t)dense_w, "gemm_dense")) return -1;
+    if (n_tiles == 0 || rows == 0) return 0;
+    if (rows > (1u << 24) || n_tiles > 65535 * 64) return set_error("gemm: too large");
+    uint64_t xq = 0;
+    if (gemm_x(c, cols, n_x, x, x_stride, act & STRATA_SAME_X, &xq)) return -1;
+    GemmLaunch g;
+    g.ty = ty; g.rows = (int)rows; g.cols = (int)cols;
+    g.tiles = (const uint64_t*)tiles; g.n_tiles = (int)n_tiles; g.n_tiles_dev = n_tiles_dev;
+    g.dense_w = dense_w; g.dense_n = (int)dense_n;
+    g.xq = (const uint8_t*)xq; g.n_x = (int)n_x; g.xrow = (const int*)xrow;
+    g.y = (float*)y; g.y_stride = (int64_t)y_stride; g.act = op;
+    STRATA_HIP(launch_gemm(g, c->stream));
+    return 0;
+}
+
+int strata_gemm(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t n_tiles, uint64_t x,
+                uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y, uint64_t y_stride, int act) {
+    if (!tiles && n_tiles) return set_error("gemm: null tile list");
+    return gemm_common(c, ty, rows, cols, tiles, n_tiles, nullptr, x, x_stride, n_x, xrow, y, y_stride, act, nullptr, 0);
+}
+
+int strata_gemm_grouped(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t max_tiles,
+                        uint64_t n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y,
+                        uint64_t y_stride, int act) {
+    if (!tiles || !n_tiles_dev) return set_error("gemm_grouped: null tile list or count");
+    return gemm_common(c, ty, rows, cols, tiles, max_tiles, (const int*)n_tiles_dev, x, x_stride, n_x, xrow, y, y_stride,
+                       act, nullptr, 0);
+}
+
+int strata_gemm_dense(strata_ctx* c, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride, uint64_t y,
+                      uint64_t y_stride, int act) {
+    if (check_tensor(w, "gemm_dense")) return -1;
+    uint64_t nt = (n + 127) / 128;
+    return gemm_common(c, w->ty, w->rows, w->cols, 0, nt, nullptr, x, x_stride, n, 0, y, y_stride, act,
+                       (const uint8_t*)w->ptr, n);
+}
+
+int strata_int8_gemm(strata_ctx* c, int ty) {
+    (void)c;
+    return supported(ty) ? 1 : 0;
+}
+
+int strata_prequant_gemm_x(strata_ctx* c, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride) {
+    if (check_ctx(c) || check_tensor(w, "prequant_gemm_x")) return -1;
+    if (w->cols % 256) return set_error("prequant_gemm_x: " + std::to_string(w->cols) + " columns (a multiple of 256)");
+    uint64_t xq;
+    return gemm_x(c, w->cols, n, x, x_stride, 1, &xq);
+}
+
+uint64_t strata_row_bytes(int ty, uint64_t cols) {
+    if (!supported(ty) || cols % block_elems(ty)) return 0;
+    return row_bytes(ty, cols);
+}
+
+int strata_event_create(strata_ctx* c, void** ev) {
+    if (check_ctx(c)) return -1;
+    hipEvent_t e;
+    STRATA_HIP(hipEventCreate(&e));
+    *ev = (void*)e;
+    return 0;
+}
+int strata_event_record(strata_ctx* c, void* ev) {
+    if (check_ctx(c)) return -1;
+    STRATA_HIP(hipEventRecord((hipEvent_t)ev, c->stream));
+    return 0;
+}
+int strata_event_elapsed(void* start, void* end, float* ms) {
+    STRATA_HIP(hipEventSynchronize((hipEvent_t)end));
+    STRATA_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+    return 0;
+}
+int strata_event_destroy(void* ev) {
+    STRATA_HIP(hipEventDestroy((hipEvent_t)ev));
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,54 @@
+// Shared definitions of the strata_hip library: type table, error plumbing, small device helpers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+namespace strata {
+
+// GGUF type ids (src/quant/mod.rs:15-19) of the types this library decodes.
+enum Ty : int { Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, IQ2_XXS = 16, IQ3_S = 21, IQ4_XS = 23 };
+
+// Block elements and bytes (GgmlType::block_elems / block_bytes, src/quant/mod.rs:37-43).
+__host__ __device__ constexpr int block_elems(int ty) { return ty == Q8_0 ? 32 : 256; }
+__host__ __device__ constexpr int block_bytes(int ty) {
+    return ty == Q8_0 ? 34 : ty == Q2_K ? 84 : ty == Q3_K ? 110 : ty == Q4_K ? 144 : ty == Q5_K ? 176
+         : ty == Q6_K ? 210 : ty == IQ2_XXS ? 66 : ty == IQ3_S ? 110 : ty == IQ4_XS ? 136 : 0;
+}
+// Bytes per 256 values: the unit the kernels call a super-block (8 Q8_0 blocks make one, 272 bytes).
+__host__ __device__ constexpr int sb_bytes(int ty) { return block_bytes(ty) * (256 / block_elems(ty)); }
+inline bool supported(int ty) { return block_bytes(ty) != 0; }
+inline uint64_t row_bytes(int ty, uint64_t cols) { return cols / block_elems(ty) * block_bytes(ty); }
+const char* type_name(int ty);
+
+// Error state of the C ABI: set_error records the message for strata_last_error and returns -1.
+int set_error(const std::string& msg);
+int hip_error(hipError_t e, const char* what);
+#define STRATA_HIP(call)                                                          \
+    do {                                                                          \
+        hipError_t e_ = (call);                                                   \
+        if (e_ != hipSuccess) return ::strata::hip_error(e_, #call);              \
+    } while (0)
+
+// ---- device helpers ----
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits) {
+    _Float16 h;
+    uint16_t b = (uint16_t)bits;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+// Bytes {hi:lo} >> 8 * (sh & 3): the 4 bytes starting at byte sh of the 8-byte pair (v_alignbyte_b32).
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t sh) {
+    return __builtin_amdgcn_alignbyte(hi, lo, sh);
+}
+// Byte j of the result is 0x01 where bit j of s is set (j < 4).
+__device__ __forceinline__ uint32_t bits_to_bytes(uint32_t s) { return ((s & 15u) * 0x00204081u) & 0x01010101u; }
+// Bytes of g negated where bit j of s (j < 4) is set. No byte of g is 0, so ~g + 1 per byte never carries.
+__device__ __forceinline__ int neg_bytes(uint32_t g, uint32_t s) {
+    uint32_t n = bits_to_bytes(s);
+    return (int)((g ^ (n * 0xFFu)) + n);
+}
+
+}  // namespace strata

@@ -1,0 +1,29 @@
+// Prefill GEMM over tile lists on int8 MFMA (Backend::gemm / gemm_dense, src/backend.rs:187-197).
+#pragma once
+#include "common.h"
+
+namespace strata {
+
+// The GEMM's X is quantized with quant_xq's layout under Q8_K numerics (one scale per 256 values: the super-block
+// accumulates in int32, see gemm.hip).
+inline uint64_t gemm_x_bytes(uint64_t cols, uint64_t n_x) { return n_x * (cols + cols / 8); }
+hipError_t launch_gemm_quant_x(const float* x, uint64_t x_stride, int cols, int n_x, uint8_t* out, int mode, hipStream_t s);
+
+struct GemmLaunch {
+    int ty = 0;
+    int rows = 0, cols = 0;
+    const uint64_t* tiles = nullptr;  // [w, m0 | cnt << 32] per tile, or null for one dense matrix
+    int n_tiles = 0;                  // tiles (or dense tiles of 128 positions); an upper bound with n_tiles_dev
+    const int* n_tiles_dev = nullptr;
+    const uint8_t* dense_w = nullptr;
+    int dense_n = 0;
+    const uint8_t* xq = nullptr;      // quantized X, n_x rows
+    int n_x = 0;
+    const int* xrow = nullptr;
+    float* y = nullptr;
+    int64_t y_stride = 0;
+    int act = 0;
+};
+hipError_t launch_gemm(const GemmLaunch& g, hipStream_t s);
+
+}  // namespace strata

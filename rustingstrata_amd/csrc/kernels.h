@@ -1,0 +1,37 @@
+// Launchers the C-ABI layer (api.hip) calls; each validates nothing and launches on `s`. Arguments are checked in
+// api.hip, where the errors of the reference's Backend methods are reproduced.
+#pragma once
+#include "common.h"
+
+namespace strata {
+
+// Bytes of the quant_xq layout for nt rows of n values: nt * n int8 then nt * n / 32 f32 scales.
+inline uint64_t xq_bytes(uint64_t n, uint64_t nt) { return nt * (n + n / 8); }
+
+hipError_t launch_dequant(int ty, const uint8_t* w, uint64_t rows, uint64_t cols, float* out, hipStream_t s);
+// quant_xq under numerics `mode` (STRATA_NUM_*): rows t < nt of x (t * x_stride floats apart) into out.
+hipError_t launch_quant_xq(const float* x, uint64_t x_stride, int n, int nt, int8_t* out, int mode, hipStream_t s);
+
+struct GemvLaunch {
+    int ty = 0;
+    const uint8_t* w = nullptr;   // matrix (dense) or expert base (moe)
+    int rows = 0, cols = 0;
+    int nt = 1;                   // inputs per weight read (1..4)
+    const int8_t* xq = nullptr;   // quant_xq layout of n_xrows rows of cols
+    int n_xrows = 1;
+    float* y = nullptr;
+    int y_stride = 0;             // floats between the outputs of consecutive inputs (dense)
+    // moe_gemv: slot j uses expert ids[j] (skipped when < 0) at w + ids[j] * stride, x row j / xg, output y + j rows
+    const int* ids = nullptr;
+    int k = 1, xg = 1;
+    int64_t stride = 0;
+    // second matrix (gemvq2 / paired moe_gemv): at byte offset w2, output at byte offset y2, rows2 rows
+    bool pair = false;
+    int64_t w2 = 0, y2 = 0;
+    int rows2 = 0;
+};
+hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s);
+// Largest row size (bytes) launch_gemv accepts.
+uint64_t gemv_max_row_bytes();
+
+}  // namespace strata

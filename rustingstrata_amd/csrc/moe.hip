@@ -1,0 +1,244 @@
+// MoE routing, the stable sort of (token, expert) pairs with its tile lists, and the combines.
+#include "moe.h"
+
+namespace strata {
+
+// exp for the router and SwiGLU: exp in double, rounded once to f32. This is the correctly rounded f32 exp except
+// in vanishingly rare cases, and so agrees with the host libm expf the reference calls (src/ops.rs:14-24) wherever
+// that one is correctly rounded.
+__device__ __forceinline__ float exp_f32(float x) { return (float)exp((double)x); }
+
+// ---- routing: one wave64 per token (Model::route src/model.rs:837-851; topk_warp src/cuda/kernels.cu:2633-2686) ----
+constexpr int ROUTE_R = 8;  // logits per lane: n <= 512
+
+__global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p, int n, int k, float extra_scale,
+                                                    const int* __restrict__ table, int* ids, float* wts, int* slots,
+                                                    float* wh, int T, int sigmoid) {
+    __shared__ float se[4][512];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= T) return;  // whole waves only
+    const float* pr = p + (uint64_t)t * n;
+    float v[ROUTE_R];
+#pragma unroll
+    for (int r = 0; r < ROUTE_R; r++) { int i = lane + 64 * r; v[r] = i < n ? pr[i] : -INFINITY; }
+    if (sigmoid) {
+#pragma unroll
+        for (int r = 0; r < ROUTE_R; r++) v[r] = 1.0f / (1.0f + exp_f32(-v[r]));  // ops::sigmoid
+    } else {
+        // ops::softmax: m = max, v = exp(v - m), s = the sum in index order, v /= s.
+        float m = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < ROUTE_R; r++) m = fmaxf(m, v[r]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+#pragma unroll
+        for (int r = 0; r < ROUTE_R; r++) {
+            int i = lane + 64 * r;
+            if (i < n) { v[r] = exp_f32(v[r] - m); se[wave][i] = v[r]; }
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        float s = 0.0f;
+        if (lane == 0) for (int i = 0; i < n; i++) s += se[wave][i];
+        s = __shfl(s, 0);
+#pragma unroll
+        for (int r = 0; r < ROUTE_R; r++) v[r] = v[r] / s;
+    }
+    // ops::top_k: k rounds of the wave's largest value, ties to the lower index. v >= 0, so its bits order as it;
+    // key = (bits + 1) << 32 | ~index, 0 for taken or absent entries.
+    unsigned taken = 0;
+    int my_id = 0;
+    float my_p = 0.0f;
+    for (int j = 0; j < k; j++) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int r = 0; r < ROUTE_R; r++) {
+            int i = lane + 64 * r;
+            if (i < n && !((taken >> r) & 1)) {
+                uint64_t key = (uint64_t)(__float_as_uint(v[r]) + 1u) << 32 | (uint32_t)~(uint32_t)i;
+                if (key > best) best = key;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            uint64_t other = __shfl_xor(best, o);
+            best = other > best ? other : best;
+        }
+        int bi = (int)~(uint32_t)best;
+        float bv = __uint_as_float((uint32_t)(best >> 32) - 1u);
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == j) { my_id = bi; my_p = bv; }
+    }
+    // Weights: p / max(sum of the top k in rank order, 2^-14) (times extra_scale when not 0).
+    float sum = 0.0f;
+    for (int j = 0; j < k; j++) sum += __shfl(my_p, j);
+    float scale = 1.0f / fmaxf(sum, 6.103515625e-5f);
+    if (extra_scale != 0.0f) scale *= extra_scale;
+    if (lane < k) {
+        int o = t * k + lane;
+        float w = my_p * scale;
+        ids[o] = my_id;
+        wts[o] = w;
+        if (table) {
+            int s = table[my_id];
+            slots[o] = s;
+            wh[o] = s >= 0 ? w : 0.0f;
+        }
+    }
+}
+
+hipError_t launch_route(const float* p, int n, int k, float extra_scale, const int* table, int* ids, float* wts,
+                        int* slots, float* wh, int t, int sigmoid, hipStream_t s) {
+    route_kernel<<<dim3((unsigned)((t + 3) / 4)), dim3(256), 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);
+    return hipGetLastError();
+}
+
+// ---- combines ----
+
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + exp_f32(-x)); }
+
+// moe_combine (mb = 0; src/cuda/kernels.cu:2742-2773): grid (ceil(n / 256), t).
+__global__ __launch_bounds__(256) void combine_kernel(float* x, const float* ye, const float* w, int k, const float* sh,
+                                                      const float* sg, int n) {
+    int tk = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    x += (uint64_t)tk * n; ye += (uint64_t)tk * k * n; w += (uint64_t)tk * k;
+    float y = 0.0f;
+    for (int j = 0; j < k; j++) if (w[j] != 0.0f) y += w[j] * ye[(uint64_t)j * n + i];
+    if (sh) y += (sg ? sigmoid_f32(sg[tk]) : 1.0f) * sh[(uint64_t)tk * n + i];
+    x[i] += y;
+}
+
+hipError_t launch_combine(float* x, const float* ye, const float* w, int k, const float* sh, const float* sg, int n,
+                          int t, hipStream_t s) {
+    combine_kernel<<<dim3((unsigned)((n + 255) / 256), (unsigned)t), dim3(256), 0, s>>>(x, ye, w, k, sh, sg, n);
+    return hipGetLastError();
+}
+
+// moe_combine_seq (src/cuda/kernels.cu:2776-2785): x[t] += sum_j wts[t, j] ye[inv[t, j]] (j in order), + the shared
+// expert. A pair the sort rejected (inv < 0) adds nothing.
+__global__ __launch_bounds__(256) void combine_seq_kernel(float* x, const float* ye, const float* wts, const int* inv,
+                                                          int k, const float* sh, const float* sg, int n) {
+    int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= n) return;
+    float y = 0.0f;
+    for (int j = 0; j < k; j++) {
+        int s = inv[t * k + j];
+        if (s >= 0) y += wts[t * k + j] * ye[(uint64_t)s * n + d];
+    }
+    uint64_t i = (uint64_t)t * n + d;
+    if (sh) y += (sg ? sigmoid_f32(sg[t]) : 1.0f) * sh[i];
+    x[i] += y;
+}
+
+hipError_t launch_combine_seq(float* x, const float* ye, const float* wts, const int* inv, int k, const float* sh,
+                              const float* sg, int n, int t, hipStream_t s) {
+    combine_seq_kernel<<<dim3((unsigned)((n + 255) / 256), (unsigned)t), dim3(256), 0, s>>>(x, ye, wts, inv, k, sh, sg, n);
+    return hipGetLastError();
+}
+
+// ---- stable sort of the (token, j) pairs by expert, and the tile lists ----
+// One block of 16 waves. Wave w owns the contiguous pair segment w; phase A counts its experts, phase B turns the
+// counts into each (wave, expert) start slot (experts ascending, waves in order within an expert), phase C walks each
+// segment in order assigning slots, 64 pairs at a time with the rank among equal experts inside the wave. The result
+// is the host counting sort of src/gpu_model/prefill.rs:563-573 exactly.
+constexpr int SORT_WAVES = 16, SORT_MAX_E = 512, GEMM_BM = 128;
+
+size_t sort_scratch_bytes(int) { return 16; }
+
+__global__ __launch_bounds__(1024) void sort_kernel(SortLaunch a) {
+    __shared__ int hist[SORT_WAVES][SORT_MAX_E];
+    __shared__ int offs[SORT_MAX_E + 1], tbase[SORT_MAX_E + 1];
+    __shared__ int bad;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, E = a.n_expert;
+    const int N = a.t * a.k, S = (N + SORT_WAVES - 1) / SORT_WAVES;
+    const int s0 = min(N, wave * S), s1 = min(N, s0 + S);
+    for (int i = tid; i < SORT_WAVES * SORT_MAX_E; i += 1024) (&hist[0][0])[i] = 0;
+    if (tid == 0) bad = 0;
+    __syncthreads();
+    for (int i = s0 + lane; i < s1; i += 64) {
+        int e = a.ids[i];
+        if (e >= 0 && e < E) atomicAdd(&hist[wave][e], 1);
+        else atomicAdd(&bad, 1);
+    }
+    __syncthreads();
+    // Per-expert counts and tile counts (thread e), then exclusive scans over experts (one wave, in order).
+    int cnt = 0;
+    if (tid < E) {
+        for (int w = 0; w < SORT_WAVES; w++) cnt += hist[w][tid];
+        offs[tid] = cnt;
+        tbase[tid] = (cnt + GEMM_BM - 1) / GEMM_BM;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int run = 0, trun = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            int e = e0 + lane;
+            int c = e < E ? offs[e] : 0, tc = e < E ? tbase[e] : 0;
+            int ic = c, itc = tc;  // inclusive scans within the wave
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                int y = __shfl_up(ic, o), ty = __shfl_up(itc, o);
+                if (lane >= o) { ic += y; itc += ty; }
+            }
+            if (e < E) { offs[e] = run + ic - c; tbase[e] = trun + itc - tc; }
+            run += __shfl(ic, 63);
+            trun += __shfl(itc, 63);
+        }
+        if (lane == 0) { offs[E] = run; tbase[E] = trun; }
+    }
+    __syncthreads();
+    if (tid < E) {  // (wave, expert) start slots
+        int b = offs[tid];
+        for (int w = 0; w < SORT_WAVES; w++) { int h = hist[w][tid]; hist[w][tid] = b; b += h; }
+    }
+    if (tid <= E) a.off[tid] = offs[tid];
+    __syncthreads();
+    // Phase C: ordered walk of the segment.
+    for (int c0 = s0; c0 < s1; c0 += 64) {
+        int i = c0 + lane;
+        bool live = i < s1;
+        int e = live ? a.ids[i] : -1;
+        bool ok = live && e >= 0 && e < E;
+        int key = ok ? e : (live ? 2046 : 2047);
+        uint64_t peers = ~0ull;
+#pragma unroll
+        for (int b = 0; b < 11; b++) {
+            uint64_t m = __ballot((key >> b) & 1);
+            peers &= ((key >> b) & 1) ? m : ~m;
+        }
+        int rank = __popcll(peers & ((1ull << lane) - 1));
+        int slot = ok ? hist[wave][e] + rank : -1;
+        __builtin_amdgcn_wave_barrier();
+        if (ok && rank == 0) hist[wave][e] += __popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+        if (live) {
+            a.inv[i] = slot;
+            if (ok) a.xrow[slot] = i / a.k;
+        }
+    }
+    // Tiles: expert e's slots off[e] .. off[e + 1] in chunks of GEMM_BM.
+    if (tid < E) {
+        int c = offs[tid + 1] - offs[tid], tb = tbase[tid];
+        for (int j = 0; j * GEMM_BM < c; j++) {
+            uint64_t m0 = (uint64_t)(offs[tid] + j * GEMM_BM), cn = (uint64_t)min(GEMM_BM, c - j * GEMM_BM);
+            for (int m = 0; m < a.n_mats; m++) {
+                uint64_t* tl = a.tiles + 2 * ((uint64_t)m * a.max_tiles + tb + j);
+                tl[0] = a.bases[m] + (uint64_t)tid * a.strides[m];
+                tl[1] = m0 | cn << 32;
+            }
+        }
+    }
+    if (tid == 0) {
+        *a.n_tiles = tbase[E];
+        if (a.err) *a.err = bad;
+    }
+}
+
+hipError_t launch_sort(const SortLaunch& a, hipStream_t s) {
+    sort_kernel<<<1, 1024, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace strata

@@ -1,0 +1,446 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle on identical seeded inputs.
+
+Bars: dequant, quantized activations, routing ids, sort/gather indices bit-exact; fp32 outputs within max relative
+error 1e-3 (floor 1e-3 max|r|), the accumulation-order tolerance of the task.
+"""
+import numpy as np
+import pytest
+
+import rustingstrata_amd as S
+from oracle import oracle as O
+from rustingstrata_amd import ggml
+from tests.helpers import max_rel_err, normal, random_blocks, rel_l2, zipf_logits
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def up(hip, a):
+    return hip.upload(np.ascontiguousarray(a))
+
+
+def down(hip, buf, dtype, n):
+    return hip.get(buf, dtype, n)
+
+
+def seen_q8k(x):
+    d, qs, _ = O.quantize_q8k(x)
+    return (d[:, None] * qs.astype(np.float32)).reshape(-1)[: x.size].astype(np.float64)
+
+
+@pytest.mark.parametrize("ty", ggml.TYPES)
+def test_dequant_bit_exact(hip, ty):
+    rows, cols = 37, 768 if ty != ggml.Q8_0 else 96
+    w = random_blocks(ty, rows, cols, seed=100 + ty)
+    t = hip.upload_tensor(ty, w)
+    out = hip.alloc(rows * cols * 4)
+    hip.dequant(t, rows, out)
+    got = down(hip, out, np.float32, rows * cols)
+    want = O.dequant(ty, w, rows * cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name,ty", [("Q2_K", ggml.Q2_K), ("Q3_K", ggml.Q3_K), ("Q4_K", ggml.Q4_K), ("Q5_K", ggml.Q5_K),
+                                     ("Q6_K", ggml.Q6_K), ("Q8_0", ggml.Q8_0), ("IQ4_XS", ggml.IQ4_XS),
+                                     ("ggml_q5_k", ggml.Q5_K), ("ggml_q8_0", ggml.Q8_0), ("ggml_iq2_xxs", ggml.IQ2_XXS)])
+def test_dequant_reference_fixtures(hip, name, ty):
+    import os
+    d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference")
+    raw = np.fromfile(os.path.join(d, name + (".blk" if name.startswith("ggml") else ".raw")), dtype=np.uint8)
+    want = np.fromfile(os.path.join(d, name + ".f32"), dtype=np.float32)
+    cols = ggml.block_elems(ty) * (raw.size // ggml.block_bytes(ty))
+    t = S.GpuTensor(ty, 1, cols, up(hip, raw))
+    out = hip.alloc(cols * 4)
+    hip.dequant(t, 1, out)
+    got = down(hip, out, np.float32, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,nt", [(2048, 1), (768, 3), (320, 2)])
+def test_quant_xq_q8k_bit_exact(hip, n, nt):
+    x = normal((nt, n), seed=n + nt)
+    x[0, 17] = -x[0].__abs__().max() * 1.5  # a negative extreme
+    xb = up(hip, x)
+    out = hip.alloc(nt * (n + n // 8))
+    hip.quant_xq(xb, n, n, nt, out)
+    raw = down(hip, out, np.uint8, nt * (n + n // 8))
+    q = raw[: nt * n].view(np.int8).reshape(nt, n)
+    sc = raw[nt * n:].view(np.float32).reshape(nt, n // 32)
+    for t in range(nt):
+        d, qs, _ = O.quantize_q8k(x[t])
+        assert np.array_equal(q[t], qs.reshape(-1)[:n])
+        assert np.array_equal(sc[t].view(np.uint32), np.repeat(d, 8)[: n // 32].view(np.uint32))
+
+
+def test_quant_xq_per32_bit_exact(hip):
+    n, nt = 1024, 2
+    x = normal((nt, n), seed=5)
+    hip.set_numerics(S.NUM_Q8_32)
+    try:
+        xb = up(hip, x)
+        out = hip.alloc(nt * (n + n // 8))
+        hip.quant_xq(xb, n, n, nt, out)
+        raw = down(hip, out, np.uint8, nt * (n + n // 8))
+    finally:
+        hip.set_numerics(S.NUM_Q8K)
+    q, sc = O.quant_xq32(x)
+    assert np.array_equal(raw[: nt * n].view(np.int8).reshape(nt, n), q)
+    assert np.array_equal(raw[nt * n:].view(np.float32).reshape(nt, n // 32).view(np.uint32), sc.view(np.uint32))
+
+
+def gemv_case(hip, ty, rows, cols, seed):
+    w = random_blocks(ty, rows, cols, seed=seed)
+    x = normal(cols, seed=seed + 1)
+    t = hip.upload_tensor(ty, w)
+    y = hip.alloc(rows * 4)
+    hip.gemv(t, up(hip, x), y)
+    return w, x, t, down(hip, y, np.float32, rows)
+
+
+@pytest.mark.parametrize("ty", ggml.TYPES)
+@pytest.mark.parametrize("rows,cols", [(257, 2048), (64, 768), (33, 4096)])
+def test_gemv_matches_cpu_matvec(hip, ty, rows, cols):
+    if ty == ggml.Q8_0 and cols == 768:
+        cols = 736  # Q8_0 rows need only a multiple of 32
+    w, x, _, got = gemv_case(hip, ty, rows, cols, seed=7 * ty + cols)
+    want = O.matvec(ty, w, rows, cols, x)
+    assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+    # and against the f64 dot of the dequantized weights with the same Q8_K activations
+    wf = O.dequant(ty, w, rows * cols).reshape(rows, cols).astype(np.float64)
+    assert rel_l2(got, wf @ seen_q8k(x)) < 1e-5
+
+
+def test_gemv_per32_numerics(hip):
+    """Reference GPU numerics (per-32 x scales): against f64 dequant times as_seen(x) (tests/kernels.rs:11-19,61)."""
+    ty, rows, cols = ggml.Q5_K, 100, 2048
+    hip.set_numerics(S.NUM_Q8_32)
+    try:
+        w, x, _, got = gemv_case(hip, ty, rows, cols, seed=9)
+    finally:
+        hip.set_numerics(S.NUM_Q8K)
+    q, sc = O.quant_xq32(x[None, :])
+    seen = (q[0].astype(np.float32) * np.repeat(sc[0], 32)).astype(np.float64)
+    wf = O.dequant(ty, w, rows * cols).reshape(rows, cols).astype(np.float64)
+    assert rel_l2(got, wf @ seen) < 1e-5
+
+
+@pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q6_K, ggml.IQ3_S, ggml.Q8_0])
+def test_gemvn_bit_equals_gemv(hip, ty):
+    """tests/kernels.rs:151-212: gemvn over nt = 1..4 inputs gives gemv's bits per input; gemvq with a
+    pre-quantized x too."""
+    rows, cols = 130, 1024
+    w = random_blocks(ty, rows, cols, seed=3)
+    t = hip.upload_tensor(ty, w)
+    xs = normal((4, cols), seed=4)
+    xb = up(hip, xs)
+    singles = []
+    for i in range(4):
+        y = hip.alloc(rows * 4)
+        hip.gemv(t, int(xb) + 4 * cols * i, y)
+        singles.append(down(hip, y, np.float32, rows))
+    for nt in range(1, 5):
+        y = hip.alloc(nt * rows * 4)
+        hip.gemvn(t, xb, cols, y, rows, nt)
+        got = down(hip, y, np.float32, nt * rows).reshape(nt, rows)
+        for i in range(nt):
+            assert np.array_equal(got[i].view(np.uint32), singles[i].view(np.uint32)), (nt, i)
+    xq = hip.alloc(4 * (cols + cols // 8))
+    hip.quant_xq(xb, cols, cols, 4, xq)
+    y = hip.alloc(4 * rows * 4)
+    hip.gemvq(t, 0, 0, xq, y, rows, 4)
+    got = down(hip, y, np.float32, 4 * rows).reshape(4, rows)
+    for i in range(4):
+        assert np.array_equal(got[i].view(np.uint32), singles[i].view(np.uint32))
+
+
+def test_gemvq2_pair(hip):
+    ty, cols = ggml.Q5_K, 2048
+    wa, wb = random_blocks(ty, 96, cols, seed=1), random_blocks(ty, 40, cols, seed=2)
+    ta, tb = hip.upload_tensor(ty, wa), hip.upload_tensor(ty, wb)
+    x = normal(cols, seed=3)
+    xb = up(hip, x)
+    ya, yb = hip.alloc(96 * 4), hip.alloc(40 * 4)
+    hip.gemvq2(ta, tb, xb, cols, 0, ya, yb, 1)
+    ga, gb = down(hip, ya, np.float32, 96), down(hip, yb, np.float32, 40)
+    y1, y2 = hip.alloc(96 * 4), hip.alloc(40 * 4)
+    hip.gemv(ta, xb, y1)
+    hip.gemv(tb, xb, y2)
+    assert np.array_equal(ga, down(hip, y1, np.float32, 96)) and np.array_equal(gb, down(hip, y2, np.float32, 40))
+
+
+def test_moe_gemv_selects_experts(hip):
+    """tests/kernels.rs:97-147,1572-1654: slot j uses expert ids[j] and x row j / xg; ids < 0 stays untouched; the
+    paired launch equals two launches."""
+    ty, E, rows, cols = ggml.Q5_K, 5, 96, 2048
+    rb = ggml.row_bytes(ty, cols)
+    w = random_blocks(ty, E * rows, cols, seed=21)
+    w2 = random_blocks(ty, E * rows, cols, seed=22)
+    wb = up(hip, np.concatenate([w, w2]))
+    ids = np.array([3, -1, 1, 4], dtype=np.int32)
+    k = ids.size
+    xs = normal((2, cols), seed=23)
+    xb = up(hip, xs)
+    sentinel = np.full(2 * k * rows, 7.25, dtype=np.float32)
+    y = up(hip, sentinel)
+    hip.moe_gemv(ty, rows, cols, wb, rows * rb, up(hip, ids), k, xb, cols, 2, y,
+                 pair=(E * rows * rb, k * rows * 4))
+    got = down(hip, y, np.float32, 2 * k * rows).reshape(2, k, rows)
+    for j, e in enumerate(ids):
+        if e < 0:
+            assert np.all(got[:, j] == 7.25)
+            continue
+        for p, wm in enumerate((w, w2)):
+            want = O.matvec(ty, wm[e * rows:(e + 1) * rows], rows, cols, xs[j // 2])
+            assert max_rel_err(got[p, j], want) <= TOL
+
+
+def test_router_topk_matches_route(hip):
+    """tests/kernels.rs:1244-1282 cases, plus a Zipf-skewed batch: ids bit-exact, weights to 1e-6."""
+    n, k, t = 256, 8, 3
+    v = np.arange(n * t, dtype=np.float32) * np.float32(0.7548777)
+    x = ((v - np.trunc(v)) - np.float32(0.5)) * np.float32(2.0) * 4.0
+    x[n + 7] = 9.0
+    x[n + 200] = 9.0
+    x[2 * n + 30] = x[2 * n + 31] = x[2 * n + 255] = 5.0
+    for logits, kk, scale, sig in [(x.reshape(t, n), k, 2.5, False), (zipf_logits(512, 128, seed=1), 8, 0.0, False),
+                                   (zipf_logits(64, 17, seed=2), 4, 1.5, True)]:
+        tt, nn = logits.shape
+        ids, wts = hip.alloc(tt * kk * 4), hip.alloc(tt * kk * 4)
+        hip.router_topk(up(hip, logits), nn, kk, scale, ids, wts, tt, sig)
+        gi = down(hip, ids, np.int32, tt * kk).reshape(tt, kk)
+        gw = down(hip, wts, np.float32, tt * kk).reshape(tt, kk)
+        wi, ww = O.route(logits, kk, sigmoid=sig, extra_scale=scale)
+        assert np.array_equal(gi, wi)
+        assert np.abs(gw - ww).max() <= 1e-6
+    assert gi is not None
+
+
+def test_moe_route_table(hip):
+    n, k, t = 128, 8, 16
+    logits = zipf_logits(t, n, seed=5)
+    table = np.arange(n, dtype=np.int32)
+    table[::3] = -1
+    bufs = [hip.alloc(t * k * 4) for _ in range(4)]
+    hip.moe_route(up(hip, logits), n, k, 0.0, up(hip, table), *bufs, t)
+    ids, wts, slots, wh = [down(hip, b, dt, t * k) for b, dt in zip(bufs, (np.int32, np.float32, np.int32, np.float32))]
+    wi, ww = O.route(logits, k)
+    assert np.array_equal(ids, wi.reshape(-1))
+    assert np.array_equal(slots, table[ids])
+    assert np.array_equal(wh, np.where(slots >= 0, wts, 0.0).astype(np.float32))
+
+
+def test_router_rejects_shapes(hip):
+    b = hip.alloc(64)
+    with pytest.raises(S.StrataError, match="router_topk: 600 experts, top 8"):
+        hip.router_topk(b, 600, 8, 0.0, b, b, 1)
+
+
+@pytest.mark.parametrize("t,k,E", [(1, 8, 128), (333, 8, 128), (4096, 8, 128), (50, 4, 7)])
+def test_sort_bit_exact(hip, t, k, E):
+    logits = zipf_logits(t, E, seed=t)
+    ids, _ = O.route(logits, k)
+    off_w, xrow_w, inv_w = O.sort_by_expert(ids, E)
+    max_tiles = t * k // 128 + E
+    off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(t * k * 4), hip.alloc(t * k * 4)
+    tiles, ntd, err = hip.alloc(3 * max_tiles * 16), hip.alloc(4), hip.alloc(4)
+    mats = [(1 << 40, 1000), (2 << 40, 2000), (3 << 40, 3000)]
+    hip.moe_sort(up(hip, ids), t, k, E, off, xrow, inv, mats, tiles, max_tiles, ntd, err)
+    assert np.array_equal(down(hip, off, np.int32, E + 1), off_w)
+    assert np.array_equal(down(hip, xrow, np.int32, t * k), xrow_w)
+    assert np.array_equal(down(hip, inv, np.int32, t * k), inv_w)
+    assert down(hip, err, np.int32, 1)[0] == 0
+    # tiles: the host tile builder of src/gpu_model/prefill.rs:618-642, per matrix
+    want = []
+    for e in range(E):
+        for m0 in range(off_w[e], off_w[e + 1], 128):
+            want.append((e, int(m0), int(min(128, off_w[e + 1] - m0))))
+    nt = int(down(hip, ntd, np.int32, 1)[0])
+    assert nt == len(want)
+    tl = down(hip, tiles, np.uint64, 3 * max_tiles * 2).reshape(3, max_tiles, 2)
+    for m, (base, stride) in enumerate(mats):
+        for i, (e, m0, c) in enumerate(want):
+            assert int(tl[m, i, 0]) == base + e * stride
+            assert int(tl[m, i, 1]) == m0 | (c << 32)
+
+
+def test_sort_counts_bad_ids(hip):
+    ids = np.array([[0, 5], [9, 1]], dtype=np.int32)  # 9 is out of range for 6 experts
+    E, t, k = 6, 2, 2
+    off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(t * k * 4), hip.alloc(t * k * 4)
+    tiles, ntd, err = hip.alloc(16 * 16), hip.alloc(4), hip.alloc(4)
+    hip.moe_sort(up(hip, ids), t, k, E, off, xrow, inv, [(0, 0)], tiles, 16, ntd, err)
+    assert down(hip, err, np.int32, 1)[0] == 1
+    assert down(hip, inv, np.int32, 4)[2] == -1
+
+
+def test_combine_seq_and_combine(hip):
+    n, k, t, ne = 300, 3, 5, 20
+    rng = np.random.default_rng(0)
+    x0 = normal((t, n), seed=1)
+    ye = normal((ne, n), seed=2)
+    wts = rng.uniform(0, 1, (t, k)).astype(np.float32)
+    inv = np.array([(i * 7) % ne for i in range(t * k)], dtype=np.int32).reshape(t, k)
+    xb = up(hip, x0)
+    hip.moe_combine_seq(xb, up(hip, ye), up(hip, wts), up(hip, inv), k, 0, 0, n, t)
+    got = down(hip, xb, np.float32, t * n).reshape(t, n)
+    want = O.combine_seq(x0, ye, wts, inv)
+    assert np.array_equal(got, want)  # same sum order
+    # decode combine with a gated shared expert
+    yek = normal((t, k, n), seed=3)
+    sh, sg = normal((t, n), seed=4), normal(t, seed=5)
+    wts[0, 1] = 0.0
+    xb = up(hip, x0)
+    hip.moe_combine(xb, up(hip, yek), up(hip, wts), k, up(hip, sh), up(hip, sg), n, t)
+    got = down(hip, xb, np.float32, t * n).reshape(t, n)
+    want = x0 + np.einsum("tj,tjd->td", wts, yek) + (1 / (1 + np.exp(-sg.astype(np.float64))))[:, None] * sh
+    assert rel_l2(got, want) < 1e-6
+
+
+def test_swiglu_q(hip):
+    n, rows = 768, 8
+    g, u = normal((rows, n), seed=1), normal((rows, n), seed=2)
+    xq = hip.alloc(rows * (n + n // 8))
+    r = hip.swiglu_q(up(hip, g), up(hip, u), n, rows, xq)
+    assert r == int(xq)
+    raw = down(hip, xq, np.uint8, rows * (n + n // 8))
+    q = raw[: rows * n].view(np.int8).reshape(rows, n)
+    a = np.array([[O.silu(v) for v in row] for row in g], dtype=np.float32) * u
+    mism = 0
+    for t in range(rows):
+        _, qs, _ = O.quantize_q8k(a[t])
+        mism += int((q[t] != qs.reshape(-1)[:n]).sum())
+    assert mism <= 2  # the GPU exp may differ from libm's in the last bit, moving a value across a rounding step
+
+
+def tile_list(hip, base, stride, spans):
+    """[w, m0 | cnt << 32] tiles (src/gpu_model/prefill.rs:618-642)."""
+    t = np.array([[base + e * stride, m0 | (c << 32)] for e, m0, c in spans], dtype=np.uint64)
+    return up(hip, t), len(spans)
+
+
+@pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
+def test_gemm_tiles_match_cpu(hip, ty):
+    """tests/kernels.rs:355-447: tiles (0, 128), (128, 16), (144, 26) with X gathered through xrow; act store, then
+    SwiGLU into the stored gate, then add."""
+    rows, cols, E, n_x = 80, 512, 3, 100
+    rb = ggml.row_bytes(ty, cols)
+    w = random_blocks(ty, E * rows, cols, seed=ty)
+    wb = up(hip, w)
+    x = normal((n_x, cols), seed=2)
+    xrow = np.random.default_rng(3).integers(0, n_x, 170).astype(np.int32)
+    spans = [(0, 0, 128), (2, 128, 16), (1, 144, 26)]
+    tiles, nt = tile_list(hip, int(wb), rows * rb, spans)
+    y = hip.alloc(170 * rows * 4)
+    xb, xr = up(hip, x), up(hip, xrow)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_STORE)
+    got = down(hip, y, np.float32, 170 * rows).reshape(170, rows)
+    want = np.zeros((170, rows), dtype=np.float32)
+    for e, m0, c in spans:
+        we = w[e * rows:(e + 1) * rows]
+        for m in range(m0, m0 + c):
+            want[m] = O.matvec(ty, we, rows, cols, x[xrow[m]])
+    assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+    # act 1: y = silu(y) * (W x) with the same x (SAME_X), then act 2: y += W x
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_SWIGLU | S.SAME_X)
+    got2 = down(hip, y, np.float32, 170 * rows).reshape(170, rows)
+    want2 = want / (1 + np.exp(-want.astype(np.float64))) * want
+    assert max_rel_err(got2, want2) <= 2 * TOL
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_ADD | S.SAME_X)
+    got3 = down(hip, y, np.float32, 170 * rows).reshape(170, rows)
+    assert max_rel_err(got3, want2 + want) <= 2 * TOL
+
+
+def test_gemm_dense(hip):
+    ty, rows, cols, n = ggml.Q5_K, 200, 1024, 300
+    w = random_blocks(ty, rows, cols, seed=8)
+    t = hip.upload_tensor(ty, w)
+    x = normal((n, cols), seed=9)
+    y = hip.alloc(n * rows * 4)
+    hip.gemm_dense(t, n, up(hip, x), cols, y, rows, S.ACT_STORE)
+    got = down(hip, y, np.float32, n * rows).reshape(n, rows)
+    want = np.stack([O.matvec(ty, w, rows, cols, x[i]) for i in range(n)])
+    assert max_rel_err(got, want) <= TOL
+
+
+def moe_weights(E, H, F, seed):
+    gate = random_blocks(ggml.Q5_K, E * F, H, seed=seed)
+    upw = random_blocks(ggml.Q5_K, E * F, H, seed=seed + 1)
+    dn = random_blocks(ggml.Q6_K, E * H, F, seed=seed + 2)
+    return gate, upw, dn
+
+
+def test_moe_prefill_layer_matches_experts_multi(hip):
+    """route -> device sort -> grouped gate / up (SwiGLU) / down -> combine_seq, against cpu_moe::experts_multi."""
+    E, H, F, T, k = 16, 512, 256, 96, 4
+    gate, upw, dn = moe_weights(E, H, F, seed=40)
+    hs = normal((T, H), seed=41)
+    logits = zipf_logits(T, E, seed=42)
+    ids_w, wts_w = O.route(logits, k)
+    want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, hs, ids_w, wts_w)
+    got = run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits)
+    assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+
+
+def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits):
+    rb_gu, rb_d = ggml.row_bytes(ggml.Q5_K, H), ggml.row_bytes(ggml.Q6_K, F)
+    g_b, u_b, d_b = up(hip, gate), up(hip, upw), up(hip, dn)
+    hb, lb = up(hip, hs), up(hip, logits)
+    ids, wts = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
+    hip.router_topk(lb, E, k, 0.0, ids, wts, T)
+    max_tiles = T * k // 128 + E
+    off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
+    tiles, ntd = hip.alloc(3 * max_tiles * 16), hip.alloc(4)
+    hip.moe_sort(ids, T, k, E, off, xrow, inv, [(int(g_b), F * rb_gu), (int(u_b), F * rb_gu), (int(d_b), H * rb_d)],
+                 tiles, max_tiles, ntd)
+    ge, ye = hip.alloc(T * k * F * 4), hip.alloc(T * k * H * 4)
+    hip.gemm_grouped(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, S.ACT_STORE)
+    hip.gemm_grouped(ggml.Q5_K, F, H, int(tiles) + max_tiles * 16, max_tiles, ntd, hb, H, T, xrow, ge, F,
+                     S.ACT_SWIGLU | S.SAME_X)
+    hip.gemm_grouped(ggml.Q6_K, H, F, int(tiles) + 2 * max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
+                     S.ACT_STORE)
+    x = hip.alloc(T * H * 4)
+    hip.moe_combine_seq(x, ye, wts, inv, k, 0, 0, H, T)
+    return down(hip, x, np.float32, T * H).reshape(T, H)
+
+
+def test_moe_decode_layer_matches_experts(hip):
+    """The decode sequence of src/gpu_model.rs:3383-3412: moe_route -> paired gate/up moe_gemv -> swiglu_q ->
+    moe_down_combine, against cpu_moe::experts."""
+    E, H, F, k = 32, 2048, 768, 8
+    gate, upw, dn = moe_weights(E, H, F, seed=50)
+    h = normal(H, seed=51)
+    logits = zipf_logits(1, E, seed=52)
+    ids_w, wts_w = O.route(logits, k)
+    want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, h[None, :], ids_w, wts_w)[0]
+    rb_gu, rb_d = ggml.row_bytes(ggml.Q5_K, H), ggml.row_bytes(ggml.Q6_K, F)
+    gu = up(hip, np.concatenate([gate, upw]))
+    d_b = up(hip, dn)
+    table = up(hip, np.arange(E, dtype=np.int32))
+    ids, wts, slots, wh = [hip.alloc(k * 4) for _ in range(4)]
+    hip.moe_route(up(hip, logits), E, k, 0.0, table, ids, wts, slots, wh, 1)
+    hb = up(hip, h)
+    xq = hip.alloc(H + H // 8)
+    hip.quant_xq(hb, H, H, 1, xq)
+    g = hip.alloc(2 * k * F * 4)
+    hip.moe_gemv(ggml.Q5_K, F, H, gu, F * rb_gu, slots, k, hb, H, k, g, pair=(E * F * rb_gu, k * F * 4), xq=xq)
+    aq = hip.alloc(k * (F + F // 8))
+    aqr = hip.swiglu_q(g, int(g) + k * F * 4, F, k, aq)
+    x = hip.alloc(H * 4)
+    ye = hip.alloc(k * H * 4)
+    hip.moe_down_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, 0, ye, aqr, x, wh, 0, 0, 1)
+    got = down(hip, x, np.float32, H)
+    assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+
+
+def test_errors_do_not_launch(hip):
+    t = S.GpuTensor(ggml.Q4_K, 4, 300, hip.alloc(4 * 2048))
+    with pytest.raises(S.StrataError, match="GEMV needs a multiple of 256"):
+        hip.gemv(t, 0, 0)
+    t = S.GpuTensor(ggml.Q4_K, 4, 512, hip.alloc(4 * 2048))
+    with pytest.raises(S.StrataError, match="gemvn: 5 inputs"):
+        hip.gemvn(t, 0, 0, 0, 0, 5)
+    with pytest.raises(S.StrataError, match="unsupported quant type"):
+        hip.gemv(S.GpuTensor(99, 1, 256, hip.alloc(64)), 0, 0)
+    b = hip.alloc(16)
+    with pytest.raises(S.StrataError, match="outside"):
+        hip.htod(np.zeros(32, dtype=np.uint8), b)
