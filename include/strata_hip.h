@@ -188,6 +188,9 @@ int strata_event_create(strata_ctx* ctx, void** ev);
 int strata_event_record(strata_ctx* ctx, void* ev);
 int strata_event_elapsed(void* start, void* end, float* ms);
 int strata_event_destroy(void* ev);
+/* A plain streaming copy kernel (16-byte loads and stores) of `bytes` (a multiple of 16) from src to dst: the known-size
+ * reference against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are scaled. */
+int strata_copy_kernel(strata_ctx* ctx, uint64_t src, uint64_t dst, uint64_t bytes);
 
 #ifdef __cplusplus
 }

@@ -15,7 +15,7 @@ import numpy as np
 
 from . import ggml
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstrata_hip.so")
+LIB_PATH = os.environ.get("STRATA_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstrata_hip.so")
 NUM_Q8K, NUM_Q8_32 = 0, 1
 ACT_STORE, ACT_SWIGLU, ACT_ADD, SAME_X = 0, 1, 2, 4
 GEMM_BM = 128  # positions per tile (src/backend.rs:16)
@@ -77,6 +77,7 @@ SIGNATURES = {
     "strata_event_record": [CTX, P],
     "strata_event_elapsed": [P, P, ctypes.POINTER(F32)],
     "strata_event_destroy": [P],
+    "strata_copy_kernel": [CTX, U64, U64, U64],
 }
 _RESTYPES = {"strata_close": None, "strata_last_error": ctypes.c_char_p, "strata_stream": P, "strata_row_bytes": U64}
 
@@ -308,6 +309,9 @@ class HipBackend:
 
     def record(self, e):
         _check(lib().strata_event_record(self._ctx, e))
+
+    def copy_kernel(self, src, dst, nbytes):
+        _check(lib().strata_copy_kernel(self._ctx, int(src), int(dst), nbytes))
 
     @staticmethod
     def elapsed_ms(e0, e1):

@@ -304,6 +304,7 @@ int strata_gemvq(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_s
     GemvLaunch g;
     g.ty = w->ty; g.w = (const uint8_t*)w->ptr; g.rows = (int)w->rows; g.cols = (int)w->cols;
     g.nt = (int)nt; g.xq = (const int8_t*)xq; g.n_xrows = (int)nt; g.y = (float*)y; g.y_stride = (int)y_stride;
+    g.numerics = c->numerics;
     STRATA_HIP(launch_gemv(g, c->stream));
     return 0;
 }
@@ -331,6 +332,7 @@ int strata_gemvq2(strata_ctx* c, const strata_tensor* a, const strata_tensor* b,
     GemvLaunch g;
     g.ty = a->ty; g.w = (const uint8_t*)a->ptr; g.rows = (int)a->rows; g.cols = (int)a->cols;
     g.nt = (int)nt; g.xq = (const int8_t*)xq; g.n_xrows = (int)nt; g.y = (float*)ya; g.y_stride = (int)a->rows;
+    g.numerics = c->numerics;
     g.pair = true; g.w2 = (int64_t)(b->ptr - a->ptr); g.y2 = (int64_t)(yb - ya); g.rows2 = (int)b->rows;
     // The second matrix's outputs are token-strided by its own row count; one stride serves both only when equal.
     if (nt > 1 && a->rows != b->rows) {
@@ -354,6 +356,7 @@ int strata_moe_gemv(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_
     GemvLaunch g;
     g.ty = ty; g.w = (const uint8_t*)w; g.rows = (int)rows; g.cols = (int)cols; g.nt = 1;
     g.xq = (const int8_t*)xq; g.n_xrows = (int)(k / xg); g.y = (float*)y; g.y_stride = 0;
+    g.numerics = c->numerics;
     g.ids = (const int*)ids; g.k = (int)k; g.xg = (int)xg; g.stride = (int64_t)stride;
     g.pair = has_pair != 0; g.w2 = w2; g.y2 = y2; g.rows2 = (int)rows;
     STRATA_HIP(launch_gemv(g, c->stream));
@@ -528,6 +531,13 @@ int strata_event_elapsed(void* start, void* end, float* ms) {
     STRATA_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
     return 0;
 }
+int strata_copy_kernel(strata_ctx* c, uint64_t src, uint64_t dst, uint64_t bytes) {
+    if (check_ctx(c)) return -1;
+    if (bytes % 16) return set_error("copy_kernel: bytes must be a multiple of 16");
+    STRATA_HIP(launch_copy((const void*)src, (void*)dst, bytes, c->stream));
+    return 0;
+}
+
 int strata_event_destroy(void* ev) {
     STRATA_HIP(hipEventDestroy((hipEvent_t)ev));
     return 0;

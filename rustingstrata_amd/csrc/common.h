@@ -38,6 +38,13 @@ __device__ __forceinline__ float f16_to_f32(uint32_t bits) {
     __builtin_memcpy(&h, &b, 2);
     return (float)h;
 }
+// Global-memory (address space 1) views of a device address. Loads through them compile to global_load, which
+// counts only in vmcnt; loads through a generic pointer become flat_load, which also counts in lgkmcnt, so every
+// later LDS wait would stall on them and a prefetch could not overlap LDS work.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(uint64_t addr) {
+    return (const __attribute__((address_space(1))) T*)addr;
+}
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 // Bytes {hi:lo} >> 8 * (sh & 3): the 4 bytes starting at byte sh of the 8-byte pair (v_alignbyte_b32).
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t sh) {

@@ -4,16 +4,20 @@
 // A block of 256 threads (4 wave64) computes R consecutive rows. It streams the rows' contiguous byte span from
 // HBM with 16-byte coalesced loads (any block alignment: the span is read from its 16-byte-aligned cover) into
 // LDS, together with the quantized x (int8 + per-32 scales, plus per-16 sums computed on the way in) and, for the
-// IQ types, the codebook tables. Then each row is reduced by G lanes (G = 16, 32 or 64, by row length): lane l
-// takes the row's 32-value tasks l, l + G, ... (a task is 32 weights decoded to int8 by task<T>), dots them with
-// sdot4 against x and scales in f32; the G partial sums meet by cross-lane reduction.
-#include "formats.h"
+// IQ types, the codebook tables. A row is then shared by G lanes (G = the power of two at or above its number of
+// 256-value super-blocks, at most 64): lane l takes super-blocks l, l + G, ... whole, accumulating each exactly in
+// int32 and closing it with one float step (sbdot.h); the G partial sums meet by cross-lane reduction.
+#include "sbdot.h"
 #include "kernels.h"
+#include "../../include/strata_hip.h"
 
 namespace strata {
 
 constexpr int GEMV_THREADS = 256;
-constexpr int GEMV_CH = 6;                                          // 16-byte chunks per thread per tile
+#ifndef STRATA_GEMV_CH
+#define STRATA_GEMV_CH 6
+#endif
+constexpr int GEMV_CH = STRATA_GEMV_CH;                              // 16-byte chunks per thread per tile
 constexpr int GEMV_TILE = GEMV_THREADS * 16 * GEMV_CH;               // 24 KB of weights per block
 uint64_t gemv_max_row_bytes() { return GEMV_TILE - 32; }
 
@@ -29,55 +33,29 @@ struct GemvArgs {
     int xg;              // moe: slots per x row
     int rows, rows2, cols, R, nt, y_stride;
     uint64_t rb;
+    int per32;           // x has per-32 scales (STRATA_NUM_Q8_32), else one per 256 (STRATA_NUM_Q8K)
+    int G;               // lanes per row: the power of two at or above the row's super-blocks, at most 64
+    int ntr, nslots, nz; // row tiles per matrix, slots (moe) and matrices (pair)
 };
 
 // LDS layout: [IqTables (IQ types)][x int8: nt * cols][x scales: nt * cols / 32 f32][x sums: nt * cols / 16
 // int32][weight tile], each section rounded up to 16 bytes.
 __host__ __device__ constexpr uint32_t up16(uint32_t v) { return (v + 15) & ~15u; }
 
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, G);
+// Sum over the g lanes of each aligned lane group (g a power of two <= 64).
+__device__ __forceinline__ float group_sum(float v, int g) {
+    for (int o = g >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
     return v;
 }
 
-template <int T, int NT, int G>
+template <int T, int NT, bool Q32>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = threadIdx.x;
-    const int z = blockIdx.z, slot = blockIdx.y;
-    const int rows = z ? a.rows2 : a.rows;
-    const int r0 = blockIdx.x * a.R;
-    if (r0 >= rows) return;
-    const int nr = min(a.R, rows - r0);
-    const uint8_t* W = a.w + (z ? a.w2 : 0);
-    float* Y = (float*)((uint8_t*)a.y + (z ? a.y2 : 0));
-    int xrow = 0;
-    if (a.ids) {
-        int e = a.ids[slot];
-        if (e < 0) return;  // slot not routed here: its output stays untouched
-        W += (int64_t)e * a.stride;
-        xrow = slot / a.xg;
-        Y += (int64_t)slot * rows;
-    }
-    const int cols = a.cols;
-
-    // 1. Issue the weight span loads into registers.
-    const uint64_t beg = (uint64_t)(W + (uint64_t)r0 * a.rb), end = beg + (uint64_t)nr * a.rb;
-    const uint64_t g0 = beg & ~(uint64_t)15;
-    const int nch = (int)(((end + 15) & ~(uint64_t)15) - g0) >> 4;
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
-    v4u wv[GEMV_CH];
-#pragma unroll
-    for (int i = 0; i < GEMV_CH; i++) {
-        int c = tid + GEMV_THREADS * i;
-        if (c < nch) wv[i] = __builtin_nontemporal_load((const v4u*)(g0 + 16 * (uint64_t)c));
-    }
-
-    // 2. x (int8 + scales, per-16 sums) and the IQ tables into LDS.
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, cols = a.cols;
+    // LDS: [IqTables][x int8][x scales][x sums][weight tile]
     uint8_t* p = smem;
     IqTables* tab = (IqTables*)p;
     if constexpr (IQ) { load_iq_tables(tab); p += up16(sizeof(IqTables)); }
@@ -88,84 +66,157 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
     int* ss = (int*)p;
     p += up16(NT * (cols / 16) * 4);
     uint8_t* tile = p;
-    for (int c = tid; c < NT * cols / 16; c += GEMV_THREADS) {
-        int t = c / (cols / 16), j = c % (cols / 16);
-        uint4 q = *(const uint4*)(a.xq + (uint64_t)(xrow + t) * cols + 16 * j);
-        *(uint4*)(sx + 16 * c) = q;
-        ss[c] = sdot4((int)q.x, 0x01010101, sdot4((int)q.y, 0x01010101, sdot4((int)q.z, 0x01010101, sdot4((int)q.w, 0x01010101, 0))));
-    }
-    for (int c = tid; c < NT * cols / 32; c += GEMV_THREADS) {
-        int t = c / (cols / 32), j = c % (cols / 32);
-        sd[c] = a.xd[(uint64_t)(xrow + t) * (cols / 32) + j];
-    }
 
-    // 3. Weights into LDS.
+    // Tiles: t -> (z, slot, row tile); block b takes tiles b, b + grid, ... and prefetches the next one into
+    // registers while it computes the current one from LDS.
+    const int total = a.ntr * a.nslots * a.nz;
+    auto valid = [&](int t) {
+        const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
+        if (rt * a.R >= (z ? a.rows2 : a.rows)) return false;
+        return !a.ids || a.ids[slot] >= 0;  // a slot not routed here leaves its output untouched
+    };
+    auto next_valid = [&](int t) {
+        while (t < total && !valid(t)) t += gridDim.x;
+        return t;
+    };
+    struct Span { const uint8_t* W; float* Y; int r0, nr, xrow; uint64_t beg, g0; int nch; };
+    auto span = [&](int t) {
+        Span sp;
+        const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
+        const int rows = z ? a.rows2 : a.rows;
+        sp.r0 = rt * a.R;
+        sp.nr = min(a.R, rows - sp.r0);
+        sp.W = a.w + (z ? a.w2 : 0);
+        sp.Y = (float*)((uint8_t*)a.y + (z ? a.y2 : 0));
+        sp.xrow = 0;
+        if (a.ids) {
+            sp.W += (int64_t)a.ids[slot] * a.stride;
+            sp.xrow = slot / a.xg;
+            sp.Y += (int64_t)slot * rows;
+        }
+        sp.beg = (uint64_t)(sp.W + (uint64_t)sp.r0 * a.rb);
+        sp.g0 = sp.beg & ~(uint64_t)15;
+        sp.nch = (int)((((sp.beg + (uint64_t)sp.nr * a.rb) + 15) & ~(uint64_t)15) - sp.g0) >> 4;
+        return sp;
+    };
+    v4u wv[GEMV_CH];
+    auto issue = [&](const Span& sp) {
 #pragma unroll
-    for (int i = 0; i < GEMV_CH; i++) {
-        int c = tid + GEMV_THREADS * i;
-        if (c < nch) *(v4u*)(tile + 16 * c) = wv[i];
-    }
-    __syncthreads();
+        for (int i = 0; i < GEMV_CH; i++) {
+            const int c = tid + GEMV_THREADS * i;
+#ifdef STRATA_GEMV_PLAIN_LOADS
+            if (c < sp.nch) wv[i] = *gptr<v4u>(sp.g0 + 16 * (uint64_t)c);
+#else
+            if (c < sp.nch) wv[i] = __builtin_nontemporal_load(gptr<v4u>(sp.g0 + 16 * (uint64_t)c));
+#endif
+        }
+    };
 
-    // 4. Rows: G lanes each, 64 / G rows per wave per pass.
-    const int wave = tid >> 6, lane = tid & 63, gl = lane & (G - 1);
-    constexpr int RPW = 64 / G;
-    const int tpr = cols / 32;  // tasks per row
-    for (int base = wave * RPW; base < nr; base += 4 * RPW) {
-        const int rr = base + lane / G;
-        float acc[NT];
+    int t = next_valid(blockIdx.x);
+    if (t >= total) return;
+    Span sp = span(t);
+    issue(sp);
+    int cur_xrow = -1;
+    const int G = a.G, wave = tid >> 6, lane = tid & 63, gl = lane & (G - 1);
+    const int RPW = 64 / G, nsb = (cols + 255) >> 8;
+    while (true) {
+        __syncthreads();  // the previous tile's readers are done with the LDS tile (and x)
+        if (sp.xrow != cur_xrow) {
+            // x (int8 + scales, per-16 sums) of this tile's input row(s)
+            for (int c = tid; c < NT * cols / 16; c += GEMV_THREADS) {
+                const int u = c / (cols / 16), j = c % (cols / 16);
+                const v4u q = *gptr<v4u>((uint64_t)(a.xq + (uint64_t)(sp.xrow + u) * cols + 16 * j));
+                *(v4u*)(sx + 16 * c) = q;
+                ss[c] = sdot4((int)q.x, 0x01010101, sdot4((int)q.y, 0x01010101, sdot4((int)q.z, 0x01010101, sdot4((int)q.w, 0x01010101, 0))));
+            }
+            for (int c = tid; c < NT * cols / 32; c += GEMV_THREADS) {
+                const int u = c / (cols / 32), j = c % (cols / 32);
+                sd[c] = *gptr<float>((uint64_t)(a.xd + (uint64_t)(sp.xrow + u) * (cols / 32) + j));
+            }
+            cur_xrow = sp.xrow;
+        }
 #pragma unroll
-        for (int t = 0; t < NT; t++) acc[t] = 0.0f;
-        if (rr < nr) {
-            const uint8_t* rowp = tile + (beg - g0) + (uint64_t)rr * a.rb;
-            for (int i = gl; i < tpr; i += G) {
-                const int sb = i >> 3;
-                Task tk;
-                task<T>(rowp + sb * SBB, i & 7, tab, tk);
-                const int x0 = sb * 256 + tk.o0, x1 = sb * 256 + tk.o1;
+        for (int i = 0; i < GEMV_CH; i++) {
+            const int c = tid + GEMV_THREADS * i;
+            if (c < sp.nch) *(v4u*)(tile + 16 * c) = wv[i];
+        }
+        __syncthreads();
+        const Span cs = sp;
+        const int tn = next_valid(t + gridDim.x);
+        if (tn < total) {
+            sp = span(tn);
+            issue(sp);  // in flight while this tile is computed
+        }
+        // Rows: G lanes each (64 / G rows per wave per pass), whole super-blocks per lane.
+        for (int base = wave * RPW; base < cs.nr; base += 4 * RPW) {
+            const int rr = base + lane / G;
+            float acc[NT];
 #pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    const int8_t* xs = sx + t * cols;
-                    uint4 u0 = *(const uint4*)(xs + x0), u1 = *(const uint4*)(xs + x1);
-                    int s0 = sdot4(tk.q[0], (int)u0.x, sdot4(tk.q[1], (int)u0.y, sdot4(tk.q[2], (int)u0.z, sdot4(tk.q[3], (int)u0.w, 0))));
-                    int s1 = sdot4(tk.q[4], (int)u1.x, sdot4(tk.q[5], (int)u1.y, sdot4(tk.q[6], (int)u1.z, sdot4(tk.q[7], (int)u1.w, 0))));
-                    const int* sst = ss + t * (cols / 16);
-                    const int xs0 = sst[x0 >> 4], xs1 = sst[x1 >> 4];
-                    if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * xs0; s1 -= Fmt<T>::BIAS * xs1; }
-                    float f0 = tk.D * (float)(tk.sc0 * s0), f1 = tk.D * (float)(tk.sc1 * s1);
-                    if constexpr (Fmt<T>::MIN) { f0 -= tk.M * (float)(tk.m0 * xs0); f1 -= tk.M * (float)(tk.m1 * xs1); }
-                    const float* sdt = sd + t * (cols / 32);
-                    acc[t] += sdt[x0 >> 5] * f0 + sdt[x1 >> 5] * f1;
+            for (int u = 0; u < NT; u++) acc[u] = 0.0f;
+            if (rr < cs.nr) {
+                const uint8_t* rowp = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb;
+                for (int sb = gl; sb < nsb; sb += G) {
+#pragma unroll
+                    for (int u = 0; u < NT; u++) {
+                        const int8_t* xq = sx + u * cols + 256 * sb;
+                        const float* xd = sd + u * (cols / 32) + 8 * sb;
+                        const int* xs = ss + u * (cols / 16) + 16 * sb;
+                        const int nv = min(256, cols - 256 * sb);
+                        acc[u] += Q32 ? sb_dot_q32<T>(rowp + sb * SBB, xq, xd, xs, tab, nv)
+                                      : sb_dot_q8k<T>(rowp + sb * SBB, xq, xd, xs, tab, nv);
+                    }
                 }
             }
-        }
 #pragma unroll
-        for (int t = 0; t < NT; t++) acc[t] = group_sum<G>(acc[t]);
-        if (rr < nr && gl == 0) {
+            for (int u = 0; u < NT; u++) acc[u] = group_sum(acc[u], G);
+            if (rr < cs.nr && gl == 0) {
 #pragma unroll
-            for (int t = 0; t < NT; t++) Y[(int64_t)t * a.y_stride + r0 + rr] = acc[t];
+                for (int u = 0; u < NT; u++) cs.Y[(int64_t)u * a.y_stride + cs.r0 + rr] = acc[u];
+            }
         }
+        if (tn >= total) break;
+        t = tn;
     }
 }
 
-template <int T, int NT>
-static hipError_t gemv_nt(const GemvArgs& a, dim3 grid, size_t smem, hipStream_t s) {
-    int tpr = a.cols / 32;
-    if (tpr >= 64) gemv_kernel<T, NT, 64><<<grid, GEMV_THREADS, smem, s>>>(a);
-    else if (tpr >= 32) gemv_kernel<T, NT, 32><<<grid, GEMV_THREADS, smem, s>>>(a);
-    else gemv_kernel<T, NT, 16><<<grid, GEMV_THREADS, smem, s>>>(a);
+// The persistent grid: as many blocks as stay resident together (the kernel's occupancy at this LDS size), at most
+// one per tile. Cached per (kernel, LDS size).
+template <int T, int NT, bool Q32>
+static hipError_t gemv_nt(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
+    static int ncu = 0;
+    static size_t cached_smem = 0;
+    static int per_cu = 0;
+    if (!ncu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+    }
+    if (cached_smem != smem) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kernel<T, NT, Q32>, GEMV_THREADS, smem) != hipSuccess || n < 1) n = 1;
+        per_cu = n;
+        cached_smem = smem;
+    }
+    long long blocks = (long long)per_cu * ncu;
+    if (blocks > tiles) blocks = tiles;
+    gemv_kernel<T, NT, Q32><<<dim3((unsigned)blocks), GEMV_THREADS, smem, s>>>(a);
     return hipGetLastError();
 }
 
-template <int T>
-static hipError_t gemv_t(const GemvArgs& a, dim3 grid, size_t smem, hipStream_t s) {
+template <int T, bool Q32>
+static hipError_t gemv_m(const GemvArgs& a, long long grid, size_t smem, hipStream_t s) {
     switch (a.nt) {
-    case 1: return gemv_nt<T, 1>(a, grid, smem, s);
-    case 2: return gemv_nt<T, 2>(a, grid, smem, s);
-    case 3: return gemv_nt<T, 3>(a, grid, smem, s);
-    case 4: return gemv_nt<T, 4>(a, grid, smem, s);
+    case 1: return gemv_nt<T, 1, Q32>(a, grid, smem, s);
+    case 2: return gemv_nt<T, 2, Q32>(a, grid, smem, s);
+    case 3: return gemv_nt<T, 3, Q32>(a, grid, smem, s);
+    case 4: return gemv_nt<T, 4, Q32>(a, grid, smem, s);
     }
     return hipErrorInvalidValue;
+}
+
+template <int T>
+static hipError_t gemv_t(const GemvArgs& a, long long grid, size_t smem, hipStream_t s) {
+    return a.per32 ? gemv_m<T, true>(a, grid, smem, s) : gemv_m<T, false>(a, grid, smem, s);
 }
 
 hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
@@ -175,11 +226,29 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     a.ids = g.ids; a.stride = g.stride; a.xg = g.xg;
     a.rows = g.rows; a.rows2 = g.pair ? g.rows2 : 0; a.cols = g.cols; a.nt = g.nt; a.y_stride = g.y_stride;
     a.rb = row_bytes(g.ty, g.cols);
-    a.R = (int)((GEMV_TILE - 32) / a.rb);
-    int maxrows = g.pair ? (g.rows > g.rows2 ? g.rows : g.rows2) : g.rows;
-    if (a.R > maxrows) a.R = maxrows;
+    a.per32 = g.numerics == STRATA_NUM_Q8_32;
+    {
+        int nsb = (g.cols + 255) / 256;
+        a.G = 1;
+        while (a.G < nsb && a.G < 64) a.G <<= 1;
+    }
+    static int ncu = 0;
+    if (!ncu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+    }
+    const int maxrows = g.pair ? (g.rows > g.rows2 ? g.rows : g.rows2) : g.rows;
+    const int nslots = g.ids ? g.k : 1, nz = g.pair ? 2 : 1;
+    // Rows per tile: as many as fit the tile, but no fewer tiles than about 4 per CU.
+    const int rmax = (int)((GEMV_TILE - 32) / a.rb);
+    long long want = (long long)maxrows * nslots * nz / (4LL * ncu);
+    a.R = (int)(want < 1 ? 1 : want > rmax ? rmax : want);
     if (a.R < 1) a.R = 1;
-    dim3 grid((unsigned)((maxrows + a.R - 1) / a.R), (unsigned)(g.ids ? g.k : 1), g.pair ? 2u : 1u);
+    a.ntr = (maxrows + a.R - 1) / a.R;
+    a.nslots = nslots;
+    a.nz = nz;
+    const long long grid = (long long)a.ntr * nslots * nz;  // tiles
     bool iq = g.ty == IQ2_XXS || g.ty == IQ3_S;
     size_t smem = (iq ? up16(sizeof(IqTables)) : 0) + up16(g.nt * g.cols) + up16(g.nt * (g.cols / 32) * 4) +
                   up16(g.nt * (g.cols / 16) * 4) + GEMV_TILE + 16;

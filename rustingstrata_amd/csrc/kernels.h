@@ -17,6 +17,7 @@ struct GemvLaunch {
     const uint8_t* w = nullptr;   // matrix (dense) or expert base (moe)
     int rows = 0, cols = 0;
     int nt = 1;                   // inputs per weight read (1..4)
+    int numerics = 0;             // STRATA_NUM_*: how xq was quantized
     const int8_t* xq = nullptr;   // quant_xq layout of n_xrows rows of cols
     int n_xrows = 1;
     float* y = nullptr;
@@ -31,6 +32,8 @@ struct GemvLaunch {
     int rows2 = 0;
 };
 hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s);
+// Streaming copy of `bytes` (multiple of 16), the reference kernel for HBM byte counters.
+hipError_t launch_copy(const void* src, void* dst, uint64_t bytes, hipStream_t s);
 // Largest row size (bytes) launch_gemv accepts.
 uint64_t gemv_max_row_bytes();
 

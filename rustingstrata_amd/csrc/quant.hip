@@ -125,4 +125,16 @@ hipError_t launch_swiglu_q(const float* g, const float* u, int n, int rows, int8
     return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_copy(const void* src, void* dst, uint64_t bytes, hipStream_t s) {
+    uint64_t n = bytes / 16;
+    if (!n) return hipSuccess;
+    uint64_t blocks = (n + 255) / 256;
+    copy_kernel<<<dim3((unsigned)(blocks < 8192 ? blocks : 8192)), dim3(256), 0, s>>>((const uint4*)src, (uint4*)dst, n);
+    return hipGetLastError();
+}
+
 }  // namespace strata

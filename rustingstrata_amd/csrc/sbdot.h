@@ -1,0 +1,219 @@
+// Super-block dot products for the GEMV: one lane takes a whole 256-value super-block of a weight row (read from
+// LDS) against the same 256 values of x (int8 in LDS, Q8_K numerics: one x scale per super-block), accumulating
+// exactly in int32, and closes it with one float step
+//     acc += dx * (D * sum_g sc_g * (q_g . x_g - bias * sum x_g) - M * sum_g m_g * sum x_g).
+// This is the structure of the reference CPU dots (src/cpu_moe.rs:319-377: exact integer group sums, then
+// d_w * d_x * s - dmin * d_x * m in f32).
+#pragma once
+#include "formats.h"
+
+namespace strata {
+
+// x of one input in LDS: int8 values, per-32 scales (8 equal ones per super-block under Q8_K), per-16 int sums.
+struct XView {
+    const int8_t* q;
+    const float* d;
+    const int* s16;
+};
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return __builtin_amdgcn_ubfe(w, 8 * i, 8); }
+__device__ __forceinline__ int sbyte_of(uint32_t w, int i) { return __builtin_amdgcn_sbfe((int)w, 8 * i, 8); }
+__device__ __forceinline__ int dot16(const uint32_t* w, const uint4& x0, const uint4& x1, int acc = 0) {
+    acc = sdot4((int)w[0], (int)x0.x, acc);
+    acc = sdot4((int)w[1], (int)x0.y, acc);
+    acc = sdot4((int)w[2], (int)x0.z, acc);
+    acc = sdot4((int)w[3], (int)x0.w, acc);
+    acc = sdot4((int)w[4], (int)x1.x, acc);
+    acc = sdot4((int)w[5], (int)x1.y, acc);
+    acc = sdot4((int)w[6], (int)x1.z, acc);
+    return sdot4((int)w[7], (int)x1.w, acc);
+}
+__device__ __forceinline__ int dot4w(uint32_t a, uint32_t b, uint32_t c, uint32_t d, const uint4& x, int acc = 0) {
+    acc = sdot4((int)a, (int)x.x, acc);
+    acc = sdot4((int)b, (int)x.y, acc);
+    acc = sdot4((int)c, (int)x.z, acc);
+    return sdot4((int)d, (int)x.w, acc);
+}
+// n words from a 2-byte-aligned LDS address: aligned reads, shifted into place (v_alignbyte_b32).
+template <int N>
+__device__ __forceinline__ void words_a2(const uint8_t* p, uint32_t* out) {
+    const uint32_t* a = (const uint32_t*)((uintptr_t)p & ~(uintptr_t)3);
+    uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    uint32_t prev = a[0];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        uint32_t nx = a[i + 1];
+        out[i] = align_bytes(nx, prev, sh);
+        prev = nx;
+    }
+}
+
+// ---- Q4_K / Q5_K: 8 sub-blocks of 32, 6-bit scales and mins (src/cpu_moe.rs:327-358) ----
+template <bool Q5>
+__device__ __forceinline__ void sb_q45(const uint8_t* b, const int8_t* xq, const int* xs16, int& isum, int& msum,
+                                       float& D, float& M) {
+    const uint4 h = *(const uint4*)b;
+    D = f16_to_f32(h.x & 0xFFFF);
+    M = f16_to_f32(h.x >> 16);
+    // packed 6-bit scales / mins of sub-blocks 0..3 and 4..7 (scale_min_k4, src/quant/mod.rs:59-62)
+    const uint32_t sc_lo = h.y & 0x3F3F3F3Fu, m_lo = h.z & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t m_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    uint4 qh0, qh1;
+    if constexpr (Q5) { qh0 = *(const uint4*)(b + 16); qh1 = *(const uint4*)(b + 32); }
+    const uint8_t* qs = b + (Q5 ? 48 : 16);
+    int is = 0;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const uint4 w0 = *(const uint4*)(qs + 32 * p), w1 = *(const uint4*)(qs + 32 * p + 16);
+        uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            lo[i] = w[i] & 0x0F0F0F0Fu;
+            hi[i] = (w[i] >> 4) & 0x0F0F0F0Fu;
+        }
+        if constexpr (Q5) {
+            uint32_t qh[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                lo[i] |= ((qh[i] >> (2 * p)) << 4) & 0x10101010u;
+                hi[i] |= ((qh[i] >> (2 * p + 1)) << 4) & 0x10101010u;
+            }
+        }
+        const uint4* xa = (const uint4*)(xq + 64 * p);
+        const int s_lo = dot16(lo, xa[0], xa[1]);
+        const int s_hi = dot16(hi, xa[2], xa[3]);
+        const uint32_t scw = p < 2 ? sc_lo : sc_hi;
+        is += (int)byte_of(scw, (2 * p) & 3) * s_lo + (int)byte_of(scw, (2 * p + 1) & 3) * s_hi;
+    }
+    isum = is;
+    // min term: sum_j m_j * (sum of x over sub-block j)
+    int ms = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) ms += (int)byte_of(j < 4 ? m_lo : m_hi, j & 3) * (xs16[2 * j] + xs16[2 * j + 1]);
+    msum = ms;
+}
+
+// ---- Q6_K: 16 groups of 16, int8 scales, values q - 32 (src/cpu_moe.rs:360-377) ----
+__device__ __forceinline__ void sb_q6(const uint8_t* b, const int8_t* xq, const int* xs16, int& isum, float& D) {
+    uint32_t sc[4];
+    words_a2<4>(b + 192, sc);
+    D = f16_to_f32(rd16(b + 208));
+    int is = 0;
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        // half n: 64 bytes of low nibbles (ql[l] = words 0..7, ql[l + 32] = words 8..15), 32 bytes of high bits
+        uint32_t ql[16], qh[8];
+        words_a2<16>(b + 64 * n, ql);
+        words_a2<8>(b + 128 + 32 * n, qh);
+#pragma unroll
+        for (int qd = 0; qd < 4; qd++)
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
+                uint32_t v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int wi = 4 * a + i;
+                    const uint32_t q = ql[(qd & 1 ? 8 : 0) + wi], hb = qh[wi];
+                    const uint32_t nib = qd & 2 ? (q >> 4) & 0x0F0F0F0Fu : q & 0x0F0F0F0Fu;
+                    v[i] = nib | (((hb >> (2 * qd)) << 4) & 0x30303030u);  // q + 32, in 0..63
+                }
+                const int xo = 128 * n + 32 * qd + 16 * a;
+                const int s = dot4w(v[0], v[1], v[2], v[3], *(const uint4*)(xq + xo)) - 32 * xs16[xo >> 4];
+                const int g = 8 * n + a + 2 * qd;  // scale index: l / 16 + 2 qd within the half
+                is += sbyte_of(sc[g >> 2], g & 3) * s;
+            }
+    }
+    isum = is;
+}
+
+// ---- Q8_0: 8 blocks of 32 with an f16 scale each (src/cpu_moe.rs:319-325): returns sum_b d_b * s_b ----
+__device__ __forceinline__ float sb_q8_0(const uint8_t* b, const int8_t* xq, int nb) {
+    float f = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        if (k >= nb) break;  // a partial last super-block (Q8_0 rows are multiples of 32 values)
+        uint32_t w[9];
+        words_a2<9>(b + 34 * k, w);  // d (low half of w[0]) then 32 int8
+        uint32_t q[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q[i] = align_bytes(w[i + 1], w[i], 2);
+        const uint4* xa = (const uint4*)(xq + 32 * k);
+        const int s = dot16(q, xa[0], xa[1]);
+        f += f16_to_f32(w[0] & 0xFFFF) * (float)s;
+    }
+    return f;
+}
+
+// ---- generic: any type through task<T> (8 tasks of 32 values) ----
+template <int T>
+__device__ __forceinline__ void sb_generic(const uint8_t* b, const int8_t* xq, const int* xs16, const IqTables* tab,
+                                           int& isum, int& msum, float& D, float& M) {
+    int is = 0, ms = 0;
+#pragma unroll 2
+    for (int k = 0; k < 8; k++) {
+        Task t;
+        task<T>(b, k, tab, t);
+        const uint4 x0 = *(const uint4*)(xq + t.o0), x1 = *(const uint4*)(xq + t.o1);
+        int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x0), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x1);
+        const int a0 = xs16[t.o0 >> 4], a1 = xs16[t.o1 >> 4];
+        if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * a0; s1 -= Fmt<T>::BIAS * a1; }
+        is += t.sc0 * s0 + t.sc1 * s1;
+        if constexpr (Fmt<T>::MIN) ms += t.m0 * a0 + t.m1 * a1;
+        if (k == 0) { D = t.D; M = t.M; }
+    }
+    isum = is;
+    msum = ms;
+}
+
+// acc += the super-block's contribution, Q8_K numerics (x scale xd[0] for the whole super-block).
+template <int T>
+__device__ __forceinline__ float sb_dot_q8k(const uint8_t* b, const int8_t* xq, const float* xd, const int* xs16,
+                                            const IqTables* tab, int nvals) {
+    const float dx = xd[0];
+    if constexpr (T == Q4_K || T == Q5_K) {
+        int is, ms;
+        float D, M;
+        sb_q45<T == Q5_K>(b, xq, xs16, is, ms, D, M);
+        return dx * (D * (float)is - M * (float)ms);
+    } else if constexpr (T == Q6_K) {
+        int is;
+        float D;
+        sb_q6(b, xq, xs16, is, D);
+        return dx * (D * (float)is);
+    } else if constexpr (T == Q8_0) {
+        return dx * sb_q8_0(b, xq, nvals >> 5);
+    } else {
+        int is, ms = 0;
+        float D, M = 0.0f;
+        sb_generic<T>(b, xq, xs16, tab, is, ms, D, M);
+        float f = D * (float)is;
+        if constexpr (Fmt<T>::MIN) f -= M * (float)ms;
+        return dx * f;
+    }
+}
+
+// The same under per-32 x scales (the reference GPU's default numerics): every 32-group has its own dx, so each task
+// closes in float.
+template <int T>
+__device__ __forceinline__ float sb_dot_q32(const uint8_t* b, const int8_t* xq, const float* xd, const int* xs16,
+                                            const IqTables* tab, int nvals) {
+    float f = 0.0f;
+#pragma unroll 2
+    for (int k = 0; k < 8; k++) {
+        if (32 * k >= nvals) break;  // a partial last super-block (Q8_0 only)
+        Task t;
+        task<T>(b, k, tab, t);
+        const uint4 x0 = *(const uint4*)(xq + t.o0), x1 = *(const uint4*)(xq + t.o1);
+        int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x0), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x1);
+        const int a0 = xs16[t.o0 >> 4], a1 = xs16[t.o1 >> 4];
+        if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * a0; s1 -= Fmt<T>::BIAS * a1; }
+        float f0 = t.D * (float)(t.sc0 * s0), f1 = t.D * (float)(t.sc1 * s1);
+        if constexpr (Fmt<T>::MIN) { f0 -= t.M * (float)(t.m0 * a0); f1 -= t.M * (float)(t.m1 * a1); }
+        f += xd[t.o0 >> 5] * f0 + xd[t.o1 >> 5] * f1;
+    }
+    return f;
+}
+
+}  // namespace strata
