@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, AMD's published peak
 INT8_PEAK_TOPS = 5000.0         # MI355X dense int8 MFMA, AMD's published peak (no sparsity)
 ROTATE_BYTES = 512 << 20        # weight copies per shape must exceed the 256 MB Infinity Cache twice over
+GRAPH_STEPS = 10                # sweep steps per recorded graph
 SWEEP = [(ty, rows, 2048) for ty in ("Q4_K", "Q5_K", "Q6_K", "Q8_0") for rows in (6144, 2048, 151936)]
 
 
@@ -66,12 +67,18 @@ class Rotated:
 
 
 def time_gemv(hip, rot, xb, yb, iters):
+    """Average GEMV time over >= iters launches, replayed from a recorded graph (Backend::graph) of one launch per
+    weight copy, so host launch gaps do not count as GPU time."""
+    key = ("gemv", id(rot))
+    n = rot.n
+    hip.graph(key, lambda: [hip.gemv(rot.next(), xb, yb) for _ in range(n)])
+    reps = max(1, -(-iters // n))
     e0, e1 = hip.event(), hip.event()
     hip.record(e0)
-    for _ in range(iters):
-        hip.gemv(rot.next(), xb, yb)
+    for _ in range(reps):
+        hip.graph(key, None)
     hip.record(e1)
-    return hip.elapsed_ms(e0, e1) / iters
+    return hip.elapsed_ms(e0, e1) / (reps * n)
 
 
 def bench_gemv(hip, S, ggml, steps, warmup):
@@ -99,20 +106,29 @@ def bench_gemv(hip, S, ggml, steps, warmup):
         if n % 10 == 0:
             hip.sync()
     hip.sync()
+    # The timed steps replay a recorded graph of GRAPH_STEPS steps (each step's GEMVs rotate their weight copies
+    # inside it), the way the reference's decode replays CUDA graphs (src/cuda/mod.rs:868-888).
+    gs = min(GRAPH_STEPS, steps)
+    hip.graph("sweep", lambda: [step() for _ in range(gs)])
+    reps = -(-steps // gs)
+    hip.graph("sweep", None)
+    hip.sync()
     e0, e1 = hip.event(), hip.event()
     hip.record(e0)
-    for _ in range(steps):
-        step()
+    for _ in range(reps):
+        hip.graph("sweep", None)
     hip.record(e1)
     ms = hip.elapsed_ms(e0, e1)
+    steps = reps * gs
     total_bytes = steps * sum(s["bytes"] for s in shapes)
+    hip.drop_graphs()
     per_shape = {}
     for s in shapes:
         us = 1000 * time_gemv(hip, s["rot"], xb, yb, max(200, steps))
         gbs = s["bytes"] / us / 1e3
         per_shape[f'{s["name"]} {s["rows"]}x{s["cols"]}'] = {"us": round(us, 2), "GB/s": round(gbs, 1),
                                                             "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
-    return shapes, ms / steps, total_bytes / (ms / 1e3) / 1e9, per_shape
+    return shapes, ms / steps, total_bytes / (ms / 1e3) / 1e9, per_shape, steps
 
 
 def bench_moe(hip, S, ggml, T, iters):
@@ -282,7 +298,7 @@ def main():
     if args.profile_gemv:
         profile_gemv(hip, S, ggml)
         return
-    shapes, ms_step, gbs, per_shape = bench_gemv(hip, S, ggml, args.steps, args.warmup)
+    shapes, ms_step, gbs, per_shape, steps = bench_gemv(hip, S, ggml, args.steps, args.warmup)
     log(f"[bench] GEMV sweep: {gbs:.1f} GB/s, {ms_step:.3f} ms/step")
     xb = hip.upload(np.random.default_rng(7).standard_normal(2048).astype(np.float32))
     yb = hip.alloc(151936 * 4)
@@ -301,7 +317,7 @@ def main():
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,

@@ -69,6 +69,16 @@ int strata_sync(strata_ctx* ctx);
 /* The context's HIP stream (a hipStream_t), for callers that order their own work against it. */
 void* strata_stream(strata_ctx* ctx);
 
+/* ---- recorded graphs: Backend::graph (src/backend.rs:118-120; CUDA graphs in src/cuda/mod.rs:868-888) ----
+ * strata_graph_begin starts recording the ops queued on the context's stream; strata_graph_end stops and returns an
+ * executable graph; strata_graph_launch replays it on the stream. As in the trait, the recorded ops must read their
+ * per-call values from device memory. Ops whose scratch would have to grow cannot be recorded (run them once
+ * before recording). */
+int strata_graph_begin(strata_ctx* ctx);
+int strata_graph_end(strata_ctx* ctx, void** graph);
+int strata_graph_launch(strata_ctx* ctx, void* graph);
+int strata_graph_destroy(void* graph);
+
 /* ---- dequant and activation quantization ---- */
 
 /* Backend::dequant (src/backend.rs:227-228): out = the first `rows` rows of w as f32, bit-identical to

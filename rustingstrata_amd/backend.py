@@ -51,6 +51,10 @@ SIGNATURES = {
     "strata_mem_info": [CTX, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)],
     "strata_sync": [CTX],
     "strata_stream": [CTX],
+    "strata_graph_begin": [CTX],
+    "strata_graph_end": [CTX, ctypes.POINTER(P)],
+    "strata_graph_launch": [CTX, P],
+    "strata_graph_destroy": [P],
     "strata_dequant": [CTX, TP, U64, U64],
     "strata_quant_xq": [CTX, U64, U64, U64, U64, U64],
     "strata_gemv": [CTX, TP, U64, U64],
@@ -229,6 +233,29 @@ class HipBackend:
         rows = blocks.shape[0]
         cols = blocks.shape[1] // ggml.block_bytes(ty) * ggml.block_elems(ty)
         return GpuTensor(ty, rows, cols, self.upload(blocks))
+
+    # ---- recorded graphs (Backend::graph, src/backend.rs:118-120) ----
+    def graph(self, key, f):
+        """Run the ops `f` queues as the graph recorded under `key`, recording it on first use; `f` runs only when
+        recording, so its ops must read per-call values from device memory."""
+        g = self._graphs.get(key) if hasattr(self, "_graphs") else None
+        if g is None:
+            if not hasattr(self, "_graphs"):
+                self._graphs = {}
+            _check(lib().strata_graph_begin(self._ctx))
+            try:
+                f()
+            finally:
+                out = P()
+                rc = lib().strata_graph_end(self._ctx, ctypes.byref(out))
+            _check(rc)
+            g = self._graphs[key] = out
+        _check(lib().strata_graph_launch(self._ctx, g))
+
+    def drop_graphs(self):
+        for g in getattr(self, "_graphs", {}).values():
+            lib().strata_graph_destroy(g)
+        self._graphs = {}
 
     # ---- ops ----
     def dequant(self, w, rows, out):

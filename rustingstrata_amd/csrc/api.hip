@@ -276,6 +276,36 @@ int strata_sync(strata_ctx* c) {
 
 void* strata_stream(strata_ctx* c) { return c ? (void*)c->stream : nullptr; }
 
+int strata_graph_begin(strata_ctx* c) {
+    if (check_ctx(c)) return -1;
+    STRATA_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    return 0;
+}
+
+int strata_graph_end(strata_ctx* c, void** graph) {
+    if (check_ctx(c)) return -1;
+    if (!graph) return set_error("strata_graph_end: null out");
+    hipGraph_t g = nullptr;
+    STRATA_HIP(hipStreamEndCapture(c->stream, &g));
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_error(e, "hipGraphInstantiate");
+    *graph = (void*)ex;
+    return 0;
+}
+
+int strata_graph_launch(strata_ctx* c, void* graph) {
+    if (check_ctx(c)) return -1;
+    STRATA_HIP(hipGraphLaunch((hipGraphExec_t)graph, c->stream));
+    return 0;
+}
+
+int strata_graph_destroy(void* graph) {
+    STRATA_HIP(hipGraphExecDestroy((hipGraphExec_t)graph));
+    return 0;
+}
+
 int strata_dequant(strata_ctx* c, const strata_tensor* w, uint64_t rows, uint64_t out) {
     if (check_ctx(c) || check_tensor(w, "dequant")) return -1;
     if (rows > w->rows) return set_error("dequant: " + std::to_string(rows) + " rows of a " + std::to_string(w->rows) + "-row tensor");
@@ -300,8 +330,10 @@ int strata_gemvq(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_s
     if (check_gemv_cols(w->ty, w->cols) || check_align(w->ty, w->ptr, "gemv")) return -1;
     if (w->rows == 0) return 0;
     if (w->rows > (1u << 30)) return set_error("gemv: too many rows");
-    if (!xq && quant_into_scratch(c, x, x_stride, w->cols, nt, &xq)) return -1;
+    // One input: the kernel quantizes x itself; several: quantize once for all blocks.
+    if (!xq && nt > 1 && quant_into_scratch(c, x, x_stride, w->cols, nt, &xq)) return -1;
     GemvLaunch g;
+    g.xf = (const float*)x; g.x_stride = x_stride;
     g.ty = w->ty; g.w = (const uint8_t*)w->ptr; g.rows = (int)w->rows; g.cols = (int)w->cols;
     g.nt = (int)nt; g.xq = (const int8_t*)xq; g.n_xrows = (int)nt; g.y = (float*)y; g.y_stride = (int)y_stride;
     g.numerics = c->numerics;
@@ -328,8 +360,9 @@ int strata_gemvq2(strata_ctx* c, const strata_tensor* a, const strata_tensor* b,
     }
     if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
     if (check_gemv_cols(a->ty, a->cols) || check_align(a->ty, a->ptr, "gemvq2") || check_align(b->ty, b->ptr, "gemvq2")) return -1;
-    if (!xq && quant_into_scratch(c, x, x_stride, a->cols, nt, &xq)) return -1;
+    if (!xq && nt > 1 && quant_into_scratch(c, x, x_stride, a->cols, nt, &xq)) return -1;
     GemvLaunch g;
+    g.xf = (const float*)x; g.x_stride = x_stride;
     g.ty = a->ty; g.w = (const uint8_t*)a->ptr; g.rows = (int)a->rows; g.cols = (int)a->cols;
     g.nt = (int)nt; g.xq = (const int8_t*)xq; g.n_xrows = (int)nt; g.y = (float*)ya; g.y_stride = (int)a->rows;
     g.numerics = c->numerics;
@@ -352,8 +385,8 @@ int strata_moe_gemv(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_
     if (xg < 1 || k % xg) return set_error("moe_gemv: " + std::to_string(k) + " slots in groups of " + std::to_string(xg));
     if (k == 0 || rows == 0) return 0;
     if (k > 65535) return set_error("moe_gemv: too many slots");
-    if (!xq && quant_into_scratch(c, x, x_stride, cols, k / xg, &xq)) return -1;
     GemvLaunch g;
+    g.xf = (const float*)x; g.x_stride = x_stride;
     g.ty = ty; g.w = (const uint8_t*)w; g.rows = (int)rows; g.cols = (int)cols; g.nt = 1;
     g.xq = (const int8_t*)xq; g.n_xrows = (int)(k / xg); g.y = (float*)y; g.y_stride = 0;
     g.numerics = c->numerics;

@@ -45,6 +45,12 @@ template <typename T>
 __device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(uint64_t addr) {
     return (const __attribute__((address_space(1))) T*)addr;
 }
+// LDS (address space 3) view of a generic pointer into shared memory. Keeping LDS reads in their own address space
+// stops the compiler from merging them with global reads into flat ones.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(3))) T* lptr(const void* p) {
+    return (const __attribute__((address_space(3))) T*)p;
+}
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 // Bytes {hi:lo} >> 8 * (sh & 3): the 4 bytes starting at byte sh of the 8-byte pair (v_alignbyte_b32).
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t sh) {

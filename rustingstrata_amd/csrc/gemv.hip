@@ -36,6 +36,8 @@ struct GemvArgs {
     int per32;           // x has per-32 scales (STRATA_NUM_Q8_32), else one per 256 (STRATA_NUM_Q8K)
     int G;               // lanes per row: the power of two at or above the row's super-blocks, at most 64
     int ntr, nslots, nz; // row tiles per matrix, slots (moe) and matrices (pair)
+    const float* xf;     // single-input kernel: x as f32 (quantized in-lane) when xq is null
+    uint64_t x_stride;   // floats between the f32 x rows
 };
 
 // LDS layout: [IqTables (IQ types)][x int8: nt * cols][x scales: nt * cols / 32 f32][x sums: nt * cols / 16
@@ -153,17 +155,19 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
             float acc[NT];
 #pragma unroll
             for (int u = 0; u < NT; u++) acc[u] = 0.0f;
+#ifdef STRATA_GEMV_NOCOMPUTE
+            if (rr < cs.nr) acc[0] = (float)tile[rr];
+            if (false) {
+#else
             if (rr < cs.nr) {
+#endif
                 const uint8_t* rowp = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb;
                 for (int sb = gl; sb < nsb; sb += G) {
 #pragma unroll
                     for (int u = 0; u < NT; u++) {
-                        const int8_t* xq = sx + u * cols + 256 * sb;
-                        const float* xd = sd + u * (cols / 32) + 8 * sb;
-                        const int* xs = ss + u * (cols / 16) + 16 * sb;
+                        const XLds xv{sx + u * cols + 256 * sb, sd + u * (cols / 32) + 8 * sb, ss + u * (cols / 16) + 16 * sb};
                         const int nv = min(256, cols - 256 * sb);
-                        acc[u] += Q32 ? sb_dot_q32<T>(rowp + sb * SBB, xq, xd, xs, tab, nv)
-                                      : sb_dot_q8k<T>(rowp + sb * SBB, xq, xd, xs, tab, nv);
+                        acc[u] += Q32 ? sb_dot_q32<T>(rowp + sb * SBB, xv, tab, nv) : sb_dot_q8k<T>(rowp + sb * SBB, xv, tab, nv);
                     }
                 }
             }
@@ -181,6 +185,227 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
 
 // The persistent grid: as many blocks as stay resident together (the kernel's occupancy at this LDS size), at most
 // one per tile. Cached per (kernel, LDS size).
+// ---- single-input GEMV with x in registers ----
+// Every lane of a row group always takes the same super-block (lane l of a group of G: super-block l), so it keeps
+// that 256-value slice of x in registers for the whole launch (reloaded only when a MoE tile switches x rows) and
+// LDS carries nothing but the weight tiles. x arrives pre-quantized (xq) or as f32, quantized by each lane for its
+// own slice with quant_xq's arithmetic (the same bits).
+#ifndef STRATA_GEMV1_CH
+#define STRATA_GEMV1_CH 12
+#endif
+constexpr int GEMV1_CH = STRATA_GEMV1_CH;
+constexpr int GEMV1_TILE = GEMV_THREADS * 16 * GEMV1_CH;
+
+// Quantize x row xr (n values) into LDS (n int8, then n / 32 scales) with quant_xq's arithmetic (quant.hip): the
+// block's 256 threads take 8 values each, a group of 32 lanes one 256-value block.
+template <bool Q32>
+__device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, float* d) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    for (int c0 = 0; c0 < n; c0 += 2048) {
+        const int i = c0 + threadIdx.x * 8;
+        const bool live = i < n;
+        float v[8];
+        if (live) {
+            const v4f p = *gptr<v4f>(xr + 4 * (uint64_t)i), r = *gptr<v4f>(xr + 4 * (uint64_t)i + 16);
+            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = r.x; v[5] = r.y; v[6] = r.z; v[7] = r.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+        }
+        float dd, mul;
+        if constexpr (!Q32) {
+            float bv = v[0];
+            int bi = i;
+#pragma unroll
+            for (int j = 1; j < 8; j++) if (fabsf(v[j]) > fabsf(bv)) { bv = v[j]; bi = i + j; }
+#pragma unroll
+            for (int o = 1; o < 32; o <<= 1) {
+                const float ov = __shfl_xor(bv, o, 32);
+                const int oi = __shfl_xor(bi, o, 32);
+                if (fabsf(ov) > fabsf(bv) || (fabsf(ov) == fabsf(bv) && oi < bi)) { bv = ov; bi = oi; }
+            }
+            const float is = bv != 0.0f ? -127.0f / bv : 0.0f;
+            dd = bv != 0.0f ? 1.0f / is : 0.0f;
+            mul = is;
+        } else {
+            float mx = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
+            mx = fmaxf(mx, __shfl_xor(mx, 1, 32));
+            mx = fmaxf(mx, __shfl_xor(mx, 2, 32));
+            dd = mx / 127.0f;
+            mul = mx > 0.0f ? 127.0f / mx : 0.0f;
+        }
+        if (live) {
+            uint32_t w[2] = {0, 0};
+#pragma unroll
+            for (int j = 0; j < 8; j++) w[j >> 2] |= (uint32_t)((int)fminf(__builtin_rintf(mul * v[j]), 127.0f) & 255) << (8 * (j & 3));
+            *(uint2*)(q + i) = make_uint2(w[0], w[1]);
+            if ((threadIdx.x & 3) == 0) d[i >> 5] = dd;
+        }
+    }
+}
+
+// x row xrow into the block's LDS copy (int8, then per-32 scales): copied from xq, or quantized from f32.
+template <bool Q32>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl, float* xld) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    if (a.xq) {
+        const uint64_t q = (uint64_t)(a.xq + (uint64_t)xrow * a.cols), d = (uint64_t)(a.xd + (uint64_t)xrow * (a.cols / 32));
+        for (int c = threadIdx.x; c < a.cols / 16; c += blockDim.x) *(v4u*)(xl + 16 * c) = *gptr<v4u>(q + 16 * c);
+        for (int c = threadIdx.x; c < a.cols / 32; c += blockDim.x) xld[c] = *gptr<float>(d + 4 * c);
+    } else {
+        quant_row_lds<Q32>((uint64_t)(a.xf + (uint64_t)xrow * a.x_stride), a.cols, xl, xld);
+    }
+    // zeros up to whole super-blocks (Q8_0 rows may end inside one)
+    const int n = a.cols, nup = (n + 255) & ~255;
+    for (int i = n + 4 * threadIdx.x; i < nup; i += 4 * blockDim.x) *(uint32_t*)(xl + i) = 0;
+    for (int j = n / 32 + threadIdx.x; j < nup / 32; j += blockDim.x) xld[j] = 0.0f;
+}
+
+// This lane's 256-value slice (super-block sb) of the staged x into registers, with its per-16 sums.
+__device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const float* xld, XReg& x) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+        const v4u t = *(const v4u*)(xl + 256 * sb + 16 * c);
+        x.w[4 * c] = t.x; x.w[4 * c + 1] = t.y; x.w[4 * c + 2] = t.z; x.w[4 * c + 3] = t.w;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) x.ds[j] = xld[8 * sb + j];
+#pragma unroll
+    for (int g = 0; g < 16; g++)
+        x.sums[g] = sdot4((int)x.w[4 * g], 0x01010101, sdot4((int)x.w[4 * g + 1], 0x01010101,
+                    sdot4((int)x.w[4 * g + 2], 0x01010101, sdot4((int)x.w[4 * g + 3], 0x01010101, 0))));
+}
+
+template <int T, bool Q32>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv1_kernel(GemvArgs a) {
+    constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
+    constexpr int SBB = sb_bytes(T);
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, cols = a.cols;
+    // LDS: [IqTables][x int8 (cols, whole super-blocks)][x scales][tile]
+    const uint32_t ncp = (cols + 255) & ~255;
+    const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + ncp, o_tile = o_xd + ncp / 8;
+    IqTables* tab = (IqTables*)smem;
+    if constexpr (IQ) load_iq_tables(tab);
+    int8_t* xl = (int8_t*)(smem + o_x);
+    float* xld = (float*)(smem + o_xd);
+    uint8_t* tile = smem + o_tile;
+
+    const int total = a.ntr * a.nslots * a.nz;
+    auto valid = [&](int t) {
+        const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
+        if (rt * a.R >= (z ? a.rows2 : a.rows)) return false;
+        return !a.ids || a.ids[slot] >= 0;  // a slot not routed here leaves its output untouched
+    };
+    auto next_valid = [&](int t) {
+        while (t < total && !valid(t)) t += gridDim.x;
+        return t;
+    };
+    struct Span { float* Y; int r0, nr, xrow; uint64_t beg, g0; int nch; };
+    auto span = [&](int t) {
+        Span sp;
+        const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
+        const int rows = z ? a.rows2 : a.rows;
+        sp.r0 = rt * a.R;
+        sp.nr = min(a.R, rows - sp.r0);
+        const uint8_t* W = a.w + (z ? a.w2 : 0);
+        sp.Y = (float*)((uint8_t*)a.y + (z ? a.y2 : 0));
+        sp.xrow = 0;
+        if (a.ids) {
+            W += (int64_t)a.ids[slot] * a.stride;
+            sp.xrow = slot / a.xg;
+            sp.Y += (int64_t)slot * rows;
+        }
+        sp.beg = (uint64_t)(W + (uint64_t)sp.r0 * a.rb);
+        sp.g0 = sp.beg & ~(uint64_t)15;
+        sp.nch = (int)((((sp.beg + (uint64_t)sp.nr * a.rb) + 15) & ~(uint64_t)15) - sp.g0) >> 4;
+        return sp;
+    };
+    v4u wv[GEMV1_CH];
+    auto issue = [&](const Span& sp) {
+#pragma unroll
+        for (int i = 0; i < GEMV1_CH; i++) {
+            const int c = tid + GEMV_THREADS * i;
+            if (c < sp.nch) wv[i] = __builtin_nontemporal_load(gptr<v4u>(sp.g0 + 16 * (uint64_t)c));
+        }
+    };
+
+    int t = next_valid(blockIdx.x);
+    if (t >= total) return;
+    Span sp = span(t);
+    issue(sp);
+    const int G = a.G, wave = tid >> 6, lane = tid & 63, gl = lane & (G - 1);
+    const int RPW = 64 / G, nsb = (cols + 255) >> 8;
+    const bool has_sb = gl < nsb;
+    XReg x;
+    int cur_xrow = -1;
+    while (true) {
+        __syncthreads();  // the previous tile's readers are done with the LDS tile
+        if (sp.xrow != cur_xrow) {
+            stage_x<Q32>(a, sp.xrow, xl, xld);
+            __syncthreads();
+            if (has_sb) load_x_slice(gl, xl, xld, x);
+            cur_xrow = sp.xrow;
+            __syncthreads();  // every lane has its slice before the LDS copy changes again
+        }
+#pragma unroll
+        for (int i = 0; i < GEMV1_CH; i++) {
+            const int c = tid + GEMV_THREADS * i;
+            if (c < sp.nch) *(v4u*)(tile + 16 * c) = wv[i];
+        }
+        __syncthreads();
+        const Span cs = sp;
+        const int tn = next_valid(t + gridDim.x);
+        if (tn < total) {
+            sp = span(tn);
+            issue(sp);  // in flight while this tile is computed
+        }
+        const int nv = min(256, cols - 256 * gl);
+        for (int base = wave * RPW; base < cs.nr; base += 4 * RPW) {
+            const int rr = base + lane / G;
+            float acc = 0.0f;
+            if (rr < cs.nr && has_sb) {
+                const uint8_t* b = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb + gl * SBB;
+                acc = Q32 ? sb_dot_q32<T>(b, x, tab, nv) : sb_dot_q8k<T>(b, x, tab, nv);
+            }
+            acc = group_sum(acc, G);
+            if (rr < cs.nr && gl == 0) cs.Y[cs.r0 + rr] = acc;
+        }
+        if (tn >= total) break;
+        t = tn;
+    }
+}
+
+template <int T, bool Q32>
+static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
+    static int ncu = 0, per_cu = 0;
+    static size_t cached_smem = 0;
+    if (!ncu) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+    }
+    if (cached_smem != smem) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv1_kernel<T, Q32>, GEMV_THREADS, smem) != hipSuccess || n < 1) n = 1;
+        per_cu = n;
+        cached_smem = smem;
+    }
+    long long blocks = (long long)per_cu * ncu;
+    if (blocks > tiles) blocks = tiles;
+    gemv1_kernel<T, Q32><<<dim3((unsigned)blocks), GEMV_THREADS, smem, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int T>
+static hipError_t gemv1_t(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
+    return a.per32 ? gemv1_launch<T, true>(a, tiles, smem, s) : gemv1_launch<T, false>(a, tiles, smem, s);
+}
+
 template <int T, int NT, bool Q32>
 static hipError_t gemv_nt(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
     static int ncu = 0;
@@ -222,7 +447,8 @@ static hipError_t gemv_t(const GemvArgs& a, long long grid, size_t smem, hipStre
 hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     GemvArgs a{};
     a.w = g.w; a.w2 = g.pair ? g.w2 : 0; a.y = g.y; a.y2 = g.pair ? g.y2 : 0;
-    a.xq = g.xq; a.xd = (const float*)(g.xq + (uint64_t)g.n_xrows * g.cols);
+    a.xq = g.xq; a.xd = g.xq ? (const float*)(g.xq + (uint64_t)g.n_xrows * g.cols) : nullptr;
+    a.xf = g.xf; a.x_stride = g.x_stride;
     a.ids = g.ids; a.stride = g.stride; a.xg = g.xg;
     a.rows = g.rows; a.rows2 = g.pair ? g.rows2 : 0; a.cols = g.cols; a.nt = g.nt; a.y_stride = g.y_stride;
     a.rb = row_bytes(g.ty, g.cols);
@@ -241,15 +467,34 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     const int maxrows = g.pair ? (g.rows > g.rows2 ? g.rows : g.rows2) : g.rows;
     const int nslots = g.ids ? g.k : 1, nz = g.pair ? 2 : 1;
     // Rows per tile: as many as fit the tile, but no fewer tiles than about 4 per CU.
-    const int rmax = (int)((GEMV_TILE - 32) / a.rb);
+    const bool single = g.nt == 1;
+    const int rmax = (int)(((single ? GEMV1_TILE : GEMV_TILE) - 32) / a.rb);
     long long want = (long long)maxrows * nslots * nz / (4LL * ncu);
     a.R = (int)(want < 1 ? 1 : want > rmax ? rmax : want);
     if (a.R < 1) a.R = 1;
+    const int rpb = 4 * (64 / a.G);  // rows one pass of the block covers
+    if (single && a.R > rpb) a.R -= a.R % rpb;
     a.ntr = (maxrows + a.R - 1) / a.R;
     a.nslots = nslots;
     a.nz = nz;
     const long long grid = (long long)a.ntr * nslots * nz;  // tiles
     bool iq = g.ty == IQ2_XXS || g.ty == IQ3_S;
+    if (single) {
+        const uint32_t ncp = (g.cols + 255) & ~255;
+        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + ncp + ncp / 8 + GEMV1_TILE + 16;
+        switch (g.ty) {
+        case Q8_0: return gemv1_t<Q8_0>(a, grid, smem1, s);
+        case Q2_K: return gemv1_t<Q2_K>(a, grid, smem1, s);
+        case Q3_K: return gemv1_t<Q3_K>(a, grid, smem1, s);
+        case Q4_K: return gemv1_t<Q4_K>(a, grid, smem1, s);
+        case Q5_K: return gemv1_t<Q5_K>(a, grid, smem1, s);
+        case Q6_K: return gemv1_t<Q6_K>(a, grid, smem1, s);
+        case IQ2_XXS: return gemv1_t<IQ2_XXS>(a, grid, smem1, s);
+        case IQ3_S: return gemv1_t<IQ3_S>(a, grid, smem1, s);
+        case IQ4_XS: return gemv1_t<IQ4_XS>(a, grid, smem1, s);
+        }
+        return hipErrorInvalidValue;
+    }
     size_t smem = (iq ? up16(sizeof(IqTables)) : 0) + up16(g.nt * g.cols) + up16(g.nt * (g.cols / 32) * 4) +
                   up16(g.nt * (g.cols / 16) * 4) + GEMV_TILE + 16;
     switch (g.ty) {

@@ -18,7 +18,9 @@ struct GemvLaunch {
     int rows = 0, cols = 0;
     int nt = 1;                   // inputs per weight read (1..4)
     int numerics = 0;             // STRATA_NUM_*: how xq was quantized
-    const int8_t* xq = nullptr;   // quant_xq layout of n_xrows rows of cols
+    const int8_t* xq = nullptr;   // quant_xq layout of n_xrows rows of cols; null: quantize xf in the kernel (nt == 1)
+    const float* xf = nullptr;    // x as f32, rows x_stride floats apart
+    uint64_t x_stride = 0;
     int n_xrows = 1;
     float* y = nullptr;
     int y_stride = 0;             // floats between the outputs of consecutive inputs (dense)

@@ -9,11 +9,25 @@
 
 namespace strata {
 
-// x of one input in LDS: int8 values, per-32 scales (8 equal ones per super-block under Q8_K), per-16 int sums.
-struct XView {
-    const int8_t* q;
-    const float* d;
-    const int* s16;
+// x of one input for one super-block, through one of two accessors with the same interface:
+//   q16(o): the 16 int8 values at offset o (a multiple of 16), s(g): the sum of the 16 values of group g,
+//   d(j): the scale of 32-group j (under Q8_K all 8 are the super-block's one scale).
+// XLds reads LDS; XReg holds the slice in registers (indices must fold to constants: callers unroll fully).
+struct XLds {
+    const int8_t* qp;
+    const float* dp;
+    const int* sp;
+    __device__ __forceinline__ uint4 q16(int o) const { return *(const uint4*)(qp + o); }
+    __device__ __forceinline__ int s(int g) const { return sp[g]; }
+    __device__ __forceinline__ float d(int j) const { return dp[j]; }
+};
+struct XReg {
+    uint32_t w[64];
+    int sums[16];
+    float ds[8];
+    __device__ __forceinline__ uint4 q16(int o) const { return make_uint4(w[o / 4], w[o / 4 + 1], w[o / 4 + 2], w[o / 4 + 3]); }
+    __device__ __forceinline__ int s(int g) const { return sums[g]; }
+    __device__ __forceinline__ float d(int j) const { return ds[j]; }
 };
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return __builtin_amdgcn_ubfe(w, 8 * i, 8); }
@@ -37,8 +51,9 @@ __device__ __forceinline__ int dot4w(uint32_t a, uint32_t b, uint32_t c, uint32_
 // n words from a 2-byte-aligned LDS address: aligned reads, shifted into place (v_alignbyte_b32).
 template <int N>
 __device__ __forceinline__ void words_a2(const uint8_t* p, uint32_t* out) {
-    const uint32_t* a = (const uint32_t*)((uintptr_t)p & ~(uintptr_t)3);
-    uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    // stay a derivation of p (pointer arithmetic, not an integer round trip), so the reads keep p's address space
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t* a = (const uint32_t*)(p - sh);
     uint32_t prev = a[0];
 #pragma unroll
     for (int i = 0; i < N; i++) {
@@ -49,9 +64,8 @@ __device__ __forceinline__ void words_a2(const uint8_t* p, uint32_t* out) {
 }
 
 // ---- Q4_K / Q5_K: 8 sub-blocks of 32, 6-bit scales and mins (src/cpu_moe.rs:327-358) ----
-template <bool Q5>
-__device__ __forceinline__ void sb_q45(const uint8_t* b, const int8_t* xq, const int* xs16, int& isum, int& msum,
-                                       float& D, float& M) {
+template <bool Q5, class X>
+__device__ __forceinline__ void sb_q45(const uint8_t* b, const X& x, int& isum, int& msum, float& D, float& M) {
     const uint4 h = *(const uint4*)b;
     D = f16_to_f32(h.x & 0xFFFF);
     M = f16_to_f32(h.x >> 16);
@@ -81,9 +95,8 @@ __device__ __forceinline__ void sb_q45(const uint8_t* b, const int8_t* xq, const
                 hi[i] |= ((qh[i] >> (2 * p + 1)) << 4) & 0x10101010u;
             }
         }
-        const uint4* xa = (const uint4*)(xq + 64 * p);
-        const int s_lo = dot16(lo, xa[0], xa[1]);
-        const int s_hi = dot16(hi, xa[2], xa[3]);
+        const int s_lo = dot16(lo, x.q16(64 * p), x.q16(64 * p + 16));
+        const int s_hi = dot16(hi, x.q16(64 * p + 32), x.q16(64 * p + 48));
         const uint32_t scw = p < 2 ? sc_lo : sc_hi;
         is += (int)byte_of(scw, (2 * p) & 3) * s_lo + (int)byte_of(scw, (2 * p + 1) & 3) * s_hi;
     }
@@ -91,12 +104,13 @@ __device__ __forceinline__ void sb_q45(const uint8_t* b, const int8_t* xq, const
     // min term: sum_j m_j * (sum of x over sub-block j)
     int ms = 0;
 #pragma unroll
-    for (int j = 0; j < 8; j++) ms += (int)byte_of(j < 4 ? m_lo : m_hi, j & 3) * (xs16[2 * j] + xs16[2 * j + 1]);
+    for (int j = 0; j < 8; j++) ms += (int)byte_of(j < 4 ? m_lo : m_hi, j & 3) * (x.s(2 * j) + x.s(2 * j + 1));
     msum = ms;
 }
 
 // ---- Q6_K: 16 groups of 16, int8 scales, values q - 32 (src/cpu_moe.rs:360-377) ----
-__device__ __forceinline__ void sb_q6(const uint8_t* b, const int8_t* xq, const int* xs16, int& isum, float& D) {
+template <class X>
+__device__ __forceinline__ void sb_q6(const uint8_t* b, const X& x, int& isum, float& D) {
     uint32_t sc[4];
     words_a2<4>(b + 192, sc);
     D = f16_to_f32(rd16(b + 208));
@@ -120,7 +134,7 @@ __device__ __forceinline__ void sb_q6(const uint8_t* b, const int8_t* xq, const 
                     v[i] = nib | (((hb >> (2 * qd)) << 4) & 0x30303030u);  // q + 32, in 0..63
                 }
                 const int xo = 128 * n + 32 * qd + 16 * a;
-                const int s = dot4w(v[0], v[1], v[2], v[3], *(const uint4*)(xq + xo)) - 32 * xs16[xo >> 4];
+                const int s = dot4w(v[0], v[1], v[2], v[3], x.q16(xo)) - 32 * x.s(xo >> 4);
                 const int g = 8 * n + a + 2 * qd;  // scale index: l / 16 + 2 qd within the half
                 is += sbyte_of(sc[g >> 2], g & 3) * s;
             }
@@ -129,7 +143,8 @@ __device__ __forceinline__ void sb_q6(const uint8_t* b, const int8_t* xq, const 
 }
 
 // ---- Q8_0: 8 blocks of 32 with an f16 scale each (src/cpu_moe.rs:319-325): returns sum_b d_b * s_b ----
-__device__ __forceinline__ float sb_q8_0(const uint8_t* b, const int8_t* xq, int nb) {
+template <class X>
+__device__ __forceinline__ float sb_q8_0(const uint8_t* b, const X& x, int nb) {
     float f = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
@@ -139,25 +154,23 @@ __device__ __forceinline__ float sb_q8_0(const uint8_t* b, const int8_t* xq, int
         uint32_t q[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = align_bytes(w[i + 1], w[i], 2);
-        const uint4* xa = (const uint4*)(xq + 32 * k);
-        const int s = dot16(q, xa[0], xa[1]);
+        const int s = dot16(q, x.q16(32 * k), x.q16(32 * k + 16));
         f += f16_to_f32(w[0] & 0xFFFF) * (float)s;
     }
     return f;
 }
 
 // ---- generic: any type through task<T> (8 tasks of 32 values) ----
-template <int T>
-__device__ __forceinline__ void sb_generic(const uint8_t* b, const int8_t* xq, const int* xs16, const IqTables* tab,
-                                           int& isum, int& msum, float& D, float& M) {
+template <int T, class X>
+__device__ __forceinline__ void sb_generic(const uint8_t* b, const X& x, const IqTables* tab, int& isum, int& msum,
+                                           float& D, float& M) {
     int is = 0, ms = 0;
-#pragma unroll 2
+#pragma unroll
     for (int k = 0; k < 8; k++) {
         Task t;
         task<T>(b, k, tab, t);
-        const uint4 x0 = *(const uint4*)(xq + t.o0), x1 = *(const uint4*)(xq + t.o1);
-        int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x0), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x1);
-        const int a0 = xs16[t.o0 >> 4], a1 = xs16[t.o1 >> 4];
+        int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x.q16(t.o0)), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x.q16(t.o1));
+        const int a0 = x.s(t.o0 >> 4), a1 = x.s(t.o1 >> 4);
         if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * a0; s1 -= Fmt<T>::BIAS * a1; }
         is += t.sc0 * s0 + t.sc1 * s1;
         if constexpr (Fmt<T>::MIN) ms += t.m0 * a0 + t.m1 * a1;
@@ -167,27 +180,26 @@ __device__ __forceinline__ void sb_generic(const uint8_t* b, const int8_t* xq, c
     msum = ms;
 }
 
-// acc += the super-block's contribution, Q8_K numerics (x scale xd[0] for the whole super-block).
-template <int T>
-__device__ __forceinline__ float sb_dot_q8k(const uint8_t* b, const int8_t* xq, const float* xd, const int* xs16,
-                                            const IqTables* tab, int nvals) {
-    const float dx = xd[0];
+// The super-block's contribution, Q8_K numerics (one x scale for the whole super-block).
+template <int T, class X>
+__device__ __forceinline__ float sb_dot_q8k(const uint8_t* b, const X& x, const IqTables* tab, int nvals) {
+    const float dx = x.d(0);
     if constexpr (T == Q4_K || T == Q5_K) {
         int is, ms;
         float D, M;
-        sb_q45<T == Q5_K>(b, xq, xs16, is, ms, D, M);
+        sb_q45<T == Q5_K>(b, x, is, ms, D, M);
         return dx * (D * (float)is - M * (float)ms);
     } else if constexpr (T == Q6_K) {
         int is;
         float D;
-        sb_q6(b, xq, xs16, is, D);
+        sb_q6(b, x, is, D);
         return dx * (D * (float)is);
     } else if constexpr (T == Q8_0) {
-        return dx * sb_q8_0(b, xq, nvals >> 5);
+        return dx * sb_q8_0(b, x, nvals >> 5);
     } else {
         int is, ms = 0;
         float D, M = 0.0f;
-        sb_generic<T>(b, xq, xs16, tab, is, ms, D, M);
+        sb_generic<T>(b, x, tab, is, ms, D, M);
         float f = D * (float)is;
         if constexpr (Fmt<T>::MIN) f -= M * (float)ms;
         return dx * f;
@@ -196,22 +208,20 @@ __device__ __forceinline__ float sb_dot_q8k(const uint8_t* b, const int8_t* xq, 
 
 // The same under per-32 x scales (the reference GPU's default numerics): every 32-group has its own dx, so each task
 // closes in float.
-template <int T>
-__device__ __forceinline__ float sb_dot_q32(const uint8_t* b, const int8_t* xq, const float* xd, const int* xs16,
-                                            const IqTables* tab, int nvals) {
+template <int T, class X>
+__device__ __forceinline__ float sb_dot_q32(const uint8_t* b, const X& x, const IqTables* tab, int nvals) {
     float f = 0.0f;
-#pragma unroll 2
+#pragma unroll
     for (int k = 0; k < 8; k++) {
         if (32 * k >= nvals) break;  // a partial last super-block (Q8_0 only)
         Task t;
         task<T>(b, k, tab, t);
-        const uint4 x0 = *(const uint4*)(xq + t.o0), x1 = *(const uint4*)(xq + t.o1);
-        int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x0), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x1);
-        const int a0 = xs16[t.o0 >> 4], a1 = xs16[t.o1 >> 4];
+        int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x.q16(t.o0)), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x.q16(t.o1));
+        const int a0 = x.s(t.o0 >> 4), a1 = x.s(t.o1 >> 4);
         if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * a0; s1 -= Fmt<T>::BIAS * a1; }
         float f0 = t.D * (float)(t.sc0 * s0), f1 = t.D * (float)(t.sc1 * s1);
         if constexpr (Fmt<T>::MIN) { f0 -= t.M * (float)(t.m0 * a0); f1 -= t.M * (float)(t.m1 * a1); }
-        f += xd[t.o0 >> 5] * f0 + xd[t.o1 >> 5] * f1;
+        f += x.d(t.o0 >> 5) * f0 + x.d(t.o1 >> 5) * f1;
     }
     return f;
 }

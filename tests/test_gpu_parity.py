@@ -444,3 +444,25 @@ def test_errors_do_not_launch(hip):
     b = hip.alloc(16)
     with pytest.raises(S.StrataError, match="outside"):
         hip.htod(np.zeros(32, dtype=np.uint8), b)
+
+
+def test_graph_replays_read_device_memory(hip):
+    """Backend::graph (src/backend.rs:118-120): a recorded GEMV sequence replays with the values device memory holds
+    at replay time; replays interleave with eager work and each one matches the eager result."""
+    ty, rows, cols = ggml.Q4_K, 300, 2048
+    w = random_blocks(ty, rows, cols, seed=61)
+    t = hip.upload_tensor(ty, w)
+    xb, y = hip.alloc(cols * 4), hip.alloc(rows * 4)
+    hip.htod(normal(cols, seed=62), xb)
+    hip.gemv(t, xb, y)  # warm: any scratch is sized before recording
+    hip.graph("g1", lambda: hip.gemv(t, xb, y))
+    for i in range(3):
+        x = normal(cols, seed=70 + i)
+        hip.htod(x, xb)
+        hip.graph("g1", None)
+        got = down(hip, y, np.float32, rows)
+        y2 = hip.alloc(rows * 4)
+        hip.gemv(t, xb, y2)  # eager work between replays
+        assert np.array_equal(got, down(hip, y2, np.float32, rows)), i
+        assert max_rel_err(got, O.matvec(ty, w, rows, cols, x)) <= TOL
+    hip.drop_graphs()
