@@ -66,9 +66,19 @@ class Rotated:
         return t
 
 
+USE_GRAPHS = True  # --eager turns them off (rocprofv3's kernel tracing does not survive graph launches)
+
+
 def time_gemv(hip, rot, xb, yb, iters):
     """Average GEMV time over >= iters launches, replayed from a recorded graph (Backend::graph) of one launch per
     weight copy, so host launch gaps do not count as GPU time."""
+    if not USE_GRAPHS:
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0)
+        for _ in range(iters):
+            hip.gemv(rot.next(), xb, yb)
+        hip.record(e1)
+        return hip.elapsed_ms(e0, e1) / iters
     key = ("gemv", id(rot))
     n = rot.n
     hip.graph(key, lambda: [hip.gemv(rot.next(), xb, yb) for _ in range(n)])
@@ -109,14 +119,16 @@ def bench_gemv(hip, S, ggml, steps, warmup):
     # The timed steps replay a recorded graph of GRAPH_STEPS steps (each step's GEMVs rotate their weight copies
     # inside it), the way the reference's decode replays CUDA graphs (src/cuda/mod.rs:868-888).
     gs = min(GRAPH_STEPS, steps)
-    hip.graph("sweep", lambda: [step() for _ in range(gs)])
     reps = -(-steps // gs)
-    hip.graph("sweep", None)
+    run = (lambda: hip.graph("sweep", None)) if USE_GRAPHS else (lambda: [step() for _ in range(gs)])
+    if USE_GRAPHS:
+        hip.graph("sweep", lambda: [step() for _ in range(gs)])
+    run()
     hip.sync()
     e0, e1 = hip.event(), hip.event()
     hip.record(e0)
     for _ in range(reps):
-        hip.graph("sweep", None)
+        run()
     hip.record(e1)
     ms = hip.elapsed_ms(e0, e1)
     steps = reps * gs
@@ -253,9 +265,17 @@ def roofline_q4k_lmhead(hip, shapes, xb, yb, iters=400):
     s = next(s for s in shapes if s["name"] == "Q4_K" and s["rows"] == 151936)
     ms = time_gemv(hip, s["rot"], xb, yb, iters)
     achieved = s["bytes"] / (ms / 1e3) / 1e9
+    # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE, scaled by a copy kernel of known size
+    # (profiles/gemv_q4k_151936x2048.md); None when that summary is absent.
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "gemv_q4k_151936x2048.md")
+    if os.path.exists(prof):
+        for line in open(prof):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(line.split(":")[1])
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "gemv_kernel<Q4_K, NT=1, G=64>, 151936x2048 (175.0 MB weights + x + y per launch)",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "algorithmic_bytes": s["bytes"],
+            "kernel": "gemv1_kernel<Q4_K>, 151936x2048: 175.03 MB weights + 8 KB x + 0.61 MB y per launch",
             "avg_launch_us": round(1000 * ms, 2)}
 
 
@@ -285,7 +305,10 @@ def main():
     ap.add_argument("--moe-iters", type=int, default=20)
     ap.add_argument("--profile-gemv", action="store_true",
                     help="only run the Q4_K lm-head GEMV and a 256 MB copy kernel 50 times each (for rocprofv3)")
+    ap.add_argument("--eager", action="store_true", help="launch every op from the host (no recorded graphs)")
     args = ap.parse_args()
+    global USE_GRAPHS
+    USE_GRAPHS = not args.eager
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (the hot path shards by output rows "
               "or by expert; that split is a design note, not run here)", file=sys.stderr)
@@ -324,6 +347,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
+        "timing": "HIP events on the library stream around recorded-graph replays" if USE_GRAPHS else "HIP events around eager launches",
         "data": "synthetic: seeded N(0,0.02) weights quantized by the library quantizer, N(0,1) activations",
         "config": {"workload": "configs[1]: batch-1 decode GEMV sweep Q4_K/Q5_K/Q6_K/Q8_0 x {6144x2048, 2048x2048, "
                                "151936x2048}, weights rotated over >512 MB of copies per shape",
