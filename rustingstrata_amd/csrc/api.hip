@@ -200,7 +200,9 @@ int strata_alloc(strata_ctx* c, size_t bytes, uint64_t* addr) {
     if (!addr) return set_error("strata_alloc: null out");
     size_t n = std::max(bytes, (size_t)1);
     void* p = nullptr;
-    STRATA_HIP(hipMalloc(&p, (n + 255) & ~(size_t)255));
+    // 256 bytes of slack past the end: kernels read weight rows in 16-byte-aligned covers, which may reach up to
+    // 15 bytes past a row's last block.
+    STRATA_HIP(hipMalloc(&p, ((n + 255) & ~(size_t)255) + 256));
     hipError_t e = hipMemsetAsync(p, 0, n, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) { hipFree(p); return hip_error(e, "zeroing a new buffer"); }

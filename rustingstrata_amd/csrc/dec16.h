@@ -1,58 +1,42 @@
 // 16 consecutive weights of a super-block (values 16 p .. 16 p + 15) as int8 digit planes for the int8 MFMA GEMM.
 //
 // A weight of a super-block is D * sc * (q - bias) - M * m with integer sc, q, m constant over its 16 (Q6_K, Q2_K,
-// Q3_K) or 32 (the others) values. The integer v = sc * (q - bias) (|v| <= 4096) is split as v = 64 HI + LO with
-// LO in 0..63 and HI in -64..63, each an int8 plane; m is a third plane where the format has mins. The split is
-// exact, so HI.x, LO.x and M.x sum exactly in int32.
+// Q3_K) or 32 (the others) values. The integer v = sc * (q - bias) (|v| <= 4096) is split as v = 256 H + L with
+// L in -128..127 and H in -16..16, each an int8 plane; m is a third plane where the format has mins. The split is
+// exact, so H.x, L.x and M.x sum exactly in int32.
 //
-// dec16<T>(b, p, hi, lo, m) reads the super-block at b (LDS, the alignment of the global copy mod 16) and writes the
-// four words of HI and LO and the min m (0 without mins). Layouts: src/quant/mod.rs (Q2_K 156-170, Q3_K 173-207,
-// Q4_K 209-221, Q5_K 223-237, Q6_K 239-256, IQ2_XXS 287-297, IQ3_S 345-361, IQ4_XS 363-376).
+// The split costs one packed 16-bit multiply-add per two values: u = sc * q + (128 - bias * sc) = v + 128 in each
+// 16-bit lane, whose high byte is H = floor(u / 256) and whose low byte minus 128 (its top bit flipped) is L.
+//
+// Dec<T>::run(b, p, tab, H, L, m) reads the super-block at b (LDS, the alignment of the global copy mod 16) and
+// writes the four words of H and L and the min m (0 without mins). Layouts: src/quant/mod.rs (Q2_K 156-170, Q3_K
+// 173-207, Q4_K 209-221, Q5_K 223-237, Q6_K 239-256, IQ2_XXS 287-297, IQ3_S 345-361, IQ4_XS 363-376).
 #pragma once
 #include "sbdot.h"
 
 namespace strata {
 
-__device__ __forceinline__ uint32_t pk_mul16(uint32_t a, uint32_t b) {  // low 16 bits of each 16-bit product
-    typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
-    v2u16 x = __builtin_bit_cast(v2u16, a), y = __builtin_bit_cast(v2u16, b);
-    return __builtin_bit_cast(uint32_t, (v2u16)(x * y));
-}
-__device__ __forceinline__ uint32_t pk_ashr6(uint32_t a) {  // arithmetic >> 6 of each signed 16-bit half
-    typedef short v2i16 __attribute__((ext_vector_type(2)));
-    v2i16 x = __builtin_bit_cast(v2i16, a);
-    return __builtin_bit_cast(uint32_t, (v2i16)(x >> (v2i16){6, 6}));
-}
-// bytes 0 and 2 of lo16 and hi16 interleaved: byte0 = lo16.b0, byte1 = hi16.b0, byte2 = lo16.b2, byte3 = hi16.b2
-__device__ __forceinline__ uint32_t pack_even_bytes(uint32_t hi16, uint32_t lo16) {
-    return __builtin_amdgcn_perm(hi16, lo16, 0x06020400u);
-}
+typedef unsigned short v2u16 __attribute__((ext_vector_type(2)));
 
-// The planes of one word of 4 values: bytes 0, 2 and 1, 3 go to 16-bit lanes, v = sc * (q - bias) in each lane
-// (|v| <= 4096), HI = v >> 6 and LO = v & 63 packed back to bytes. UNSIGNED: q and sc are non-negative and bias is
-// 0 (the K-quants with mins); otherwise q is signed (SGN, the IQ codebook values) or biased by `bias`.
-template <bool UNSIGNED>
-__device__ __forceinline__ void planes4(uint32_t q, uint32_t sc16, uint32_t bias16, bool sgn, uint32_t& hi, uint32_t& lo) {
-    typedef short v2i16 __attribute__((ext_vector_type(2)));
-    uint32_t a = q & 0x00FF00FFu, b = (q >> 8) & 0x00FF00FFu;
-    if constexpr (!UNSIGNED) {
-        v2i16 va16 = __builtin_bit_cast(v2i16, a), vb16 = __builtin_bit_cast(v2i16, b);
-        if (sgn) {  // sign-extend each byte to 16 bits
-            va16 = (va16 ^ (v2i16){0x80, 0x80}) - (v2i16){0x80, 0x80};
-            vb16 = (vb16 ^ (v2i16){0x80, 0x80}) - (v2i16){0x80, 0x80};
-        } else {
-            const v2i16 bb = __builtin_bit_cast(v2i16, bias16);
-            va16 -= bb;
-            vb16 -= bb;
-        }
-        a = __builtin_bit_cast(uint32_t, va16);
-        b = __builtin_bit_cast(uint32_t, vb16);
-    }
-    const uint32_t va = pk_mul16(a, sc16), vb = pk_mul16(b, sc16);
-    const uint32_t ha = UNSIGNED ? (va >> 6) & 0x03FF03FFu : pk_ashr6(va), hb = UNSIGNED ? (vb >> 6) & 0x03FF03FFu : pk_ashr6(vb);
-    hi = pack_even_bytes(hb, ha);
-    lo = pack_even_bytes(vb & 0x003F003Fu, va & 0x003F003Fu);
+// Split of u = sc * q + add per 16-bit lane (mod 2^16) for the bytes of q given as qa (bytes 0 and 2 in the low
+// byte of each 16-bit lane) and qb (bytes 1 and 3): H = high bytes, L = low bytes ^ 0x80, in value order.
+__device__ __forceinline__ void split16(uint32_t qa, uint32_t qb, uint32_t sc16, uint32_t add16, uint32_t& H, uint32_t& L) {
+    const v2u16 sc = __builtin_bit_cast(v2u16, sc16), ad = __builtin_bit_cast(v2u16, add16);
+    const uint32_t ua = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, qa) * sc + ad));
+    const uint32_t ub = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, qb) * sc + ad));
+    H = __builtin_amdgcn_perm(ub, ua, 0x07030501u);
+    L = __builtin_amdgcn_perm(ub, ua, 0x06020400u) ^ 0x80808080u;
 }
+// The planes of 4 unsigned bytes q: v = sc * q - bias * sc; add16 = (128 - bias * sc) in both halves.
+__device__ __forceinline__ void planes_u(uint32_t q, uint32_t sc16, uint32_t add16, uint32_t& H, uint32_t& L) {
+    split16(q & 0x00FF00FFu, __builtin_amdgcn_perm(q, q, 0x0c030c01u), sc16, add16, H, L);
+}
+// The planes of 4 signed bytes q (sign-extended to 16 bits by the byte permute): v = sc * q; add16 = 128.
+__device__ __forceinline__ void planes_s(uint32_t q, uint32_t sc16, uint32_t& H, uint32_t& L) {
+    split16(__builtin_amdgcn_perm(0u, q << 8, 0x09030801u), __builtin_amdgcn_perm(0u, q, 0x09030801u), sc16,
+            0x00800080u, H, L);
+}
+__device__ __forceinline__ uint32_t rep16(int v) { return ((uint32_t)v & 0xFFFFu) * 0x00010001u; }
 
 template <int T> struct Dec;
 
@@ -70,12 +54,13 @@ __device__ __forceinline__ void dec16_q45(const uint8_t* b, int p, uint32_t* hi,
         const uint4 qh = *(const uint4*)(b + 16 + l0);
         hs[0] = qh.x; hs[1] = qh.y; hs[2] = qh.z; hs[3] = qh.w;
     }
-    const uint32_t sc16 = (uint32_t)sc * 0x00010001u;
+    const uint32_t sc16 = rep16(sc);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         uint32_t q = (ws[i] >> (4 * (j & 1))) & 0x0F0F0F0Fu;
-        if constexpr (Q5) q |= ((hs[i] >> j) << 4) & 0x10101010u;
-        planes4<true>(q, sc16, 0, false, hi[i], lo[i]);
+        // bit j of each qh byte to bit 4: a rotate right by j - 4 (mod 32); bits that wrap are masked off
+        if constexpr (Q5) q |= __builtin_amdgcn_alignbit(hs[i], hs[i], (uint32_t)(j + 28) & 31) & 0x10101010u;
+        planes_u(q, sc16, 0x00800080u, hi[i], lo[i]);
     }
 }
 template <> struct Dec<Q4_K> {
@@ -100,11 +85,13 @@ template <> struct Dec<Q6_K> {
         words_a2<4>(b + 64 * n + 32 * (qd & 1) + l0, ql);
         words_a2<4>(b + 128 + 32 * n + l0, qh);
         const int sc = (int8_t)b[192 + 8 * n + (l0 >> 4) + 2 * qd];
-        const uint32_t sc16 = (uint32_t)(sc & 0xFFFF) * 0x00010001u;
+        const uint32_t sc16 = rep16(sc), add16 = rep16(128 - 32 * sc);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t q = ((ql[i] >> (4 * (qd >> 1))) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * qd)) << 4) & 0x30303030u);
-            planes4<false>(q, sc16, 0x00200020u, false, hi[i], lo[i]);
+            // bits 2 qd, 2 qd + 1 of each qh byte to bits 4, 5: a rotate right by 2 qd - 4 (mod 32), masked
+            const uint32_t q = ((ql[i] >> (4 * (qd >> 1))) & 0x0F0F0F0Fu) |
+                               (__builtin_amdgcn_alignbit(qh[i], qh[i], (uint32_t)(2 * qd + 28) & 31) & 0x30303030u);
+            planes_u(q, sc16, add16, hi[i], lo[i]);
         }
         m = 0;
     }
@@ -123,8 +110,13 @@ template <> struct Dec<Q2_K> {
         const uint32_t s = b[p];
         const uint32_t sc16 = (s & 0xF) * 0x00010001u;
         m = (int)(s >> 4);
+        // sc * q <= 45: each byte's product stays in its byte, so one packed 16-bit multiply scales all four
 #pragma unroll
-        for (int i = 0; i < 4; i++) planes4<true>((ws[i] >> (2 * j)) & 0x03030303u, sc16, 0, false, hi[i], lo[i]);
+        for (int i = 0; i < 4; i++) {
+            lo[i] = __builtin_bit_cast(uint32_t, (v2u16)(__builtin_bit_cast(v2u16, (ws[i] >> (2 * j)) & 0x03030303u) *
+                                                         __builtin_bit_cast(v2u16, sc16)));
+            hi[i] = 0;
+        }
     }
     __device__ static void scales(const uint8_t* b, float& D, float& M) { D = f16_to_f32(rd16(b + 80)); M = f16_to_f32(rd16(b + 82)); }
 };
@@ -139,11 +131,11 @@ template <> struct Dec<Q3_K> {
         words_a2<4>(b + 32 + 32 * n + l0, qs);
         words_a2<4>(b + l0, hm);
         const int sc = q3k_scale(b + 96, p) - 32;
-        const uint32_t sc16 = (uint32_t)(sc & 0xFFFF) * 0x00010001u;
+        const uint32_t sc16 = rep16(sc), add16 = rep16(128 - 4 * sc);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t q = ((qs[i] >> (2 * j)) & 0x03030303u) | (((hm[i] >> hb) & 0x01010101u) << 2);
-            planes4<false>(q, sc16, 0x00040004u, false, hi[i], lo[i]);
+            planes_u(q, sc16, add16, hi[i], lo[i]);
         }
         m = 0;
     }
@@ -159,9 +151,9 @@ template <> struct Dec<IQ4_XS> {
         const uint32_t ws[4] = {w0.x, w0.y, w1.x, w1.y};
         const uint32_t sh = rd16(b + 2);
         const int ls = ((b[4 + ib / 2] >> (4 * (ib & 1))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4);
-        const uint32_t sc16 = (uint32_t)((ls - 32) & 0xFFFF) * 0x00010001u;
+        const uint32_t sc16 = rep16(ls - 32);
 #pragma unroll
-        for (int i = 0; i < 4; i++) planes4<false>((uint32_t)iq4nl_lut((ws[i] >> (4 * nib)) & 0x0F0F0F0Fu), sc16, 0, true, hi[i], lo[i]);
+        for (int i = 0; i < 4; i++) planes_s((uint32_t)iq4nl_lut((ws[i] >> (4 * nib)) & 0x0F0F0F0Fu), sc16, hi[i], lo[i]);
         m = 0;
     }
     __device__ static void scales(const uint8_t* b, float& D, float& M) { D = f16_to_f32(rd16(b)); M = 0.0f; }
@@ -180,8 +172,8 @@ template <> struct Dec<IQ2_XXS> {
             const int l = 2 * h + e;
             const uint64_t grid = tab->iq2xxs[(g >> (8 * l)) & 255];
             const uint32_t s = tab->ksigns[(aux >> (7 * l)) & 127];
-            planes4<false>((uint32_t)neg_bytes((uint32_t)grid, s), sc16, 0, true, hi[2 * e], lo[2 * e]);
-            planes4<false>((uint32_t)neg_bytes((uint32_t)(grid >> 32), s >> 4), sc16, 0, true, hi[2 * e + 1], lo[2 * e + 1]);
+            planes_s((uint32_t)neg_bytes((uint32_t)grid, s), sc16, hi[2 * e], lo[2 * e]);
+            planes_s((uint32_t)neg_bytes((uint32_t)(grid >> 32), s >> 4), sc16, hi[2 * e + 1], lo[2 * e + 1]);
         }
         m = 0;
     }
@@ -203,8 +195,8 @@ template <> struct Dec<IQ3_S> {
             const uint32_t g1 = tab->iq3s[(q2 & 255) | ((hb << (8 - 2 * l)) & 256)];
             const uint32_t g2 = tab->iq3s[((q2 >> 8) & 255) | ((hb << (7 - 2 * l)) & 256)];
             const uint32_t s = sg >> (8 * e);
-            planes4<false>((uint32_t)neg_bytes(g1, s), sc16, 0, true, hi[2 * e], lo[2 * e]);
-            planes4<false>((uint32_t)neg_bytes(g2, s >> 4), sc16, 0, true, hi[2 * e + 1], lo[2 * e + 1]);
+            planes_s((uint32_t)neg_bytes(g1, s), sc16, hi[2 * e], lo[2 * e]);
+            planes_s((uint32_t)neg_bytes(g2, s >> 4), sc16, hi[2 * e + 1], lo[2 * e + 1]);
         }
         m = 0;
     }

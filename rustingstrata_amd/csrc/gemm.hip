@@ -4,17 +4,29 @@
 //
 // Exact integer super-blocks. X is int8 with one scale per 256 values (Q8_K). A weight of a super-block is
 // D * sc * (q - bias) - M * m with integer sc, q, m per 16/32-value group and float D, M per super-block; the integer
-// v = sc * (q - bias) is split into two int8 digit planes v = 64 HI + LO, and the group min m is a third plane
+// v = sc * (q - bias) is split into two int8 digit planes v = 256 H + L, and the group min m is a third plane
 // (dec16.h). Each plane is an int8 matrix over the whole super-block, so one MFMA of K = 64 covers any mix of groups
-// and the int32 sums HI.x, LO.x, M.x (exact) close the super-block as
-//     acc += dx * (D * (64 HI.x + LO.x) - M * M.x).
+// and the int32 sums H.x, L.x, M.x (exact) close the super-block as
+//     acc += dx * (D * (256 H.x + L.x) - M * M.x).
 // No per-group scaling happens in the K loop.
 //
-// Block: 256 threads, one tile of up to 128 positions x 64 weight rows. Wave w owns weight rows 16 w .. 16 w + 15 and
-// all positions (8 MFMA tiles of 16 positions), so every weight is decoded once per block, by the lane that feeds it
-// to the MFMA: lane l decodes row l % 16, values 16 (l / 16) .. of each 64-deep K step, straight into its B operand.
-// Per super-block the raw weight blocks of the 64 rows and the 128 gathered X rows are staged in LDS; the next
-// super-block's are loaded into registers meanwhile.
+// Block: 512 threads (8 waves, two per SIMD), a tile of up to GM = 128 positions x GN = 128 weight rows. Wave w owns
+// weight rows 16 w .. 16 w + 15 (one 16-row MFMA column) and every position (8 MFMA tiles of 16 positions), so each
+// weight is decoded once per block, by the lane that feeds it to the MFMA. Per super-block s the two waves that
+// share a SIMD (w and w + 4) take opposite orders:
+//   role 0 (waves 0-3): MFMAs and close of s (B of s decoded earlier), then decode of s + 1;
+//   role 1 (waves 4-7): decode of s, then MFMAs and close of s;
+// so one wave's VALU work (decode: weights to digit-plane B operands; close: int32 sums to float) runs while the
+// other's MFMAs occupy the matrix core. Within the tile loop the close of one tile runs while the matrix core works
+// on the next (tiles in pairs, two sets of int32 sums).
+// Loads go straight from global memory into LDS (global_load_lds_dwordx4: lane l of a wave's instruction writes the
+// 16 bytes at its own address to LDS base + 16 l), one super-block ahead for X (double buffer) and two for the raw
+// weights (triple buffer), so one barrier per super-block suffices and every load has a whole super-block to land.
+// X sits in LDS as [position][256 bytes] with 16-byte chunk c of position p at chunk c ^ (p & 15): a 16-lane MFMA
+// fragment read (16 positions, one chunk) then touches 16 distinct bank groups.
+#include <algorithm>
+#include <type_traits>
+
 #include "dec16.h"
 #include "gemm.h"
 #include "kernels.h"
@@ -23,19 +35,21 @@
 namespace strata {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
-constexpr int NXCD = 8;                        // MI355X: 8 XCDs, each with its own L2
-constexpr int GM = 128, GN = 64;               // positions, weight rows per block
-constexpr int XP = 256 + 16;                   // LDS pitch of an X row (one super-block of int8, bank-offset)
-constexpr int XCH = GM * 16 / 256;             // 16-byte X chunks per thread per super-block
+constexpr int NXCD = 8;              // MI355X: 8 XCDs, each with its own L2
+constexpr int GM = 128, GN = 128;    // positions, weight rows per block
+constexpr int NW = 8;                // waves per block
+constexpr int NTT = GM / 16;         // MFMA position tiles per block
+constexpr int XBUF = GM * 256;       // bytes of one X buffer
 
 template <int T> struct GemmFmt {
     static constexpr bool MIN = Dec<T>::MIN;
-    static constexpr bool HI = T != Q2_K;                        // Q2_K's sc * q <= 45 fits the LO plane
-    static constexpr int NP = (HI ? 2 : 1) + (MIN ? 1 : 0);       // planes
-    static constexpr int RAWP = ((sb_bytes(T) + 15) & ~15) + 16;  // raw super-block slot per row in LDS
-    static constexpr int WCH = (GN * (RAWP / 16) + 255) / 256;    // 16-byte weight chunks per thread
+    static constexpr bool HI = T != Q2_K;                         // Q2_K's sc * q <= 45 fits the LO plane
+    static constexpr int NP = (HI ? 2 : 1) + (MIN ? 1 : 0);        // planes
+    static constexpr int NCH0 = (sb_bytes(T) + 15 + 15) / 16;     // 16-byte chunks covering a super-block at any offset
+    static constexpr int NCH = NCH0 | 1;                           // odd: rows of the raw tile start in spread banks
+    static constexpr int RAWP = 16 * NCH;                          // LDS pitch of a raw weight row
+    static constexpr int WBUF = GN * RAWP;                         // bytes of one raw weight buffer
 };
 
 struct GemmArgs {
@@ -51,179 +65,317 @@ struct GemmArgs {
     int rows, cols, act;
     uint64_t rb;
     int max_tiles;        // tiles in the grid (an upper bound when the count is on the device)
+    int gx;               // blocks per XCD
 };
 
 __device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + (float)exp(-(double)v)); }
 
+// 16 bytes per lane from global address g into LDS at lds + 16 * lane (global_load_lds_dwordx4, LDS base in M0).
+// Issued as inline assembly so that the compiler's wait insertion does not tie it to later LDS reads: it would
+// otherwise wait for every outstanding load before the first LDS read, and a load issued for a later super-block
+// could not overlap this one. The kernel waits for these loads itself (wait_loads) before the barrier that
+// publishes them. `lds` must be the same for every lane of the wave.
+__device__ __forceinline__ void load_lds16(uint64_t g, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(m0) : "memory", "m0");
+}
+// This wave's loads into LDS are complete (vmcnt 0; the barrier that follows publishes them to the block).
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+#ifdef STRATA_GEMM_TRACE
+// Debug builds: shader clock at the phases of the first steps of a few waves (read with strata_debug_gemm_trace).
+__device__ uint64_t g_gemm_trace[8][64][6];
+#define TRACE(ph)                                                                                         \
+    do {                                                                                                  \
+        const int tb_ = blockIdx.x == 0 ? 0 : blockIdx.x == 37 ? 1 : -1;                                  \
+        if (tb_ >= 0 && (wave == 0 || wave == 4) && lane == 0 && g < 64)                                  \
+            g_gemm_trace[tb_ * 2 + (wave >> 2)][g][ph] = __builtin_amdgcn_s_memtime();                    \
+    } while (0)
+#else
+#define TRACE(ph) do {} while (0)
+#endif
+
+// f(std::integral_constant<int, I>) for I = B .. E - 1: the index is a constant expression in the body, so register
+// arrays indexed by it stay in registers.
+template <int B, int E, typename Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 template <int T>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
+__global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     using F = GemmFmt<T>;
-    constexpr int NP = F::NP, SBB = sb_bytes(T), RAWP = F::RAWP, WCH = F::WCH;
+    constexpr int NP = F::NP, SBB = sb_bytes(T), NCH = F::NCH, RAWP = F::RAWP, WBUF = F::WBUF;
     constexpr int P_HI = 0, P_LO = F::HI ? 1 : 0, P_M = F::HI ? 2 : 1;
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     extern __shared__ __align__(16) uint8_t smem[];
-    // LDS: [X: GM x XP][raw W: GN x RAWP][dx: GM][xr: GM][IqTables]
+    // LDS: [X: 2 x GM x 256][raw W: 3 x GN x RAWP][dx: 2 x GM][IqTables]
     int8_t* xs = (int8_t*)smem;
-    uint8_t* raw = smem + GM * XP;
-    float* dxs = (float*)(raw + GN * RAWP);
-    int* xr = (int*)(dxs + GM);
-    IqTables* tab = (IqTables*)(xr + GM);
+    uint8_t* raw = smem + 2 * XBUF;
+    float* dxs = (float*)(raw + 3 * WBUF);
+    IqTables* tab = (IqTables*)(dxs + 2 * GM);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    // XCD-aware order: the hardware deals consecutive block ids to the 8 XCDs in turn, so logical block
-    // (tile, row block) = consecutive ids within one XCD; a tile's row blocks and an expert's tiles then share that
-    // XCD's L2 (its X rows and the expert's weights are read from L2 after the first block).
+    const int cols = a.cols, nsb = cols / 256;
+
+    // Items are (tile, row block) pairs, item = tile * nrb + row block. XCD x (the hardware deals consecutive block
+    // ids to the 8 XCDs in turn) takes the items x * per .. (x + 1) * per - 1, so a tile's row blocks and an
+    // expert's tiles run on one XCD and share its L2 (X rows, expert weights); its a.gx blocks take every a.gx-th
+    // item from their index j.
     const int ntiles = a.n_tiles_dev ? min(*a.n_tiles_dev, a.max_tiles) : a.max_tiles;
     const int nrb = (a.rows + GN - 1) / GN, total = nrb * ntiles;
-    const int per_xcd = (total + NXCD - 1) / NXCD;
-    const int lid = (blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
-    if (blockIdx.x / NXCD >= per_xcd || lid >= total) return;
-    const int tile = lid / nrb, rb_idx = lid % nrb;
-    const uint8_t* W;
-    int m0, cnt;
-    if (a.tiles) {
-        const uint64_t t0 = a.tiles[2 * tile], t1 = a.tiles[2 * tile + 1];
-        W = (const uint8_t*)t0;
-        m0 = (int)(uint32_t)t1;
-        cnt = min(GM, (int)(t1 >> 32));
-    } else {
-        W = a.dense_w;
-        m0 = GM * tile;
-        cnt = min(GM, a.dense_n - m0);
-    }
-    if (cnt <= 0) return;
-    const int n0 = rb_idx * GN;
-    const int nrows = min(GN, a.rows - n0);
-    const int cols = a.cols, nsb = cols / 256;
-    const int ntt = (cnt + 15) >> 4;  // 16-position MFMA tiles with work
+    const int per = (total + NXCD - 1) / NXCD, xcd = blockIdx.x % NXCD, jb = blockIdx.x / NXCD;
+    const int ibeg = xcd * per + jb, iend = min((xcd + 1) * per, total);
+    if (ibeg >= iend) return;
+    const int nitems = (iend - ibeg + a.gx - 1) / a.gx;
 
-    if constexpr (IQ) load_iq_tables(tab);
-    if (tid < GM) xr[tid] = tid < cnt ? (a.xrow ? a.xrow[m0 + tid] : m0 + tid) : -1;
-    __syncthreads();
-
-    // Prefetch registers: X chunk c (position c / 16, 16 bytes at 16 (c % 16)), weight chunk c (row c / (RAWP / 16)).
-    v4u xv[XCH], wv[WCH];
-    float dxv = 0.0f;
-    auto issue = [&](int s) {
-#pragma unroll
-        for (int i = 0; i < XCH; i++) {
-            const int c = tid + 256 * i, m = c >> 4, x = xr[m];
-            xv[i] = (v4u){0, 0, 0, 0};
-            if (x >= 0) xv[i] = *gptr<v4u>((uint64_t)(a.xq + (uint64_t)x * cols + 256 * s + 16 * (c & 15)));
+    struct Item {
+        uint64_t w;
+        int m0, cnt, n0;
+    };
+    auto item_at = [&](int k) __attribute__((always_inline)) {
+        Item it{0, 0, 0, 0};
+        if (k >= nitems) return it;
+        const int id = ibeg + k * a.gx, tile = id / nrb;
+        it.n0 = (id - tile * nrb) * GN;
+        if (a.tiles) {
+            const uint64_t t0 = a.tiles[2 * tile], t1 = a.tiles[2 * tile + 1];
+            it.w = t0;
+            it.m0 = (int)(uint32_t)t1;
+            it.cnt = min(GM, (int)(t1 >> 32));
+        } else {
+            it.w = (uint64_t)a.dense_w;
+            it.m0 = GM * tile;
+            it.cnt = min(GM, a.dense_n - it.m0);
         }
-#pragma unroll
-        for (int i = 0; i < WCH; i++) {
-            const int c = tid + 256 * i, r = c / (RAWP / 16), j = c % (RAWP / 16);
-            if (r < nrows) {
-                const uint64_t beg = (uint64_t)(W + (uint64_t)(n0 + r) * a.rb + (uint64_t)s * SBB), g0 = beg & ~(uint64_t)15;
-                if (g0 + 16 * j < beg + SBB) wv[i] = *gptr<v4u>(g0 + 16 * j);
-            }
-        }
-        if (tid < GM) {
-            const int x = xr[tid];
-            dxv = x >= 0 ? *gptr<float>((uint64_t)(a.xd + (uint64_t)x * (cols / 32) + 8 * s)) : 0.0f;
-        }
+        return it;
     };
 
-    float acc[8][4];
+    if constexpr (IQ) load_iq_tables(tab);
+
+    // Per-lane load addresses of an item. Instruction j of wave w fills 1 KB of LDS: X positions 4 (XI w + j) + l / 16,
+    // LDS chunk l % 16, which holds X chunk (l % 16) ^ (p & 15); weight chunks c = 64 (w + NW i) + l (row c / NCH,
+    // chunk c % NCH, LDS offset 16 c). Positions past cnt and rows past `rows` read valid memory (position 0, the
+    // last row); their results are never stored. The scale of position tid (tid < GM) goes through a register.
+    constexpr int XI = GM * 16 / 64 / NW;                     // X instructions per wave per super-block
+    constexpr int WI = (GN * NCH + 64 * NW - 1) / (64 * NW);  // weight instructions per wave per super-block
+    struct Addr {
+        uint32_t xo[XI];  // X byte offset of each instruction's position row (+ chunk)
+        uint32_t dxo;     // scale offset of position tid
+        uint32_t rbeg;    // this lane's weight row: byte offset from W, plus W mod 16
+    };
+    const int rl = 16 * wave + (lane & 15);  // this lane's weight row in the block
+    auto addr_of = [&](const Item& it) __attribute__((always_inline)) {
+        Addr ad;
+        auto xrow_of = [&](int p) { p = p < it.cnt ? p : 0; return a.xrow ? a.xrow[it.m0 + p] : it.m0 + p; };
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+        for (int j = 0; j < XI; j++) {
+            const int p = 4 * (XI * wave + j) + (lane >> 4);
+            ad.xo[j] = (uint32_t)xrow_of(p) * (uint32_t)cols + 16 * ((lane & 15) ^ (p & 15));
+        }
+        ad.dxo = (uint32_t)xrow_of(tid & (GM - 1)) * (uint32_t)(cols / 32);
+        ad.rbeg = (uint32_t)(it.w & 15) + (uint32_t)min(it.n0 + rl, a.rows - 1) * (uint32_t)a.rb;
+        return ad;
+    };
+    int wr[WI], wjj[WI];  // row in the block and chunk index within the row's cover (-1 past the tile)
+#pragma unroll
+    for (int i = 0; i < WI; i++) {
+        const int c = 64 * (wave + NW * i) + lane;
+        wr[i] = min(c / NCH, GN - 1);
+        wjj[i] = c < GN * NCH ? c % NCH : -1;
+    }
+    // Loads of global super-block step g (buffers rotate by step: X and dx by 2, raw weights by 3).
+    auto load_x = [&](const Addr& ad, int s, int g) __attribute__((always_inline)) {
+        int8_t* xb = xs + (g & 1) * XBUF;
+#pragma unroll
+        for (int j = 0; j < XI; j++) load_lds16((uint64_t)(a.xq + ad.xo[j] + 256 * s), xb + 1024 * (XI * wave + j));
+    };
+    auto load_w = [&](const Item& it, int s, int g) __attribute__((always_inline)) {
+        uint8_t* wb = raw + (g % 3) * WBUF;
+#pragma unroll
+        for (int i = 0; i < WI; i++) {
+            const uint64_t beg = it.w + (uint64_t)min(it.n0 + wr[i], a.rows - 1) * a.rb + (uint64_t)s * SBB;
+            const uint64_t gp = (beg & ~(uint64_t)15) + 16 * (uint64_t)wjj[i];
+            if (wjj[i] >= 0 && gp < beg + SBB) load_lds16(gp, wb + 1024 * (wave + NW * i));
+        }
+    };
+    float dxv = 0.0f;
+    auto load_dx = [&](const Addr& ad, int s) __attribute__((always_inline)) {
+        if (tid < GM) dxv = *gptr<float>((uint64_t)(a.xd + ad.dxo + 8 * s));
+    };
+    auto store_dx = [&](int g) __attribute__((always_inline)) {
+        if (tid < GM) dxs[(g & 1) * GM + tid] = dxv;
+    };
+
+    float acc[NTT][4];
+#pragma unroll
+    for (int i = 0; i < NTT; i++)
 #pragma unroll
         for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
-    const int r = 16 * wave + (lane & 15);  // this lane's weight row in the block
-    const uint64_t rbeg0 = (uint64_t)(W + (uint64_t)(n0 + r) * a.rb);
+    const int kl = lane >> 4;                    // this lane's 16-value slot in each K step of 64
+    const int aswz = lane & 15;                  // position & 15 of this lane's X fragment rows
 
-    issue(0);
-    for (int s = 0; s < nsb; s++) {
-        __syncthreads();  // the previous super-block's readers are done
-#pragma unroll
-        for (int i = 0; i < XCH; i++) {
-            const int c = tid + 256 * i;
-            *(v4u*)(xs + (c >> 4) * XP + 16 * (c & 15)) = xv[i];
-        }
-#pragma unroll
-        for (int i = 0; i < WCH; i++) {
-            const int c = tid + 256 * i, rr = c / (RAWP / 16), j = c % (RAWP / 16);
-            if (rr < GN) *(v4u*)(raw + rr * RAWP + 16 * j) = wv[i];
-        }
-        if (tid < GM) dxs[tid] = dxv;
-        __syncthreads();
-        if (s + 1 < nsb) issue(s + 1);
-
-        const uint8_t* b = raw + r * RAWP + ((rbeg0 + (uint64_t)s * SBB) & 15);
-        v4i ia[NP][8];
-#pragma unroll
-        for (int pl = 0; pl < NP; pl++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) ia[pl][i] = (v4i){0, 0, 0, 0};
+    v4i B[4][NP];
+    float D = 0.0f, M = 0.0f;
+    // Decode super-block s of the item whose lane row offset is rbeg, from the raw buffer of step g.
+    auto decode = [&](uint32_t rbeg, int s, int g) __attribute__((always_inline)) {
+        const uint8_t* b = raw + (g % 3) * WBUF + rl * RAWP + ((rbeg + (uint32_t)s * SBB) & 15);
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             uint32_t hi[4], lo[4];
             int m;
-#ifdef STRATA_GEMM_NODECODE
-            hi[0] = hi[1] = hi[2] = hi[3] = lo[0] = lo[1] = lo[2] = lo[3] = (uint32_t)kk * 0x01010101u + b[0];
-            m = 1;
-#else
-            Dec<T>::run(b, 4 * kk + (lane >> 4), tab, hi, lo, m);
-#endif
-            const v4i bh = {(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-            const v4i bl = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
-            const int mw = (int)((uint32_t)m * 0x01010101u);
-            const v4i bm = {mw, mw, mw, mw};
-            const int ko = 64 * kk + 16 * (lane >> 4);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                if (i >= ntt) break;
-                const v4i av = *(const v4i*)(xs + (16 * i + (lane & 15)) * XP + ko);
-#ifdef STRATA_GEMM_NOMFMA
-                ia[P_LO][i] += av + bh + bl + bm;
-                continue;
-#endif
-                if constexpr (F::HI) ia[P_HI][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bh, ia[P_HI][i], 0, 0, 0);
-                ia[P_LO][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bl, ia[P_LO][i], 0, 0, 0);
-                if constexpr (F::MIN) ia[P_M][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bm, ia[P_M][i], 0, 0, 0);
+            Dec<T>::run(b, 4 * kk + kl, tab, hi, lo, m);
+            if constexpr (F::HI) B[kk][P_HI] = (v4i){(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+            B[kk][P_LO] = (v4i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+            if constexpr (F::MIN) {
+                const int mw = (int)((uint32_t)m * 0x01010101u);
+                B[kk][P_M] = (v4i){mw, mw, mw, mw};
             }
         }
-        // Close the super-block: lane's outputs are weight row r, positions 16 i + 4 (l / 16) + q.
-        float D, M;
         Dec<T>::scales(b, D, M);
-#ifdef STRATA_GEMM_NOCLOSE
-        acc[0][0] += (float)ia[P_LO][0][0] * D + (float)ia[0][ntt - 1][3];
-        continue;
-#endif
+    };
+    auto mfma_tile = [&](const int i, int g, v4i (&c)[NP]) __attribute__((always_inline)) {
+        const int8_t* xb = xs + (g & 1) * XBUF;
+        v4i av[4];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            if (i >= ntt) break;
-            const float4 d4 = *(const float4*)(dxs + 16 * i + 4 * (lane >> 4));
-            const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
+        for (int kk = 0; kk < 4; kk++) av[kk] = *(const v4i*)(xb + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int iv = F::HI ? 64 * ia[P_HI][i][q] + ia[P_LO][i][q] : ia[P_LO][i][q];
-                float f = D * (float)iv;
-                if constexpr (F::MIN) f -= M * (float)ia[P_M][i][q];
-                acc[i][q] += dq[q] * f;
-            }
-        }
-    }
-    // Epilogue.
-    if (r >= nrows) return;
+        for (int pl = 0; pl < NP; pl++) c[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], B[0][pl], (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        if (i >= ntt) break;
+        for (int kk = 1; kk < 4; kk++)
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++) c[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[kk], B[kk][pl], c[pl], 0, 0, 0);
+    };
+    // Lane's outputs of a tile: weight row rl, positions 16 i + 4 kl + q.
+    auto close_tile = [&](const int i, int g, const v4i (&c)[NP]) __attribute__((always_inline)) {
+        const float4 d4 = *(const float4*)(dxs + (g & 1) * GM + 16 * i + 4 * kl);
+        const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int m = 16 * i + 4 * (lane >> 4) + q;
-            if (m >= cnt) continue;
-            float* yp = a.y + (int64_t)(m0 + m) * a.y_stride + n0 + r;
-            const float v = acc[i][q];
-            *yp = a.act == STRATA_ACT_STORE ? v : a.act == STRATA_ACT_SWIGLU ? silu_dev(*yp) * v : *yp + v;
+            const int iv = F::HI ? (c[P_HI][q] << 8) + c[P_LO][q] : c[P_LO][q];
+            float f;
+            if constexpr (F::MIN) f = __builtin_fmaf(D, (float)iv, -(M * (float)c[P_M][q]));
+            else f = D * (float)iv;
+            acc[i][q] = __builtin_fmaf(dq[q], f, acc[i][q]);
         }
+    };
+    // Position tiles of step g with ntt tiles of work. When every tile has work they form one branch-free stream;
+    // otherwise tiles go in pairs (the close of the first runs while the MFMAs of the second work), and a pair
+    // runs whole when its first tile has work (the second's extra positions are never stored).
+    auto tiles = [&](int g, int ntt) __attribute__((always_inline)) {
+        if (ntt == NTT) {
+            v4i c[2][NP];
+            static_for<0, NTT>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                mfma_tile(i, g, c[i & 1]);
+                if constexpr (i > 0) close_tile(i - 1, g, c[(i - 1) & 1]);
+            });
+            close_tile(NTT - 1, g, c[(NTT - 1) & 1]);
+            return;
+        }
+        static_for<0, NTT / 2>([&](auto I) {
+            constexpr int i = 2 * decltype(I)::value;
+            if (i < ntt) {
+                v4i c0[NP], c1[NP];
+                mfma_tile(i, g, c0);
+                mfma_tile(i + 1, g, c1);
+                close_tile(i, g, c0);
+                close_tile(i + 1, g, c1);
+            }
+        });
+    };
+    // Results of an item: y[m0 + m, n0 + row] (op) acc; then the accumulators restart.
+    auto store = [&](const Item& it) __attribute__((always_inline)) {
+        const int row = it.n0 + rl, ntt = (it.cnt + 15) >> 4;
+        if (row < a.rows) {
+            static_for<0, NTT>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                if (i < ntt) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int m = 16 * i + 4 * kl + q;
+                        if (m < it.cnt) {
+                            float* yp = a.y + (int64_t)(it.m0 + m) * a.y_stride + row;
+                            const float v = acc[i][q];
+                            *yp = a.act == STRATA_ACT_STORE ? v : a.act == STRATA_ACT_SWIGLU ? silu_dev(*yp) * v : *yp + v;
+                        }
+                    }
+                }
+            });
+        }
+#pragma unroll
+        for (int i = 0; i < NTT; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
+    };
+
+    // The super-block steps of this block's items run as one stream g = k * nsb + s. Step g loads X of g + 1 and the
+    // raw weights of g + 2 (of the next item near an item's end; the launch gives each block one item when nsb is 1),
+    // so every load has a whole step to land and one barrier per step suffices.
+    const bool role0 = wave < NW / 2;
+    Item cur = item_at(0), nxt = item_at(1);
+    Addr acur = addr_of(cur), anxt = addr_of(nxt);
+    load_x(acur, 0, 0);
+    load_dx(acur, 0);
+    load_w(cur, 0, 0);
+    if (nsb > 1) load_w(cur, 1, 1);
+    store_dx(0);
+    wait_loads();
+    __syncthreads();
+    if (role0) decode(acur.rbeg, 0, 0);
+    int s = 0;
+    for (int g = 0, k = 0; k < nitems; g++) {
+        TRACE(0);
+        const bool last = s + 1 == nsb, more = k + 1 < nitems;
+        // loads of step g + 1 (X, dx) and g + 2 (raw weights)
+        if (!last) {
+            load_x(acur, s + 1, g + 1);
+            load_dx(acur, s + 1);
+        } else if (more) {
+            load_x(anxt, 0, g + 1);
+            load_dx(anxt, 0);
+        }
+        if (s + 2 < nsb) load_w(cur, s + 2, g + 2);
+        else if (more) load_w(nxt, s + 2 - nsb, g + 2);
+        const int ntt = (cur.cnt + 15) >> 4;
+        TRACE(1);
+        if (role0) {
+            tiles(g, ntt);
+            TRACE(2);
+            if (last) store(cur);
+            if (!last) decode(acur.rbeg, s + 1, g + 1);
+            else if (more) decode(anxt.rbeg, 0, g + 1);
+        } else {
+            decode(acur.rbeg, s, g);
+            TRACE(2);
+            tiles(g, ntt);
+            if (last) store(cur);
+        }
+        TRACE(3);
+        if (!last || more) store_dx(g + 1);
+        if (last) {
+            k++;
+            s = 0;
+            cur = nxt;
+            acur = anxt;
+            nxt = item_at(k + 1);
+            anxt = addr_of(nxt);
+        } else {
+            s++;
+        }
+        wait_loads();
+        TRACE(4);
+        __syncthreads();
+        TRACE(5);
     }
 }
 
 template <int T>
 static size_t gemm_smem() {
-    size_t b = GM * XP + GN * GemmFmt<T>::RAWP + GM * 4 + GM * 4;
+    size_t b = 2 * (size_t)XBUF + 3 * (size_t)GemmFmt<T>::WBUF + 2 * GM * 4;
     if (T == IQ2_XXS || T == IQ3_S) b += sizeof(IqTables);
     return b;
 }
@@ -243,11 +395,29 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
         attr = true;
     }
     a.max_tiles = g.n_tiles;
+    // Persistent blocks, one per CU, when an item has at least two super-blocks (the step stream prefetches two
+    // steps ahead); otherwise one block per item.
+    static int ncu = 0;
+    if (!ncu) {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+    }
     const long long total = (long long)((g.rows + GN - 1) / GN) * g.n_tiles;
-    const long long grid = (total + NXCD - 1) / NXCD * NXCD;
-    gemm_kernel<T><<<dim3((unsigned)grid), 256, smem, s>>>(a);
+    const long long per = (total + NXCD - 1) / NXCD;
+    const long long gx = g.cols / 256 >= 2 ? std::min<long long>(per, std::max(ncu / NXCD, 1)) : per;
+    a.gx = (int)std::max<long long>(gx, 1);
+    const long long grid = (long long)a.gx * NXCD;
+    gemm_kernel<T><<<dim3((unsigned)grid), 64 * NW, smem, s>>>(a);
     return hipGetLastError();
 }
+
+#ifdef STRATA_GEMM_TRACE
+extern "C" int strata_debug_gemm_trace(uint64_t* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_gemm_trace), sizeof(g_gemm_trace)) == hipSuccess ? 0 : -1;
+}
+#endif
 
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t s) {
     switch (g.ty) {
