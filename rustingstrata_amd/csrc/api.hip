@@ -498,6 +498,8 @@ static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint
     if (dense_w && check_align(ty, (uint64_t)dense_w, "gemm_dense")) return -1;
     if (n_tiles == 0 || rows == 0) return 0;
     if (rows > (1u << 24) || n_tiles > 65535 * 64) return set_error("gemm: too large");
+    // the kernel addresses X and a weight matrix with 32-bit byte offsets
+    if (n_x * cols >= (1ull << 32) || rows * row_bytes(ty, cols) >= (1ull << 32)) return set_error("gemm: X or W of 4 GiB or more");
     uint64_t xq = 0;
     if (gemm_x(c, cols, n_x, x, x_stride, act & STRATA_SAME_X, &xq)) return -1;
     GemmLaunch g;

@@ -79,6 +79,14 @@ __device__ __forceinline__ void load_lds16(uint64_t g, const void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(m0) : "memory", "m0");
 }
+// The same from a wave-uniform 64-bit base plus a per-lane 32-bit byte offset (the base stays in scalar registers).
+__device__ __forceinline__ void load_lds16_so(uint64_t base, uint32_t off, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    // readfirstlane returns int: widen through uint32_t, or bit 31 of the low half would spread into the high half
+    const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32)) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(sb), "s"(m0) : "memory", "m0");
+}
 // This wave's loads into LDS are complete (vmcnt 0; the barrier that follows publishes them to the block).
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -163,11 +171,19 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     constexpr int XI = GM * 16 / 64 / NW;                     // X instructions per wave per super-block
     constexpr int WI = (GN * NCH + 64 * NW - 1) / (64 * NW);  // weight instructions per wave per super-block
     struct Addr {
-        uint32_t xo[XI];  // X byte offset of each instruction's position row (+ chunk)
-        uint32_t dxo;     // scale offset of position tid
-        uint32_t rbeg;    // this lane's weight row: byte offset from W, plus W mod 16
+        uint32_t xo[XI];   // X byte offset of each instruction's position row (+ chunk)
+        uint32_t dxo;      // scale offset of position tid
+        uint32_t rbeg;     // this lane's weight row: byte offset from W, plus W mod 16
+        uint32_t wro[WI];  // byte offset from W of each weight instruction's row
     };
     const int rl = 16 * wave + (lane & 15);  // this lane's weight row in the block
+    int wr[WI], wjj[WI];  // row in the block and chunk index within the row's cover (-1 past the tile)
+#pragma unroll
+    for (int i = 0; i < WI; i++) {
+        const int c = 64 * (wave + NW * i) + lane;
+        wr[i] = min(c / NCH, GN - 1);
+        wjj[i] = c < GN * NCH ? c % NCH : -1;
+    }
     auto addr_of = [&](const Item& it) __attribute__((always_inline)) {
         Addr ad;
         auto xrow_of = [&](int p) { p = p < it.cnt ? p : 0; return a.xrow ? a.xrow[it.m0 + p] : it.m0 + p; };
@@ -178,28 +194,27 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         }
         ad.dxo = (uint32_t)xrow_of(tid & (GM - 1)) * (uint32_t)(cols / 32);
         ad.rbeg = (uint32_t)(it.w & 15) + (uint32_t)min(it.n0 + rl, a.rows - 1) * (uint32_t)a.rb;
+#pragma unroll
+        for (int i = 0; i < WI; i++) ad.wro[i] = (uint32_t)min(it.n0 + wr[i], a.rows - 1) * (uint32_t)a.rb;
         return ad;
     };
-    int wr[WI], wjj[WI];  // row in the block and chunk index within the row's cover (-1 past the tile)
-#pragma unroll
-    for (int i = 0; i < WI; i++) {
-        const int c = 64 * (wave + NW * i) + lane;
-        wr[i] = min(c / NCH, GN - 1);
-        wjj[i] = c < GN * NCH ? c % NCH : -1;
-    }
     // Loads of global super-block step g (buffers rotate by step: X and dx by 2, raw weights by 3).
     auto load_x = [&](const Addr& ad, int s, int g) __attribute__((always_inline)) {
         int8_t* xb = xs + (g & 1) * XBUF;
+        const uint64_t base = (uint64_t)(a.xq + 256 * s);
 #pragma unroll
-        for (int j = 0; j < XI; j++) load_lds16((uint64_t)(a.xq + ad.xo[j] + 256 * s), xb + 1024 * (XI * wave + j));
+        for (int j = 0; j < XI; j++) load_lds16_so(base, ad.xo[j], xb + 1024 * (XI * wave + j));
     };
-    auto load_w = [&](const Item& it, int s, int g) __attribute__((always_inline)) {
+    // Raw weights of super-block s: the 16-byte covers of each row's super-block, from the scalar base
+    // (w + s * SBB) & ~15 and per-lane offsets ((w + s * SBB) & 15) + row offset, rounded down to 16, + 16 chunk.
+    auto load_w = [&](const Item& it, const Addr& ad, int s, int g) __attribute__((always_inline)) {
         uint8_t* wb = raw + (g % 3) * WBUF;
+        const uint64_t beg = it.w + (uint64_t)s * SBB, base = beg & ~(uint64_t)15;
+        const uint32_t lo = (uint32_t)(beg & 15);
 #pragma unroll
         for (int i = 0; i < WI; i++) {
-            const uint64_t beg = it.w + (uint64_t)min(it.n0 + wr[i], a.rows - 1) * a.rb + (uint64_t)s * SBB;
-            const uint64_t gp = (beg & ~(uint64_t)15) + 16 * (uint64_t)wjj[i];
-            if (wjj[i] >= 0 && gp < beg + SBB) load_lds16(gp, wb + 1024 * (wave + NW * i));
+            const uint32_t t = lo + ad.wro[i], o = (t & ~15u) + 16 * (uint32_t)wjj[i];
+            if (wjj[i] >= 0 && o < t + SBB) load_lds16_so(base, o, wb + 1024 * (wave + NW * i));
         }
     };
     float dxv = 0.0f;
@@ -291,14 +306,16 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     auto store = [&](const Item& it) __attribute__((always_inline)) {
         const int row = it.n0 + rl, ntt = (it.cnt + 15) >> 4;
         if (row < a.rows) {
+            // row pointer of position 4 kl; position 16 i + 4 kl + q is (16 i + q) rows further
+            float* yb = a.y + (int64_t)(it.m0 + 4 * kl) * a.y_stride + row;
+            const int left = it.cnt - 4 * kl;  // positions of this lane's column left from yb
             static_for<0, NTT>([&](auto I) {
                 constexpr int i = decltype(I)::value;
                 if (i < ntt) {
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const int m = 16 * i + 4 * kl + q;
-                        if (m < it.cnt) {
-                            float* yp = a.y + (int64_t)(it.m0 + m) * a.y_stride + row;
+                        if (16 * i + q < left) {
+                            float* yp = yb + (int64_t)(16 * i + q) * a.y_stride;
                             const float v = acc[i][q];
                             *yp = a.act == STRATA_ACT_STORE ? v : a.act == STRATA_ACT_SWIGLU ? silu_dev(*yp) * v : *yp + v;
                         }
@@ -320,8 +337,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     Addr acur = addr_of(cur), anxt = addr_of(nxt);
     load_x(acur, 0, 0);
     load_dx(acur, 0);
-    load_w(cur, 0, 0);
-    if (nsb > 1) load_w(cur, 1, 1);
+    load_w(cur, acur, 0, 0);
+    if (nsb > 1) load_w(cur, acur, 1, 1);
     store_dx(0);
     wait_loads();
     __syncthreads();
@@ -338,8 +355,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             load_x(anxt, 0, g + 1);
             load_dx(anxt, 0);
         }
-        if (s + 2 < nsb) load_w(cur, s + 2, g + 2);
-        else if (more) load_w(nxt, s + 2 - nsb, g + 2);
+        if (s + 2 < nsb) load_w(cur, acur, s + 2, g + 2);
+        else if (more) load_w(nxt, anxt, s + 2 - nsb, g + 2);
         const int ntt = (cur.cnt + 15) >> 4;
         TRACE(1);
         if (role0) {
