@@ -70,26 +70,6 @@ struct GemmArgs {
 
 __device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + (float)exp(-(double)v)); }
 
-// 16 bytes per lane from global address g into LDS at lds + 16 * lane (global_load_lds_dwordx4, LDS base in M0).
-// Issued as inline assembly so that the compiler's wait insertion does not tie it to later LDS reads: it would
-// otherwise wait for every outstanding load before the first LDS read, and a load issued for a later super-block
-// could not overlap this one. The kernel waits for these loads itself (wait_loads) before the barrier that
-// publishes them. `lds` must be the same for every lane of the wave.
-__device__ __forceinline__ void load_lds16(uint64_t g, const void* lds) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(m0) : "memory", "m0");
-}
-// The same from a wave-uniform 64-bit base plus a per-lane 32-bit byte offset (the base stays in scalar registers).
-__device__ __forceinline__ void load_lds16_so(uint64_t base, uint32_t off, const void* lds) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    // readfirstlane returns int: widen through uint32_t, or bit 31 of the low half would spread into the high half
-    const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32)) << 32) |
-                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(sb), "s"(m0) : "memory", "m0");
-}
-// This wave's loads into LDS are complete (vmcnt 0; the barrier that follows publishes them to the block).
-__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 #ifdef STRATA_GEMM_TRACE
 // Debug builds: shader clock at the phases of the first steps of a few waves (read with strata_debug_gemm_trace).
 __device__ uint64_t g_gemm_trace[8][64][6];

@@ -7,6 +7,8 @@
 // IQ types, the codebook tables. A row is then shared by G lanes (G = the power of two at or above its number of
 // 256-value super-blocks, at most 64): lane l takes super-blocks l, l + G, ... whole, accumulating each exactly in
 // int32 and closing it with one float step (sbdot.h); the G partial sums meet by cross-lane reduction.
+#include <algorithm>
+
 #include "sbdot.h"
 #include "kernels.h"
 #include "../../include/strata_hip.h"
@@ -473,6 +475,9 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     a.R = (int)(want < 1 ? 1 : want > rmax ? rmax : want);
     if (a.R < 1) a.R = 1;
     const int rpb = 4 * (64 / a.G);  // rows one pass of the block covers
+    // A single-input tile covers at least one pass of the block: fewer, fuller blocks beat idle lanes on small
+    // matrices (each block also quantizes x itself).
+    if (single && a.R < rpb) a.R = std::min(rpb, rmax);
     if (single && a.R > rpb) a.R -= a.R % rpb;
     a.ntr = (maxrows + a.R - 1) / a.R;
     a.nslots = nslots;
