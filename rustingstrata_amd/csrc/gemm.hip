@@ -232,17 +232,24 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         }
         Dec<T>::scales(b, D, M);
     };
-    auto mfma_tile = [&](const int i, int g, v4i (&c)[NP]) __attribute__((always_inline)) {
+    // X fragments of tile i (16 positions x 4 K steps of 64) and the MFMAs of a tile on given fragments.
+    auto read_a = [&](const int i, int g, v4i (&av)[4]) __attribute__((always_inline)) {
         const int8_t* xb = xs + (g & 1) * XBUF;
-        v4i av[4];
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) av[kk] = *(const v4i*)(xb + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
+    };
+    auto mfma_av = [&](const v4i (&av)[4], v4i (&c)[NP]) __attribute__((always_inline)) {
 #pragma unroll
         for (int pl = 0; pl < NP; pl++) c[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], B[0][pl], (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
         for (int kk = 1; kk < 4; kk++)
 #pragma unroll
             for (int pl = 0; pl < NP; pl++) c[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[kk], B[kk][pl], c[pl], 0, 0, 0);
+    };
+    auto mfma_tile = [&](const int i, int g, v4i (&c)[NP]) __attribute__((always_inline)) {
+        v4i av[4];
+        read_a(i, g, av);
+        mfma_av(av, c);
     };
     // Lane's outputs of a tile: weight row rl, positions 16 i + 4 kl + q.
     auto close_tile = [&](const int i, int g, const v4i (&c)[NP]) __attribute__((always_inline)) {
@@ -262,10 +269,14 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     // runs whole when its first tile has work (the second's extra positions are never stored).
     auto tiles = [&](int g, int ntt) __attribute__((always_inline)) {
         if (ntt == NTT) {
-            v4i c[2][NP];
+            // The fragments of tile i + 1 are read while the MFMAs of tile i run (LDS latency off the MFMA path),
+            // and the close of tile i - 1 runs with them.
+            v4i c[2][NP], av[2][4];
+            read_a(0, g, av[0]);
             static_for<0, NTT>([&](auto I) {
                 constexpr int i = decltype(I)::value;
-                mfma_tile(i, g, c[i & 1]);
+                if constexpr (i + 1 < NTT) read_a(i + 1, g, av[(i + 1) & 1]);
+                mfma_av(av[i & 1], c[i & 1]);
                 if constexpr (i > 0) close_tile(i - 1, g, c[(i - 1) & 1]);
             });
             close_tile(NTT - 1, g, c[(NTT - 1) & 1]);
@@ -289,19 +300,28 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             // row pointer of position 4 kl; position 16 i + 4 kl + q is (16 i + q) rows further
             float* yb = a.y + (int64_t)(it.m0 + 4 * kl) * a.y_stride + row;
             const int left = it.cnt - 4 * kl;  // positions of this lane's column left from yb
-            static_for<0, NTT>([&](auto I) {
-                constexpr int i = decltype(I)::value;
-                if (i < ntt) {
+            // the op is chosen once per item: one straight store loop per op
+            auto put = [&](auto OP) __attribute__((always_inline)) {
+                constexpr int op = decltype(OP)::value;
+                static_for<0, NTT>([&](auto I) {
+                    constexpr int i = decltype(I)::value;
+                    if (i < ntt) {
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        if (16 * i + q < left) {
-                            float* yp = yb + (int64_t)(16 * i + q) * a.y_stride;
-                            const float v = acc[i][q];
-                            *yp = a.act == STRATA_ACT_STORE ? v : a.act == STRATA_ACT_SWIGLU ? silu_dev(*yp) * v : *yp + v;
+                        for (int q = 0; q < 4; q++) {
+                            if (16 * i + q < left) {
+                                float* yp = yb + (int64_t)(16 * i + q) * a.y_stride;
+                                const float v = acc[i][q];
+                                if constexpr (op == STRATA_ACT_STORE) *yp = v;
+                                else if constexpr (op == STRATA_ACT_SWIGLU) *yp = silu_dev(*yp) * v;
+                                else *yp += v;
+                            }
                         }
                     }
-                }
-            });
+                });
+            };
+            if (a.act == STRATA_ACT_STORE) put(std::integral_constant<int, STRATA_ACT_STORE>{});
+            else if (a.act == STRATA_ACT_SWIGLU) put(std::integral_constant<int, STRATA_ACT_SWIGLU>{});
+            else put(std::integral_constant<int, STRATA_ACT_ADD>{});
         }
 #pragma unroll
         for (int i = 0; i < NTT; i++)
@@ -312,7 +332,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     // The super-block steps of this block's items run as one stream g = k * nsb + s. Step g loads X of g + 1 and the
     // raw weights of g + 2 (of the next item near an item's end; the launch gives each block one item when nsb is 1),
     // so every load has a whole step to land and one barrier per step suffices.
+#ifdef STRATA_GEMM_ANALYZE_ROLE0
+    const bool role0 = true;  // instruction-count analysis only: one role's path
+#else
     const bool role0 = wave < NW / 2;
+#endif
     Item cur = item_at(0), nxt = item_at(1);
     Addr acur = addr_of(cur), anxt = addr_of(nxt);
     load_x(acur, 0, 0);
@@ -337,7 +361,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         }
         if (s + 2 < nsb) load_w(cur, acur, s + 2, g + 2);
         else if (more) load_w(nxt, anxt, s + 2 - nsb, g + 2);
+#ifdef STRATA_GEMM_ANALYZE_ROLE0
+        const int ntt = NTT;
+#else
         const int ntt = (cur.cnt + 15) >> 4;
+#endif
         TRACE(1);
         if (role0) {
             tiles(g, ntt);
