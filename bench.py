@@ -160,7 +160,8 @@ def bench_moe(hip, S, ggml, T, iters):
     hs = rng.standard_normal((T, H)).astype(np.float32)
     lb, hb = hip.upload(logits), hip.upload(hs)
     ids, wts = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
-    max_tiles = T * k // 128 + E
+    chunk = hip.gemm_block_positions()  # tile lists sized to the GEMM's blocks
+    max_tiles = T * k // chunk + E
     off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
     tiles, ntd = hip.alloc(3 * max_tiles * 16), hip.alloc(4)
     ge, ye, x = hip.alloc(T * k * F * 4), hip.alloc(T * k * H * 4), hip.alloc(T * H * 4)
@@ -169,7 +170,7 @@ def bench_moe(hip, S, ggml, T, iters):
 
     def layer(timed=False):
         hip.router_topk(lb, E, k, 0.0, ids, wts, T)
-        hip.moe_sort(ids, T, k, E, off, xrow, inv, mats, tiles, max_tiles, ntd)
+        hip.moe_sort(ids, T, k, E, off, xrow, inv, mats, tiles, max_tiles, ntd, chunk=chunk)
         if timed:
             hip.record(ev[1])
         hip.gemm_grouped(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, S.ACT_STORE)

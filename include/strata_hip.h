@@ -150,15 +150,17 @@ int strata_moe_combine_seq(strata_ctx* ctx, uint64_t x, uint64_t ye, uint64_t wt
 /* The host half of GpuModel's prefill MoE block moved onto the device (src/gpu_model/prefill.rs:554-575 and the
  * tile builder 618-642): sorts the (token, j) pairs by expert stably, writes off[n_expert + 1] (exclusive prefix counts),
  * xrow[t * k] (token of each sorted slot), inv[t * k] (slot of pair t * k + j), and for each of the n_mats
- * matrices m a tile list of 16-byte tiles [w_m(e), m0 | cnt << 32] (chunks of at most 128 slots per expert,
- * experts ascending, w_m(e) = bases[m] + e * strides[m]) at tiles + m * max_tiles * 16. The tile count is written
- * to *n_tiles_dev (device int32). max_tiles must be at least t * k / 128 + n_expert. No host synchronisation:
+ * matrices m a tile list of 16-byte tiles [w_m(e), m0 | cnt << 32] (chunks of at most `chunk` slots per expert,
+ * experts ascending, w_m(e) = bases[m] + e * strides[m]) at tiles + m * max_tiles * 16. chunk: 128 (0) is the
+ * reference's GEMM_BM (src/backend.rs:16); strata_gemm_block_positions() (256) fills this backend's GEMM blocks.
+ * The tile count is written to *n_tiles_dev (device int32). max_tiles must be at least t * k / chunk + n_expert.
+ * No host synchronisation:
  * pass the same max_tiles and n_tiles_dev to strata_gemm_grouped. An id outside 0..n_expert is replaced by no
  * tile, counted in err_dev (device int32, may be 0), and the caller checks it after a sync (the reference fails the
  * prefill there, src/gpu_model/prefill.rs:557-560). */
 int strata_moe_sort(strata_ctx* ctx, uint64_t ids, uint64_t t, uint64_t k, uint64_t n_expert, uint64_t off,
                     uint64_t xrow, uint64_t inv, uint64_t n_mats, const uint64_t* bases, const uint64_t* strides,
-                    uint64_t tiles, uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t err_dev);
+                    uint64_t tiles, uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t err_dev, uint64_t chunk);
 /* Backend::gemm (src/backend.rs:187-191): for each tile [w, m0 | cnt << 32] of the device tile list, positions
  * m0 .. m0 + cnt get y[m, 0..rows] (op) W x[xrow[m]] (x row m when xrow is 0), W the rows x cols matrix of type ty
  * at w. act: STRATA_ACT_STORE, STRATA_ACT_SWIGLU (y = silu(y) * result), STRATA_ACT_ADD, | STRATA_SAME_X (x is
@@ -176,6 +178,9 @@ int strata_gemm_grouped(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, u
  * src/cuda/mod.rs:908-910). */
 int strata_gemm_dense(strata_ctx* ctx, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride, uint64_t y,
                       uint64_t y_stride, int act);
+/* Positions per block of this backend's GEMM (no counterpart in the reference): tile lists with chunks of this
+ * size (strata_moe_sort's chunk) give every block a full tile. */
+uint64_t strata_gemm_block_positions(void);
 /* Backend::int8_gemm (src/backend.rs:192-194): 1 if gemm of type ty runs on int8 matrix cores (every supported
  * type does here), 0 for an unsupported type. */
 int strata_int8_gemm(strata_ctx* ctx, int ty);

@@ -69,10 +69,11 @@ SIGNATURES = {
     "strata_moe_down_combine": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64],
     "strata_moe_combine_seq": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64],
     "strata_moe_sort": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.POINTER(U64), ctypes.POINTER(U64),
-                        U64, U64, U64, U64],
+                        U64, U64, U64, U64, U64],
     "strata_gemm": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32],
     "strata_gemm_grouped": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32],
     "strata_gemm_dense": [CTX, TP, U64, U64, U64, U64, U64, I32],
+    "strata_gemm_block_positions": [],
     "strata_int8_gemm": [CTX, I32],
     "strata_prequant_gemm_x": [CTX, TP, U64, U64, U64],
     "strata_quantize_rows": [I32, P, U64, U64, P],
@@ -83,7 +84,8 @@ SIGNATURES = {
     "strata_event_destroy": [P],
     "strata_copy_kernel": [CTX, U64, U64, U64],
 }
-_RESTYPES = {"strata_close": None, "strata_last_error": ctypes.c_char_p, "strata_stream": P, "strata_row_bytes": U64}
+_RESTYPES = {"strata_close": None, "strata_last_error": ctypes.c_char_p, "strata_stream": P, "strata_row_bytes": U64,
+             "strata_gemm_block_positions": U64}
 
 _lib = None
 
@@ -303,13 +305,17 @@ class HipBackend:
     def moe_combine_seq(self, x, ye, wts, inv, k, sh, sg, n, t):
         _check(lib().strata_moe_combine_seq(self._ctx, int(x), int(ye), int(wts), int(inv), k, int(sh), int(sg), n, t))
 
-    def moe_sort(self, ids, t, k, n_expert, off, xrow, inv, mats, tiles, max_tiles, n_tiles_dev, err_dev=0):
-        """Device counting sort of the (token, j) pairs by expert + tile lists; mats = [(base, stride), ...]."""
+    def moe_sort(self, ids, t, k, n_expert, off, xrow, inv, mats, tiles, max_tiles, n_tiles_dev, err_dev=0, chunk=0):
+        """Device counting sort of the (token, j) pairs by expert + tile lists; mats = [(base, stride), ...];
+        chunk = positions per tile (0: the reference's 128)."""
         n = len(mats)
         bases = (U64 * max(n, 1))(*[m[0] for m in mats])
         strides = (U64 * max(n, 1))(*[m[1] for m in mats])
         _check(lib().strata_moe_sort(self._ctx, int(ids), t, k, n_expert, int(off), int(xrow), int(inv), n, bases,
-                                     strides, int(tiles), max_tiles, int(n_tiles_dev), int(err_dev)))
+                                     strides, int(tiles), max_tiles, int(n_tiles_dev), int(err_dev), chunk))
+
+    def gemm_block_positions(self):
+        return int(lib().strata_gemm_block_positions())
 
     def gemm(self, ty, rows, cols, tiles, n_tiles, x, x_stride, n_x, xrow, y, y_stride, act):
         _check(lib().strata_gemm(self._ctx, ty, rows, cols, int(tiles), n_tiles, int(x), x_stride, n_x, int(xrow),

@@ -455,18 +455,22 @@ int strata_moe_combine_seq(strata_ctx* c, uint64_t x, uint64_t ye, uint64_t wts,
 
 int strata_moe_sort(strata_ctx* c, uint64_t ids, uint64_t t, uint64_t k, uint64_t n_expert, uint64_t off,
                     uint64_t xrow, uint64_t inv, uint64_t n_mats, const uint64_t* bases, const uint64_t* strides,
-                    uint64_t tiles, uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t err_dev) {
+                    uint64_t tiles, uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t err_dev, uint64_t chunk) {
     if (check_ctx(c)) return -1;
+    if (chunk == 0) chunk = 128;
+    if (chunk > 256 || chunk % 16) return set_error("moe_sort: chunk " + std::to_string(chunk) + " (a multiple of 16, at most 256)");
     if (n_expert == 0 || n_expert > 512) return set_error("moe_sort: " + std::to_string(n_expert) + " experts (1 to 512)");
     if (n_mats > 3 || (n_mats && (!bases || !strides))) return set_error("moe_sort: at most 3 matrices, with bases and strides");
     if (t * k > (1u << 30)) return set_error("moe_sort: too many pairs");
-    if (max_tiles < (t * k) / 128 + n_expert) return set_error("moe_sort: max_tiles " + std::to_string(max_tiles) + " < pairs / 128 + experts");
+    if (max_tiles < (t * k) / chunk + n_expert)
+        return set_error("moe_sort: max_tiles " + std::to_string(max_tiles) + " < pairs / chunk + experts");
     SortLaunch s;
     s.ids = (const int*)ids; s.t = (int)t; s.k = (int)k; s.n_expert = (int)n_expert;
     s.off = (int*)off; s.xrow = (int*)xrow; s.inv = (int*)inv;
     s.n_mats = (int)n_mats;
     for (uint64_t m = 0; m < n_mats; m++) { s.bases[m] = bases[m]; s.strides[m] = strides[m]; }
     s.tiles = (uint64_t*)tiles; s.max_tiles = (int)max_tiles; s.n_tiles = (int*)n_tiles_dev; s.err = (int*)err_dev;
+    s.chunk = (int)chunk;
     STRATA_HIP(c->misc.need(sort_scratch_bytes((int)n_expert), c->stream));
     s.scratch = (int*)c->misc.p;
     STRATA_HIP(launch_sort(s, c->stream));
@@ -529,10 +533,13 @@ int strata_gemm_grouped(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uin
 int strata_gemm_dense(strata_ctx* c, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride, uint64_t y,
                       uint64_t y_stride, int act) {
     if (check_tensor(w, "gemm_dense")) return -1;
-    uint64_t nt = (n + 127) / 128;
+    const uint64_t bp = gemm_block_positions();
+    uint64_t nt = (n + bp - 1) / bp;
     return gemm_common(c, w->ty, w->rows, w->cols, 0, nt, nullptr, x, x_stride, n, 0, y, y_stride, act,
                        (const uint8_t*)w->ptr, n);
 }
+
+uint64_t strata_gemm_block_positions(void) { return gemm_block_positions(); }
 
 int strata_int8_gemm(strata_ctx* c, int ty) {
     (void)c;

@@ -13,7 +13,7 @@ struct GemmLaunch {
     int ty = 0;
     int rows = 0, cols = 0;
     const uint64_t* tiles = nullptr;  // [w, m0 | cnt << 32] per tile, or null for one dense matrix
-    int n_tiles = 0;                  // tiles (or dense tiles of 128 positions); an upper bound with n_tiles_dev
+    int n_tiles = 0;                  // tiles (or dense tiles of gemm_block_positions()); an upper bound with n_tiles_dev
     const int* n_tiles_dev = nullptr;
     const uint8_t* dense_w = nullptr;
     int dense_n = 0;
@@ -25,5 +25,7 @@ struct GemmLaunch {
     int act = 0;
 };
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t s);
+// Positions of one GEMM block (a tile list's chunks of this size give every block a full tile).
+uint64_t gemm_block_positions();
 
 }  // namespace strata

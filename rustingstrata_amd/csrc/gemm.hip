@@ -10,18 +10,18 @@
 //     acc += dx * (D * (256 H.x + L.x) - M * M.x).
 // No per-group scaling happens in the K loop.
 //
-// Block: 512 threads (8 waves, two per SIMD), a tile of up to GM = 128 positions x GN = 128 weight rows. Wave w owns
-// weight rows 16 w .. 16 w + 15 (one 16-row MFMA column) and every position (8 MFMA tiles of 16 positions), so each
-// weight is decoded once per block, by the lane that feeds it to the MFMA. Per super-block s the two waves that
-// share a SIMD (w and w + 4) take opposite orders:
-//   role 0 (waves 0-3): MFMAs and close of s (B of s decoded earlier), then decode of s + 1;
-//   role 1 (waves 4-7): decode of s, then MFMAs and close of s;
-// so one wave's VALU work (decode: weights to digit-plane B operands; close: int32 sums to float) runs while the
-// other's MFMAs occupy the matrix core. Within the tile loop the close of one tile runs while the matrix core works
-// on the next (tiles in pairs, two sets of int32 sums).
+// Block: 512 threads (8 waves, two per SIMD), a tile of up to GM = 256 positions x GN = 128 weight rows. Wave w owns
+// weight rows 16 w .. 16 w + 15 (one 16-row MFMA column) and every position (16 MFMA tiles of 16 positions), so each
+// weight is decoded once per block, by the lane that feeds it to the MFMA, and serves 256 positions. Per super-block
+// step every wave
+//   1. decodes its rows' super-block into digit-plane B operands (registers), issuing the next step's X loads
+//      between the decode units;
+//   2. after a barrier (the raw weights' one LDS buffer is free) issues the next step's raw-weight loads;
+//   3. runs its 16 position tiles: the MFMAs of tile i with the float close of tile i - 1.
+// The two waves of a SIMD overlap one's VALU work (decode, close) with the other's MFMAs.
 // Loads go straight from global memory into LDS (global_load_lds_dwordx4: lane l of a wave's instruction writes the
-// 16 bytes at its own address to LDS base + 16 l), one super-block ahead for X (double buffer) and two for the raw
-// weights (triple buffer), so one barrier per super-block suffices and every load has a whole super-block to land.
+// 16 bytes at its own address to LDS base + 16 l); X is double-buffered, so a step's X loads have the whole step to
+// land.
 // X sits in LDS as [position][256 bytes] with 16-byte chunk c of position p at chunk c ^ (p & 15): a 16-lane MFMA
 // fragment read (16 positions, one chunk) then touches 16 distinct bank groups.
 #include <algorithm>
@@ -37,7 +37,7 @@ namespace strata {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int NXCD = 8;              // MI355X: 8 XCDs, each with its own L2
-constexpr int GM = 128, GN = 128;    // positions, weight rows per block
+constexpr int GM = 256, GN = 128;    // positions, weight rows per block
 constexpr int NW = 8;                // waves per block
 constexpr int NTT = GM / 16;         // MFMA position tiles per block
 constexpr int XBUF = GM * 256;       // bytes of one X buffer
@@ -100,10 +100,10 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     constexpr int P_HI = 0, P_LO = F::HI ? 1 : 0, P_M = F::HI ? 2 : 1;
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     extern __shared__ __align__(16) uint8_t smem[];
-    // LDS: [X: 2 x GM x 256][raw W: 3 x GN x RAWP][dx: 2 x GM][IqTables]
+    // LDS: [X: 2 x GM x 256][raw W: GN x RAWP][dx: 2 x GM][IqTables]
     int8_t* xs = (int8_t*)smem;
     uint8_t* raw = smem + 2 * XBUF;
-    float* dxs = (float*)(raw + 3 * WBUF);
+    float* dxs = (float*)(raw + WBUF);
     IqTables* tab = (IqTables*)(dxs + 2 * GM);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -144,57 +144,51 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
 
     if constexpr (IQ) load_iq_tables(tab);
 
-    // Per-lane load addresses of an item. Instruction j of wave w fills 1 KB of LDS: X positions 4 (XI w + j) + l / 16,
-    // LDS chunk l % 16, which holds X chunk (l % 16) ^ (p & 15); weight chunks c = 64 (w + NW i) + l (row c / NCH,
-    // chunk c % NCH, LDS offset 16 c). Positions past cnt and rows past `rows` read valid memory (position 0, the
-    // last row); their results are never stored. The scale of position tid (tid < GM) goes through a register.
-    constexpr int XI = GM * 16 / 64 / NW;                     // X instructions per wave per super-block
-    constexpr int WI = (GN * NCH + 64 * NW - 1) / (64 * NW);  // weight instructions per wave per super-block
+    // Per-lane load addresses of an item. X instruction j of wave w fills 1 KB of LDS: positions 4 (XI w + j) + l / 16,
+    // LDS chunk l % 16, which holds X chunk (l % 16) ^ (p & 15). Weight instruction i of wave w fills chunks
+    // c = 64 (w + NW i) + l (row c / NCH, chunk c % NCH, LDS offset 16 c). Positions past cnt are not loaded (their
+    // LDS rows hold stale bytes, their results are never stored); rows past `rows` read the last row. The scale of
+    // position tid (tid < GM) goes through a register.
+    constexpr int XI = GM * 16 / 64 / NW;                     // X instructions per wave per step
+    constexpr int WI = (GN * NCH + 64 * NW - 1) / (64 * NW);  // weight instructions per wave per step
+    static_assert(XI % 4 == 0, "X instructions spread evenly over the 4 decode units");
     struct Addr {
         uint32_t xo[XI];   // X byte offset of each instruction's position row (+ chunk)
         uint32_t dxo;      // scale offset of position tid
         uint32_t rbeg;     // this lane's weight row: byte offset from W, plus W mod 16
-        uint32_t wro[WI];  // byte offset from W of each weight instruction's row
+        int live;          // bit j: X instruction j's position has work
     };
     const int rl = 16 * wave + (lane & 15);  // this lane's weight row in the block
-    int wr[WI], wjj[WI];  // row in the block and chunk index within the row's cover (-1 past the tile)
-#pragma unroll
-    for (int i = 0; i < WI; i++) {
-        const int c = 64 * (wave + NW * i) + lane;
-        wr[i] = min(c / NCH, GN - 1);
-        wjj[i] = c < GN * NCH ? c % NCH : -1;
-    }
+    auto wchunk = [&](int i) __attribute__((always_inline)) { return 64 * (wave + NW * i) + lane; };
     auto addr_of = [&](const Item& it) __attribute__((always_inline)) {
         Addr ad;
+        ad.live = 0;
         auto xrow_of = [&](int p) { p = p < it.cnt ? p : 0; return a.xrow ? a.xrow[it.m0 + p] : it.m0 + p; };
 #pragma unroll
         for (int j = 0; j < XI; j++) {
             const int p = 4 * (XI * wave + j) + (lane >> 4);
             ad.xo[j] = (uint32_t)xrow_of(p) * (uint32_t)cols + 16 * ((lane & 15) ^ (p & 15));
+            if (p < it.cnt) ad.live |= 1 << j;
         }
         ad.dxo = (uint32_t)xrow_of(tid & (GM - 1)) * (uint32_t)(cols / 32);
         ad.rbeg = (uint32_t)(it.w & 15) + (uint32_t)min(it.n0 + rl, a.rows - 1) * (uint32_t)a.rb;
-#pragma unroll
-        for (int i = 0; i < WI; i++) ad.wro[i] = (uint32_t)min(it.n0 + wr[i], a.rows - 1) * (uint32_t)a.rb;
         return ad;
     };
-    // Loads of global super-block step g (buffers rotate by step: X and dx by 2, raw weights by 3).
-    auto load_x = [&](const Addr& ad, int s, int g) __attribute__((always_inline)) {
-        int8_t* xb = xs + (g & 1) * XBUF;
-        const uint64_t base = (uint64_t)(a.xq + 256 * s);
-#pragma unroll
-        for (int j = 0; j < XI; j++) load_lds16_so(base, ad.xo[j], xb + 1024 * (XI * wave + j));
+    // X instruction j of super-block s of an item into the X buffer of step g (X and dx rotate by 2).
+    auto load_x1 = [&](const Addr& ad, int s, int g, const int j) __attribute__((always_inline)) {
+        if (ad.live & (1 << j))
+            load_lds16_so((uint64_t)(a.xq + 256 * s), ad.xo[j], xs + (g & 1) * XBUF + 1024 * (XI * wave + j));
     };
-    // Raw weights of super-block s: the 16-byte covers of each row's super-block, from the scalar base
+    // Raw weights of super-block s: the 16-byte covers of the rows' super-block, from the scalar base
     // (w + s * SBB) & ~15 and per-lane offsets ((w + s * SBB) & 15) + row offset, rounded down to 16, + 16 chunk.
-    auto load_w = [&](const Item& it, const Addr& ad, int s, int g) __attribute__((always_inline)) {
-        uint8_t* wb = raw + (g % 3) * WBUF;
+    auto load_w = [&](const Item& it, int s) __attribute__((always_inline)) {
         const uint64_t beg = it.w + (uint64_t)s * SBB, base = beg & ~(uint64_t)15;
-        const uint32_t lo = (uint32_t)(beg & 15);
 #pragma unroll
         for (int i = 0; i < WI; i++) {
-            const uint32_t t = lo + ad.wro[i], o = (t & ~15u) + 16 * (uint32_t)wjj[i];
-            if (wjj[i] >= 0 && o < t + SBB) load_lds16_so(base, o, wb + 1024 * (wave + NW * i));
+            const int c = wchunk(i);
+            const uint32_t wro = (uint32_t)min(it.n0 + min(c / NCH, GN - 1), a.rows - 1) * (uint32_t)a.rb;
+            const uint32_t t = (uint32_t)(beg & 15) + wro, o = (t & ~15u) + 16 * (uint32_t)(c % NCH);
+            if (c < GN * NCH && o < t + SBB) load_lds16_so(base, o, raw + 1024 * (wave + NW * i));
         }
     };
     float dxv = 0.0f;
@@ -215,9 +209,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
 
     v4i B[4][NP];
     float D = 0.0f, M = 0.0f;
-    // Decode super-block s of the item whose lane row offset is rbeg, from the raw buffer of step g.
-    auto decode = [&](uint32_t rbeg, int s, int g) __attribute__((always_inline)) {
-        const uint8_t* b = raw + (g % 3) * WBUF + rl * RAWP + ((rbeg + (uint32_t)s * SBB) & 15);
+    // Decode super-block s of the item whose lane row offset is rbeg; hook(kk) runs after unit kk.
+    auto decode = [&](uint32_t rbeg, int s, auto&& hook) __attribute__((always_inline)) {
+        const uint8_t* b = raw + rl * RAWP + ((rbeg + (uint32_t)s * SBB) & 15);
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             uint32_t hi[4], lo[4];
@@ -229,27 +223,21 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
                 const int mw = (int)((uint32_t)m * 0x01010101u);
                 B[kk][P_M] = (v4i){mw, mw, mw, mw};
             }
+            hook(kk);
         }
         Dec<T>::scales(b, D, M);
     };
-    // X fragments of tile i (16 positions x 4 K steps of 64) and the MFMAs of a tile on given fragments.
-    auto read_a = [&](const int i, int g, v4i (&av)[4]) __attribute__((always_inline)) {
+    auto mfma_tile = [&](const int i, int g, v4i (&c)[NP]) __attribute__((always_inline)) {
         const int8_t* xb = xs + (g & 1) * XBUF;
+        v4i av[4];
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) av[kk] = *(const v4i*)(xb + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
-    };
-    auto mfma_av = [&](const v4i (&av)[4], v4i (&c)[NP]) __attribute__((always_inline)) {
 #pragma unroll
         for (int pl = 0; pl < NP; pl++) c[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], B[0][pl], (v4i){0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
         for (int kk = 1; kk < 4; kk++)
 #pragma unroll
             for (int pl = 0; pl < NP; pl++) c[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[kk], B[kk][pl], c[pl], 0, 0, 0);
-    };
-    auto mfma_tile = [&](const int i, int g, v4i (&c)[NP]) __attribute__((always_inline)) {
-        v4i av[4];
-        read_a(i, g, av);
-        mfma_av(av, c);
     };
     // Lane's outputs of a tile: weight row rl, positions 16 i + 4 kl + q.
     auto close_tile = [&](const int i, int g, const v4i (&c)[NP]) __attribute__((always_inline)) {
@@ -264,24 +252,10 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             acc[i][q] = __builtin_fmaf(dq[q], f, acc[i][q]);
         }
     };
-    // Position tiles of step g with ntt tiles of work. When every tile has work they form one branch-free stream;
-    // otherwise tiles go in pairs (the close of the first runs while the MFMAs of the second work), and a pair
-    // runs whole when its first tile has work (the second's extra positions are never stored).
+    // Position tiles of step g with ntt tiles of work: tiles in pairs (the close of the first runs while the
+    // MFMAs of the second work); a pair runs whole when its first tile has work (the second's extra positions are
+    // never stored).
     auto tiles = [&](int g, int ntt) __attribute__((always_inline)) {
-        if (ntt == NTT) {
-            // The fragments of tile i + 1 are read while the MFMAs of tile i run (LDS latency off the MFMA path),
-            // and the close of tile i - 1 runs with them.
-            v4i c[2][NP], av[2][4];
-            read_a(0, g, av[0]);
-            static_for<0, NTT>([&](auto I) {
-                constexpr int i = decltype(I)::value;
-                if constexpr (i + 1 < NTT) read_a(i + 1, g, av[(i + 1) & 1]);
-                mfma_av(av[i & 1], c[i & 1]);
-                if constexpr (i > 0) close_tile(i - 1, g, c[(i - 1) & 1]);
-            });
-            close_tile(NTT - 1, g, c[(NTT - 1) & 1]);
-            return;
-        }
         static_for<0, NTT / 2>([&](auto I) {
             constexpr int i = 2 * decltype(I)::value;
             if (i < ntt) {
@@ -329,56 +303,43 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
     };
 
-    // The super-block steps of this block's items run as one stream g = k * nsb + s. Step g loads X of g + 1 and the
-    // raw weights of g + 2 (of the next item near an item's end; the launch gives each block one item when nsb is 1),
-    // so every load has a whole step to land and one barrier per step suffices.
-#ifdef STRATA_GEMM_ANALYZE_ROLE0
-    const bool role0 = true;  // instruction-count analysis only: one role's path
-#else
-    const bool role0 = wave < NW / 2;
-#endif
+    // The super-block steps of this block's items run as one stream g = k * nsb + s: step g loads the X rows and
+    // scales of step g + 1 (of the next item at an item's last step) and, once every wave has decoded, the raw
+    // weights of step g + 1 into the buffer just decoded.
     Item cur = item_at(0), nxt = item_at(1);
     Addr acur = addr_of(cur), anxt = addr_of(nxt);
-    load_x(acur, 0, 0);
+#pragma unroll
+    for (int j = 0; j < XI; j++) load_x1(acur, 0, 0, j);
+    load_w(cur, 0);
     load_dx(acur, 0);
-    load_w(cur, acur, 0, 0);
-    if (nsb > 1) load_w(cur, acur, 1, 1);
     store_dx(0);
     wait_loads();
     __syncthreads();
-    if (role0) decode(acur.rbeg, 0, 0);
     int s = 0;
     for (int g = 0, k = 0; k < nitems; g++) {
         TRACE(0);
         const bool last = s + 1 == nsb, more = k + 1 < nitems;
-        // loads of step g + 1 (X, dx) and g + 2 (raw weights)
-        if (!last) {
-            load_x(acur, s + 1, g + 1);
-            load_dx(acur, s + 1);
-        } else if (more) {
-            load_x(anxt, 0, g + 1);
-            load_dx(anxt, 0);
-        }
-        if (s + 2 < nsb) load_w(cur, acur, s + 2, g + 2);
-        else if (more) load_w(nxt, anxt, s + 2 - nsb, g + 2);
-#ifdef STRATA_GEMM_ANALYZE_ROLE0
-        const int ntt = NTT;
-#else
-        const int ntt = (cur.cnt + 15) >> 4;
-#endif
+        if (!last) load_dx(acur, s + 1);
+        else if (more) load_dx(anxt, 0);
         TRACE(1);
-        if (role0) {
-            tiles(g, ntt);
-            TRACE(2);
-            if (last) store(cur);
-            if (!last) decode(acur.rbeg, s + 1, g + 1);
-            else if (more) decode(anxt.rbeg, 0, g + 1);
-        } else {
-            decode(acur.rbeg, s, g);
-            TRACE(2);
-            tiles(g, ntt);
-            if (last) store(cur);
-        }
+        decode(acur.rbeg, s, [&](int kk) __attribute__((always_inline)) {
+#pragma unroll
+            for (int h = 0; h < XI / 4; h++) {
+                const int j = (XI / 4) * kk + h;
+                if (!last) load_x1(acur, s + 1, g + 1, j);
+                else if (more) load_x1(anxt, 0, g + 1, j);
+            }
+        });
+        __syncthreads();  // every wave has decoded: the raw buffer takes the next step's weights
+        if (!last) load_w(cur, s + 1);
+        else if (more) load_w(nxt, 0);
+        TRACE(2);
+#ifdef STRATA_GEMM_ANALYZE_ROLE0
+        tiles(g, NTT);
+#else
+        tiles(g, (cur.cnt + 15) >> 4);
+#endif
+        if (last) store(cur);
         TRACE(3);
         if (!last || more) store_dx(g + 1);
         if (last) {
@@ -400,7 +361,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
 
 template <int T>
 static size_t gemm_smem() {
-    size_t b = 2 * (size_t)XBUF + 3 * (size_t)GemmFmt<T>::WBUF + 2 * GM * 4;
+    size_t b = 2 * (size_t)XBUF + (size_t)GemmFmt<T>::WBUF + 2 * GM * 4;
     if (T == IQ2_XXS || T == IQ3_S) b += sizeof(IqTables);
     return b;
 }
@@ -420,8 +381,7 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
         attr = true;
     }
     a.max_tiles = g.n_tiles;
-    // Persistent blocks, one per CU, when an item has at least two super-blocks (the step stream prefetches two
-    // steps ahead); otherwise one block per item.
+    // Persistent blocks, one per CU.
     static int ncu = 0;
     if (!ncu) {
         int dev = 0;
@@ -431,7 +391,7 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
     }
     const long long total = (long long)((g.rows + GN - 1) / GN) * g.n_tiles;
     const long long per = (total + NXCD - 1) / NXCD;
-    const long long gx = g.cols / 256 >= 2 ? std::min<long long>(per, std::max(ncu / NXCD, 1)) : per;
+    const long long gx = std::min<long long>(per, std::max(ncu / NXCD, 1));
     a.gx = (int)std::max<long long>(gx, 1);
     const long long grid = (long long)a.gx * NXCD;
     gemm_kernel<T><<<dim3((unsigned)grid), 64 * NW, smem, s>>>(a);
@@ -443,6 +403,8 @@ extern "C" int strata_debug_gemm_trace(uint64_t* out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_gemm_trace), sizeof(g_gemm_trace)) == hipSuccess ? 0 : -1;
 }
 #endif
+
+uint64_t gemm_block_positions() { return GM; }
 
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t s) {
     switch (g.ty) {

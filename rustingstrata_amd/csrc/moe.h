@@ -23,6 +23,7 @@ struct SortLaunch {
     uint64_t bases[3] = {0, 0, 0}, strides[3] = {0, 0, 0};
     uint64_t* tiles = nullptr;  // n_mats lists of max_tiles 16-byte tiles
     int max_tiles = 0;
+    int chunk = 128;            // positions per tile
     int* n_tiles = nullptr;
     int* err = nullptr;
     int* scratch = nullptr;

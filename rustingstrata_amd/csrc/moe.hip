@@ -143,7 +143,7 @@ hipError_t launch_combine_seq(float* x, const float* ye, const float* wts, const
 // counts into each (wave, expert) start slot (experts ascending, waves in order within an expert), phase C walks each
 // segment in order assigning slots, 64 pairs at a time with the rank among equal experts inside the wave. The result
 // is the host counting sort of src/gpu_model/prefill.rs:563-573 exactly.
-constexpr int SORT_WAVES = 16, SORT_MAX_E = 512, GEMM_BM = 128;
+constexpr int SORT_WAVES = 16, SORT_MAX_E = 512;
 
 size_t sort_scratch_bytes(int) { return 16; }
 
@@ -168,7 +168,7 @@ __global__ __launch_bounds__(1024) void sort_kernel(SortLaunch a) {
     if (tid < E) {
         for (int w = 0; w < SORT_WAVES; w++) cnt += hist[w][tid];
         offs[tid] = cnt;
-        tbase[tid] = (cnt + GEMM_BM - 1) / GEMM_BM;
+        tbase[tid] = (cnt + a.chunk - 1) / a.chunk;
     }
     __syncthreads();
     if (wave == 0) {
@@ -218,11 +218,11 @@ __global__ __launch_bounds__(1024) void sort_kernel(SortLaunch a) {
             if (ok) a.xrow[slot] = i / a.k;
         }
     }
-    // Tiles: expert e's slots off[e] .. off[e + 1] in chunks of GEMM_BM.
+    // Tiles: expert e's slots off[e] .. off[e + 1] in chunks of a.chunk positions.
     if (tid < E) {
         int c = offs[tid + 1] - offs[tid], tb = tbase[tid];
-        for (int j = 0; j * GEMM_BM < c; j++) {
-            uint64_t m0 = (uint64_t)(offs[tid] + j * GEMM_BM), cn = (uint64_t)min(GEMM_BM, c - j * GEMM_BM);
+        for (int j = 0; j * a.chunk < c; j++) {
+            uint64_t m0 = (uint64_t)(offs[tid] + j * a.chunk), cn = (uint64_t)min(a.chunk, c - j * a.chunk);
             for (int m = 0; m < a.n_mats; m++) {
                 uint64_t* tl = a.tiles + 2 * ((uint64_t)m * a.max_tiles + tb + j);
                 tl[0] = a.bases[m] + (uint64_t)tid * a.strides[m];

@@ -235,16 +235,18 @@ def test_router_rejects_shapes(hip):
         hip.router_topk(b, 600, 8, 0.0, b, b, 1)
 
 
-@pytest.mark.parametrize("t,k,E", [(1, 8, 128), (333, 8, 128), (4096, 8, 128), (50, 4, 7)])
-def test_sort_bit_exact(hip, t, k, E):
+@pytest.mark.parametrize("t,k,E,chunk", [(1, 8, 128, 128), (333, 8, 128, 128), (4096, 8, 128, 128), (50, 4, 7, 128),
+                                         (4096, 8, 128, 256), (333, 8, 128, 256)])
+def test_sort_bit_exact(hip, t, k, E, chunk):
+    """chunk 128 is the reference's tile size (GEMM_BM, src/backend.rs:16); 256 fills this backend's GEMM blocks."""
     logits = zipf_logits(t, E, seed=t)
     ids, _ = O.route(logits, k)
     off_w, xrow_w, inv_w = O.sort_by_expert(ids, E)
-    max_tiles = t * k // 128 + E
+    max_tiles = t * k // chunk + E
     off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(t * k * 4), hip.alloc(t * k * 4)
     tiles, ntd, err = hip.alloc(3 * max_tiles * 16), hip.alloc(4), hip.alloc(4)
     mats = [(1 << 40, 1000), (2 << 40, 2000), (3 << 40, 3000)]
-    hip.moe_sort(up(hip, ids), t, k, E, off, xrow, inv, mats, tiles, max_tiles, ntd, err)
+    hip.moe_sort(up(hip, ids), t, k, E, off, xrow, inv, mats, tiles, max_tiles, ntd, err, chunk=0 if chunk == 128 else chunk)
     assert np.array_equal(down(hip, off, np.int32, E + 1), off_w)
     assert np.array_equal(down(hip, xrow, np.int32, t * k), xrow_w)
     assert np.array_equal(down(hip, inv, np.int32, t * k), inv_w)
@@ -252,8 +254,8 @@ def test_sort_bit_exact(hip, t, k, E):
     # tiles: the host tile builder of src/gpu_model/prefill.rs:618-642, per matrix
     want = []
     for e in range(E):
-        for m0 in range(off_w[e], off_w[e + 1], 128):
-            want.append((e, int(m0), int(min(128, off_w[e + 1] - m0))))
+        for m0 in range(off_w[e], off_w[e + 1], chunk):
+            want.append((e, int(m0), int(min(chunk, off_w[e + 1] - m0))))
     nt = int(down(hip, ntd, np.int32, 1)[0])
     assert nt == len(want)
     tl = down(hip, tiles, np.uint64, 3 * max_tiles * 2).reshape(3, max_tiles, 2)
@@ -321,20 +323,21 @@ def tile_list(hip, base, stride, spans):
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
 def test_gemm_tiles_match_cpu(hip, ty):
     """tests/kernels.rs:355-447: tiles (0, 128), (128, 16), (144, 26) with X gathered through xrow; act store, then
-    SwiGLU into the stored gate, then add."""
+    SwiGLU into the stored gate, then add. Tiles (170, 256) and (426, 200) fill this backend's 256-position blocks."""
     rows, cols, E, n_x = 80, 512, 3, 100
     rb = ggml.row_bytes(ty, cols)
     w = random_blocks(ty, E * rows, cols, seed=ty)
     wb = up(hip, w)
     x = normal((n_x, cols), seed=2)
-    xrow = np.random.default_rng(3).integers(0, n_x, 170).astype(np.int32)
-    spans = [(0, 0, 128), (2, 128, 16), (1, 144, 26)]
+    npos = 626
+    xrow = np.random.default_rng(3).integers(0, n_x, npos).astype(np.int32)
+    spans = [(0, 0, 128), (2, 128, 16), (1, 144, 26), (2, 170, 256), (0, 426, 200)]
     tiles, nt = tile_list(hip, int(wb), rows * rb, spans)
-    y = hip.alloc(170 * rows * 4)
+    y = hip.alloc(npos * rows * 4)
     xb, xr = up(hip, x), up(hip, xrow)
     hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_STORE)
-    got = down(hip, y, np.float32, 170 * rows).reshape(170, rows)
-    want = np.zeros((170, rows), dtype=np.float32)
+    got = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
+    want = np.zeros((npos, rows), dtype=np.float32)
     for e, m0, c in spans:
         we = w[e * rows:(e + 1) * rows]
         for m in range(m0, m0 + c):
@@ -342,11 +345,11 @@ def test_gemm_tiles_match_cpu(hip, ty):
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
     # act 1: y = silu(y) * (W x) with the same x (SAME_X), then act 2: y += W x
     hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_SWIGLU | S.SAME_X)
-    got2 = down(hip, y, np.float32, 170 * rows).reshape(170, rows)
+    got2 = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
     want2 = want / (1 + np.exp(-want.astype(np.float64))) * want
     assert max_rel_err(got2, want2) <= 2 * TOL
     hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_ADD | S.SAME_X)
-    got3 = down(hip, y, np.float32, 170 * rows).reshape(170, rows)
+    got3 = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
     assert max_rel_err(got3, want2 + want) <= 2 * TOL
 
 
@@ -387,11 +390,12 @@ def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits):
     hb, lb = up(hip, hs), up(hip, logits)
     ids, wts = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
     hip.router_topk(lb, E, k, 0.0, ids, wts, T)
-    max_tiles = T * k // 128 + E
+    chunk = hip.gemm_block_positions()
+    max_tiles = T * k // chunk + E
     off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
     tiles, ntd = hip.alloc(3 * max_tiles * 16), hip.alloc(4)
     hip.moe_sort(ids, T, k, E, off, xrow, inv, [(int(g_b), F * rb_gu), (int(u_b), F * rb_gu), (int(d_b), H * rb_d)],
-                 tiles, max_tiles, ntd)
+                 tiles, max_tiles, ntd, chunk=chunk)
     ge, ye = hip.alloc(T * k * F * 4), hip.alloc(T * k * H * 4)
     hip.gemm_grouped(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, S.ACT_STORE)
     hip.gemm_grouped(ggml.Q5_K, F, H, int(tiles) + max_tiles * 16, max_tiles, ntd, hb, H, T, xrow, ge, F,
