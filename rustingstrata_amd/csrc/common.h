@@ -45,6 +45,12 @@ template <typename T>
 __device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(uint64_t addr) {
     return (const __attribute__((address_space(1))) T*)addr;
 }
+// Read of a value that no kernel of the launch writes, at a wave-uniform address, through the scalar cache
+// (s_load: its wait is lgkmcnt, so it does not wait for the wave's vector loads in flight).
+template <class T>
+__device__ __forceinline__ T sload(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)(uintptr_t)p;
+}
 // LDS (address space 3) view of a generic pointer into shared memory. Keeping LDS reads in their own address space
 // stops the compiler from merging them with global reads into flat ones.
 template <typename T>

@@ -47,8 +47,21 @@ struct GemvArgs {
 __host__ __device__ constexpr uint32_t up16(uint32_t v) { return (v + 15) & ~15u; }
 
 // Sum over the g lanes of each aligned lane group (g a power of two <= 64).
+// v of lane i + (CTRL's source offset) within the 16-lane row, 0 where the source leaves the row (DPP).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// Sum over aligned groups of g lanes (g a power of two), complete in the group's first lane: in-row steps by DPP
+// (xor 1, xor 2 by quad permutes, then + lane i + 4, + lane i + 8), wider ones by lane permutes. The additions pair
+// the same values in the same order as an xor butterfly.
 __device__ __forceinline__ float group_sum(float v, int g) {
-    for (int o = g >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if (g >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    if (g >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    if (g >= 8) v += dpp_f<0x104>(v);  // row_shl:4
+    if (g >= 16) v += dpp_f<0x108>(v); // row_shl:8
+    if (g >= 32) v += __shfl_xor(v, 16);
+    if (g >= 64) v += __shfl_xor(v, 32);
     return v;
 }
 
@@ -281,8 +294,13 @@ __device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const flo
                     sdot4((int)x.w[4 * g + 2], 0x01010101, sdot4((int)x.w[4 * g + 3], 0x01010101, 0))));
 }
 
+#ifdef STRATA_GEMV1_WPE
+#define GEMV1_ATTR __attribute__((amdgpu_waves_per_eu(STRATA_GEMV1_WPE)))
+#else
+#define GEMV1_ATTR
+#endif
 template <int T, bool Q32>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv1_kernel(GemvArgs a) {
+__global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs a) {
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -290,7 +308,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv1_kernel(GemvArgs a) {
     const int tid = threadIdx.x, cols = a.cols;
     // LDS: [IqTables][x int8 (cols, whole super-blocks)][x scales][tile]
     const uint32_t ncp = (cols + 255) & ~255;
+#ifdef STRATA_GEMV1_XLDS
+    const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + ncp, o_ss = o_xd + ncp / 8, o_tile = o_ss + ncp / 4;
+    int* xss = (int*)(smem + o_ss);
+#else
     const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + ncp, o_tile = o_xd + ncp / 8;
+#endif
     IqTables* tab = (IqTables*)smem;
     if constexpr (IQ) load_iq_tables(tab);
     int8_t* xl = (int8_t*)(smem + o_x);
@@ -301,7 +324,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv1_kernel(GemvArgs a) {
     auto valid = [&](int t) {
         const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
         if (rt * a.R >= (z ? a.rows2 : a.rows)) return false;
-        return !a.ids || a.ids[slot] >= 0;  // a slot not routed here leaves its output untouched
+        return !a.ids || sload(a.ids + slot) >= 0;  // a slot not routed here leaves its output untouched
     };
     auto next_valid = [&](int t) {
         while (t < total && !valid(t)) t += gridDim.x;
@@ -318,7 +341,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv1_kernel(GemvArgs a) {
         sp.Y = (float*)((uint8_t*)a.y + (z ? a.y2 : 0));
         sp.xrow = 0;
         if (a.ids) {
-            W += (int64_t)a.ids[slot] * a.stride;
+            W += (int64_t)sload(a.ids + slot) * a.stride;
             sp.xrow = slot / a.xg;
             sp.Y += (int64_t)slot * rows;
         }
@@ -328,11 +351,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv1_kernel(GemvArgs a) {
         return sp;
     };
     v4u wv[GEMV1_CH];
+    // every lane loads every instruction (chunks past the span repeat its last chunk and land past the tile's bytes
+    // in LDS), so no load or store sits under a branch and the LDS stores wait for their own loads only
     auto issue = [&](const Span& sp) {
 #pragma unroll
         for (int i = 0; i < GEMV1_CH; i++) {
-            const int c = tid + GEMV_THREADS * i;
-            if (c < sp.nch) wv[i] = __builtin_nontemporal_load(gptr<v4u>(sp.g0 + 16 * (uint64_t)c));
+            const int c = min(tid + GEMV_THREADS * i, sp.nch - 1);
+            wv[i] = __builtin_nontemporal_load(gptr<v4u>(sp.g0 + 16 * (uint64_t)c));
         }
     };
 
@@ -340,45 +365,67 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv1_kernel(GemvArgs a) {
     if (t >= total) return;
     Span sp = span(t);
     issue(sp);
+    // the tile after next is located while the next one is in flight
+    int tn = next_valid(t + gridDim.x);
+    Span spn = sp;
+    if (tn < total) spn = span(tn);
     const int G = a.G, wave = tid >> 6, lane = tid & 63, gl = lane & (G - 1);
     const int RPW = 64 / G, nsb = (cols + 255) >> 8;
     const bool has_sb = gl < nsb;
+#ifndef STRATA_GEMV1_XLDS
     XReg x;
+#endif
     int cur_xrow = -1;
     while (true) {
         __syncthreads();  // the previous tile's readers are done with the LDS tile
         if (sp.xrow != cur_xrow) {
             stage_x<Q32>(a, sp.xrow, xl, xld);
             __syncthreads();
+#ifdef STRATA_GEMV1_XLDS
+            for (int c = tid; c < (int)ncp / 16; c += GEMV_THREADS) {
+                const v4u q = *(const v4u*)(xl + 16 * c);
+                xss[c] = sdot4((int)q.x, 0x01010101, sdot4((int)q.y, 0x01010101, sdot4((int)q.z, 0x01010101, sdot4((int)q.w, 0x01010101, 0))));
+            }
+#else
             if (has_sb) load_x_slice(gl, xl, xld, x);
+#endif
             cur_xrow = sp.xrow;
             __syncthreads();  // every lane has its slice before the LDS copy changes again
         }
 #pragma unroll
-        for (int i = 0; i < GEMV1_CH; i++) {
-            const int c = tid + GEMV_THREADS * i;
-            if (c < sp.nch) *(v4u*)(tile + 16 * c) = wv[i];
-        }
+        for (int i = 0; i < GEMV1_CH; i++) *(v4u*)(tile + 16 * (tid + GEMV_THREADS * i)) = wv[i];
         __syncthreads();
         const Span cs = sp;
-        const int tn = next_valid(t + gridDim.x);
-        if (tn < total) {
-            sp = span(tn);
+        const bool more = tn < total;
+        if (more) {
+            sp = spn;
             issue(sp);  // in flight while this tile is computed
+            t = tn;
+            tn = next_valid(t + gridDim.x);
+            if (tn < total) spn = span(tn);
         }
         const int nv = min(256, cols - 256 * gl);
         for (int base = wave * RPW; base < cs.nr; base += 4 * RPW) {
             const int rr = base + lane / G;
             float acc = 0.0f;
+#ifdef STRATA_GEMV1_NOCOMPUTE
+            if (rr < cs.nr && has_sb) acc = (float)tile[rr * a.rb + gl];
+            if (false) {
+#else
             if (rr < cs.nr && has_sb) {
+#endif
                 const uint8_t* b = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb + gl * SBB;
+#ifdef STRATA_GEMV1_XLDS
+                const XLds xv{xl + 256 * gl, xld + 8 * gl, xss + 16 * gl};
+                acc = Q32 ? sb_dot_q32<T>(b, xv, tab, nv) : sb_dot_q8k<T>(b, xv, tab, nv);
+#else
                 acc = Q32 ? sb_dot_q32<T>(b, x, tab, nv) : sb_dot_q8k<T>(b, x, tab, nv);
+#endif
             }
             acc = group_sum(acc, G);
             if (rr < cs.nr && gl == 0) cs.Y[cs.r0 + rr] = acc;
         }
-        if (tn >= total) break;
-        t = tn;
+        if (!more) break;
     }
 }
 
@@ -486,7 +533,11 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     bool iq = g.ty == IQ2_XXS || g.ty == IQ3_S;
     if (single) {
         const uint32_t ncp = (g.cols + 255) & ~255;
+#ifdef STRATA_GEMV1_XLDS
+        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + ncp + ncp / 8 + ncp / 4 + GEMV1_TILE + 16;
+#else
         const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + ncp + ncp / 8 + GEMV1_TILE + 16;
+#endif
         switch (g.ty) {
         case Q8_0: return gemv1_t<Q8_0>(a, grid, smem1, s);
         case Q2_K: return gemv1_t<Q2_K>(a, grid, smem1, s);
