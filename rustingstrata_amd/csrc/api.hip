@@ -501,7 +501,7 @@ static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint
     if (op < 0 || op > 2) return set_error("gemm: act " + std::to_string(act));
     if (dense_w && check_align(ty, (uint64_t)dense_w, "gemm_dense")) return -1;
     if (n_tiles == 0 || rows == 0) return 0;
-    if (rows > (1u << 24) || n_tiles > 65535 * 64) return set_error("gemm: too large");
+    if (rows > (1u << 24) || row_bytes(ty, cols) >= (1u << 24) || n_tiles > 65535 * 64) return set_error("gemm: too large");
     // the kernel addresses X and a weight matrix with 32-bit byte offsets
     if (n_x * cols >= (1ull << 32) || rows * row_bytes(ty, cols) >= (1ull << 32)) return set_error("gemm: X or W of 4 GiB or more");
     uint64_t xq = 0;

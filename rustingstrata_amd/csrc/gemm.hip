@@ -17,7 +17,7 @@
 //   1. decodes its rows' super-block into digit-plane B operands (registers), issuing the next step's X loads
 //      between the decode units;
 //   2. after a barrier (the raw weights' one LDS buffer is free) issues the next step's raw-weight loads;
-//   3. runs its 16 position tiles: the MFMAs of tile i with the float close of tile i - 1.
+//   3. runs its 16 position tiles in pairs: the two tiles' MFMA chains interleaved, then their float close.
 // The two waves of a SIMD overlap one's VALU work (decode, close) with the other's MFMAs.
 // Loads go straight from global memory into LDS (global_load_lds_dwordx4: lane l of a wave's instruction writes the
 // 16 bytes at its own address to LDS base + 16 l); X is double-buffered, so a step's X loads have the whole step to
@@ -106,14 +106,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     float* dxs = (float*)(raw + WBUF);
     IqTables* tab = (IqTables*)(dxs + 2 * GM);
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index through a scalar register: LDS destinations and chunk numbers built from it stay scalar
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int cols = a.cols, nsb = cols / 256;
 
     // Items are (tile, row block) pairs, item = tile * nrb + row block. XCD x (the hardware deals consecutive block
     // ids to the 8 XCDs in turn) takes the items x * per .. (x + 1) * per - 1, so a tile's row blocks and an
     // expert's tiles run on one XCD and share its L2 (X rows, expert weights); its a.gx blocks take every a.gx-th
     // item from their index j.
-    const int ntiles = a.n_tiles_dev ? min(*a.n_tiles_dev, a.max_tiles) : a.max_tiles;
+    const int ntiles = a.n_tiles_dev ? min(sload(a.n_tiles_dev), a.max_tiles) : a.max_tiles;
     const int nrb = (a.rows + GN - 1) / GN, total = nrb * ntiles;
     const int per = (total + NXCD - 1) / NXCD, xcd = blockIdx.x % NXCD, jb = blockIdx.x / NXCD;
     const int ibeg = xcd * per + jb, iend = min((xcd + 1) * per, total);
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         const int id = ibeg + k * a.gx, tile = id / nrb;
         it.n0 = (id - tile * nrb) * GN;
         if (a.tiles) {
-            const uint64_t t0 = a.tiles[2 * tile], t1 = a.tiles[2 * tile + 1];
+            const uint64_t t0 = sload(a.tiles + 2 * tile), t1 = sload(a.tiles + 2 * tile + 1);
             it.w = t0;
             it.m0 = (int)(uint32_t)t1;
             it.cnt = min(GM, (int)(t1 >> 32));
@@ -146,49 +147,58 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
 
     // Per-lane load addresses of an item. X instruction j of wave w fills 1 KB of LDS: positions 4 (XI w + j) + l / 16,
     // LDS chunk l % 16, which holds X chunk (l % 16) ^ (p & 15). Weight instruction i of wave w fills chunks
-    // c = 64 (w + NW i) + l (row c / NCH, chunk c % NCH, LDS offset 16 c). Positions past cnt are not loaded (their
-    // LDS rows hold stale bytes, their results are never stored); rows past `rows` read the last row. The scale of
-    // position tid (tid < GM) goes through a register.
+    // c = 64 (w + NW i) + l (row c / NCH, chunk c % NCH, LDS offset 16 c). An X instruction whose 4 positions are all
+    // past cnt is skipped; positions past cnt in a partly live one load the item's first row (their results are never
+    // stored); rows past `rows` read the last row. The scale of position tid (tid < GM) goes through a register.
     constexpr int XI = GM * 16 / 64 / NW;                     // X instructions per wave per step
     constexpr int WI = (GN * NCH + 64 * NW - 1) / (64 * NW);  // weight instructions per wave per step
+    static_assert(NCH <= 15 && WI <= 8, "chunk numbers of a lane's weight instructions fit one word");
+    static_assert(SBB < 225, "the no-chunk number 15 lands past every super-block");
     static_assert(XI % 4 == 0, "X instructions spread evenly over the 4 decode units");
     struct Addr {
         uint32_t xo[XI];   // X byte offset of each instruction's position row (+ chunk)
         uint32_t dxo;      // scale offset of position tid
         uint32_t rbeg;     // this lane's weight row: byte offset from W, plus W mod 16
-        int live;          // bit j: X instruction j's position has work
+        uint32_t wro[WI];  // byte offsets from W of the rows of this lane's weight chunks
+        int cnt;           // the item's positions
     };
     const int rl = 16 * wave + (lane & 15);  // this lane's weight row in the block
     auto wchunk = [&](int i) __attribute__((always_inline)) { return 64 * (wave + NW * i) + lane; };
     auto addr_of = [&](const Item& it) __attribute__((always_inline)) {
         Addr ad;
-        ad.live = 0;
+        ad.cnt = it.cnt;
         auto xrow_of = [&](int p) { p = p < it.cnt ? p : 0; return a.xrow ? a.xrow[it.m0 + p] : it.m0 + p; };
 #pragma unroll
         for (int j = 0; j < XI; j++) {
             const int p = 4 * (XI * wave + j) + (lane >> 4);
             ad.xo[j] = (uint32_t)xrow_of(p) * (uint32_t)cols + 16 * ((lane & 15) ^ (p & 15));
-            if (p < it.cnt) ad.live |= 1 << j;
         }
         ad.dxo = (uint32_t)xrow_of(tid & (GM - 1)) * (uint32_t)(cols / 32);
-        ad.rbeg = (uint32_t)(it.w & 15) + (uint32_t)min(it.n0 + rl, a.rows - 1) * (uint32_t)a.rb;
+        ad.rbeg = (uint32_t)(it.w & 15) + __umul24((uint32_t)min(it.n0 + rl, a.rows - 1), (uint32_t)a.rb);
+#pragma unroll
+        for (int i = 0; i < WI; i++)
+            ad.wro[i] = __umul24((uint32_t)min(it.n0 + min(wchunk(i) / NCH, GN - 1), a.rows - 1), (uint32_t)a.rb);
         return ad;
     };
     // X instruction j of super-block s of an item into the X buffer of step g (X and dx rotate by 2).
     auto load_x1 = [&](const Addr& ad, int s, int g, const int j) __attribute__((always_inline)) {
-        if (ad.live & (1 << j))
+        if (4 * (XI * wave + j) < ad.cnt)
             load_lds16_so((uint64_t)(a.xq + 256 * s), ad.xo[j], xs + (g & 1) * XBUF + 1024 * (XI * wave + j));
     };
+    // Chunk numbers c % NCH of this lane's weight instructions, 4 bits each (15: no chunk; NCH <= 15).
+    uint32_t wcc = 0;
+#pragma unroll
+    for (int i = 0; i < WI; i++) wcc |= (uint32_t)(wchunk(i) < GN * NCH ? wchunk(i) % NCH : 15) << (4 * i);
     // Raw weights of super-block s: the 16-byte covers of the rows' super-block, from the scalar base
-    // (w + s * SBB) & ~15 and per-lane offsets ((w + s * SBB) & 15) + row offset, rounded down to 16, + 16 chunk.
-    auto load_w = [&](const Item& it, int s) __attribute__((always_inline)) {
+    // (w + s * SBB) & ~15 and per-lane offsets ((w + s * SBB) & 15) + row offset, rounded down to 16, + 16 chunk
+    // (a chunk past the super-block, or no chunk: offset 240 past the rounded start, is not loaded).
+    auto load_w = [&](const Item& it, const Addr& ad, int s) __attribute__((always_inline)) {
         const uint64_t beg = it.w + (uint64_t)s * SBB, base = beg & ~(uint64_t)15;
+        const uint32_t b15 = (uint32_t)(beg & 15);
 #pragma unroll
         for (int i = 0; i < WI; i++) {
-            const int c = wchunk(i);
-            const uint32_t wro = (uint32_t)min(it.n0 + min(c / NCH, GN - 1), a.rows - 1) * (uint32_t)a.rb;
-            const uint32_t t = (uint32_t)(beg & 15) + wro, o = (t & ~15u) + 16 * (uint32_t)(c % NCH);
-            if (c < GN * NCH && o < t + SBB) load_lds16_so(base, o, raw + 1024 * (wave + NW * i));
+            const uint32_t t = b15 + ad.wro[i], o = (t & ~15u) + 16 * ((wcc >> (4 * i)) & 15);
+            if (o < t + SBB) load_lds16_so(base, o, raw + 1024 * (wave + NW * i));
         }
     };
     float dxv = 0.0f;
@@ -227,43 +237,53 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         }
         Dec<T>::scales(b, D, M);
     };
-    auto mfma_tile = [&](const int i, int g, v4i (&c)[NP]) __attribute__((always_inline)) {
+    // Tiles i and i + 1 together: their 2 NP accumulator chains interleave in the K loop, so an MFMA's result
+    // feeds the next MFMA of its chain 2 NP issues later (the MFMA pipe stays full).
+    auto mfma_pair = [&](const int i, int g, v4i (&c0)[NP], v4i (&c1)[NP]) __attribute__((always_inline)) {
         const int8_t* xb = xs + (g & 1) * XBUF;
-        v4i av[4];
+        v4i a0[4], a1[4];
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) av[kk] = *(const v4i*)(xb + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
+        for (int kk = 0; kk < 4; kk++) {
+            a0[kk] = *(const v4i*)(xb + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
+            a1[kk] = *(const v4i*)(xb + (16 * (i + 1) + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
+        }
 #pragma unroll
-        for (int pl = 0; pl < NP; pl++) c[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], B[0][pl], (v4i){0, 0, 0, 0}, 0, 0, 0);
+        for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-        for (int kk = 1; kk < 4; kk++)
-#pragma unroll
-            for (int pl = 0; pl < NP; pl++) c[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[kk], B[kk][pl], c[pl], 0, 0, 0);
+            for (int pl = 0; pl < NP; pl++) {
+                c0[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[kk], B[kk][pl], kk ? c0[pl] : (v4i){0, 0, 0, 0}, 0, 0, 0);
+                c1[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[kk], B[kk][pl], kk ? c1[pl] : (v4i){0, 0, 0, 0}, 0, 0, 0);
+            }
     };
-    // Lane's outputs of a tile: weight row rl, positions 16 i + 4 kl + q.
-    auto close_tile = [&](const int i, int g, const v4i (&c)[NP]) __attribute__((always_inline)) {
-        const float4 d4 = *(const float4*)(dxs + (g & 1) * GM + 16 * i + 4 * kl);
-        const float dq[4] = {d4.x, d4.y, d4.z, d4.w};
+    // Lane's outputs of tiles i and i + 1: weight row rl, positions 16 i + 4 kl + q (and 16 further), closed in one
+    // loop so both accumulator chains end together (the compiler then keeps their MFMAs interleaved).
+    auto close_pair = [&](const int i, int g, const v4i (&c0)[NP], const v4i (&c1)[NP]) __attribute__((always_inline)) {
+        const float4 d0 = *(const float4*)(dxs + (g & 1) * GM + 16 * i + 4 * kl);
+        const float4 d1 = *(const float4*)(dxs + (g & 1) * GM + 16 * (i + 1) + 4 * kl);
+        const float dq0[4] = {d0.x, d0.y, d0.z, d0.w}, dq1[4] = {d1.x, d1.y, d1.z, d1.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int iv = F::HI ? (c[P_HI][q] << 8) + c[P_LO][q] : c[P_LO][q];
-            float f;
-            if constexpr (F::MIN) f = __builtin_fmaf(D, (float)iv, -(M * (float)c[P_M][q]));
-            else f = D * (float)iv;
-            acc[i][q] = __builtin_fmaf(dq[q], f, acc[i][q]);
+            const int iv0 = F::HI ? (c0[P_HI][q] << 8) + c0[P_LO][q] : c0[P_LO][q];
+            const int iv1 = F::HI ? (c1[P_HI][q] << 8) + c1[P_LO][q] : c1[P_LO][q];
+            float f0, f1;
+            if constexpr (F::MIN) {
+                f0 = __builtin_fmaf(D, (float)iv0, -(M * (float)c0[P_M][q]));
+                f1 = __builtin_fmaf(D, (float)iv1, -(M * (float)c1[P_M][q]));
+            } else {
+                f0 = D * (float)iv0;
+                f1 = D * (float)iv1;
+            }
+            acc[i][q] = __builtin_fmaf(dq0[q], f0, acc[i][q]);
+            acc[i + 1][q] = __builtin_fmaf(dq1[q], f1, acc[i + 1][q]);
         }
     };
-    // Position tiles of step g with ntt tiles of work: tiles in pairs (the close of the first runs while the
-    // MFMAs of the second work); a pair runs whole when its first tile has work (the second's extra positions are
-    // never stored).
     auto tiles = [&](int g, int ntt) __attribute__((always_inline)) {
         static_for<0, NTT / 2>([&](auto I) {
             constexpr int i = 2 * decltype(I)::value;
             if (i < ntt) {
                 v4i c0[NP], c1[NP];
-                mfma_tile(i, g, c0);
-                mfma_tile(i + 1, g, c1);
-                close_tile(i, g, c0);
-                close_tile(i + 1, g, c1);
+                mfma_pair(i, g, c0, c1);
+                close_pair(i, g, c0, c1);
             }
         });
     };
@@ -303,55 +323,56 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
     };
 
-    // The super-block steps of this block's items run as one stream g = k * nsb + s: step g loads the X rows and
-    // scales of step g + 1 (of the next item at an item's last step) and, once every wave has decoded, the raw
-    // weights of step g + 1 into the buffer just decoded.
-    Item cur = item_at(0), nxt = item_at(1);
-    Addr acur = addr_of(cur), anxt = addr_of(nxt);
+    // The super-block steps of this block's items run as one stream g = k * nsb + s (G steps): step g loads the X rows
+    // and scales of step g + 1 and, once every wave has decoded, the raw weights of step g + 1 into the buffer just
+    // decoded. The load state (iL, aL, sL) describes step g + 1; cur and rbeg describe step g.
+    const int G = nitems * nsb;
+    int kL = 0, sL = 0;
+    Item iL = item_at(0);
+    Addr aL = addr_of(iL);
 #pragma unroll
-    for (int j = 0; j < XI; j++) load_x1(acur, 0, 0, j);
-    load_w(cur, 0);
-    load_dx(acur, 0);
+    for (int j = 0; j < XI; j++) load_x1(aL, 0, 0, j);
+    load_w(iL, aL, 0);
+    load_dx(aL, 0);
     store_dx(0);
     wait_loads();
     __syncthreads();
+    Item cur = iL;
+    uint32_t rbeg = aL.rbeg;
+    auto advance = [&]() __attribute__((always_inline)) {
+        if (++sL == nsb) {
+            sL = 0;
+            iL = item_at(++kL);
+            aL = addr_of(iL);
+        }
+    };
+    advance();
     int s = 0;
-    for (int g = 0, k = 0; k < nitems; g++) {
+    for (int g = 0; g < G; g++) {
         TRACE(0);
-        const bool last = s + 1 == nsb, more = k + 1 < nitems;
-        if (!last) load_dx(acur, s + 1);
-        else if (more) load_dx(anxt, 0);
+        const bool nx = g + 1 < G;
+        if (nx) load_dx(aL, sL);
         TRACE(1);
-        decode(acur.rbeg, s, [&](int kk) __attribute__((always_inline)) {
+        decode(rbeg, s, [&](int kk) __attribute__((always_inline)) {
 #pragma unroll
-            for (int h = 0; h < XI / 4; h++) {
-                const int j = (XI / 4) * kk + h;
-                if (!last) load_x1(acur, s + 1, g + 1, j);
-                else if (more) load_x1(anxt, 0, g + 1, j);
-            }
+            for (int h = 0; h < XI / 4; h++)
+                if (nx) load_x1(aL, sL, g + 1, (XI / 4) * kk + h);
         });
         __syncthreads();  // every wave has decoded: the raw buffer takes the next step's weights
-        if (!last) load_w(cur, s + 1);
-        else if (more) load_w(nxt, 0);
+        if (nx) load_w(iL, aL, sL);
         TRACE(2);
 #ifdef STRATA_GEMM_ANALYZE_ROLE0
         tiles(g, NTT);
 #else
         tiles(g, (cur.cnt + 15) >> 4);
 #endif
-        if (last) store(cur);
+        if (s + 1 == nsb) store(cur);
         TRACE(3);
-        if (!last || more) store_dx(g + 1);
-        if (last) {
-            k++;
-            s = 0;
-            cur = nxt;
-            acur = anxt;
-            nxt = item_at(k + 1);
-            anxt = addr_of(nxt);
-        } else {
-            s++;
-        }
+        if (nx) store_dx(g + 1);
+        cur = iL;
+        rbeg = aL.rbeg;
+        s = sL;
+        advance();
         wait_loads();
         TRACE(4);
         __syncthreads();
