@@ -65,6 +65,7 @@ struct GemmArgs {
     int rows, cols, act;
     uint64_t rb;
     int max_tiles;        // tiles in the grid (an upper bound when the count is on the device)
+    int yvec;             // y 16-byte aligned with a row stride of a multiple of 4 floats
     int gx;               // blocks per XCD
 };
 
@@ -287,12 +288,57 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             }
         });
     };
-    // Results of an item: y[m0 + m, n0 + row] (op) acc; then the accumulators restart.
-    auto store = [&](const Item& it) __attribute__((always_inline)) {
-        const int row = it.n0 + rl, ntt = (it.cnt + 15) >> 4;
-        if (row < a.rows) {
+    // Results of an item: y[m0 + m, n0 + row] (op) acc; then the accumulators restart. With the whole row block
+    // present and y rows 16-byte aligned, the block stages its outputs through the X buffer of step g (free once every
+    // wave has run its tiles) as [128 positions][128 rows] floats, 128 positions a round, and writes whole 512-byte
+    // rows with 16-byte accesses; the stage's row index is XOR-swizzled by (position / 4) & 3 so a wave's 4 position
+    // groups write distinct banks. Otherwise each lane stores its own values.
+    auto store = [&](const Item& it, int g) __attribute__((always_inline)) {
+        const int ntt = (it.cnt + 15) >> 4;
+        if (a.yvec && it.n0 + GN <= a.rows) {
+            float* S = (float*)(xs + (g & 1) * XBUF);
+            const int c4 = 4 * (lane & 31);
+            auto put = [&](auto OP) __attribute__((always_inline)) {
+                constexpr int op = decltype(OP)::value;
+                static_for<0, 2>([&](auto R) {
+                    constexpr int r = decltype(R)::value;
+                    if (128 * r < it.cnt) {
+                        __syncthreads();  // the tiles (round 0) or the previous round's reads are done
+                        static_for<0, 8>([&](auto I) {
+                            constexpr int il = decltype(I)::value, i = 8 * r + il;
+#pragma unroll
+                            for (int q = 0; q < 4; q++) S[(16 * il + 4 * kl + q) * 128 + (rl ^ (kl << 4))] = acc[i][q];
+                        });
+                        __syncthreads();
+#pragma unroll
+                        for (int jj = 0; jj < 8; jj++) {
+                            const int pr = 16 * wave + 2 * jj + (lane >> 5), m = 128 * r + pr;
+                            if (m < it.cnt) {
+                                const float4 v = *(const float4*)(S + pr * 128 + (c4 ^ (((pr >> 2) & 3) << 4)));
+                                float4* yp = (float4*)(a.y + (int64_t)(it.m0 + m) * a.y_stride + it.n0 + c4);
+                                if constexpr (op == STRATA_ACT_STORE) {
+                                    *yp = v;
+                                } else {
+                                    float4 o = *yp;
+                                    if constexpr (op == STRATA_ACT_SWIGLU) {
+                                        o.x = silu_dev(o.x) * v.x; o.y = silu_dev(o.y) * v.y;
+                                        o.z = silu_dev(o.z) * v.z; o.w = silu_dev(o.w) * v.w;
+                                    } else {
+                                        o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+                                    }
+                                    *yp = o;
+                                }
+                            }
+                        }
+                    }
+                });
+            };
+            if (a.act == STRATA_ACT_STORE) put(std::integral_constant<int, STRATA_ACT_STORE>{});
+            else if (a.act == STRATA_ACT_SWIGLU) put(std::integral_constant<int, STRATA_ACT_SWIGLU>{});
+            else put(std::integral_constant<int, STRATA_ACT_ADD>{});
+        } else if (it.n0 + rl < a.rows) {
             // row pointer of position 4 kl; position 16 i + 4 kl + q is (16 i + q) rows further
-            float* yb = a.y + (int64_t)(it.m0 + 4 * kl) * a.y_stride + row;
+            float* yb = a.y + (int64_t)(it.m0 + 4 * kl) * a.y_stride + it.n0 + rl;
             const int left = it.cnt - 4 * kl;  // positions of this lane's column left from yb
             // the op is chosen once per item: one straight store loop per op
             auto put = [&](auto OP) __attribute__((always_inline)) {
@@ -366,7 +412,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
 #else
         tiles(g, (cur.cnt + 15) >> 4);
 #endif
-        if (s + 1 == nsb) store(cur);
+        if (s + 1 == nsb) store(cur, g);
         TRACE(3);
         if (nx) store_dx(g + 1);
         cur = iL;
@@ -393,6 +439,7 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
     a.tiles = g.tiles; a.n_tiles_dev = g.n_tiles_dev; a.dense_w = g.dense_w; a.dense_n = g.dense_n;
     a.xq = (const int8_t*)g.xq; a.xd = (const float*)(g.xq + (uint64_t)g.n_x * g.cols);
     a.xrow = g.xrow; a.y = g.y; a.y_stride = g.y_stride; a.rows = g.rows; a.cols = g.cols; a.act = g.act;
+    a.yvec = ((uintptr_t)g.y % 16 == 0) && (g.y_stride % 4 == 0);
     a.rb = row_bytes(T, g.cols);
     const size_t smem = gemm_smem<T>();
     static bool attr = false;

@@ -323,8 +323,9 @@ def tile_list(hip, base, stride, spans):
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
 def test_gemm_tiles_match_cpu(hip, ty):
     """tests/kernels.rs:355-447: tiles (0, 128), (128, 16), (144, 26) with X gathered through xrow; act store, then
-    SwiGLU into the stored gate, then add. Tiles (170, 256) and (426, 200) fill this backend's 256-position blocks."""
-    rows, cols, E, n_x = 80, 512, 3, 100
+    SwiGLU into the stored gate, then add. Tiles (170, 256) and (426, 200) fill this backend's 256-position blocks;
+    200 rows give one whole 128-row block (outputs staged through LDS) and a partial one (stored lane by lane)."""
+    rows, cols, E, n_x = 200, 512, 3, 100
     rb = ggml.row_bytes(ty, cols)
     w = random_blocks(ty, E * rows, cols, seed=ty)
     wb = up(hip, w)
