@@ -11,6 +11,7 @@
 
 #include "sbdot.h"
 #include "kernels.h"
+#include "xlane.h"
 #include "../../include/strata_hip.h"
 
 namespace strata {
@@ -233,12 +234,19 @@ __device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, flo
             int bi = i;
 #pragma unroll
             for (int j = 1; j < 8; j++) if (fabsf(v[j]) > fabsf(bv)) { bv = v[j]; bi = i + j; }
-#pragma unroll
-            for (int o = 1; o < 32; o <<= 1) {
-                const float ov = __shfl_xor(bv, o, 32);
-                const int oi = __shfl_xor(bi, o, 32);
+            // the first value of largest magnitude over the 32 lanes: the choice is unique, so the pairing of the
+            // exchange steps does not matter
+            auto step = [&](auto S) __attribute__((always_inline)) {
+                constexpr int st = decltype(S)::value;
+                const float ov = xl32f<st>(bv);
+                const int oi = xl32<st>(bi);
                 if (fabsf(ov) > fabsf(bv) || (fabsf(ov) == fabsf(bv) && oi < bi)) { bv = ov; bi = oi; }
-            }
+            };
+            step(std::integral_constant<int, 0>{});
+            step(std::integral_constant<int, 1>{});
+            step(std::integral_constant<int, 2>{});
+            step(std::integral_constant<int, 3>{});
+            step(std::integral_constant<int, 4>{});
             const float is = bv != 0.0f ? -127.0f / bv : 0.0f;
             dd = bv != 0.0f ? 1.0f / is : 0.0f;
             mul = is;
@@ -246,8 +254,8 @@ __device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, flo
             float mx = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
-            mx = fmaxf(mx, __shfl_xor(mx, 1, 32));
-            mx = fmaxf(mx, __shfl_xor(mx, 2, 32));
+            mx = fmaxf(mx, xl32f<0>(mx));
+            mx = fmaxf(mx, xl32f<1>(mx));
             dd = mx / 127.0f;
             mul = mx > 0.0f ? 127.0f / mx : 0.0f;
         }

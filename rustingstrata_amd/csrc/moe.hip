@@ -1,5 +1,6 @@
 // MoE routing, the stable sort of (token, expert) pairs with its tile lists, and the combines.
 #include "moe.h"
+#include "xlane.h"
 
 namespace strata {
 
@@ -39,8 +40,20 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        // one lane adds in index order (the reference's sum), reading 4 values per LDS access
         float s = 0.0f;
-        if (lane == 0) for (int i = 0; i < n; i++) s += se[wave][i];
+        if (lane == 0) {
+            int i = 0;
+#pragma unroll 4
+            for (; i + 4 <= n; i += 4) {
+                const float4 q = *(const float4*)&se[wave][i];
+                s += q.x;
+                s += q.y;
+                s += q.z;
+                s += q.w;
+            }
+            for (; i < n; i++) s += se[wave][i];
+        }
         s = __shfl(s, 0);
 #pragma unroll
         for (int r = 0; r < ROUTE_R; r++) v[r] = v[r] / s;
@@ -60,10 +73,23 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
                 if (key > best) best = key;
             }
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            uint64_t other = __shfl_xor(best, o);
+        // the largest key within each 32 lanes (DPP and swizzle steps), then the larger of the two halves
+        auto step = [&](auto S) __attribute__((always_inline)) {
+            constexpr int st = decltype(S)::value;
+            const uint64_t other = (uint64_t)(uint32_t)xl32<st>((int)(best >> 32)) << 32 | (uint32_t)xl32<st>((int)best);
             best = other > best ? other : best;
+        };
+        step(std::integral_constant<int, 0>{});
+        step(std::integral_constant<int, 1>{});
+        step(std::integral_constant<int, 2>{});
+        step(std::integral_constant<int, 3>{});
+        step(std::integral_constant<int, 4>{});
+        {
+            const uint64_t b0 = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(best >> 32), 0) << 32 |
+                                (uint32_t)__builtin_amdgcn_readlane((int)best, 0);
+            const uint64_t b1 = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(best >> 32), 32) << 32 |
+                                (uint32_t)__builtin_amdgcn_readlane((int)best, 32);
+            best = b0 > b1 ? b0 : b1;
         }
         int bi = (int)~(uint32_t)best;
         float bv = __uint_as_float((uint32_t)(best >> 32) - 1u);
@@ -104,8 +130,20 @@ __global__ __launch_bounds__(256) void combine_kernel(float* x, const float* ye,
     int tk = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     x += (uint64_t)tk * n; ye += (uint64_t)tk * k * n; w += (uint64_t)tk * k;
+    // 8 slots' loads at a time, then their products in slot order (a slot with weight 0 may hold anything; its
+    // product is not added)
     float y = 0.0f;
-    for (int j = 0; j < k; j++) if (w[j] != 0.0f) y += w[j] * ye[(uint64_t)j * n + i];
+    for (int j0 = 0; j0 < k; j0 += 8) {
+        float wv[8], yv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u < k ? j0 + u : k - 1;
+            wv[u] = j0 + u < k ? w[j] : 0.0f;
+            yv[u] = ye[(uint64_t)j * n + i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) if (wv[u] != 0.0f) y += wv[u] * yv[u];
+    }
     if (sh) y += (sg ? sigmoid_f32(sg[tk]) : 1.0f) * sh[(uint64_t)tk * n + i];
     x[i] += y;
 }
@@ -122,10 +160,21 @@ __global__ __launch_bounds__(256) void combine_seq_kernel(float* x, const float*
                                                           int k, const float* sh, const float* sg, int n) {
     int t = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
     if (d >= n) return;
+    // 8 pairs' loads at a time (their slots, then their ye rows), then the products in pair order
     float y = 0.0f;
-    for (int j = 0; j < k; j++) {
-        int s = inv[t * k + j];
-        if (s >= 0) y += wts[t * k + j] * ye[(uint64_t)s * n + d];
+    for (int j0 = 0; j0 < k; j0 += 8) {
+        int sv[8];
+        float wv[8], yv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u < k ? j0 + u : k - 1;
+            sv[u] = j0 + u < k ? inv[t * k + j] : -1;
+            wv[u] = wts[t * k + j];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) yv[u] = ye[(uint64_t)(sv[u] >= 0 ? sv[u] : 0) * n + d];
+#pragma unroll
+        for (int u = 0; u < 8; u++) if (sv[u] >= 0) y += wv[u] * yv[u];
     }
     uint64_t i = (uint64_t)t * n + d;
     if (sh) y += (sg ? sigmoid_f32(sg[t]) : 1.0f) * sh[i];

@@ -1,6 +1,7 @@
 // Dequantization (the Backend::dequant test op) and activation quantization (Backend::quant_xq).
 #include "formats.h"
 #include "kernels.h"
+#include "xlane.h"
 #include "moe.h"
 #include "../../include/strata_hip.h"
 
@@ -83,12 +84,19 @@ __global__ __launch_bounds__(256) void quant_xq_kernel(const float* __restrict__
         int bi = i;
 #pragma unroll
         for (int j = 1; j < 8; j++) if (fabsf(v[j]) > fabsf(bv)) { bv = v[j]; bi = i + j; }
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) {
-            float ov = __shfl_xor(bv, o, 32);
-            int oi = __shfl_xor(bi, o, 32);
-            if (fabsf(ov) > fabsf(bv) || (fabsf(ov) == fabsf(bv) && oi < bi)) { bv = ov; bi = oi; }
-        }
+            // the first value of largest magnitude over the 32 lanes: the choice is unique, so the pairing of the
+            // exchange steps does not matter
+            auto step = [&](auto S) __attribute__((always_inline)) {
+                constexpr int st = decltype(S)::value;
+                const float ov = xl32f<st>(bv);
+                const int oi = xl32<st>(bi);
+                if (fabsf(ov) > fabsf(bv) || (fabsf(ov) == fabsf(bv) && oi < bi)) { bv = ov; bi = oi; }
+            };
+            step(std::integral_constant<int, 0>{});
+            step(std::integral_constant<int, 1>{});
+            step(std::integral_constant<int, 2>{});
+            step(std::integral_constant<int, 3>{});
+            step(std::integral_constant<int, 4>{});
         float is = bv != 0.0f ? -127.0f / bv : 0.0f;
         d = bv != 0.0f ? 1.0f / is : 0.0f;
         mul = is;
@@ -96,8 +104,8 @@ __global__ __launch_bounds__(256) void quant_xq_kernel(const float* __restrict__
         float mx = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
-        mx = fmaxf(mx, __shfl_xor(mx, 1, 32));
-        mx = fmaxf(mx, __shfl_xor(mx, 2, 32));
+        mx = fmaxf(mx, xl32f<0>(mx));
+        mx = fmaxf(mx, xl32f<1>(mx));
         d = mx / 127.0f;
         mul = mx > 0.0f ? 127.0f / mx : 0.0f;
     }
