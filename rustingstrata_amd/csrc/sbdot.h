@@ -2,6 +2,7 @@
 // LDS) against the same 256 values of x (int8 in LDS, Q8_K numerics: one x scale per super-block), accumulating
 // exactly in int32, and closes it with one float step
 //     acc += dx * (D * sum_g sc_g * (q_g . x_g - bias * sum x_g) - M * sum_g m_g * sum x_g).
+// Integer products of a group scale (|sc| < 2^8) and a group sum (|s| < 2^18) use 24-bit multiplies.
 // This is the structure of the reference CPU dots (src/cpu_moe.rs:319-377: exact integer group sums, then
 // d_w * d_x * s - dmin * d_x * m in f32).
 #pragma once
@@ -48,6 +49,8 @@ __device__ __forceinline__ int dot4w(uint32_t a, uint32_t b, uint32_t c, uint32_
     acc = sdot4((int)c, (int)x.z, acc);
     return sdot4((int)d, (int)x.w, acc);
 }
+// v << n for n >= 0, v >> -n otherwise: one shift once n is a constant (the callers' loops unroll fully).
+__device__ __forceinline__ uint32_t shl_by(uint32_t v, int n) { return n >= 0 ? v << n : v >> -n; }
 // n words from a 2-byte-aligned LDS address: aligned reads, shifted into place (v_alignbyte_b32).
 template <int N>
 __device__ __forceinline__ void words_a2(const uint8_t* p, uint32_t* out) {
@@ -91,20 +94,21 @@ __device__ __forceinline__ void sb_q45(const uint8_t* b, const X& x, int& isum, 
             uint32_t qh[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                lo[i] |= ((qh[i] >> (2 * p)) << 4) & 0x10101010u;
-                hi[i] |= ((qh[i] >> (2 * p + 1)) << 4) & 0x10101010u;
+                // bit 2p (2p + 1) of each qh byte to bit 4: one shift by a constant, then the mask
+                lo[i] |= shl_by(qh[i], 4 - 2 * p) & 0x10101010u;
+                hi[i] |= shl_by(qh[i], 3 - 2 * p) & 0x10101010u;
             }
         }
         const int s_lo = dot16(lo, x.q16(64 * p), x.q16(64 * p + 16));
         const int s_hi = dot16(hi, x.q16(64 * p + 32), x.q16(64 * p + 48));
         const uint32_t scw = p < 2 ? sc_lo : sc_hi;
-        is += (int)byte_of(scw, (2 * p) & 3) * s_lo + (int)byte_of(scw, (2 * p + 1) & 3) * s_hi;
+        is += __mul24((int)byte_of(scw, (2 * p) & 3), s_lo) + __mul24((int)byte_of(scw, (2 * p + 1) & 3), s_hi);
     }
     isum = is;
     // min term: sum_j m_j * (sum of x over sub-block j)
     int ms = 0;
 #pragma unroll
-    for (int j = 0; j < 8; j++) ms += (int)byte_of(j < 4 ? m_lo : m_hi, j & 3) * (x.s(2 * j) + x.s(2 * j + 1));
+    for (int j = 0; j < 8; j++) ms += __mul24((int)byte_of(j < 4 ? m_lo : m_hi, j & 3), x.s(2 * j) + x.s(2 * j + 1));
     msum = ms;
 }
 
@@ -131,12 +135,12 @@ __device__ __forceinline__ void sb_q6(const uint8_t* b, const X& x, int& isum, f
                     const int wi = 4 * a + i;
                     const uint32_t q = ql[(qd & 1 ? 8 : 0) + wi], hb = qh[wi];
                     const uint32_t nib = qd & 2 ? (q >> 4) & 0x0F0F0F0Fu : q & 0x0F0F0F0Fu;
-                    v[i] = nib | (((hb >> (2 * qd)) << 4) & 0x30303030u);  // q + 32, in 0..63
+                    v[i] = nib | (shl_by(hb, 4 - 2 * qd) & 0x30303030u);  // q + 32, in 0..63
                 }
                 const int xo = 128 * n + 32 * qd + 16 * a;
                 const int s = dot4w(v[0], v[1], v[2], v[3], x.q16(xo)) - 32 * x.s(xo >> 4);
                 const int g = 8 * n + a + 2 * qd;  // scale index: l / 16 + 2 qd within the half
-                is += sbyte_of(sc[g >> 2], g & 3) * s;
+                is += __mul24(sbyte_of(sc[g >> 2], g & 3), s);
             }
     }
     isum = is;
@@ -172,8 +176,8 @@ __device__ __forceinline__ void sb_generic(const uint8_t* b, const X& x, const I
         int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x.q16(t.o0)), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x.q16(t.o1));
         const int a0 = x.s(t.o0 >> 4), a1 = x.s(t.o1 >> 4);
         if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * a0; s1 -= Fmt<T>::BIAS * a1; }
-        is += t.sc0 * s0 + t.sc1 * s1;
-        if constexpr (Fmt<T>::MIN) ms += t.m0 * a0 + t.m1 * a1;
+        is += __mul24(t.sc0, s0) + __mul24(t.sc1, s1);
+        if constexpr (Fmt<T>::MIN) ms += __mul24(t.m0, a0) + __mul24(t.m1, a1);
         if (k == 0) { D = t.D; M = t.M; }
     }
     isum = is;
@@ -219,8 +223,8 @@ __device__ __forceinline__ float sb_dot_q32(const uint8_t* b, const X& x, const 
         int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x.q16(t.o0)), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x.q16(t.o1));
         const int a0 = x.s(t.o0 >> 4), a1 = x.s(t.o1 >> 4);
         if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * a0; s1 -= Fmt<T>::BIAS * a1; }
-        float f0 = t.D * (float)(t.sc0 * s0), f1 = t.D * (float)(t.sc1 * s1);
-        if constexpr (Fmt<T>::MIN) { f0 -= t.M * (float)(t.m0 * a0); f1 -= t.M * (float)(t.m1 * a1); }
+        float f0 = t.D * (float)__mul24(t.sc0, s0), f1 = t.D * (float)__mul24(t.sc1, s1);
+        if constexpr (Fmt<T>::MIN) { f0 -= t.M * (float)__mul24(t.m0, a0); f1 -= t.M * (float)__mul24(t.m1, a1); }
         f += x.d(t.o0 >> 5) * f0 + x.d(t.o1 >> 5) * f1;
     }
     return f;
