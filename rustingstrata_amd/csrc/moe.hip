@@ -31,8 +31,13 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
         float m = -INFINITY;
 #pragma unroll
         for (int r = 0; r < ROUTE_R; r++) m = fmaxf(m, v[r]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = fmaxf(m, xl32f<0>(m));
+        m = fmaxf(m, xl32f<1>(m));
+        m = fmaxf(m, xl32f<2>(m));
+        m = fmaxf(m, xl32f<3>(m));
+        m = fmaxf(m, xl32f<4>(m));
+        m = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
+                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)));
 #pragma unroll
         for (int r = 0; r < ROUTE_R; r++) {
             int i = lane + 64 * r;
@@ -98,7 +103,7 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
     }
     // Weights: p / max(sum of the top k in rank order, 2^-14) (times extra_scale when not 0).
     float sum = 0.0f;
-    for (int j = 0; j < k; j++) sum += __shfl(my_p, j);
+    for (int j = 0; j < k; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), j));
     float scale = 1.0f / fmaxf(sum, 6.103515625e-5f);
     if (extra_scale != 0.0f) scale *= extra_scale;
     if (lane < k) {
