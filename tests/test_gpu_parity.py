@@ -72,6 +72,25 @@ def test_quant_xq_q8k_bit_exact(hip, n, nt):
         assert np.array_equal(sc[t].view(np.uint32), np.repeat(d, 8)[: n // 32].view(np.uint32))
 
 
+def test_quant_xq_q8k_magnitude_tie(hip):
+    """Equal largest magnitudes of opposite sign in one 256-block, in different 16-lane rows: the first one sets the
+    scale's sign (src/cpu_moe.rs:28-46), whatever order the lanes compare in."""
+    n = 512
+    x = normal((1, n), seed=9) * 0.1
+    x[0, 200] = 7.0
+    x[0, 60] = -7.0
+    x[0, 300] = 3.0
+    x[0, 511] = -3.0
+    xb = up(hip, x)
+    out = hip.alloc(n + n // 8)
+    hip.quant_xq(xb, n, n, 1, out)
+    raw = down(hip, out, np.uint8, n + n // 8)
+    d, qs, _ = O.quantize_q8k(x[0])
+    assert np.array_equal(raw[:n].view(np.int8), qs.reshape(-1)[:n])
+    assert np.array_equal(raw[n:].view(np.float32).view(np.uint32), np.repeat(d, 8)[: n // 32].view(np.uint32))
+    assert raw[n:].view(np.float32)[0] > 0  # -127 / (-7): the negative value came first
+
+
 def test_quant_xq_per32_bit_exact(hip):
     n, nt = 1024, 2
     x = normal((nt, n), seed=5)
@@ -202,8 +221,13 @@ def test_router_topk_matches_route(hip):
     x[n + 7] = 9.0
     x[n + 200] = 9.0
     x[2 * n + 30] = x[2 * n + 31] = x[2 * n + 255] = 5.0
+    # the widest case (512 experts, top 32) with equal maxima in both 32-lane halves and past lane 64 (index 5 wins)
+    wide = zipf_logits(6, 512, seed=3)
+    wide[0, 5] = wide[0, 40] = wide[0, 300] = 20.0
+    wide[1, 63] = wide[1, 64] = 20.0
     for logits, kk, scale, sig in [(x.reshape(t, n), k, 2.5, False), (zipf_logits(512, 128, seed=1), 8, 0.0, False),
-                                   (zipf_logits(64, 17, seed=2), 4, 1.5, True)]:
+                                   (zipf_logits(64, 17, seed=2), 4, 1.5, True), (wide, 32, 0.0, False),
+                                   (wide, 32, 0.0, True)]:
         tt, nn = logits.shape
         ids, wts = hip.alloc(tt * kk * 4), hip.alloc(tt * kk * 4)
         hip.router_topk(up(hip, logits), nn, kk, scale, ids, wts, tt, sig)
