@@ -242,6 +242,81 @@ def bench_moe_decode(hip, S, ggml, iters):
             "pct_peak": round(100 * bts / us / 1e3 / HBM_PEAK_GBS, 1)}
 
 
+def codebook_blocks(ggml, ty, rows, cols, seed):
+    """configs[3] weights: grid indices, sign bits and sub-block scales uniform from a seed (random block bytes), with
+    each block's f16 d set to 2^-6 so every value is finite."""
+    rng = np.random.default_rng(seed)
+    bb = ggml.block_bytes(ty)
+    nb = rows * cols // 256
+    blk = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    blk[:, 0:2] = np.frombuffer(np.float16(2.0 ** -6).tobytes(), dtype=np.uint8)
+    return blk.reshape(rows, -1)
+
+
+def bench_codebook(hip, S, ggml, iters):
+    """IQ2_XXS / IQ3_S / IQ4_XS experts of 2048 x 768 (out x in), 128 experts.
+    T = 1: moe_gemv over 8 Zipf-routed experts, the 128 experts rotated over copies past 512 MB (GB/s of the 8 experts'
+    bytes). T = 512: route -> device sort -> grouped GEMM over the 128 experts (int8 TOP/s on routed pairs)."""
+    E, rows, cols, k = 128, 2048, 768, 8
+    out = {}
+    for ty in (ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS):
+        name = ggml.NAMES[ty]
+        rb = ggml.row_bytes(ty, cols)
+        uniq = 16
+        blk = codebook_blocks(ggml, ty, uniq * rows, cols, seed=300 + ty)
+        one = E * rows * rb
+        ncopy = max(2, -(-ROTATE_BYTES // one) + 1)
+        pool = hip.alloc(ncopy * one)
+        base = hip.upload(np.tile(blk, (E // uniq, 1)))
+        for c in range(ncopy):
+            hip.dtod(base, 0, pool, c * one, one)
+        rng = np.random.default_rng(400 + ty)
+        # T = 1
+        x = hip.upload(rng.standard_normal(cols).astype(np.float32))
+        y = hip.alloc(k * rows * 4)
+        sel = [hip.upload(rng.choice(E, k, replace=False).astype(np.int32)) for _ in range(8)]
+        call = lambda i: hip.moe_gemv(ty, rows, cols, int(pool) + (i % ncopy) * one, rows * rb, sel[i % 8], k, x, cols, k, y)
+        for i in range(20):
+            call(i)
+        hip.sync()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0)
+        for i in range(iters):
+            call(i)
+        hip.record(e1)
+        us = 1000 * hip.elapsed_ms(e0, e1) / iters
+        bts = k * rows * rb
+        # T = 512
+        T = 512
+        perm = rng.permutation(E) + 1
+        logits = (rng.standard_normal((T, E)) + 8.0 * perm.astype(np.float64) ** -1.1).astype(np.float32)
+        lb, hb = hip.upload(logits), hip.upload(rng.standard_normal((T, cols)).astype(np.float32))
+        ids, wts = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
+        chunk = hip.gemm_block_positions()
+        max_tiles = T * k // chunk + E
+        off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
+        tiles, ntd = hip.alloc(max_tiles * 16), hip.alloc(4)
+        ye = hip.alloc(T * k * rows * 4)
+        hip.router_topk(lb, E, k, 0.0, ids, wts, T)
+        gemm_ms = 0.0
+        for i in range(iters // 4 + 3):
+            c = i % ncopy
+            hip.moe_sort(ids, T, k, E, off, xrow, inv, [(int(pool) + c * one, rows * rb)], tiles, max_tiles, ntd, chunk=chunk)
+            e0, e1 = hip.event(), hip.event()
+            hip.record(e0)
+            hip.gemm_grouped(ty, rows, cols, tiles, max_tiles, ntd, hb, cols, T, xrow, ye, rows, S.ACT_STORE)
+            hip.record(e1)
+            if i >= 3:
+                gemm_ms += hip.elapsed_ms(e0, e1)
+        gemm_ms /= iters // 4
+        ops = T * k * rows * cols * 2
+        out[name] = {"decode_us": round(us, 2), "decode_GB/s": round(bts / us / 1e3, 1),
+                     "decode_pct_peak": round(100 * bts / us / 1e3 / HBM_PEAK_GBS, 1),
+                     "prefill512_gemm_ms": round(gemm_ms, 4), "prefill512_int8_TOPS": round(ops / (gemm_ms / 1e3) / 1e12, 1)}
+        hip.drop_graphs()
+    return out
+
+
 def cpu_baseline(shapes, budget_s=12.0):
     """The oracle's C restatement of cpu_moe::matvec (Q8_K activations, scalar dots compiled with gcc -O3
     -march=x86-64-v3, threads over 32-row chunks like rayon's par_chunks_mut(32)) over the same GEMV sweep."""
@@ -335,6 +410,8 @@ def main():
         extra["moe_prefill_512"] = bench_moe(hip, S, ggml, 512, args.moe_iters)
         extra["moe_decode_1"] = bench_moe_decode(hip, S, ggml, 200)
         log(f"[bench] MoE decode: {extra['moe_decode_1']}")
+        extra["codebook_experts"] = bench_codebook(hip, S, ggml, 100)
+        log(f"[bench] configs[3] codebook experts: {extra['codebook_experts']}")
     cpu = None if args.no_cpu else cpu_baseline(shapes)
     out = {
         "metric": "Q-GEMV achieved HBM GB/s (% peak); MoE grouped-GEMM prefill tok/s at 4K",
