@@ -404,6 +404,16 @@ def main():
     roof = roofline_q4k_lmhead(hip, shapes, xb, yb)
     log(f"[bench] Q4_K lm head: {roof['achieved']} GB/s ({100 * roof['frac']:.1f}% of peak)")
     extra = {}
+    # configs[0] on the GPU: Q4_K 4096 x 4096 (9.47 MB), rotated copies, graph replays
+    b1 = synth_weights(S, ggml, ggml.Q4_K, 4096, 4096, seed=999)
+    r1 = Rotated(hip, S, ggml.Q4_K, b1, 4096, 4096)
+    x1, y1 = hip.upload(np.random.default_rng(8).standard_normal(4096).astype(np.float32)), hip.alloc(4096 * 4)
+    us1 = 1000 * time_gemv(hip, r1, x1, y1, 400)
+    by1 = b1.nbytes + 4 * 4096 * 2
+    extra["config0_q4k_4096x4096"] = {"us": round(us1, 2), "GB/s": round(by1 / us1 / 1e3, 1),
+                                      "pct_peak": round(100 * by1 / us1 / 1e3 / HBM_PEAK_GBS, 1)}
+    hip.drop_graphs()
+    log(f"[bench] configs[0] Q4_K 4096x4096: {extra['config0_q4k_4096x4096']}")
     if not args.no_moe:
         extra["moe_prefill_4k"] = bench_moe(hip, S, ggml, 4096, args.moe_iters)
         log(f"[bench] MoE prefill 4K: {extra['moe_prefill_4k']}")
