@@ -472,10 +472,115 @@ extern "C" int strata_debug_gemm_trace(uint64_t* out) {
 }
 #endif
 
+// ---- Q8_0 (src/cuda/kernels.cu:380-388): blocks of 32 int8 values, each with its own f16 scale ----
+// The block scales are floats that differ within a super-block, so they cannot fold into integer planes; instead one
+// K=64 MFMA step yields the two blocks' int32 sums separately (lanes 0-31 of the weight operand carry the first
+// block's values and zeros for the second, lanes 32-63 the reverse: two MFMAs per step, no extra MFMA work), and each
+// block closes in float at once: acc += dx (d0 s0 + d1 s1). A block of 4 waves takes a 64-row block of one tile and
+// walks the tile's positions 64 at a time; wave w owns rows 16 w .. 16 w + 15.
+constexpr int Q8_ROWS = 64, Q8_POS = 64, Q8_SB = 272, Q8_RP = 280;  // rows, positions per pass, bytes per 256 values, LDS row pitch
+
+__global__ __launch_bounds__(256) void gemm_q8_0_kernel(GemmArgs a) {
+    __shared__ __align__(16) int8_t xs8[Q8_POS * 256];
+    __shared__ __align__(16) uint8_t ws8[Q8_ROWS * Q8_RP];
+    __shared__ float dx8[Q8_POS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, kl = lane >> 4, aswz = lane & 15;
+    const int ntiles = a.n_tiles_dev ? min(sload(a.n_tiles_dev), a.max_tiles) : a.max_tiles;
+    const int tile = blockIdx.y, n0 = blockIdx.x * Q8_ROWS;
+    if (tile >= ntiles) return;
+    uint64_t w;
+    int m0, cnt;
+    if (a.tiles) {
+        const uint64_t t0 = sload(a.tiles + 2 * tile), t1 = sload(a.tiles + 2 * tile + 1);
+        w = t0;
+        m0 = (int)(uint32_t)t1;
+        cnt = min(GM, (int)(t1 >> 32));
+    } else {
+        w = (uint64_t)a.dense_w;
+        m0 = GM * tile;
+        cnt = min(GM, a.dense_n - m0);
+    }
+    const int cols = a.cols, nsb = cols / 256, rl = 16 * wave + (lane & 15);
+    auto xrow_of = [&](int p) { p = p < cnt ? p : 0; return a.xrow ? a.xrow[m0 + p] : m0 + p; };
+    for (int p0 = 0; p0 < cnt; p0 += Q8_POS) {
+        float acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
+        for (int sb = 0; sb < nsb; sb++) {
+            __syncthreads();  // the previous step's readers are done
+            // X: 64 positions x 256 bytes, 16-byte chunk c of position p at chunk c ^ (p & 15)
+            for (int c = tid; c < Q8_POS * 16; c += 256) {
+                const int p = c >> 4, ch = c & 15;
+                const uint32_t xr = (uint32_t)xrow_of(p0 + p);
+                *(v4i*)(xs8 + p * 256 + 16 * (ch ^ (p & 15))) = *gptr<v4i>((uint64_t)(a.xq + (uint64_t)xr * cols + 256 * sb + 16 * ch));
+            }
+            if (tid < Q8_POS) dx8[tid] = *gptr<float>((uint64_t)(a.xd + (uint64_t)xrow_of(p0 + tid) * (cols / 32) + 8 * sb));
+            // weights: each row's 272 bytes of the step from their 4-byte-aligned cover (rows past `rows` read the last)
+            for (int c = tid; c < Q8_ROWS * (Q8_RP / 4); c += 256) {
+                const int r = c / (Q8_RP / 4), j = c % (Q8_RP / 4);
+                const uint64_t beg = w + (uint64_t)min(n0 + r, a.rows - 1) * a.rb + (uint64_t)sb * Q8_SB;
+                const uint64_t a4 = beg & ~(uint64_t)3;
+                if (a4 + 4 * (uint64_t)j < beg + Q8_SB) *(uint32_t*)(ws8 + r * Q8_RP + 4 * j) = *gptr<uint32_t>(a4 + 4 * (uint64_t)j);
+            }
+            __syncthreads();
+            const uint64_t rbeg = w + (uint64_t)min(n0 + rl, a.rows - 1) * a.rb + (uint64_t)sb * Q8_SB;
+            const uint8_t* wr = ws8 + rl * Q8_RP + (uint32_t)(rbeg & 3);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                // this lane's 16 values: block 2 kk + kl / 2, values 16 (kl & 1) ..
+                uint32_t qv[4];
+                words_a2<4>(wr + 34 * (2 * kk + (kl >> 1)) + 2 + 16 * (kl & 1), qv);
+                const v4i qw = {(int)qv[0], (int)qv[1], (int)qv[2], (int)qv[3]}, z = {0, 0, 0, 0};
+                const v4i b0 = kl < 2 ? qw : z, b1 = kl < 2 ? z : qw;
+                const float d0 = h16(wr + 34 * (2 * kk)), d1 = h16(wr + 34 * (2 * kk + 1));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const v4i av = *(const v4i*)(xs8 + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
+                    const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b0, z, 0, 0, 0);
+                    const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b1, z, 0, 0, 0);
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        acc[i][q] = __builtin_fmaf(dx8[16 * i + 4 * kl + q], __builtin_fmaf(d0, (float)c0[q], d1 * (float)c1[q]), acc[i][q]);
+                }
+            }
+        }
+        // outputs: weight row n0 + rl, positions p0 + 16 i + 4 kl + q
+        if (n0 + rl < a.rows) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int m = p0 + 16 * i + 4 * kl + q;
+                    if (m < cnt) {
+                        float* yp = a.y + (int64_t)(m0 + m) * a.y_stride + n0 + rl;
+                        if (a.act == STRATA_ACT_STORE) *yp = acc[i][q];
+                        else if (a.act == STRATA_ACT_SWIGLU) *yp = silu_dev(*yp) * acc[i][q];
+                        else *yp += acc[i][q];
+                    }
+                }
+        }
+    }
+}
+
+static hipError_t gemm_q8_0(const GemmLaunch& g, hipStream_t s) {
+    GemmArgs a{};
+    a.tiles = g.tiles; a.n_tiles_dev = g.n_tiles_dev; a.dense_w = g.dense_w; a.dense_n = g.dense_n;
+    a.xq = (const int8_t*)g.xq; a.xd = (const float*)(g.xq + (uint64_t)g.n_x * g.cols);
+    a.xrow = g.xrow; a.y = g.y; a.y_stride = g.y_stride; a.rows = g.rows; a.cols = g.cols; a.act = g.act;
+    a.rb = row_bytes(Q8_0, g.cols);
+    a.max_tiles = g.n_tiles;
+    if (g.n_tiles > 65535) return hipErrorInvalidValue;
+    gemm_q8_0_kernel<<<dim3((unsigned)((g.rows + Q8_ROWS - 1) / Q8_ROWS), (unsigned)g.n_tiles), 256, 0, s>>>(a);
+    return hipGetLastError();
+}
+
 uint64_t gemm_block_positions() { return GM; }
 
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t s) {
     switch (g.ty) {
+    case Q8_0: return gemm_q8_0(g, s);
     case Q2_K: return gemm_t<Q2_K>(g, s);
     case Q3_K: return gemm_t<Q3_K>(g, s);
     case Q4_K: return gemm_t<Q4_K>(g, s);

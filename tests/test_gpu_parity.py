@@ -344,7 +344,8 @@ def tile_list(hip, base, stride, spans):
     return up(hip, t), len(spans)
 
 
-@pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
+@pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K,
+                                ggml.Q8_0])
 def test_gemm_tiles_match_cpu(hip, ty):
     """tests/kernels.rs:355-447: tiles (0, 128), (128, 16), (144, 26) with X gathered through xrow; act store, then
     SwiGLU into the stored gate, then add. Tiles (170, 256) and (426, 200) fill this backend's 256-position blocks;
@@ -378,8 +379,9 @@ def test_gemm_tiles_match_cpu(hip, ty):
     assert max_rel_err(got3, want2 + want) <= 2 * TOL
 
 
-def test_gemm_dense(hip):
-    ty, rows, cols, n = ggml.Q5_K, 200, 1024, 300
+@pytest.mark.parametrize("ty", [ggml.Q5_K, ggml.Q8_0])
+def test_gemm_dense(hip, ty):
+    rows, cols, n = 200, 1024, 300
     w = random_blocks(ty, rows, cols, seed=8)
     t = hip.upload_tensor(ty, w)
     x = normal((n, cols), seed=9)
