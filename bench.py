@@ -332,9 +332,37 @@ def cpu_baseline(shapes, budget_s=12.0):
         if time.time() - t0 >= budget_s:
             break
     dt = time.time() - t0
-    return {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} pass(es) of the full 12-GEMV sweep in {dt:.1f} s with {threads} threads "
-                      "(C restatement of cpu_moe::matvec)"}
+    out = {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"{reps} pass(es) of the full 12-GEMV sweep in {dt:.1f} s with {threads} threads "
+                     "(C restatement of cpu_moe::matvec)"}
+    # one thread (tests/cpu_moe.rs:50-66 report both): the 6144-row shapes, about 2 s
+    small = [s for s in shapes if s["rows"] == 6144]
+    t0, nbytes = time.time(), 0
+    while time.time() - t0 < 2.0:
+        for s in small:
+            O.matvec(s["ty"], s["host"], s["rows"], s["cols"], x, threads=1)
+            nbytes += s["bytes"]
+    out["one_thread_GB/s"] = round(nbytes / (time.time() - t0) / 1e9, 2)
+    # configs[2] on the CPU: cpu_moe::experts_multi over 64 tokens of the MoE layer (E=128, top-8, Q5_K gate/up,
+    # Q6_K down; 16 distinct experts repeated), about 3-6 s
+    E, H, F, k, T = 128, 2048, 768, 8, 64
+    rng = np.random.default_rng(13)
+    import rustingstrata_amd as S
+    from rustingstrata_amd import ggml
+    uniq = 16
+    gate = np.tile(S.quantize_rows(ggml.Q5_K, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32)), (E // uniq, 1))
+    up = np.tile(S.quantize_rows(ggml.Q5_K, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32)), (E // uniq, 1))
+    dn = np.tile(S.quantize_rows(ggml.Q6_K, (rng.standard_normal((uniq * H, F)) * 0.02).astype(np.float32)), (E // uniq, 1))
+    perm = rng.permutation(E) + 1
+    logits = (rng.standard_normal((T, E)) + 8.0 * perm.astype(np.float64) ** -1.1).astype(np.float32)
+    hs = rng.standard_normal((T, H)).astype(np.float32)
+    ids, wts = O.route(logits, k)
+    t0 = time.time()
+    O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, up, dn, H, F, hs, ids, wts, threads=threads)
+    dt = time.time() - t0
+    out["moe_layer"] = {"tok_per_s": round(T / dt, 1), "ms_per_token": round(1000 * dt / T, 3), "tokens": T,
+                        "cores": threads, "sample": "cpu_moe::experts_multi restated in C, 64 tokens of configs[2]"}
+    return out
 
 
 def roofline_q4k_lmhead(hip, shapes, xb, yb, iters=400):
