@@ -127,6 +127,15 @@ int strata_router_topk(strata_ctx* ctx, uint64_t p, uint64_t n, uint64_t k, floa
  * wts[j] on a hit, else 0. */
 int strata_moe_route(strata_ctx* ctx, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t table,
                      uint64_t ids, uint64_t wts, uint64_t slots, uint64_t wh, uint64_t t, int sigmoid);
+/* Backend::rms_norm (src/backend.rs:232; ops::rms_norm src/ops.rs:3-7; kernel src/cuda/kernels.cu:1504-1550): `rows`
+ * rows (x_stride, out_stride in floats), out[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * w; out may be x. */
+int strata_rms_norm(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t out_stride,
+                    uint64_t n, uint64_t rows, float eps);
+/* Backend::rms_norm_q (src/backend.rs:233-235): strata_rms_norm that first adds res (rows x_stride apart, when not 0)
+ * into x in place, and also writes out quantized as strata_quant_xq does into xq (when not 0; n a multiple of 32):
+ * [rows x n int8][rows x n / 32 f32 scales]. */
+int strata_rms_norm_q(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t out_stride,
+                      uint64_t n, uint64_t rows, float eps, uint64_t xq, uint64_t res);
 /* Backend::swiglu_q (src/backend.rs:313-318; kernel src/cuda/kernels.cu:1826-1839): silu(g) * u over `rows` rows
  * of n floats, quantized into xq as strata_quant_xq does; g is left as is. *ret = xq (the address the following
  * GEMV reads). */

@@ -41,6 +41,7 @@ def lib():
             "or_combine_seq": ([P, P, P, P, I, I, I], None),
             "or_experts_multi": ([I, I, P, P, P, I, I, P, I, P, P, I, P, I], None),
             "or_silu": ([F], F),
+            "or_rms_norm": ([P, P, F, I, P], None),
             "or_f16": ([ctypes.c_uint16], F),
         }
         for n, (a, r) in sig.items():
@@ -149,6 +150,16 @@ def experts_multi(ty_gu, ty_down, gate, up, down, n_embd, n_ff, hs, ids, wts, th
     lib().or_experts_multi(ty_gu, ty_down, _p(gate), _p(up), _p(down), n_embd, n_ff, _p(hs), t, _p(ids), _p(wts), k,
                            _p(ys), threads)
     return ys
+
+
+def rms_norm(x, w, eps):
+    """ops::rms_norm (src/ops.rs:3-7) per row of x."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    for r in range(x.shape[0]):
+        lib().or_rms_norm(_p(x[r]), _p(w), ctypes.c_float(eps), x.shape[1], _p(out[r]))
+    return out
 
 
 def silu(x):

@@ -512,6 +512,15 @@ void or_quant_xq32(const float* x, size_t x_stride, size_t n, size_t nt, uint8_t
 
 float or_silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* ops::rms_norm (src/ops.rs:3-7): ms = the sum of x^2 in index order / n, s = 1 / sqrt(ms + eps), out = x * s * w. */
+void or_rms_norm(const float* x, const float* w, float eps, int n, float* out) {
+    float ss = 0.0f;
+    for (int i = 0; i < n; i++) ss += x[i] * x[i];
+    const float ms = ss / (float)n;
+    const float s = 1.0f / sqrtf(ms + eps);
+    for (int i = 0; i < n; i++) out[i] = x[i] * s * w[i];
+}
+
 void or_route(const float* logits, int n, int k, int sigmoid, float extra_scale, int32_t* ids, float* wts) {
     float* p = (float*)malloc((size_t)n * sizeof(float));
     memcpy(p, logits, (size_t)n * sizeof(float));

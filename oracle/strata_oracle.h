@@ -48,6 +48,7 @@ void or_experts_multi(int ty_gu, int ty_down, const uint8_t* gate, const uint8_t
                       float* ys, int threads);
 /* ops::silu, src/ops.rs:14. */
 float or_silu(float x);
+void or_rms_norm(const float* x, const float* w, float eps, int n, float* out);
 
 #ifdef __cplusplus
 }

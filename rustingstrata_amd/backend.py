@@ -57,6 +57,8 @@ SIGNATURES = {
     "strata_graph_destroy": [P],
     "strata_dequant": [CTX, TP, U64, U64],
     "strata_quant_xq": [CTX, U64, U64, U64, U64, U64],
+    "strata_rms_norm": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float],
+    "strata_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
     "strata_gemv": [CTX, TP, U64, U64],
     "strata_gemvn": [CTX, TP, U64, U64, U64, U64, U64],
     "strata_gemvq": [CTX, TP, U64, U64, U64, U64, U64, U64],
@@ -265,6 +267,13 @@ class HipBackend:
 
     def quant_xq(self, x, x_stride, n, nt, out):
         _check(lib().strata_quant_xq(self._ctx, int(x), x_stride, n, nt, int(out)))
+
+    def rms_norm(self, x, x_stride, w, out, out_stride, n, rows, eps):
+        _check(lib().strata_rms_norm(self._ctx, int(x), x_stride, int(w), int(out), out_stride, n, rows, eps))
+
+    def rms_norm_q(self, x, x_stride, w, out, out_stride, n, rows, eps, xq=0, res=0):
+        _check(lib().strata_rms_norm_q(self._ctx, int(x), x_stride, int(w), int(out), out_stride, n, rows, eps, int(xq),
+                                       int(res)))
 
     def gemv(self, w, x, y):
         _check(lib().strata_gemv(self._ctx, w._c(), int(x), int(y)))

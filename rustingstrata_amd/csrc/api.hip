@@ -325,6 +325,22 @@ int strata_quant_xq(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t n, ui
     return 0;
 }
 
+int strata_rms_norm_q(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t out_stride,
+                      uint64_t n, uint64_t rows, float eps, uint64_t xq, uint64_t res) {
+    if (check_ctx(c)) return -1;
+    if (!x || !w || !out) return set_error("rms_norm: null x, w or out");
+    if (xq && n % 32) return set_error("rms_norm_q: " + std::to_string(n) + " values (a multiple of 32 to quantize)");
+    if (n > (1u << 30) || rows > (1u << 31)) return set_error("rms_norm: too large");
+    STRATA_HIP(launch_rms_norm_q((float*)x, x_stride, (const float*)w, (float*)out, out_stride, (int)n, (int)rows, eps,
+                                 (int8_t*)xq, (const float*)res, c->numerics, c->stream));
+    return 0;
+}
+
+int strata_rms_norm(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t out_stride, uint64_t n,
+                    uint64_t rows, float eps) {
+    return strata_rms_norm_q(c, x, x_stride, w, out, out_stride, n, rows, eps, 0, 0);
+}
+
 int strata_gemvq(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t xq, uint64_t y,
                  uint64_t y_stride, uint64_t nt) {
     if (check_ctx(c) || check_tensor(w, "gemv")) return -1;

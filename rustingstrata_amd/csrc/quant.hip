@@ -55,6 +55,54 @@ hipError_t launch_dequant(int ty, const uint8_t* w, uint64_t rows, uint64_t cols
 // SWIGLU: the values are silu(g) * u (swiglu_q, src/cuda/kernels.cu:1826-1839), with g at x and u at u.
 __device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + (float)exp(-(double)v)); }
 
+// The quantization of 8 consecutive values v (positions i..i + 7 of a row; lanes past n hold zeros) by a group of 32
+// lanes covering 256 values, as quant_xq does: the int8 values into q (the row's base) and one scale per 32 values into
+// qd (the row's base). Every lane of the group takes part (the block maximum is a cross-lane reduction).
+__device__ __forceinline__ void quant8_group(const float (&v)[8], int i, bool live, int mode, int8_t* q, float* qd) {
+    float d, mul;
+    if (mode == STRATA_NUM_Q8K) {
+        // Candidate: the first value of largest magnitude among this lane's 8, then across the 32 lanes (lowest index).
+        float bv = v[0];
+        int bi = i;
+#pragma unroll
+        for (int j = 1; j < 8; j++) if (fabsf(v[j]) > fabsf(bv)) { bv = v[j]; bi = i + j; }
+        // the first value of largest magnitude over the 32 lanes: the choice is unique, so the pairing of the
+        // exchange steps does not matter
+        auto step = [&](auto S) __attribute__((always_inline)) {
+            constexpr int st = decltype(S)::value;
+            const float ov = xl32f<st>(bv);
+            const int oi = xl32<st>(bi);
+            if (fabsf(ov) > fabsf(bv) || (fabsf(ov) == fabsf(bv) && oi < bi)) { bv = ov; bi = oi; }
+        };
+        step(std::integral_constant<int, 0>{});
+        step(std::integral_constant<int, 1>{});
+        step(std::integral_constant<int, 2>{});
+        step(std::integral_constant<int, 3>{});
+        step(std::integral_constant<int, 4>{});
+        float is = bv != 0.0f ? -127.0f / bv : 0.0f;
+        d = bv != 0.0f ? 1.0f / is : 0.0f;
+        mul = is;
+    } else {
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
+        mx = fmaxf(mx, xl32f<0>(mx));
+        mx = fmaxf(mx, xl32f<1>(mx));
+        d = mx / 127.0f;
+        mul = mx > 0.0f ? 127.0f / mx : 0.0f;
+    }
+    if (!live) return;
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        float r = __builtin_rintf(mul * v[j]);
+        int qq = (int)fminf(r, 127.0f);
+        w[j >> 2] |= (uint32_t)(qq & 255) << (8 * (j & 3));
+    }
+    *(uint2*)(q + i) = make_uint2(w[0], w[1]);
+    if ((threadIdx.x & 3) == 0) qd[i / 32] = d;
+}
+
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void quant_xq_kernel(const float* __restrict__ x, const float* __restrict__ u,
                                                        uint64_t x_stride, int n, int nt, int8_t* __restrict__ out, int mode) {
@@ -77,48 +125,61 @@ __global__ __launch_bounds__(256) void quant_xq_kernel(const float* __restrict__
 #pragma unroll
         for (int j = 0; j < 8; j++) v[j] = 0.0f;
     }
-    float d, mul;
-    if (mode == STRATA_NUM_Q8K) {
-        // Candidate: the first value of largest magnitude among this lane's 8, then across the 32 lanes (lowest index).
-        float bv = v[0];
-        int bi = i;
-#pragma unroll
-        for (int j = 1; j < 8; j++) if (fabsf(v[j]) > fabsf(bv)) { bv = v[j]; bi = i + j; }
-            // the first value of largest magnitude over the 32 lanes: the choice is unique, so the pairing of the
-            // exchange steps does not matter
-            auto step = [&](auto S) __attribute__((always_inline)) {
-                constexpr int st = decltype(S)::value;
-                const float ov = xl32f<st>(bv);
-                const int oi = xl32<st>(bi);
-                if (fabsf(ov) > fabsf(bv) || (fabsf(ov) == fabsf(bv) && oi < bi)) { bv = ov; bi = oi; }
-            };
-            step(std::integral_constant<int, 0>{});
-            step(std::integral_constant<int, 1>{});
-            step(std::integral_constant<int, 2>{});
-            step(std::integral_constant<int, 3>{});
-            step(std::integral_constant<int, 4>{});
-        float is = bv != 0.0f ? -127.0f / bv : 0.0f;
-        d = bv != 0.0f ? 1.0f / is : 0.0f;
-        mul = is;
+    quant8_group(v, i, live, mode, out + (uint64_t)t * n, (float*)(out + (uint64_t)nt * n) + (uint64_t)t * (n / 32));
+}
+
+// rms_norm_q (Backend::rms_norm_q, src/backend.rs:232-235; ops::rms_norm src/ops.rs:3-7): per row, x += res first
+// (when res is not null, in place), then out = x * (1 / sqrt(mean(x^2) + eps)) * w, and (when xq is not null) out
+// quantized as quant_xq does into xq ([rows x n int8][rows x n / 32 f32]). One block of 256 threads per row; the sum
+// of squares is a fixed tree (per-thread strided sums, DPP within 32 lanes, then the 8 half-waves in order).
+__global__ __launch_bounds__(256) void rms_norm_q_kernel(float* x, uint64_t x_stride, const float* __restrict__ w,
+                                                         float* out, uint64_t out_stride, int n, float eps,
+                                                         int8_t* xq, const float* __restrict__ res, int rows, int mode) {
+    __shared__ float part[8];
+    const int r = blockIdx.x, tid = threadIdx.x;
+    float* xr = x + (uint64_t)r * x_stride;
+    float* o = out + (uint64_t)r * out_stride;
+    float s = 0.0f;
+    if (res) {
+        const float* rr = res + (uint64_t)r * x_stride;
+        for (int i = tid; i < n; i += 256) {
+            const float a = xr[i] + rr[i];
+            xr[i] = a;
+            s += a * a;
+        }
     } else {
-        float mx = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) mx = fmaxf(mx, fabsf(v[j]));
-        mx = fmaxf(mx, xl32f<0>(mx));
-        mx = fmaxf(mx, xl32f<1>(mx));
-        d = mx / 127.0f;
-        mul = mx > 0.0f ? 127.0f / mx : 0.0f;
+        for (int i = tid; i < n; i += 256) s += xr[i] * xr[i];
     }
-    if (!live) return;
-    uint32_t w[2] = {0, 0};
+    s += xl32f<0>(s);
+    s += xl32f<1>(s);
+    s += xl32f<2>(s);
+    s += xl32f<3>(s);
+    s += xl32f<4>(s);
+    if ((tid & 31) == 0) part[tid >> 5] = s;
+    __syncthreads();  // also: every thread's reads of x are done before out (which may be x) is written
+    float tot = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        float r = __builtin_rintf(mul * v[j]);
-        int q = (int)fminf(r, 127.0f);
-        w[j >> 2] |= (uint32_t)(q & 255) << (8 * (j & 3));
+    for (int h = 0; h < 8; h++) tot += part[h];
+    const float sc = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int i0 = 0; i0 < n; i0 += 2048) {
+        const int i = i0 + tid * 8;
+        const bool live = i < n;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = (live && i + j < n) ? xr[i + j] * sc * w[i + j] : 0.0f;
+        if (live) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) if (i + j < n) o[i + j] = v[j];
+        }
+        if (xq) quant8_group(v, i, live, mode, xq + (uint64_t)r * n, (float*)(xq + (uint64_t)rows * n) + (uint64_t)r * (n / 32));
     }
-    *(uint2*)(out + (uint64_t)t * n + i) = make_uint2(w[0], w[1]);
-    if ((threadIdx.x & 3) == 0) ((float*)(out + (uint64_t)nt * n))[(uint64_t)t * (n / 32) + i / 32] = d;
+}
+
+hipError_t launch_rms_norm_q(float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride, int n, int rows,
+                             float eps, int8_t* xq, const float* res, int mode, hipStream_t s) {
+    if (!n || !rows) return hipSuccess;
+    rms_norm_q_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, x_stride, w, out, out_stride, n, eps, xq, res, rows, mode);
+    return hipGetLastError();
 }
 
 hipError_t launch_quant_xq(const float* x, uint64_t x_stride, int n, int nt, int8_t* out, int mode, hipStream_t s) {

@@ -91,6 +91,35 @@ def test_quant_xq_q8k_magnitude_tie(hip):
     assert raw[n:].view(np.float32)[0] > 0  # -127 / (-7): the negative value came first
 
 
+@pytest.mark.parametrize("n,rows,res,inplace", [(2048, 3, False, False), (768, 5, True, False), (4096, 2, True, True),
+                                               (320, 4, False, True)])
+def test_rms_norm_q(hip, n, rows, res, inplace):
+    """Backend::rms_norm_q (src/backend.rs:233-235): x += res (bit-exact), out against ops::rms_norm (src/ops.rs:3-7)
+    to 1e-6 (the GPU sums the squares in a tree, the CPU in index order), xq bit-exact against quant_xq of the same
+    out; out may be x."""
+    x = normal((rows, n), seed=n + rows)
+    r = normal((rows, n), seed=n + rows + 1) if res else None
+    w = np.random.default_rng(n).uniform(0.5, 1.5, n).astype(np.float32)
+    xb, wb = up(hip, x), up(hip, w)
+    rb = up(hip, r) if res else 0
+    ob = xb if inplace else hip.alloc(rows * n * 4)
+    xq = hip.alloc(rows * (n + n // 8))
+    hip.rms_norm_q(xb, n, wb, ob, n, n, rows, 1e-6, xq=xq, res=rb)
+    xs = x + r if res else x
+    if res and not inplace:
+        assert np.array_equal(down(hip, xb, np.float32, rows * n).reshape(rows, n), xs)
+    got = down(hip, ob, np.float32, rows * n).reshape(rows, n)
+    want = O.rms_norm(xs, w, 1e-6)
+    assert np.abs(got - want).max() / np.abs(want).max() < 1e-6
+    q2 = hip.alloc(rows * (n + n // 8))
+    hip.quant_xq(ob, n, n, rows, q2)
+    assert np.array_equal(down(hip, xq, np.uint8, rows * (n + n // 8)), down(hip, q2, np.uint8, rows * (n + n // 8)))
+    # without xq and res: rms_norm
+    o2 = hip.alloc(rows * n * 4)
+    hip.rms_norm(ob, n, wb, o2, n, n, rows, 1e-6)
+    assert np.abs(down(hip, o2, np.float32, rows * n).reshape(rows, n) - O.rms_norm(got, w, 1e-6)).max() < 1e-5
+
+
 def test_quant_xq_per32_bit_exact(hip):
     n, nt = 1024, 2
     x = normal((nt, n), seed=5)

@@ -222,3 +222,23 @@ def test_experts_multi_matches_f64():
             want += wts[tt, j] * (D[e] @ seen(a))
         err = np.abs(ys[tt] - want).max() / np.abs(want).max()
         assert err < 2e-3, err  # the f32 SwiGLU may round an activation to the other int8 step
+
+
+def test_rms_norm_pinned():
+    """ops::rms_norm (src/ops.rs:3-7) pinned by what the mathematics fixes: a constant row normalizes to exactly 1
+    (0.5 * 256 squares sum exactly); the result is invariant under power-of-two scaling of x (every step scales
+    exactly) and linear in w; mean(out^2 / w^2) = 1 with eps = 0; and the float64 formula to 1e-6."""
+    n = 256
+    out = O.rms_norm(np.full(n, 0.5, np.float32), np.ones(n, np.float32), 0.0)
+    assert np.array_equal(out, np.ones((1, n), np.float32))
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 768)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 768).astype(np.float32)
+    a = O.rms_norm(x, w, 0.0)
+    assert np.array_equal(O.rms_norm(x * np.float32(8.0), w, 0.0), a)
+    assert np.array_equal(O.rms_norm(x, w * np.float32(2.0), 0.0), a * np.float32(2.0))
+    assert np.abs((O.rms_norm(x, np.ones(768, np.float32), 0.0).astype(np.float64) ** 2).mean(axis=1) - 1).max() < 1e-5
+    eps = 1e-6
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + eps) * w
+    assert np.abs(O.rms_norm(x, w, eps) - want).max() / np.abs(want).max() < 1e-6
