@@ -526,3 +526,33 @@ def test_graph_replays_read_device_memory(hip):
         assert np.array_equal(got, down(hip, y2, np.float32, rows)), i
         assert max_rel_err(got, O.matvec(ty, w, rows, cols, x)) <= TOL
     hip.drop_graphs()
+
+
+def test_moe_gemv_from_gguf_slots(hip, tmp_path):
+    """A MoE layer read from a GGUF into expert slots (gate | up | down per slot, src/expert_cache.rs:66-90): the
+    paired gate/up moe_gemv and the down moe_gemv address each expert at base + off + e * slot_bytes."""
+    from rustingstrata_amd import gguf
+    from tests.test_gguf import moe_layer_file
+    E, H, F = 4, 512, 256
+    p = str(tmp_path / "moe.gguf")
+    gate, upw, dn = moe_layer_file(p, E, H, F)
+    g = gguf.Gguf(p)
+    buf, mats, slot = gguf.upload_experts(hip, g, 0)
+    ids = np.array([2, 0, 3], dtype=np.int32)
+    k = len(ids)
+    x = normal(H, seed=77)
+    idb = up(hip, ids)
+    y = hip.alloc(2 * k * F * 4)
+    hip.moe_gemv(ggml.Q5_K, F, H, int(buf) + mats[0].off, slot, idb, k, up(hip, x), H, k, y,
+                 pair=(mats[1].off - mats[0].off, k * F * 4))
+    got = down(hip, y, np.float32, 2 * k * F).reshape(2, k, F)
+    for j, e in enumerate(ids):
+        assert max_rel_err(got[0, j], O.matvec(ggml.Q5_K, gate[e * F:(e + 1) * F], F, H, x)) <= TOL
+        assert max_rel_err(got[1, j], O.matvec(ggml.Q5_K, upw[e * F:(e + 1) * F], F, H, x)) <= TOL
+    act = normal((k, F), seed=78)
+    yd = hip.alloc(k * H * 4)
+    hip.moe_gemv(ggml.Q6_K, H, F, int(buf) + mats[2].off, slot, idb, k, up(hip, act), F, 1, yd)
+    gd = down(hip, yd, np.float32, k * H).reshape(k, H)
+    for j, e in enumerate(ids):
+        assert max_rel_err(gd[j], O.matvec(ggml.Q6_K, dn[e * H:(e + 1) * H], H, F, act[j])) <= TOL
+
