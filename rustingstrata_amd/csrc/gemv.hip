@@ -214,20 +214,10 @@ constexpr int GEMV1_TILE = GEMV_THREADS * 16 * GEMV1_CH;
 
 // Quantize x row xr (n values) into LDS (n int8, then n / 32 scales) with quant_xq's arithmetic (quant.hip): the
 // block's 256 threads take 8 values each, a group of 32 lanes one 256-value block.
+// This thread's 8 values v (positions i.., zeros past n) of one 2048-value chunk, quantized into LDS.
 template <bool Q32>
-__device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, float* d) {
-    typedef float v4f __attribute__((ext_vector_type(4)));
-    for (int c0 = 0; c0 < n; c0 += 2048) {
-        const int i = c0 + threadIdx.x * 8;
-        const bool live = i < n;
-        float v[8];
-        if (live) {
-            const v4f p = *gptr<v4f>(xr + 4 * (uint64_t)i), r = *gptr<v4f>(xr + 4 * (uint64_t)i + 16);
-            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = r.x; v[5] = r.y; v[6] = r.z; v[7] = r.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = 0.0f;
-        }
+__device__ __forceinline__ void quant8_lds(const float (&v)[8], int i, bool live, int8_t* q, float* d) {
+    {
         float dd, mul;
         if constexpr (!Q32) {
             float bv = v[0];
@@ -269,6 +259,24 @@ __device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, flo
     }
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+template <bool Q32>
+__device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, float* d) {
+    for (int c0 = 0; c0 < n; c0 += 2048) {
+        const int i = c0 + threadIdx.x * 8;
+        const bool live = i < n;
+        float v[8];
+        if (live) {
+            const v4f p = *gptr<v4f>(xr + 4 * (uint64_t)i), r = *gptr<v4f>(xr + 4 * (uint64_t)i + 16);
+            v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = r.x; v[5] = r.y; v[6] = r.z; v[7] = r.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+        }
+        quant8_lds<Q32>(v, i, live, q, d);
+    }
+}
+
 // x row xrow into the block's LDS copy (int8, then per-32 scales): copied from xq, or quantized from f32.
 template <bool Q32>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl, float* xld) {
@@ -284,6 +292,47 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl,
     const int n = a.cols, nup = (n + 255) & ~255;
     for (int i = n + 4 * threadIdx.x; i < nup; i += 4 * blockDim.x) *(uint32_t*)(xl + i) = 0;
     for (int j = n / 32 + threadIdx.x; j < nup / 32; j += blockDim.x) xld[j] = 0.0f;
+}
+
+// The first tile's x row when it has at most 2048 values, requested before the tile's weights so that its arrival
+// and quantization overlap the weights' flight: (f32 x) this thread's 8 values; (xq) its 16-byte chunk and scale.
+struct XEarly {
+    v4f f0, f1;
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    v4u q;
+    float d;
+};
+__device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const int tid = threadIdx.x;
+    if (a.xq) {
+        if (tid < a.cols / 16) e.q = *gptr<v4u>((uint64_t)(a.xq + (uint64_t)xrow * a.cols) + 16 * tid);
+        if (tid < a.cols / 32) e.d = *gptr<float>((uint64_t)(a.xd + (uint64_t)xrow * (a.cols / 32)) + 4 * tid);
+    } else if (8 * tid < a.cols) {
+        const uint64_t xr = (uint64_t)(a.xf + (uint64_t)xrow * a.x_stride) + 32 * (uint64_t)tid;
+        e.f0 = *gptr<v4f>(xr);
+        e.f1 = *gptr<v4f>(xr + 16);
+    }
+}
+template <bool Q32>
+__device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t* xl, float* xld) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const int tid = threadIdx.x, n = a.cols;
+    if (a.xq) {
+        if (tid < n / 16) *(v4u*)(xl + 16 * tid) = e.q;
+        if (tid < n / 32) xld[tid] = e.d;
+    } else {
+        const bool live = 8 * tid < n;
+        float v[8] = {e.f0.x, e.f0.y, e.f0.z, e.f0.w, e.f1.x, e.f1.y, e.f1.z, e.f1.w};
+        if (!live) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+        }
+        quant8_lds<Q32>(v, 8 * tid, live, xl, xld);
+    }
+    const int nup = (n + 255) & ~255;
+    for (int i = n + 4 * tid; i < nup; i += 4 * blockDim.x) *(uint32_t*)(xl + i) = 0;
+    for (int j = n / 32 + tid; j < nup / 32; j += blockDim.x) xld[j] = 0.0f;
 }
 
 // This lane's 256-value slice (super-block sb) of the staged x into registers, with its per-16 sums.
@@ -372,6 +421,9 @@ __global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs
     int t = next_valid(blockIdx.x);
     if (t >= total) return;
     Span sp = span(t);
+    const bool early = a.cols <= 2048;
+    XEarly xe;
+    if (early) x_fetch(a, sp.xrow, xe);
     issue(sp);
     // the tile after next is located while the next one is in flight
     int tn = next_valid(t + gridDim.x);
@@ -387,7 +439,8 @@ __global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs
     while (true) {
         __syncthreads();  // the previous tile's readers are done with the LDS tile
         if (sp.xrow != cur_xrow) {
-            stage_x<Q32>(a, sp.xrow, xl, xld);
+            if (early && cur_xrow < 0) x_put<Q32>(a, xe, xl, xld);
+            else stage_x<Q32>(a, sp.xrow, xl, xld);
             __syncthreads();
 #ifdef STRATA_GEMV1_XLDS
             for (int c = tid; c < (int)ncp / 16; c += GEMV_THREADS) {
