@@ -210,7 +210,12 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
 #define STRATA_GEMV1_CH 12
 #endif
 constexpr int GEMV1_CH = STRATA_GEMV1_CH;
-constexpr int GEMV1_TILE = GEMV_THREADS * 16 * GEMV1_CH;
+#ifndef STRATA_GEMV1_WAVES
+#define STRATA_GEMV1_WAVES 4
+#endif
+constexpr int GEMV1_WAVES = STRATA_GEMV1_WAVES;          // waves of a single-input GEMV block
+constexpr int GEMV1_THREADS = 64 * GEMV1_WAVES;
+constexpr int GEMV1_TILE = GEMV1_THREADS * 16 * GEMV1_CH;
 
 // Quantize x row xr (n values) into LDS (n int8, then n / 32 scales) with quant_xq's arithmetic (quant.hip): the
 // block's 256 threads take 8 values each, a group of 32 lanes one 256-value block.
@@ -262,7 +267,7 @@ __device__ __forceinline__ void quant8_lds(const float (&v)[8], int i, bool live
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <bool Q32>
 __device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, float* d) {
-    for (int c0 = 0; c0 < n; c0 += 2048) {
+    for (int c0 = 0; c0 < n; c0 += 8 * (int)blockDim.x) {
         const int i = c0 + threadIdx.x * 8;
         const bool live = i < n;
         float v[8];
@@ -357,7 +362,7 @@ __device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const flo
 #define GEMV1_ATTR
 #endif
 template <int T, bool Q32>
-__global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs a) {
+__global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs a) {
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -413,7 +418,7 @@ __global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs
     auto issue = [&](const Span& sp) {
 #pragma unroll
         for (int i = 0; i < GEMV1_CH; i++) {
-            const int c = min(tid + GEMV_THREADS * i, sp.nch - 1);
+            const int c = min(tid + GEMV1_THREADS * i, sp.nch - 1);
             wv[i] = __builtin_nontemporal_load(gptr<v4u>(sp.g0 + 16 * (uint64_t)c));
         }
     };
@@ -421,7 +426,7 @@ __global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs
     int t = next_valid(blockIdx.x);
     if (t >= total) return;
     Span sp = span(t);
-    const bool early = a.cols <= 2048;
+    const bool early = a.cols <= 8 * GEMV1_THREADS;
     XEarly xe;
     if (early) x_fetch(a, sp.xrow, xe);
     issue(sp);
@@ -443,7 +448,7 @@ __global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs
             else stage_x<Q32>(a, sp.xrow, xl, xld);
             __syncthreads();
 #ifdef STRATA_GEMV1_XLDS
-            for (int c = tid; c < (int)ncp / 16; c += GEMV_THREADS) {
+            for (int c = tid; c < (int)ncp / 16; c += GEMV1_THREADS) {
                 const v4u q = *(const v4u*)(xl + 16 * c);
                 xss[c] = sdot4((int)q.x, 0x01010101, sdot4((int)q.y, 0x01010101, sdot4((int)q.z, 0x01010101, sdot4((int)q.w, 0x01010101, 0))));
             }
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs
             __syncthreads();  // every lane has its slice before the LDS copy changes again
         }
 #pragma unroll
-        for (int i = 0; i < GEMV1_CH; i++) *(v4u*)(tile + 16 * (tid + GEMV_THREADS * i)) = wv[i];
+        for (int i = 0; i < GEMV1_CH; i++) *(v4u*)(tile + 16 * (tid + GEMV1_THREADS * i)) = wv[i];
         __syncthreads();
         const Span cs = sp;
         const bool more = tn < total;
@@ -466,7 +471,7 @@ __global__ __launch_bounds__(GEMV_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs
             if (tn < total) spn = span(tn);
         }
         const int nv = min(256, cols - 256 * gl);
-        for (int base = wave * RPW; base < cs.nr; base += 4 * RPW) {
+        for (int base = wave * RPW; base < cs.nr; base += GEMV1_WAVES * RPW) {
             const int rr = base + lane / G;
             float acc = 0.0f;
 #ifdef STRATA_GEMV1_NOCOMPUTE
@@ -501,13 +506,13 @@ static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, 
     }
     if (cached_smem != smem) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv1_kernel<T, Q32>, GEMV_THREADS, smem) != hipSuccess || n < 1) n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv1_kernel<T, Q32>, GEMV1_THREADS, smem) != hipSuccess || n < 1) n = 1;
         per_cu = n;
         cached_smem = smem;
     }
     long long blocks = (long long)per_cu * ncu;
     if (blocks > tiles) blocks = tiles;
-    gemv1_kernel<T, Q32><<<dim3((unsigned)blocks), GEMV_THREADS, smem, s>>>(a);
+    gemv1_kernel<T, Q32><<<dim3((unsigned)blocks), GEMV1_THREADS, smem, s>>>(a);
     return hipGetLastError();
 }
 
@@ -582,7 +587,7 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     long long want = (long long)maxrows * nslots * nz / (4LL * ncu);
     a.R = (int)(want < 1 ? 1 : want > rmax ? rmax : want);
     if (a.R < 1) a.R = 1;
-    const int rpb = 4 * (64 / a.G);  // rows one pass of the block covers
+    const int rpb = (single ? GEMV1_WAVES : 4) * (64 / a.G);  // rows one pass of the block covers
     // A single-input tile covers at least one pass of the block: fewer, fuller blocks beat idle lanes on small
     // matrices (each block also quantizes x itself).
     if (single && a.R < rpb) a.R = std::min(rpb, rmax);
