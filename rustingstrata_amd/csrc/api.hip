@@ -439,6 +439,7 @@ int strata_swiglu_q(strata_ctx* c, uint64_t g, uint64_t u, uint64_t n, uint64_t 
     if (check_ctx(c)) return -1;
     if (n % 32) return set_error("swiglu_q: " + std::to_string(n) + " values (a multiple of 32)");
     if (!xq) return set_error("swiglu_q: null xq");
+    if (rows > 65535 || n > (1u << 30)) return set_error("swiglu_q: too large (rows at most 65535)");
     STRATA_HIP(launch_swiglu_q((const float*)g, (const float*)u, (int)n, (int)rows, (int8_t*)xq, c->numerics, c->stream));
     if (ret) *ret = xq;
     return 0;
@@ -448,6 +449,7 @@ int strata_moe_combine(strata_ctx* c, uint64_t x, uint64_t ye, uint64_t w, uint6
                        uint64_t n, uint64_t t) {
     if (check_ctx(c)) return -1;
     if (!n || !t) return 0;
+    if (t > 65535 || n > (1u << 30)) return set_error("moe_combine: too large (at most 65535 tokens a call)");
     STRATA_HIP(launch_combine((float*)x, (const float*)ye, (const float*)w, (int)k, (const float*)sh, (const float*)sg,
                               (int)n, (int)t, c->stream));
     return 0;
@@ -464,6 +466,7 @@ int strata_moe_combine_seq(strata_ctx* c, uint64_t x, uint64_t ye, uint64_t wts,
                            uint64_t sg, uint64_t n, uint64_t t) {
     if (check_ctx(c)) return -1;
     if (!n || !t) return 0;
+    if (t > 65535 || n > (1u << 30)) return set_error("moe_combine_seq: too large (at most 65535 tokens a call)");
     STRATA_HIP(launch_combine_seq((float*)x, (const float*)ye, (const float*)wts, (const int*)inv, (int)k,
                                   (const float*)sh, (const float*)sg, (int)n, (int)t, c->stream));
     return 0;
@@ -518,6 +521,7 @@ static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint
     if (dense_w && check_align(ty, (uint64_t)dense_w, "gemm_dense")) return -1;
     if (n_tiles == 0 || rows == 0) return 0;
     if (rows > (1u << 24) || row_bytes(ty, cols) >= (1u << 24) || n_tiles > 65535 * 64) return set_error("gemm: too large");
+    if (ty == Q8_0 && n_tiles > 65535) return set_error("gemm: Q8_0 with more than 65535 tiles");
     // the kernel addresses X and a weight matrix with 32-bit byte offsets
     if (n_x * cols >= (1ull << 32) || rows * row_bytes(ty, cols) >= (1ull << 32)) return set_error("gemm: X or W of 4 GiB or more");
     uint64_t xq = 0;

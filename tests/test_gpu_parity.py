@@ -282,6 +282,17 @@ def test_moe_route_table(hip):
     assert np.array_equal(wh, np.where(slots >= 0, wts, 0.0).astype(np.float32))
 
 
+def test_rejects_oversized_grids(hip):
+    """Token and row counts past what one launch addresses are errors before anything runs."""
+    b = hip.alloc(64)
+    with pytest.raises(S.StrataError, match="moe_combine_seq: too large"):
+        hip.moe_combine_seq(b, b, b, b, 8, 0, 0, 2048, 70000)
+    with pytest.raises(S.StrataError, match="moe_combine: too large"):
+        hip.moe_combine(b, b, b, 8, 0, 0, 2048, 70000)
+    with pytest.raises(S.StrataError, match="swiglu_q: too large"):
+        hip.swiglu_q(b, b, 768, 70000, b)
+
+
 def test_router_rejects_shapes(hip):
     b = hip.alloc(64)
     with pytest.raises(S.StrataError, match="router_topk: 600 experts, top 8"):
