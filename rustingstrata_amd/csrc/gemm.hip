@@ -69,7 +69,15 @@ struct GemmArgs {
     int gx;               // blocks per XCD
 };
 
-__device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + (float)exp(-(double)v)); }
+// silu(v) = v / (1 + e^-v) for the SwiGLU epilogue. e^-v = 2^t with t = -v log2(e) carried as th + tl (the product's
+// rounding error and the tail of log2(e) in tl): 2^th by v_exp_f32 and 2^tl as 1 + tl ln 2. Within a few ulp of the
+// correctly rounded value over the whole range (e^-v overflowing to inf gives -0, as silu's limit).
+__device__ __forceinline__ float silu_dev(float v) {
+    constexpr float L = 1.44269504088896341f, LLO = 1.9259630335e-08f, LN2 = 0.693147180559945f;
+    const float x = -v, th = x * L, tl = __builtin_fmaf(x, L, -th) + x * LLO;
+    const float e = __builtin_amdgcn_exp2f(th) * __builtin_fmaf(tl, LN2, 1.0f);
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 #ifdef STRATA_GEMM_TRACE
 // Debug builds: shader clock at the phases of the first steps of a few waves (read with strata_debug_gemm_trace).
