@@ -201,8 +201,9 @@ def bench_moe(hip, S, ggml, T, iters):
 
 
 def bench_moe_decode(hip, S, ggml, iters):
-    """configs[2] at 1 token: route -> paired gate/up moe_gemv -> swiglu_q -> moe_down_combine (src/gpu_model.rs:
-    3383-3412), over 2 copies of the 128 experts (884 MB, past the Infinity Cache)."""
+    """configs[2] at 1 token: route -> paired gate/up moe_gemv (h quantized inside it) -> swiglu_q +
+    moe_down_combine as one down GEMV (the SwiGLU quantized inside it) + combine (src/gpu_model.rs:3383-3412), over 2 copies of the 128 experts
+    (884 MB, past the Infinity Cache)."""
     E, H, F, k = 128, 2048, 768, 8
     rng = np.random.default_rng(12)
     rb_gu, rb_d = ggml.row_bytes(ggml.Q5_K, H), ggml.row_bytes(ggml.Q6_K, F)
@@ -218,15 +219,15 @@ def bench_moe_decode(hip, S, ggml, iters):
     logits = [hip.upload((rng.standard_normal(E) + 3 * (rng.permutation(E) + 1.0) ** -1.1).astype(np.float32))
               for _ in range(4)]
     ids, wts, slots, wh = [hip.alloc(k * 4) for _ in range(4)]
-    xq, g, aq, ye, x = hip.alloc(H + H // 8), hip.alloc(2 * k * F * 4), hip.alloc(k * (F + F // 8)), hip.alloc(k * H * 4), hip.alloc(H * 4)
+    g, ye, x = hip.alloc(2 * k * F * 4), hip.alloc(k * H * 4), hip.alloc(H * 4)
 
     def token(i):
         gu, d = copies[i % 2]
         hip.moe_route(logits[i % 4], E, k, 0.0, table, ids, wts, slots, wh, 1)
-        hip.quant_xq(h, H, H, 1, xq)
-        hip.moe_gemv(ggml.Q5_K, F, H, gu, F * rb_gu, slots, k, h, H, k, g, pair=(E * F * rb_gu, k * F * 4), xq=xq)
-        hip.swiglu_q(g, int(g) + k * F * 4, F, k, aq)
-        hip.moe_down_combine(ggml.Q6_K, H, F, d, H * rb_d, slots, k, 0, ye, aq, x, wh, 0, 0, 1)
+        # h is quantized inside the gate/up GEMV (quant_xq's arithmetic, the same bits)
+        hip.moe_gemv(ggml.Q5_K, F, H, gu, F * rb_gu, slots, k, h, H, k, g, pair=(E * F * rb_gu, k * F * 4))
+        # swiglu_q + moe_down_combine with the SwiGLU and its quantization inside the down GEMV (same bits)
+        hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d, H * rb_d, slots, k, g, int(g) + k * F * 4, ye, x, wh, 0, 0, 1)
 
     for i in range(20):
         token(i)

@@ -149,6 +149,13 @@ int strata_moe_combine(strata_ctx* ctx, uint64_t x, uint64_t ye, uint64_t w, uin
 int strata_moe_down_combine(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
                             uint64_t slots, uint64_t k, uint64_t h, uint64_t ye, uint64_t xq, uint64_t x, uint64_t wh,
                             uint64_t sh, uint64_t sg, uint64_t t);
+/* Backend::swiglu_q followed by Backend::moe_down_combine with mb = 0 (src/backend.rs:313-318, 436-442; the decode
+ * sequence src/gpu_model.rs:3383-3412) in one GEMV launch: the x row of slot j is silu(g[j]) * u[j] (t * k rows of
+ * cols floats each, g and u with the same layout), quantized inside the down GEMV with swiglu_q's arithmetic (the same
+ * int8 values and scales), then moe_combine of ye into x with weights wh. */
+int strata_moe_down_swiglu_combine(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
+                                   uint64_t slots, uint64_t k, uint64_t g, uint64_t u, uint64_t ye, uint64_t x,
+                                   uint64_t wh, uint64_t sh, uint64_t sg, uint64_t t);
 /* Backend::moe_combine_seq (src/backend.rs:356; kernel src/cuda/kernels.cu:2776-2785): x[t] += sum_{j<k}
  * wts[t, j] ye[inv[t, j]] (+ sigmoid(sg[t]) sh[t], or + sh[t] when sg is 0; sh 0 = none), j in order. */
 int strata_moe_combine_seq(strata_ctx* ctx, uint64_t x, uint64_t ye, uint64_t wts, uint64_t inv, uint64_t k,

@@ -69,6 +69,7 @@ SIGNATURES = {
     "strata_swiglu_q": [CTX, U64, U64, U64, U64, U64, ctypes.POINTER(U64)],
     "strata_moe_combine": [CTX, U64, U64, U64, U64, U64, U64, U64, U64],
     "strata_moe_down_combine": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64],
+    "strata_moe_down_swiglu_combine": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64],
     "strata_moe_combine_seq": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64],
     "strata_moe_sort": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.POINTER(U64), ctypes.POINTER(U64),
                         U64, U64, U64, U64, U64],
@@ -310,6 +311,11 @@ class HipBackend:
     def moe_down_combine(self, ty, rows, cols, w, stride, slots, k, h, ye, xq, x, wh, sh, sg, t):
         _check(lib().strata_moe_down_combine(self._ctx, ty, rows, cols, int(w), stride, int(slots), k, int(h),
                                              int(ye), int(xq), int(x), int(wh), int(sh), int(sg), t))
+
+    def moe_down_swiglu_combine(self, ty, rows, cols, w, stride, slots, k, g, u, ye, x, wh, sh, sg, t):
+        """swiglu_q(g, u) then moe_down_combine in one GEMV launch (the x rows quantized inside it)."""
+        _check(lib().strata_moe_down_swiglu_combine(self._ctx, ty, rows, cols, int(w), stride, int(slots), k, int(g),
+                                                    int(u), int(ye), int(x), int(wh), int(sh), int(sg), t))
 
     def moe_combine_seq(self, x, ye, wts, inv, k, sh, sg, n, t):
         _check(lib().strata_moe_combine_seq(self._ctx, int(x), int(ye), int(wts), int(inv), k, int(sh), int(sg), n, t))

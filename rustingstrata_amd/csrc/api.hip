@@ -394,9 +394,10 @@ int strata_gemvq2(strata_ctx* c, const strata_tensor* a, const strata_tensor* b,
     return 0;
 }
 
-int strata_moe_gemv(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride, uint64_t ids,
-                    uint64_t k, uint64_t x, uint64_t x_stride, uint64_t xg, uint64_t y, int has_pair, int64_t w2,
-                    int64_t y2, uint64_t xq) {
+// moe_gemv with x = silu(x) * xu per row when xu is not 0 (quantized in the kernel; xq must be 0 then).
+static int moe_gemv_impl(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride, uint64_t ids,
+                         uint64_t k, uint64_t x, uint64_t x_stride, uint64_t xg, uint64_t y, int has_pair, int64_t w2,
+                         int64_t y2, uint64_t xq, uint64_t xu) {
     if (check_ctx(c) || check_type(ty)) return -1;
     if (check_gemv_cols(ty, cols) || check_align(ty, w, "moe_gemv")) return -1;
     if (check_align(ty, stride, "moe_gemv stride") || (has_pair && check_align(ty, (uint64_t)w2, "moe_gemv pair offset"))) return -1;
@@ -404,7 +405,7 @@ int strata_moe_gemv(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_
     if (k == 0 || rows == 0) return 0;
     if (k > 65535) return set_error("moe_gemv: too many slots");
     GemvLaunch g;
-    g.xf = (const float*)x; g.x_stride = x_stride;
+    g.xf = (const float*)x; g.xu = (const float*)xu; g.x_stride = x_stride;
     g.ty = ty; g.w = (const uint8_t*)w; g.rows = (int)rows; g.cols = (int)cols; g.nt = 1;
     g.xq = (const int8_t*)xq; g.n_xrows = (int)(k / xg); g.y = (float*)y; g.y_stride = 0;
     g.numerics = c->numerics;
@@ -412,6 +413,12 @@ int strata_moe_gemv(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_
     g.pair = has_pair != 0; g.w2 = w2; g.y2 = y2; g.rows2 = (int)rows;
     STRATA_HIP(launch_gemv(g, c->stream));
     return 0;
+}
+
+int strata_moe_gemv(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride, uint64_t ids,
+                    uint64_t k, uint64_t x, uint64_t x_stride, uint64_t xg, uint64_t y, int has_pair, int64_t w2,
+                    int64_t y2, uint64_t xq) {
+    return moe_gemv_impl(c, ty, rows, cols, w, stride, ids, k, x, x_stride, xg, y, has_pair, w2, y2, xq, 0);
 }
 
 int strata_router_topk(strata_ctx* c, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t ids,
@@ -459,6 +466,15 @@ int strata_moe_down_combine(strata_ctx* c, int ty, uint64_t rows, uint64_t cols,
                             uint64_t slots, uint64_t k, uint64_t h, uint64_t ye, uint64_t xq, uint64_t x, uint64_t wh,
                             uint64_t sh, uint64_t sg, uint64_t t) {
     if (strata_moe_gemv(c, ty, rows, cols, w, stride, slots, t * k, h, cols, 1, ye, 0, 0, 0, xq)) return -1;
+    return strata_moe_combine(c, x, ye, wh, k, sh, sg, rows, t);
+}
+
+int strata_moe_down_swiglu_combine(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
+                                   uint64_t slots, uint64_t k, uint64_t g, uint64_t u, uint64_t ye, uint64_t x,
+                                   uint64_t wh, uint64_t sh, uint64_t sg, uint64_t t) {
+    if (check_ctx(c)) return -1;
+    if (!g || !u) return set_error("moe_down_swiglu_combine: null g or u");
+    if (moe_gemv_impl(c, ty, rows, cols, w, stride, slots, t * k, g, cols, 1, ye, 0, 0, 0, 0, u)) return -1;
     return strata_moe_combine(c, x, ye, wh, k, sh, sg, rows, t);
 }
 

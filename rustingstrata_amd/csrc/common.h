@@ -57,6 +57,9 @@ template <typename T>
 __device__ __forceinline__ const __attribute__((address_space(3))) T* lptr(const void* p) {
     return (const __attribute__((address_space(3))) T*)p;
 }
+// silu(v) = v / (1 + e^-v) with e^-v in double rounded once to f32 (the correctly rounded f32 exp but in vanishingly
+// rare cases), for silu(g) * u ahead of a quantization (src/ops.rs:14; swiglu_q src/cuda/kernels.cu:1826-1839).
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + (float)exp(-(double)v)); }
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 // Bytes {hi:lo} >> 8 * (sh & 3): the 4 bytes starting at byte sh of the 8-byte pair (v_alignbyte_b32).
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t sh) {

@@ -40,6 +40,7 @@ struct GemvArgs {
     int G;               // lanes per row: the power of two at or above the row's super-blocks, at most 64
     int ntr, nslots, nz; // row tiles per matrix, slots (moe) and matrices (pair)
     const float* xf;     // single-input kernel: x as f32 (quantized in-lane) when xq is null
+    const float* xu;     // with xf: x = silu(xf) * xu, rows x_stride floats apart (swiglu_q fused), or null
     uint64_t x_stride;   // floats between the f32 x rows
 };
 
@@ -266,7 +267,7 @@ __device__ __forceinline__ void quant8_lds(const float (&v)[8], int i, bool live
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <bool Q32>
-__device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, float* d) {
+__device__ __forceinline__ void quant_row_lds(uint64_t xr, uint64_t ur, int n, int8_t* q, float* d) {
     for (int c0 = 0; c0 < n; c0 += 8 * (int)blockDim.x) {
         const int i = c0 + threadIdx.x * 8;
         const bool live = i < n;
@@ -274,6 +275,12 @@ __device__ __forceinline__ void quant_row_lds(uint64_t xr, int n, int8_t* q, flo
         if (live) {
             const v4f p = *gptr<v4f>(xr + 4 * (uint64_t)i), r = *gptr<v4f>(xr + 4 * (uint64_t)i + 16);
             v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = r.x; v[5] = r.y; v[6] = r.z; v[7] = r.w;
+            if (ur) {
+                const v4f pu = *gptr<v4f>(ur + 4 * (uint64_t)i), ru = *gptr<v4f>(ur + 4 * (uint64_t)i + 16);
+                const float u[8] = {pu.x, pu.y, pu.z, pu.w, ru.x, ru.y, ru.z, ru.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = silu_f32(v[j]) * u[j];
+            }
         } else {
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = 0.0f;
@@ -291,7 +298,8 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl,
         for (int c = threadIdx.x; c < a.cols / 16; c += blockDim.x) *(v4u*)(xl + 16 * c) = *gptr<v4u>(q + 16 * c);
         for (int c = threadIdx.x; c < a.cols / 32; c += blockDim.x) xld[c] = *gptr<float>(d + 4 * c);
     } else {
-        quant_row_lds<Q32>((uint64_t)(a.xf + (uint64_t)xrow * a.x_stride), a.cols, xl, xld);
+        quant_row_lds<Q32>((uint64_t)(a.xf + (uint64_t)xrow * a.x_stride),
+                           a.xu ? (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) : 0, a.cols, xl, xld);
     }
     // zeros up to whole super-blocks (Q8_0 rows may end inside one)
     const int n = a.cols, nup = (n + 255) & ~255;
@@ -302,7 +310,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl,
 // The first tile's x row when it has at most 2048 values, requested before the tile's weights so that its arrival
 // and quantization overlap the weights' flight: (f32 x) this thread's 8 values; (xq) its 16-byte chunk and scale.
 struct XEarly {
-    v4f f0, f1;
+    v4f f0, f1, u0, u1;
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     v4u q;
     float d;
@@ -317,6 +325,11 @@ __device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) 
         const uint64_t xr = (uint64_t)(a.xf + (uint64_t)xrow * a.x_stride) + 32 * (uint64_t)tid;
         e.f0 = *gptr<v4f>(xr);
         e.f1 = *gptr<v4f>(xr + 16);
+        if (a.xu) {
+            const uint64_t ur = (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) + 32 * (uint64_t)tid;
+            e.u0 = *gptr<v4f>(ur);
+            e.u1 = *gptr<v4f>(ur + 16);
+        }
     }
 }
 template <bool Q32>
@@ -329,6 +342,11 @@ __device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t
     } else {
         const bool live = 8 * tid < n;
         float v[8] = {e.f0.x, e.f0.y, e.f0.z, e.f0.w, e.f1.x, e.f1.y, e.f1.z, e.f1.w};
+        if (a.xu) {
+            const float u[8] = {e.u0.x, e.u0.y, e.u0.z, e.u0.w, e.u1.x, e.u1.y, e.u1.z, e.u1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = silu_f32(v[j]) * u[j];
+        }
         if (!live) {
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = 0.0f;
@@ -563,7 +581,7 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     GemvArgs a{};
     a.w = g.w; a.w2 = g.pair ? g.w2 : 0; a.y = g.y; a.y2 = g.pair ? g.y2 : 0;
     a.xq = g.xq; a.xd = g.xq ? (const float*)(g.xq + (uint64_t)g.n_xrows * g.cols) : nullptr;
-    a.xf = g.xf; a.x_stride = g.x_stride;
+    a.xf = g.xf; a.xu = g.xu; a.x_stride = g.x_stride;
     a.ids = g.ids; a.stride = g.stride; a.xg = g.xg;
     a.rows = g.rows; a.rows2 = g.pair ? g.rows2 : 0; a.cols = g.cols; a.nt = g.nt; a.y_stride = g.y_stride;
     a.rb = row_bytes(g.ty, g.cols);

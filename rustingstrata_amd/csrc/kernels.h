@@ -22,6 +22,7 @@ struct GemvLaunch {
     int numerics = 0;             // STRATA_NUM_*: how xq was quantized
     const int8_t* xq = nullptr;   // quant_xq layout of n_xrows rows of cols; null: quantize xf in the kernel (nt == 1)
     const float* xf = nullptr;    // x as f32, rows x_stride floats apart
+    const float* xu = nullptr;    // with xf (nt == 1): x = silu(xf) * xu, same row layout
     uint64_t x_stride = 0;
     int n_xrows = 1;
     float* y = nullptr;

@@ -53,7 +53,6 @@ hipError_t launch_dequant(int ty, const uint8_t* w, uint64_t rows, uint64_t cols
 //       round-half-even(is * v)), d = 1 / is for each of its 32-groups (src/cpu_moe.rs:28-46).
 //  Q8_32: per 32 values (4 lanes) d = max|v| / 127, q = round-half-even(v * 127 / max|v|) (src/cuda/kernels.cu:640-660).
 // SWIGLU: the values are silu(g) * u (swiglu_q, src/cuda/kernels.cu:1826-1839), with g at x and u at u.
-__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + (float)exp(-(double)v)); }
 
 // The quantization of 8 consecutive values v (positions i..i + 7 of a row; lanes past n hold zeros) by a group of 32
 // lanes covering 256 values, as quant_xq does: the int8 values into q (the row's base) and one scale per 32 values into

@@ -501,6 +501,45 @@ def test_moe_decode_layer_matches_experts(hip):
     hip.moe_down_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, 0, ye, aqr, x, wh, 0, 0, 1)
     got = down(hip, x, np.float32, H)
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+    # h quantized inside the gate/up GEMV and the fused tail (swiglu inside the down GEMV): the same bits
+    g2, x2 = hip.alloc(2 * k * F * 4), hip.alloc(H * 4)
+    hip.moe_gemv(ggml.Q5_K, F, H, gu, F * rb_gu, slots, k, hb, H, k, g2, pair=(E * F * rb_gu, k * F * 4))
+    assert np.array_equal(down(hip, g2, np.float32, 2 * k * F), down(hip, g, np.float32, 2 * k * F))
+    hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, g2, int(g2) + k * F * 4, ye, x2, wh, 0, 0, 1)
+    assert np.array_equal(down(hip, x2, np.float32, H), got)
+
+
+@pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])
+def test_moe_down_swiglu_combine_matches_unfused(hip, numerics):
+    """The fused decode tail (swiglu inside the down GEMV) gives the same bits as swiglu_q followed by
+    moe_down_combine (src/gpu_model.rs:3383-3412): same int8 x, same GEMV, same combine; 3 tokens, a shared expert."""
+    E, H, F, k, t = 16, 512, 768, 8, 3
+    _, _, dn = moe_weights(E, H, F, seed=60)
+    rb_d = ggml.row_bytes(ggml.Q6_K, F)
+    d_b = up(hip, dn)
+    rng = np.random.default_rng(61)
+    slots = up(hip, rng.integers(0, E, t * k).astype(np.int32))
+    wh = up(hip, rng.random(t * k).astype(np.float32))
+    gu = rng.standard_normal((2, t * k, F)).astype(np.float32) * 3
+    g = up(hip, gu)
+    u = int(g) + t * k * F * 4
+    sh, sg = up(hip, normal((t, H), seed=62)), up(hip, normal(t, seed=63))
+    x0 = normal((t, H), seed=64)
+    old = hip.numerics()
+    hip.set_numerics(numerics)
+    try:
+        xa, xb = up(hip, x0), up(hip, x0)
+        ya, yb = hip.alloc(t * k * H * 4), hip.alloc(t * k * H * 4)
+        aq = hip.alloc(t * k * (F + F // 8))
+        aqr = hip.swiglu_q(g, u, F, t * k, aq)
+        hip.moe_down_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, 0, ya, aqr, xa, wh, sh, sg, t)
+        hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, g, u, yb, xb, wh, sh, sg, t)
+    finally:
+        hip.set_numerics(old)
+    assert np.array_equal(down(hip, ya, np.float32, t * k * H), down(hip, yb, np.float32, t * k * H))
+    assert np.array_equal(down(hip, xa, np.float32, t * H), down(hip, xb, np.float32, t * H))
+    with pytest.raises(S.StrataError, match="null g or u"):
+        hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, g, 0, yb, xb, wh, 0, 0, t)
 
 
 def test_errors_do_not_launch(hip):
