@@ -10,12 +10,12 @@ namespace strata {
 __device__ __forceinline__ float exp_f32(float x) { return (float)exp((double)x); }
 
 // ---- routing: one wave64 per token (Model::route src/model.rs:837-851; topk_warp src/cuda/kernels.cu:2633-2686) ----
-constexpr int ROUTE_R = 8;  // logits per lane: n <= 512
-
+// ROUTE_R logits per lane (n <= 64 ROUTE_R): an instantiation per 1, 2, 4, 8, so a 128-expert router scans 2 a lane.
+template <int ROUTE_R>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p, int n, int k, float extra_scale,
                                                     const int* __restrict__ table, int* ids, float* wts, int* slots,
                                                     float* wh, int T, int sigmoid) {
-    __shared__ float se[4][512];
+    __shared__ float se[4][64 * ROUTE_R];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + wave;
     if (t >= T) return;  // whole waves only
@@ -121,7 +121,11 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
 
 hipError_t launch_route(const float* p, int n, int k, float extra_scale, const int* table, int* ids, float* wts,
                         int* slots, float* wh, int t, int sigmoid, hipStream_t s) {
-    route_kernel<<<dim3((unsigned)((t + 3) / 4)), dim3(256), 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);
+    const dim3 grid((unsigned)((t + 3) / 4)), block(256);
+    if (n <= 64) route_kernel<1><<<grid, block, 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);
+    else if (n <= 128) route_kernel<2><<<grid, block, 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);
+    else if (n <= 256) route_kernel<4><<<grid, block, 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);
+    else route_kernel<8><<<grid, block, 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);
     return hipGetLastError();
 }
 

@@ -243,7 +243,8 @@ def test_moe_gemv_selects_experts(hip):
 
 
 def test_router_topk_matches_route(hip):
-    """tests/kernels.rs:1244-1282 cases, plus a Zipf-skewed batch: ids bit-exact, weights to 1e-6."""
+    """tests/kernels.rs:1244-1282 cases, plus Zipf-skewed batches at the edges of 1, 2, 4 and 8 logits a lane: ids
+    bit-exact, weights to 1e-6."""
     n, k, t = 256, 8, 3
     v = np.arange(n * t, dtype=np.float32) * np.float32(0.7548777)
     x = ((v - np.trunc(v)) - np.float32(0.5)) * np.float32(2.0) * 4.0
@@ -256,7 +257,9 @@ def test_router_topk_matches_route(hip):
     wide[1, 63] = wide[1, 64] = 20.0
     for logits, kk, scale, sig in [(x.reshape(t, n), k, 2.5, False), (zipf_logits(512, 128, seed=1), 8, 0.0, False),
                                    (zipf_logits(64, 17, seed=2), 4, 1.5, True), (wide, 32, 0.0, False),
-                                   (wide, 32, 0.0, True)]:
+                                   (wide, 32, 0.0, True), (zipf_logits(9, 64, seed=4), 8, 0.0, False),
+                                   (zipf_logits(9, 65, seed=5), 8, 0.0, False), (zipf_logits(9, 129, seed=6), 8, 0.0, False),
+                                   (zipf_logits(9, 257, seed=7), 8, 0.0, False)]:
         tt, nn = logits.shape
         ids, wts = hip.alloc(tt * kk * 4), hip.alloc(tt * kk * 4)
         hip.router_topk(up(hip, logits), nn, kk, scale, ids, wts, tt, sig)
