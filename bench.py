@@ -12,7 +12,7 @@ headline shape), the Qwen3-30B-A3B-shaped MoE layer at 4096 tokens 
 its grouped GEMMs) and at 1 token (decode GB/s), and the reference's CPU path (the oracle's C restatement of
 cpu_moe::matvec) timed on this host on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-moe] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-moe] [--no-cpu] [--profile-gemv | --profile-moe]
 """
 import argparse
 import json
@@ -410,6 +410,8 @@ def main():
     ap.add_argument("--moe-iters", type=int, default=20)
     ap.add_argument("--profile-gemv", action="store_true",
                     help="only run the Q4_K lm-head GEMV and a 256 MB copy kernel 50 times each (for rocprofv3)")
+    ap.add_argument("--profile-moe", action="store_true",
+                    help="only run the configs[2] 4K-token MoE prefill layer (--moe-iters times, for rocprofv3)")
     ap.add_argument("--eager", action="store_true", help="launch every op from the host (no recorded graphs)")
     args = ap.parse_args()
     global USE_GRAPHS
@@ -425,6 +427,9 @@ def main():
     log(f"[bench] {hip.device()}")
     if args.profile_gemv:
         profile_gemv(hip, S, ggml)
+        return
+    if args.profile_moe:
+        print(json.dumps({"moe_prefill_4k": bench_moe(hip, S, ggml, 4096, args.moe_iters)}), flush=True)
         return
     shapes, ms_step, gbs, per_shape, steps = bench_gemv(hip, S, ggml, args.steps, args.warmup)
     log(f"[bench] GEMV sweep: {gbs:.1f} GB/s, {ms_step:.3f} ms/step")
