@@ -201,7 +201,7 @@ hipError_t launch_combine_seq(float* x, const float* ye, const float* wts, const
 // counts into each (wave, expert) start slot (experts ascending, waves in order within an expert), phase C walks each
 // segment in order assigning slots, 64 pairs at a time with the rank among equal experts inside the wave. The result
 // is the host counting sort of src/gpu_model/prefill.rs:563-573 exactly.
-constexpr int SORT_WAVES = 16, SORT_MAX_E = 512;
+constexpr int SORT_WAVES = 16, SORT_MAX_E = 512, SORT_U = 8;
 
 size_t sort_scratch_bytes(int) { return 16; }
 
@@ -215,10 +215,22 @@ __global__ __launch_bounds__(1024) void sort_kernel(SortLaunch a) {
     for (int i = tid; i < SORT_WAVES * SORT_MAX_E; i += 1024) (&hist[0][0])[i] = 0;
     if (tid == 0) bad = 0;
     __syncthreads();
-    for (int i = s0 + lane; i < s1; i += 64) {
-        int e = a.ids[i];
-        if (e >= 0 && e < E) atomicAdd(&hist[wave][e], 1);
-        else atomicAdd(&bad, 1);
+    // the ids arrive SORT_U rounds of 64 at a time (their loads in flight together), then are taken in order
+    for (int c0 = s0; c0 < s1; c0 += 64 * SORT_U) {
+        int eu[SORT_U];
+#pragma unroll
+        for (int u = 0; u < SORT_U; u++) {
+            const int i = c0 + 64 * u + lane;
+            eu[u] = i < s1 ? a.ids[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < SORT_U; u++) {
+            if (c0 + 64 * u + lane < s1) {
+                const int e = eu[u];
+                if (e >= 0 && e < E) atomicAdd(&hist[wave][e], 1);
+                else atomicAdd(&bad, 1);
+            }
+        }
     }
     __syncthreads();
     // Per-expert counts and tile counts (thread e), then exclusive scans over experts (one wave, in order).
@@ -253,11 +265,21 @@ __global__ __launch_bounds__(1024) void sort_kernel(SortLaunch a) {
     }
     if (tid <= E) a.off[tid] = offs[tid];
     __syncthreads();
-    // Phase C: ordered walk of the segment.
-    for (int c0 = s0; c0 < s1; c0 += 64) {
+    // Phase C: ordered walk of the segment (ids loaded SORT_U rounds at a time).
+    for (int c1 = s0; c1 < s1; c1 += 64 * SORT_U) {
+      int eu[SORT_U];
+#pragma unroll
+      for (int u = 0; u < SORT_U; u++) {
+          const int i = c1 + 64 * u + lane;
+          eu[u] = i < s1 ? a.ids[i] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < SORT_U; u++) {
+        const int c0 = c1 + 64 * u;
+        if (c0 >= s1) break;
         int i = c0 + lane;
         bool live = i < s1;
-        int e = live ? a.ids[i] : -1;
+        int e = eu[u];
         bool ok = live && e >= 0 && e < E;
         int key = ok ? e : (live ? 2046 : 2047);
         uint64_t peers = ~0ull;
@@ -275,6 +297,7 @@ __global__ __launch_bounds__(1024) void sort_kernel(SortLaunch a) {
             a.inv[i] = slot;
             if (ok) a.xrow[slot] = i / a.k;
         }
+      }
     }
     // Tiles: expert e's slots off[e] .. off[e + 1] in chunks of a.chunk positions.
     if (tid < E) {

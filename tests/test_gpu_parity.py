@@ -303,7 +303,7 @@ def test_router_rejects_shapes(hip):
 
 
 @pytest.mark.parametrize("t,k,E,chunk", [(1, 8, 128, 128), (333, 8, 128, 128), (4096, 8, 128, 128), (50, 4, 7, 128),
-                                         (4096, 8, 128, 256), (333, 8, 128, 256)])
+                                         (4096, 8, 128, 256), (333, 8, 128, 256), (9001, 8, 128, 256)])
 def test_sort_bit_exact(hip, t, k, E, chunk):
     """chunk 128 is the reference's tile size (GEMM_BM, src/backend.rs:16); 256 fills this backend's GEMM blocks."""
     logits = zipf_logits(t, E, seed=t)
