@@ -190,9 +190,51 @@ __global__ __launch_bounds__(256) void combine_seq_kernel(float* x, const float*
     x[i] += y;
 }
 
+// The same, 4 consecutive outputs a thread (n % 4 == 0, x, ye and sh 16-byte aligned): the token's slots and weights
+// come through scalar loads, each output's sum keeps the pair order above.
+__global__ __launch_bounds__(256) void combine_seq4_kernel(float* x, const float* ye, const float* wts, const int* inv,
+                                                           int k, const float* sh, const float* sg, int n) {
+    const int t = blockIdx.y, d = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (d >= n) return;
+    float4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j0 = 0; j0 < k; j0 += 8) {
+        int sv[8];
+        float wv[8];
+        float4 yv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u < k ? j0 + u : k - 1;
+            sv[u] = j0 + u < k ? sload(inv + t * k + j) : -1;
+            wv[u] = sload(wts + t * k + j);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) yv[u] = *(const float4*)(ye + (uint64_t)(sv[u] >= 0 ? sv[u] : 0) * n + d);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (sv[u] >= 0) {
+                y.x += wv[u] * yv[u].x; y.y += wv[u] * yv[u].y;
+                y.z += wv[u] * yv[u].z; y.w += wv[u] * yv[u].w;
+            }
+        }
+    }
+    const uint64_t i = (uint64_t)t * n + d;
+    if (sh) {
+        const float gs = sg ? sigmoid_f32(sg[t]) : 1.0f;
+        const float4 s4 = *(const float4*)(sh + i);
+        y.x += gs * s4.x; y.y += gs * s4.y; y.z += gs * s4.z; y.w += gs * s4.w;
+    }
+    float4 o = *(const float4*)(x + i);
+    o.x += y.x; o.y += y.y; o.z += y.z; o.w += y.w;
+    *(float4*)(x + i) = o;
+}
+
 hipError_t launch_combine_seq(float* x, const float* ye, const float* wts, const int* inv, int k, const float* sh,
                               const float* sg, int n, int t, hipStream_t s) {
-    combine_seq_kernel<<<dim3((unsigned)((n + 255) / 256), (unsigned)t), dim3(256), 0, s>>>(x, ye, wts, inv, k, sh, sg, n);
+    const bool v4 = n % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)ye % 16 == 0 && (uintptr_t)sh % 16 == 0;
+    if (v4)
+        combine_seq4_kernel<<<dim3((unsigned)((n / 4 + 255) / 256), (unsigned)t), dim3(256), 0, s>>>(x, ye, wts, inv, k, sh, sg, n);
+    else
+        combine_seq_kernel<<<dim3((unsigned)((n + 255) / 256), (unsigned)t), dim3(256), 0, s>>>(x, ye, wts, inv, k, sh, sg, n);
     return hipGetLastError();
 }
 

@@ -365,6 +365,32 @@ def test_combine_seq_and_combine(hip):
     assert rel_l2(got, want) < 1e-6
 
 
+@pytest.mark.parametrize("n,k", [(300, 3), (302, 3), (2048, 9), (302, 9)])
+def test_combine_seq_paths(hip, n, k):
+    """moe_combine_seq in both of its kernels (4 outputs a thread when n % 4 == 0, else 1), more than 8 pairs a
+    token, rejected pairs (inv < 0) and a gated shared expert: bit-exact against the same float32 sums in pair order."""
+    t, ne = 6, 40
+    rng = np.random.default_rng(n + k)
+    x0, ye = normal((t, n), seed=7), normal((ne, n), seed=8)
+    wts = rng.uniform(0, 1, (t, k)).astype(np.float32)
+    inv = rng.integers(0, ne, (t, k)).astype(np.int32)
+    inv[1, 0] = inv[4, k - 1] = -1
+    sh, sg = normal((t, n), seed=9), normal(t, seed=10)
+    xb = up(hip, x0)
+    hip.moe_combine_seq(xb, up(hip, ye), up(hip, wts), up(hip, inv), k, up(hip, sh), up(hip, sg), n, t)
+    got = down(hip, xb, np.float32, t * n).reshape(t, n)
+    want = x0.copy()
+    for i in range(t):
+        y = np.zeros(n, dtype=np.float32)
+        for j in range(k):
+            if inv[i, j] >= 0:
+                y = y + wts[i, j] * ye[inv[i, j]]
+        gs = np.float32(1.0) / (np.float32(1.0) + np.float32(np.exp(-np.float64(sg[i]))))
+        y = y + gs * sh[i]
+        want[i] = want[i] + y
+    assert np.array_equal(got, want)
+
+
 def test_swiglu_q(hip):
     n, rows = 768, 8
     g, u = normal((rows, n), seed=1), normal((rows, n), seed=2)
