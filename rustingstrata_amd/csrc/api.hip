@@ -320,7 +320,7 @@ int strata_dequant(strata_ctx* c, const strata_tensor* w, uint64_t rows, uint64_
 int strata_quant_xq(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t n, uint64_t nt, uint64_t out) {
     if (check_ctx(c)) return -1;
     if (n % 32) return set_error("quant_xq: " + std::to_string(n) + " values (a multiple of 32)");
-    if (n > (1u << 30) || nt > 65535) return set_error("quant_xq: too large");
+    if (n > (1u << 30) || nt > (1u << 30) || nt * ((n + 255) / 256) > (1ull << 34)) return set_error("quant_xq: too large");
     STRATA_HIP(launch_quant_xq((const float*)x, x_stride, (int)n, (int)nt, (int8_t*)out, c->numerics, c->stream));
     return 0;
 }
@@ -446,7 +446,8 @@ int strata_swiglu_q(strata_ctx* c, uint64_t g, uint64_t u, uint64_t n, uint64_t 
     if (check_ctx(c)) return -1;
     if (n % 32) return set_error("swiglu_q: " + std::to_string(n) + " values (a multiple of 32)");
     if (!xq) return set_error("swiglu_q: null xq");
-    if (rows > 65535 || n > (1u << 30)) return set_error("swiglu_q: too large (rows at most 65535)");
+    if (rows > (1u << 30) || n > (1u << 30) || rows * ((n + 255) / 256) > (1ull << 34))
+        return set_error("swiglu_q: too large");
     STRATA_HIP(launch_swiglu_q((const float*)g, (const float*)u, (int)n, (int)rows, (int8_t*)xq, c->numerics, c->stream));
     if (ret) *ret = xq;
     return 0;

@@ -266,7 +266,7 @@ __device__ __forceinline__ void quant8_lds(const float (&v)[8], int i, bool live
 }
 
 typedef float v4f __attribute__((ext_vector_type(4)));
-template <bool Q32>
+template <bool Q32, bool SW>
 __device__ __forceinline__ void quant_row_lds(uint64_t xr, uint64_t ur, int n, int8_t* q, float* d) {
     for (int c0 = 0; c0 < n; c0 += 8 * (int)blockDim.x) {
         const int i = c0 + threadIdx.x * 8;
@@ -275,7 +275,7 @@ __device__ __forceinline__ void quant_row_lds(uint64_t xr, uint64_t ur, int n, i
         if (live) {
             const v4f p = *gptr<v4f>(xr + 4 * (uint64_t)i), r = *gptr<v4f>(xr + 4 * (uint64_t)i + 16);
             v[0] = p.x; v[1] = p.y; v[2] = p.z; v[3] = p.w; v[4] = r.x; v[5] = r.y; v[6] = r.z; v[7] = r.w;
-            if (ur) {
+            if constexpr (SW) {
                 const v4f pu = *gptr<v4f>(ur + 4 * (uint64_t)i), ru = *gptr<v4f>(ur + 4 * (uint64_t)i + 16);
                 const float u[8] = {pu.x, pu.y, pu.z, pu.w, ru.x, ru.y, ru.z, ru.w};
 #pragma unroll
@@ -290,7 +290,7 @@ __device__ __forceinline__ void quant_row_lds(uint64_t xr, uint64_t ur, int n, i
 }
 
 // x row xrow into the block's LDS copy (int8, then per-32 scales): copied from xq, or quantized from f32.
-template <bool Q32>
+template <bool Q32, bool SW>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl, float* xld) {
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     if (a.xq) {
@@ -298,8 +298,8 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl,
         for (int c = threadIdx.x; c < a.cols / 16; c += blockDim.x) *(v4u*)(xl + 16 * c) = *gptr<v4u>(q + 16 * c);
         for (int c = threadIdx.x; c < a.cols / 32; c += blockDim.x) xld[c] = *gptr<float>(d + 4 * c);
     } else {
-        quant_row_lds<Q32>((uint64_t)(a.xf + (uint64_t)xrow * a.x_stride),
-                           a.xu ? (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) : 0, a.cols, xl, xld);
+        quant_row_lds<Q32, SW>((uint64_t)(a.xf + (uint64_t)xrow * a.x_stride),
+                               SW ? (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) : 0, a.cols, xl, xld);
     }
     // zeros up to whole super-blocks (Q8_0 rows may end inside one)
     const int n = a.cols, nup = (n + 255) & ~255;
@@ -315,6 +315,7 @@ struct XEarly {
     v4u q;
     float d;
 };
+template <bool SW>
 __device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) {
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x;
@@ -325,14 +326,14 @@ __device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) 
         const uint64_t xr = (uint64_t)(a.xf + (uint64_t)xrow * a.x_stride) + 32 * (uint64_t)tid;
         e.f0 = *gptr<v4f>(xr);
         e.f1 = *gptr<v4f>(xr + 16);
-        if (a.xu) {
+        if constexpr (SW) {
             const uint64_t ur = (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) + 32 * (uint64_t)tid;
             e.u0 = *gptr<v4f>(ur);
             e.u1 = *gptr<v4f>(ur + 16);
         }
     }
 }
-template <bool Q32>
+template <bool Q32, bool SW>
 __device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t* xl, float* xld) {
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, n = a.cols;
@@ -342,7 +343,7 @@ __device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t
     } else {
         const bool live = 8 * tid < n;
         float v[8] = {e.f0.x, e.f0.y, e.f0.z, e.f0.w, e.f1.x, e.f1.y, e.f1.z, e.f1.w};
-        if (a.xu) {
+        if constexpr (SW) {
             const float u[8] = {e.u0.x, e.u0.y, e.u0.z, e.u0.w, e.u1.x, e.u1.y, e.u1.z, e.u1.w};
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = silu_f32(v[j]) * u[j];
@@ -379,7 +380,9 @@ __device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const flo
 #else
 #define GEMV1_ATTR
 #endif
-template <int T, bool Q32>
+// SW: x rows are silu(xf) * xu (the fused SwiGLU input of the down projection); a separate instantiation, so the
+// plain GEMV carries none of it.
+template <int T, bool Q32, bool SW>
 __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs a) {
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
@@ -446,7 +449,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     Span sp = span(t);
     const bool early = a.cols <= 8 * GEMV1_THREADS;
     XEarly xe;
-    if (early) x_fetch(a, sp.xrow, xe);
+    if (early) x_fetch<SW>(a, sp.xrow, xe);
     issue(sp);
     // the tile after next is located while the next one is in flight
     int tn = next_valid(t + gridDim.x);
@@ -462,8 +465,8 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     while (true) {
         __syncthreads();  // the previous tile's readers are done with the LDS tile
         if (sp.xrow != cur_xrow) {
-            if (early && cur_xrow < 0) x_put<Q32>(a, xe, xl, xld);
-            else stage_x<Q32>(a, sp.xrow, xl, xld);
+            if (early && cur_xrow < 0) x_put<Q32, SW>(a, xe, xl, xld);
+            else stage_x<Q32, SW>(a, sp.xrow, xl, xld);
             __syncthreads();
 #ifdef STRATA_GEMV1_XLDS
             for (int c = tid; c < (int)ncp / 16; c += GEMV1_THREADS) {
@@ -513,7 +516,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     }
 }
 
-template <int T, bool Q32>
+template <int T, bool Q32, bool SW>
 static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
     static int ncu = 0, per_cu = 0;
     static size_t cached_smem = 0;
@@ -524,19 +527,20 @@ static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, 
     }
     if (cached_smem != smem) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv1_kernel<T, Q32>, GEMV1_THREADS, smem) != hipSuccess || n < 1) n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv1_kernel<T, Q32, SW>, GEMV1_THREADS, smem) != hipSuccess || n < 1) n = 1;
         per_cu = n;
         cached_smem = smem;
     }
     long long blocks = (long long)per_cu * ncu;
     if (blocks > tiles) blocks = tiles;
-    gemv1_kernel<T, Q32><<<dim3((unsigned)blocks), GEMV1_THREADS, smem, s>>>(a);
+    gemv1_kernel<T, Q32, SW><<<dim3((unsigned)blocks), GEMV1_THREADS, smem, s>>>(a);
     return hipGetLastError();
 }
 
 template <int T>
 static hipError_t gemv1_t(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
-    return a.per32 ? gemv1_launch<T, true>(a, tiles, smem, s) : gemv1_launch<T, false>(a, tiles, smem, s);
+    if (a.xu) return a.per32 ? gemv1_launch<T, true, true>(a, tiles, smem, s) : gemv1_launch<T, false, true>(a, tiles, smem, s);
+    return a.per32 ? gemv1_launch<T, true, false>(a, tiles, smem, s) : gemv1_launch<T, false, false>(a, tiles, smem, s);
 }
 
 template <int T, int NT, bool Q32>

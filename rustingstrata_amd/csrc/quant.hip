@@ -47,8 +47,8 @@ hipError_t launch_dequant(int ty, const uint8_t* w, uint64_t rows, uint64_t cols
     return hipErrorInvalidValue;
 }
 
-// quant_xq. A group of 32 lanes covers 256 values, 8 per lane (the Q8_K block); a block of 256 threads covers 2048
-// values of one row (grid = (ceil(n / 2048), nt)). Lanes past n hold zeros, which is quantize_q8k's zero padding.
+// quant_xq. A group of 32 lanes covers 256 values, 8 per lane (the Q8_K block); the launch's groups walk the rows'
+// blocks in order, 8 groups to a 256-thread block. Lanes past n hold zeros, which is quantize_q8k's zero padding.
 //  Q8K: the block's scale is -127 / (the signed value of largest magnitude, the first such), q = min(127,
 //       round-half-even(is * v)), d = 1 / is for each of its 32-groups (src/cpu_moe.rs:28-46).
 //  Q8_32: per 32 values (4 lanes) d = max|v| / 127, q = round-half-even(v * 127 / max|v|) (src/cuda/kernels.cu:640-660).
@@ -105,8 +105,13 @@ __device__ __forceinline__ void quant8_group(const float (&v)[8], int i, bool li
 template <bool SWIGLU>
 __global__ __launch_bounds__(256) void quant_xq_kernel(const float* __restrict__ x, const float* __restrict__ u,
                                                        uint64_t x_stride, int n, int nt, int8_t* __restrict__ out, int mode) {
-    int t = blockIdx.y;
-    int i = blockIdx.x * 2048 + threadIdx.x * 8;
+    // 32-lane group gi of the launch quantizes 256-value block gi mod gpr of row gi / gpr (rows narrower than 2048
+    // values share a block); a group past the last row leaves as a whole, so its exchange steps involve only itself
+    const int gpr = (n + 255) >> 8;
+    const uint64_t gi = (uint64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int t = (int)(gi / (uint64_t)gpr);
+    if (t >= nt) return;
+    const int i = (int)(gi - (uint64_t)t * gpr) * 256 + (threadIdx.x & 31) * 8;
     const float* xr = x + (uint64_t)t * x_stride;
     float v[8];
     bool live = i < n;
@@ -183,13 +188,15 @@ hipError_t launch_rms_norm_q(float* x, uint64_t x_stride, const float* w, float*
 
 hipError_t launch_quant_xq(const float* x, uint64_t x_stride, int n, int nt, int8_t* out, int mode, hipStream_t s) {
     if (!n || !nt) return hipSuccess;
-    quant_xq_kernel<false><<<dim3((unsigned)((n + 2047) / 2048), (unsigned)nt), dim3(256), 0, s>>>(x, nullptr, x_stride, n, nt, out, mode);
+    const uint64_t groups = (uint64_t)nt * ((n + 255) / 256);
+    quant_xq_kernel<false><<<dim3((unsigned)((groups + 7) / 8)), dim3(256), 0, s>>>(x, nullptr, x_stride, n, nt, out, mode);
     return hipGetLastError();
 }
 
 hipError_t launch_swiglu_q(const float* g, const float* u, int n, int rows, int8_t* xq, int mode, hipStream_t s) {
     if (!n || !rows) return hipSuccess;
-    quant_xq_kernel<true><<<dim3((unsigned)((n + 2047) / 2048), (unsigned)rows), dim3(256), 0, s>>>(g, u, n, n, rows, xq, mode);
+    const uint64_t groups = (uint64_t)rows * ((n + 255) / 256);
+    quant_xq_kernel<true><<<dim3((unsigned)((groups + 7) / 8)), dim3(256), 0, s>>>(g, u, n, n, rows, xq, mode);
     return hipGetLastError();
 }
 

@@ -72,6 +72,22 @@ def test_quant_xq_q8k_bit_exact(hip, n, nt):
         assert np.array_equal(sc[t].view(np.uint32), np.repeat(d, 8)[: n // 32].view(np.uint32))
 
 
+def test_quant_xq_many_rows(hip):
+    """More rows than one grid dimension addresses (66000 rows of 256): sampled rows bit-exact."""
+    n, nt = 256, 66000
+    x = normal((nt, n), seed=77)
+    xb = up(hip, x)
+    out = hip.alloc(nt * (n + n // 8))
+    hip.quant_xq(xb, n, n, nt, out)
+    raw = down(hip, out, np.uint8, nt * (n + n // 8))
+    q = raw[: nt * n].view(np.int8).reshape(nt, n)
+    sc = raw[nt * n:].view(np.float32).reshape(nt, n // 32)
+    for t in [0, 1, 65534, 65535, 65536, nt - 1] + list(np.random.default_rng(1).integers(0, nt, 10)):
+        d, qs, _ = O.quantize_q8k(x[t])
+        assert np.array_equal(q[t], qs.reshape(-1))
+        assert np.array_equal(sc[t].view(np.uint32), np.repeat(d, 8).view(np.uint32))
+
+
 def test_quant_xq_q8k_magnitude_tie(hip):
     """Equal largest magnitudes of opposite sign in one 256-block, in different 16-lane rows: the first one sets the
     scale's sign (src/cpu_moe.rs:28-46), whatever order the lanes compare in."""
@@ -293,7 +309,9 @@ def test_rejects_oversized_grids(hip):
     with pytest.raises(S.StrataError, match="moe_combine: too large"):
         hip.moe_combine(b, b, b, 8, 0, 0, 2048, 70000)
     with pytest.raises(S.StrataError, match="swiglu_q: too large"):
-        hip.swiglu_q(b, b, 768, 70000, b)
+        hip.swiglu_q(b, b, 768, 1 << 31, b)
+    with pytest.raises(S.StrataError, match="quant_xq: too large"):
+        hip.quant_xq(b, 768, 768, 1 << 31, b)
 
 
 def test_router_rejects_shapes(hip):
