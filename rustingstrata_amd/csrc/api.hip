@@ -507,7 +507,7 @@ int strata_moe_sort(strata_ctx* c, uint64_t ids, uint64_t t, uint64_t k, uint64_
     for (uint64_t m = 0; m < n_mats; m++) { s.bases[m] = bases[m]; s.strides[m] = strides[m]; }
     s.tiles = (uint64_t*)tiles; s.max_tiles = (int)max_tiles; s.n_tiles = (int*)n_tiles_dev; s.err = (int*)err_dev;
     s.chunk = (int)chunk;
-    STRATA_HIP(c->misc.need(sort_scratch_bytes((int)n_expert), c->stream));
+    STRATA_HIP(c->misc.need(sort_scratch_bytes((int)n_expert, (int)(t * k)), c->stream));
     s.scratch = (int*)c->misc.p;
     STRATA_HIP(launch_sort(s, c->stream));
     return 0;

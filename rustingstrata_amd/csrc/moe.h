@@ -26,9 +26,9 @@ struct SortLaunch {
     int chunk = 128;            // positions per tile
     int* n_tiles = nullptr;
     int* err = nullptr;
-    int* scratch = nullptr;
+    int* scratch = nullptr;     // sort_scratch_bytes(n_expert, t * k) bytes
 };
-size_t sort_scratch_bytes(int n_expert);
+size_t sort_scratch_bytes(int n_expert, int n_pairs);
 hipError_t launch_sort(const SortLaunch& a, hipStream_t s);
 
 }  // namespace strata

@@ -239,113 +239,120 @@ hipError_t launch_combine_seq(float* x, const float* ye, const float* wts, const
 }
 
 // ---- stable sort of the (token, j) pairs by expert, and the tile lists ----
-// One block of 16 waves. Wave w owns the contiguous pair segment w; phase A counts its experts, phase B turns the
-// counts into each (wave, expert) start slot (experts ascending, waves in order within an expert), phase C walks each
-// segment in order assigning slots, 64 pairs at a time with the rank among equal experts inside the wave. The result
-// is the host counting sort of src/gpu_model/prefill.rs:563-573 exactly.
-constexpr int SORT_WAVES = 16, SORT_MAX_E = 512, SORT_U = 8;
+// The host counting sort of src/gpu_model/prefill.rs:563-573, exactly, in three launches over W waves, wave gw owning
+// the contiguous pair segment [gw S, (gw + 1) S):
+//   count:   each wave counts its segment's experts into cnt[e * W + gw] (expert-major) and its bad ids into bad[gw];
+//   scan:    one block turns each expert's row of cnt into exclusive prefixes over the waves (a wave of the block
+//            per expert, coalesced) and the experts' totals into off (experts ascending); writes the tile lists, the
+//            tile count and the bad-id count;
+//   scatter: each wave starts expert e at off[e] + its prefix (waves in order within an expert) and walks its
+//            segment in order, 64 pairs at a time, assigning slots with the rank among equal experts inside the 64
+//            (ballot match on the key bits).
+constexpr int SORT_WAVES = 16, SORT_MAX_E = 512, SORT_U = 4, SORT_SEG = 64 * SORT_U;
 
-size_t sort_scratch_bytes(int) { return 16; }
+static int sort_waves(int n_pairs) { return n_pairs > 0 ? (n_pairs + SORT_SEG - 1) / SORT_SEG : 1; }
+size_t sort_scratch_bytes(int n_expert, int n_pairs) {
+    const int W = sort_waves(n_pairs);
+    return ((size_t)n_expert * W + W) * sizeof(int);
+}
 
-__global__ __launch_bounds__(1024) void sort_kernel(SortLaunch a) {
+// The ids of a wave's segment, SORT_U rounds of 64 (their loads in flight together); -1 past the segment.
+__device__ __forceinline__ void sort_ids(const int* ids, int s0, int s1, int lane, int (&eu)[SORT_U]) {
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+        const int i = s0 + 64 * u + lane;
+        eu[u] = i < s1 ? ids[i] : -1;
+    }
+}
+
+__global__ __launch_bounds__(1024) void sort_count_kernel(SortLaunch a, int W) {
     __shared__ int hist[SORT_WAVES][SORT_MAX_E];
-    __shared__ int offs[SORT_MAX_E + 1], tbase[SORT_MAX_E + 1];
-    __shared__ int bad;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, E = a.n_expert;
-    const int N = a.t * a.k, S = (N + SORT_WAVES - 1) / SORT_WAVES;
-    const int s0 = min(N, wave * S), s1 = min(N, s0 + S);
-    for (int i = tid; i < SORT_WAVES * SORT_MAX_E; i += 1024) (&hist[0][0])[i] = 0;
-    if (tid == 0) bad = 0;
-    __syncthreads();
-    // the ids arrive SORT_U rounds of 64 at a time (their loads in flight together), then are taken in order
-    for (int c0 = s0; c0 < s1; c0 += 64 * SORT_U) {
-        int eu[SORT_U];
+    const int gw = blockIdx.x * SORT_WAVES + wave, N = a.t * a.k;
+    for (int e = lane; e < E; e += 64) hist[wave][e] = 0;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    if (gw >= W) return;
+    const int s0 = min(N, gw * SORT_SEG), s1 = min(N, s0 + SORT_SEG);
+    int eu[SORT_U];
+    sort_ids(a.ids, s0, s1, lane, eu);
+    int bad = 0;
 #pragma unroll
-        for (int u = 0; u < SORT_U; u++) {
-            const int i = c0 + 64 * u + lane;
-            eu[u] = i < s1 ? a.ids[i] : 0;
-        }
-#pragma unroll
-        for (int u = 0; u < SORT_U; u++) {
-            if (c0 + 64 * u + lane < s1) {
-                const int e = eu[u];
-                if (e >= 0 && e < E) atomicAdd(&hist[wave][e], 1);
-                else atomicAdd(&bad, 1);
-            }
+    for (int u = 0; u < SORT_U; u++) {
+        if (s0 + 64 * u + lane < s1) {
+            const int e = eu[u];
+            if (e >= 0 && e < E) atomicAdd(&hist[wave][e], 1);
+            else bad++;
         }
     }
-    __syncthreads();
-    // Per-expert counts and tile counts (thread e), then exclusive scans over experts (one wave, in order).
-    int cnt = 0;
-    if (tid < E) {
-        for (int w = 0; w < SORT_WAVES; w++) cnt += hist[w][tid];
-        offs[tid] = cnt;
-        tbase[tid] = (cnt + a.chunk - 1) / a.chunk;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    for (int e = lane; e < E; e += 64) a.scratch[(uint64_t)e * W + gw] = hist[wave][e];
+    bad += __shfl_xor(bad, 1);
+    bad += __shfl_xor(bad, 2);
+    bad += __shfl_xor(bad, 4);
+    bad += __shfl_xor(bad, 8);
+    bad += __shfl_xor(bad, 16);
+    bad += __shfl_xor(bad, 32);
+    if (lane == 0) a.scratch[(uint64_t)E * W + gw] = bad;
+}
+
+__global__ __launch_bounds__(1024) void sort_scan_kernel(SortLaunch a, int W) {
+    __shared__ int part[16];
+    __shared__ int offs[SORT_MAX_E + 1], tbase[SORT_MAX_E + 1];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, E = a.n_expert;
+    int* cnt = a.scratch;
+    const uint64_t L = (uint64_t)E * W;
+    // expert e's row of wave counts (coalesced, 64 waves at a time) into exclusive prefixes within the expert; the
+    // expert's total into offs[e]
+    for (int e = wave; e < E; e += 16) {
+        int carry = 0;
+        for (int w0 = 0; w0 < W; w0 += 64) {
+            const int w = w0 + lane;
+            const int c = w < W ? cnt[(uint64_t)e * W + w] : 0;
+            const int inc = wave_incl_scan(c);
+            if (w < W) cnt[(uint64_t)e * W + w] = carry + inc - c;
+            carry += __builtin_amdgcn_readlane(inc, 63);
+        }
+        if (lane == 0) offs[e] = carry;
     }
+    // the bad-id count: each thread sums waves tid, tid + 1024, ..., then the block in order
+    int bad = 0;
+    if (a.err)
+        for (int w = tid; w < W; w += 1024) bad += cnt[L + w];
     __syncthreads();
-    if (wave == 0) {
-        int run = 0, trun = 0;
+    if (wave == 0) {  // exclusive scan of the expert totals, in expert order
+        int run = 0;
         for (int e0 = 0; e0 < E; e0 += 64) {
-            int e = e0 + lane;
-            int c = e < E ? offs[e] : 0, tc = e < E ? tbase[e] : 0;
-            int ic = c, itc = tc;  // inclusive scans within the wave
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                int y = __shfl_up(ic, o), ty = __shfl_up(itc, o);
-                if (lane >= o) { ic += y; itc += ty; }
-            }
-            if (e < E) { offs[e] = run + ic - c; tbase[e] = trun + itc - tc; }
-            run += __shfl(ic, 63);
-            trun += __shfl(itc, 63);
+            const int e = e0 + lane;
+            const int c = e < E ? offs[e] : 0;
+            const int ic = wave_incl_scan(c);
+            if (e < E) offs[e] = run + ic - c;
+            run += __builtin_amdgcn_readlane(ic, 63);
         }
-        if (lane == 0) { offs[E] = run; tbase[E] = trun; }
+        if (lane == 0) offs[E] = run;
     }
     __syncthreads();
-    if (tid < E) {  // (wave, expert) start slots
-        int b = offs[tid];
-        for (int w = 0; w < SORT_WAVES; w++) { int h = hist[w][tid]; hist[w][tid] = b; b += h; }
+    if (tid < E) tbase[tid] = (offs[tid + 1] - offs[tid] + a.chunk - 1) / a.chunk;
+    __syncthreads();
+    if (wave == 0) {  // exclusive scan of the tile counts over experts, in order
+        int trun = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + lane;
+            const int tc = e < E ? tbase[e] : 0;
+            const int itc = wave_incl_scan(tc);
+            if (e < E) tbase[e] = trun + itc - tc;
+            trun += __builtin_amdgcn_readlane(itc, 63);
+        }
+        if (lane == 0) tbase[E] = trun;
     }
+    __syncthreads();
     if (tid <= E) a.off[tid] = offs[tid];
-    __syncthreads();
-    // Phase C: ordered walk of the segment (ids loaded SORT_U rounds at a time).
-    for (int c1 = s0; c1 < s1; c1 += 64 * SORT_U) {
-      int eu[SORT_U];
-#pragma unroll
-      for (int u = 0; u < SORT_U; u++) {
-          const int i = c1 + 64 * u + lane;
-          eu[u] = i < s1 ? a.ids[i] : -1;
-      }
-#pragma unroll
-      for (int u = 0; u < SORT_U; u++) {
-        const int c0 = c1 + 64 * u;
-        if (c0 >= s1) break;
-        int i = c0 + lane;
-        bool live = i < s1;
-        int e = eu[u];
-        bool ok = live && e >= 0 && e < E;
-        int key = ok ? e : (live ? 2046 : 2047);
-        uint64_t peers = ~0ull;
-#pragma unroll
-        for (int b = 0; b < 11; b++) {
-            uint64_t m = __ballot((key >> b) & 1);
-            peers &= ((key >> b) & 1) ? m : ~m;
-        }
-        int rank = __popcll(peers & ((1ull << lane) - 1));
-        int slot = ok ? hist[wave][e] + rank : -1;
-        __builtin_amdgcn_wave_barrier();
-        if (ok && rank == 0) hist[wave][e] += __popcll(peers);
-        __builtin_amdgcn_wave_barrier();
-        if (live) {
-            a.inv[i] = slot;
-            if (ok) a.xrow[slot] = i / a.k;
-        }
-      }
-    }
     // Tiles: expert e's slots off[e] .. off[e + 1] in chunks of a.chunk positions.
     if (tid < E) {
-        int c = offs[tid + 1] - offs[tid], tb = tbase[tid];
+        const int c = offs[tid + 1] - offs[tid], tb = tbase[tid];
         for (int j = 0; j * a.chunk < c; j++) {
-            uint64_t m0 = (uint64_t)(offs[tid] + j * a.chunk), cn = (uint64_t)min(a.chunk, c - j * a.chunk);
+            const uint64_t m0 = (uint64_t)(offs[tid] + j * a.chunk), cn = (uint64_t)min(a.chunk, c - j * a.chunk);
             for (int m = 0; m < a.n_mats; m++) {
                 uint64_t* tl = a.tiles + 2 * ((uint64_t)m * a.max_tiles + tb + j);
                 tl[0] = a.bases[m] + (uint64_t)tid * a.strides[m];
@@ -353,14 +360,65 @@ __global__ __launch_bounds__(1024) void sort_kernel(SortLaunch a) {
             }
         }
     }
+    if (a.err) {
+        bad = __builtin_amdgcn_readlane(wave_incl_scan(bad), 63);
+        if (lane == 0) part[wave] = bad;
+    }
+    __syncthreads();
     if (tid == 0) {
         *a.n_tiles = tbase[E];
-        if (a.err) *a.err = bad;
+        if (a.err) {
+            int b = 0;
+            for (int w = 0; w < 16; w++) b += part[w];
+            *a.err = b;
+        }
+    }
+}
+
+__global__ __launch_bounds__(1024) void sort_scatter_kernel(SortLaunch a, int W) {
+    __shared__ int hist[SORT_WAVES][SORT_MAX_E];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, E = a.n_expert;
+    const int gw = blockIdx.x * SORT_WAVES + wave, N = a.t * a.k;
+    if (gw >= W) return;
+    const int s0 = min(N, gw * SORT_SEG), s1 = min(N, s0 + SORT_SEG);
+    int eu[SORT_U];
+    sort_ids(a.ids, s0, s1, lane, eu);
+    for (int e = lane; e < E; e += 64) hist[wave][e] = a.off[e] + a.scratch[(uint64_t)e * W + gw];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int u = 0; u < SORT_U; u++) {
+        const int c0 = s0 + 64 * u;
+        if (c0 >= s1) break;
+        const int i = c0 + lane;
+        const bool live = i < s1;
+        const int e = eu[u];
+        const bool ok = live && e >= 0 && e < E;
+        const int key = ok ? e : (live ? 2046 : 2047);
+        uint64_t peers = ~0ull;
+#pragma unroll
+        for (int b = 0; b < 11; b++) {
+            const uint64_t m = __ballot((key >> b) & 1);
+            peers &= ((key >> b) & 1) ? m : ~m;
+        }
+        const int rank = __popcll(peers & ((1ull << lane) - 1));
+        const int slot = ok ? hist[wave][e] + rank : -1;
+        __builtin_amdgcn_wave_barrier();
+        if (ok && rank == 0) hist[wave][e] += __popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (live) {
+            a.inv[i] = slot;
+            if (ok) a.xrow[slot] = i / a.k;
+        }
     }
 }
 
 hipError_t launch_sort(const SortLaunch& a, hipStream_t s) {
-    sort_kernel<<<1, 1024, 0, s>>>(a);
+    const int W = sort_waves(a.t * a.k), blocks = (W + SORT_WAVES - 1) / SORT_WAVES;
+    sort_count_kernel<<<blocks, 1024, 0, s>>>(a, W);
+    sort_scan_kernel<<<1, 1024, 0, s>>>(a, W);
+    sort_scatter_kernel<<<blocks, 1024, 0, s>>>(a, W);
     return hipGetLastError();
 }
 

@@ -21,4 +21,17 @@ __device__ __forceinline__ int xl32(int v) {
 template <int STEP>
 __device__ __forceinline__ float xl32f(float v) { return __int_as_float(xl32<STEP>(__float_as_int(v))); }
 
+// Inclusive prefix sum over the 64 lanes of a wave in lane order, by DPP: Hillis-Steele shifts within each row of 16
+// (lanes shifted in from outside the row read 0), then row 0's and row 2's totals added into rows 1 and 3, then
+// lane 31's into rows 2 and 3.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1 and 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
 }  // namespace strata
