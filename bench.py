@@ -163,9 +163,9 @@ def bench_moe(hip, S, ggml, T, iters):
     chunk = hip.gemm_block_positions()  # tile lists sized to the GEMM's blocks
     max_tiles = T * k // chunk + E
     off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
-    tiles, ntd = hip.alloc(3 * max_tiles * 16), hip.alloc(4)
+    tiles, ntd = hip.alloc(2 * max_tiles * 16), hip.alloc(4)
     ge, ye, x = hip.alloc(T * k * F * 4), hip.alloc(T * k * H * 4), hip.alloc(T * H * 4)
-    mats = [(int(g_b), F * rb_gu), (int(u_b), F * rb_gu), (int(d_b), H * rb_d)]
+    mats = [(int(g_b), F * rb_gu), (int(d_b), H * rb_d)]  # tile lists of the gate (up: + u_b - g_b) and down
     ev = [hip.event() for _ in range(4)]
 
     def layer(timed=False):
@@ -173,10 +173,9 @@ def bench_moe(hip, S, ggml, T, iters):
         hip.moe_sort(ids, T, k, E, off, xrow, inv, mats, tiles, max_tiles, ntd, chunk=chunk)
         if timed:
             hip.record(ev[1])
-        hip.gemm_grouped(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, S.ACT_STORE)
-        hip.gemm_grouped(ggml.Q5_K, F, H, int(tiles) + max_tiles * 16, max_tiles, ntd, hb, H, T, xrow, ge, F,
-                         S.ACT_SWIGLU | S.SAME_X)
-        hip.gemm_grouped(ggml.Q6_K, H, F, int(tiles) + 2 * max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
+        # gate and up in one grouped GEMM: ge = silu(W_gate x) * (W_up x) (the bits of the two-call sequence)
+        hip.gemm_grouped_gate_up(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b))
+        hip.gemm_grouped(ggml.Q6_K, H, F, int(tiles) + max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
                          S.ACT_STORE)
         if timed:
             hip.record(ev[2])

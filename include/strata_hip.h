@@ -190,6 +190,14 @@ int strata_gemm(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t 
 int strata_gemm_grouped(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t max_tiles,
                         uint64_t n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y,
                         uint64_t y_stride, int act);
+/* The gate and up projections of the prefill MoE block in one grouped GEMM (src/gpu_model/prefill.rs: gemm of the
+ * gate experts with act store, then of the up experts with act SwiGLU over the same tiles and X): for each tile the
+ * up matrix is the gate matrix's address + up_offset bytes, and y[m, 0..rows) = silu(W_gate x) * (W_up x), the same
+ * bits as the two calls. rows must be a multiple of 64, y rows 16-byte aligned; not for Q8_0. flags: STRATA_SAME_X
+ * or 0, as in strata_gemm. */
+int strata_gemm_grouped_gate_up(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t tiles,
+                                uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x,
+                                uint64_t xrow, uint64_t y, uint64_t y_stride, int64_t up_offset, int flags);
 /* Backend::gemm_dense (src/backend.rs:196): y[m] (op) W x[m] for m < n, one matrix (tiles of 128 positions,
  * src/cuda/mod.rs:908-910). */
 int strata_gemm_dense(strata_ctx* ctx, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride, uint64_t y,

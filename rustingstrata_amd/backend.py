@@ -75,6 +75,7 @@ SIGNATURES = {
                         U64, U64, U64, U64, U64],
     "strata_gemm": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32],
     "strata_gemm_grouped": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32],
+    "strata_gemm_grouped_gate_up": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_int64, I32],
     "strata_gemm_dense": [CTX, TP, U64, U64, U64, U64, U64, I32],
     "strata_gemm_block_positions": [],
     "strata_int8_gemm": [CTX, I32],
@@ -335,6 +336,12 @@ class HipBackend:
     def gemm(self, ty, rows, cols, tiles, n_tiles, x, x_stride, n_x, xrow, y, y_stride, act):
         _check(lib().strata_gemm(self._ctx, ty, rows, cols, int(tiles), n_tiles, int(x), x_stride, n_x, int(xrow),
                                  int(y), y_stride, act))
+
+    def gemm_grouped_gate_up(self, ty, rows, cols, tiles, max_tiles, n_tiles_dev, x, x_stride, n_x, xrow, y,
+                             y_stride, up_offset, flags=0):
+        """y = silu(W_gate x) * (W_up x) over a gate tile list; the up matrix sits up_offset bytes after each gate."""
+        _check(lib().strata_gemm_grouped_gate_up(self._ctx, ty, rows, cols, int(tiles), max_tiles, int(n_tiles_dev),
+                                                 int(x), x_stride, n_x, int(xrow), int(y), y_stride, up_offset, flags))
 
     def gemm_grouped(self, ty, rows, cols, tiles, max_tiles, n_tiles_dev, x, x_stride, n_x, xrow, y, y_stride, act):
         _check(lib().strata_gemm_grouped(self._ctx, ty, rows, cols, int(tiles), max_tiles, int(n_tiles_dev), int(x),

@@ -529,7 +529,8 @@ static int gemm_x(strata_ctx* c, uint64_t cols, uint64_t n_x, uint64_t x, uint64
 
 static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t n_tiles,
                        const int* n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y,
-                       uint64_t y_stride, int act, const uint8_t* dense_w, uint64_t dense_n) {
+                       uint64_t y_stride, int act, const uint8_t* dense_w, uint64_t dense_n, bool pair = false,
+                       int64_t w2 = 0) {
     if (check_ctx(c) || check_type(ty)) return -1;
     if (cols == 0 || cols % 256)
         return set_error(std::string(type_name(ty)) + " matrix with " + std::to_string(cols) + " columns: GEMM needs a multiple of 256");
@@ -549,6 +550,7 @@ static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint
     g.dense_w = dense_w; g.dense_n = (int)dense_n;
     g.xq = (const uint8_t*)xq; g.n_x = (int)n_x; g.xrow = (const int*)xrow;
     g.y = (float*)y; g.y_stride = (int64_t)y_stride; g.act = op;
+    g.pair = pair; g.w2 = w2;
     STRATA_HIP(launch_gemm(g, c->stream));
     return 0;
 }
@@ -565,6 +567,20 @@ int strata_gemm_grouped(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uin
     if (!tiles || !n_tiles_dev) return set_error("gemm_grouped: null tile list or count");
     return gemm_common(c, ty, rows, cols, tiles, max_tiles, (const int*)n_tiles_dev, x, x_stride, n_x, xrow, y, y_stride,
                        act, nullptr, 0);
+}
+
+int strata_gemm_grouped_gate_up(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t tiles,
+                                uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x,
+                                uint64_t xrow, uint64_t y, uint64_t y_stride, int64_t up_offset, int flags) {
+    if (check_ctx(c) || check_type(ty)) return -1;
+    if (!tiles || !n_tiles_dev) return set_error("gemm_grouped_gate_up: null tile list or count");
+    if (ty == Q8_0) return set_error("gemm_grouped_gate_up: Q8_0 has no fused gate/up kernel (use two gemm_grouped calls)");
+    if (rows % 64) return set_error("gemm_grouped_gate_up: " + std::to_string(rows) + " rows (a multiple of 64)");
+    if (y % 16 || y_stride % 4) return set_error("gemm_grouped_gate_up: y rows must be 16-byte aligned");
+    if (check_align(ty, (uint64_t)up_offset, "gemm_grouped_gate_up up offset")) return -1;
+    if (flags & ~STRATA_SAME_X) return set_error("gemm_grouped_gate_up: flags " + std::to_string(flags));
+    return gemm_common(c, ty, rows, cols, tiles, max_tiles, (const int*)n_tiles_dev, x, x_stride, n_x, xrow, y, y_stride,
+                       flags, nullptr, 0, true, up_offset);
 }
 
 int strata_gemm_dense(strata_ctx* c, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride, uint64_t y,

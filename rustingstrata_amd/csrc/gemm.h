@@ -23,6 +23,11 @@ struct GemmLaunch {
     float* y = nullptr;
     int64_t y_stride = 0;
     int act = 0;
+    // pair: a block's 128 weight rows are 64 rows of the tile's matrix and the same 64 rows of the matrix w2 bytes
+    // further (gate and up), and it stores y = silu(first) * second for those 64 columns (rows % 64 == 0, y rows
+    // 16-byte aligned)
+    bool pair = false;
+    int64_t w2 = 0;
 };
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t s);
 // Positions of one GEMM block (a tile list's chunks of this size give every block a full tile).

@@ -67,6 +67,8 @@ struct GemmArgs {
     int max_tiles;        // tiles in the grid (an upper bound when the count is on the device)
     int yvec;             // y 16-byte aligned with a row stride of a multiple of 4 floats
     int gx;               // blocks per XCD
+    int pair;             // gate/up pair mode (GemmLaunch::pair)
+    int64_t w2;           // pair: byte offset of the second matrix
 };
 
 // silu(v) = v / (1 + e^-v) for the SwiGLU epilogue. e^-v = 2^t with t = -v log2(e) carried as th + tl (the product's
@@ -124,7 +126,10 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     // expert's tiles run on one XCD and share its L2 (X rows, expert weights); its a.gx blocks take every a.gx-th
     // item from their index j.
     const int ntiles = a.n_tiles_dev ? min(sload(a.n_tiles_dev), a.max_tiles) : a.max_tiles;
-    const int nrb = (a.rows + GN - 1) / GN, total = nrb * ntiles;
+    // pair mode: an item covers 64 output columns (64 rows of each of the two matrices)
+    const bool pair = a.pair != 0;
+    const int GNO = pair ? GN / 2 : GN;
+    const int nrb = (a.rows + GNO - 1) / GNO, total = nrb * ntiles;
     const int per = (total + NXCD - 1) / NXCD, xcd = blockIdx.x % NXCD, jb = blockIdx.x / NXCD;
     const int ibeg = xcd * per + jb, iend = min((xcd + 1) * per, total);
     if (ibeg >= iend) return;
@@ -138,7 +143,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         Item it{0, 0, 0, 0};
         if (k >= nitems) return it;
         const int id = ibeg + k * a.gx, tile = id / nrb;
-        it.n0 = (id - tile * nrb) * GN;
+        it.n0 = (id - tile * nrb) * GNO;
         if (a.tiles) {
             const uint64_t t0 = sload(a.tiles + 2 * tile), t1 = sload(a.tiles + 2 * tile + 1);
             it.w = t0;
@@ -172,7 +177,13 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         int cnt;           // the item's positions
     };
     const int rl = 16 * wave + (lane & 15);  // this lane's weight row in the block
-    auto wchunk = [&](int i) __attribute__((always_inline)) { return 64 * (wave + NW * i) + lane; };
+    // Weight instruction i of this wave: chunk wchunk(i) of the block (of the wave's matrix half in pair mode, waves
+    // 0-3 the first matrix's 64 rows, 4-7 the second's), row wchunk / NCH within it; LDS chunk wchunk + whalf.
+    const int whalf = pair ? 64 * NCH * (wave >> 2) : 0;
+    const int wlim = pair ? 64 * NCH : GN * NCH;
+    auto wchunk = [&](int i) __attribute__((always_inline)) {
+        return pair ? 64 * ((wave & 3) + 4 * i) + lane : 64 * (wave + NW * i) + lane;
+    };
     auto addr_of = [&](const Item& it) __attribute__((always_inline)) {
         Addr ad;
         ad.cnt = it.cnt;
@@ -183,10 +194,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             ad.xo[j] = (uint32_t)xrow_of(p) * (uint32_t)cols + 16 * ((lane & 15) ^ (p & 15));
         }
         ad.dxo = (uint32_t)xrow_of(tid & (GM - 1)) * (uint32_t)(cols / 32);
-        ad.rbeg = (uint32_t)(it.w & 15) + __umul24((uint32_t)min(it.n0 + rl, a.rows - 1), (uint32_t)a.rb);
+        ad.rbeg = (uint32_t)(it.w & 15) + (pair && wave >= 4 ? (uint32_t)(a.w2 & 15) : 0u) +
+                  __umul24((uint32_t)min(it.n0 + (pair ? (rl & 63) : rl), a.rows - 1), (uint32_t)a.rb);
 #pragma unroll
         for (int i = 0; i < WI; i++)
-            ad.wro[i] = __umul24((uint32_t)min(it.n0 + min(wchunk(i) / NCH, GN - 1), a.rows - 1), (uint32_t)a.rb);
+            ad.wro[i] = __umul24((uint32_t)min(it.n0 + min(wchunk(i) / NCH, GNO - 1), a.rows - 1), (uint32_t)a.rb);
         return ad;
     };
     // X instruction j of super-block s of an item into the X buffer of step g (X and dx rotate by 2).
@@ -197,17 +209,17 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     // Chunk numbers c % NCH of this lane's weight instructions, 4 bits each (15: no chunk; NCH <= 15).
     uint32_t wcc = 0;
 #pragma unroll
-    for (int i = 0; i < WI; i++) wcc |= (uint32_t)(wchunk(i) < GN * NCH ? wchunk(i) % NCH : 15) << (4 * i);
+    for (int i = 0; i < WI; i++) wcc |= (uint32_t)(wchunk(i) < wlim ? wchunk(i) % NCH : 15) << (4 * i);
     // Raw weights of super-block s: the 16-byte covers of the rows' super-block, from the scalar base
     // (w + s * SBB) & ~15 and per-lane offsets ((w + s * SBB) & 15) + row offset, rounded down to 16, + 16 chunk
     // (a chunk past the super-block, or no chunk: offset 240 past the rounded start, is not loaded).
     auto load_w = [&](const Item& it, const Addr& ad, int s) __attribute__((always_inline)) {
-        const uint64_t beg = it.w + (uint64_t)s * SBB, base = beg & ~(uint64_t)15;
+        const uint64_t beg = it.w + (pair && wave >= 4 ? (uint64_t)a.w2 : 0) + (uint64_t)s * SBB, base = beg & ~(uint64_t)15;
         const uint32_t b15 = (uint32_t)(beg & 15);
 #pragma unroll
         for (int i = 0; i < WI; i++) {
             const uint32_t t = b15 + ad.wro[i], o = (t & ~15u) + 16 * ((wcc >> (4 * i)) & 15);
-            if (o < t + SBB) load_lds16_so(base, o, raw + 1024 * (wave + NW * i));
+            if (o < t + SBB) load_lds16_so(base, o, raw + 16 * (whalf + wchunk(i) - lane));
         }
     };
     float dxv = 0.0f;
@@ -303,7 +315,36 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     // groups write distinct banks. Otherwise each lane stores its own values.
     auto store = [&](const Item& it, int g) __attribute__((always_inline)) {
         const int ntt = (it.cnt + 15) >> 4;
-        if (a.yvec && it.n0 + GN <= a.rows) {
+        if (pair) {
+            // y[m0 + m, n0 + c] = silu(first[c]) * second[c], c < 64: the stage holds the first matrix's outputs in
+            // rows 0..63 and the second's in 64..127; each thread writes 4 float4 a round
+            float* S = (float*)(xs + (g & 1) * XBUF);
+            static_for<0, 2>([&](auto R) {
+                constexpr int r = decltype(R)::value;
+                if (128 * r < it.cnt) {
+                    __syncthreads();  // the tiles (round 0) or the previous round's reads are done
+                    static_for<0, 8>([&](auto I) {
+                        constexpr int il = decltype(I)::value, i = 8 * r + il;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) S[(16 * il + 4 * kl + q) * 128 + (rl ^ (kl << 4))] = acc[i][q];
+                    });
+                    __syncthreads();
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) {
+                        const int idx = tid + 512 * jj, pr = idx >> 4, c4 = 4 * (idx & 15), m = 128 * r + pr;
+                        if (m < it.cnt) {
+                            const int swz = ((pr >> 2) & 3) << 4;
+                            const float4 gv = *(const float4*)(S + pr * 128 + (c4 ^ swz));
+                            const float4 uv = *(const float4*)(S + pr * 128 + ((64 + c4) ^ swz));
+                            float4 o;
+                            o.x = silu_dev(gv.x) * uv.x; o.y = silu_dev(gv.y) * uv.y;
+                            o.z = silu_dev(gv.z) * uv.z; o.w = silu_dev(gv.w) * uv.w;
+                            *(float4*)(a.y + (int64_t)(it.m0 + m) * a.y_stride + it.n0 + c4) = o;
+                        }
+                    }
+                }
+            });
+        } else if (a.yvec && it.n0 + GN <= a.rows) {
             float* S = (float*)(xs + (g & 1) * XBUF);
             const int c4 = 4 * (lane & 31);
             auto put = [&](auto OP) __attribute__((always_inline)) {
@@ -448,6 +489,8 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
     a.xq = (const int8_t*)g.xq; a.xd = (const float*)(g.xq + (uint64_t)g.n_x * g.cols);
     a.xrow = g.xrow; a.y = g.y; a.y_stride = g.y_stride; a.rows = g.rows; a.cols = g.cols; a.act = g.act;
     a.yvec = ((uintptr_t)g.y % 16 == 0) && (g.y_stride % 4 == 0);
+    a.pair = g.pair ? 1 : 0;
+    a.w2 = g.w2;
     a.rb = row_bytes(T, g.cols);
     const size_t smem = gemm_smem<T>();
     static bool attr = false;
@@ -465,7 +508,8 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
         if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
     }
-    const long long total = (long long)((g.rows + GN - 1) / GN) * g.n_tiles;
+    const int gno = g.pair ? GN / 2 : GN;
+    const long long total = (long long)((g.rows + gno - 1) / gno) * g.n_tiles;
     const long long per = (total + NXCD - 1) / NXCD;
     const long long gx = std::min<long long>(per, std::max(ncu / NXCD, 1));
     a.gx = (int)std::max<long long>(gx, 1);

@@ -466,6 +466,45 @@ def test_gemm_tiles_match_cpu(hip, ty):
     assert max_rel_err(got3, want2 + want) <= 2 * TOL
 
 
+@pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
+def test_gemm_gate_up_fused_matches_two_calls(hip, ty):
+    """gemm_grouped_gate_up gives the bits of gemm (gate, act store) followed by gemm (up, act SwiGLU, same X) over the
+    same tiles (src/gpu_model/prefill.rs), with partial and full 256-position tiles and 3 column blocks of 64."""
+    rows, cols, E, n_x = 192, 512, 3, 100
+    rb = ggml.row_bytes(ty, cols)
+    w = random_blocks(ty, 2 * E * rows, cols, seed=100 + ty)  # gate experts, then up experts
+    wb = up(hip, w)
+    up_off = E * rows * rb
+    x = normal((n_x, cols), seed=5)
+    npos = 626
+    xrow = np.random.default_rng(6).integers(0, n_x, npos).astype(np.int32)
+    spans = [(0, 0, 128), (2, 128, 16), (1, 144, 26), (2, 170, 256), (0, 426, 200)]
+    tg, nt = tile_list(hip, int(wb), rows * rb, spans)
+    tu, _ = tile_list(hip, int(wb) + up_off, rows * rb, spans)
+    ntd = up(hip, np.array([nt], dtype=np.int32))
+    xb, xr = up(hip, x), up(hip, xrow)
+    y1, y2 = hip.alloc(npos * rows * 4), hip.alloc(npos * rows * 4)
+    hip.gemm(ty, rows, cols, tg, nt, xb, cols, n_x, xr, y1, rows, S.ACT_STORE)
+    hip.gemm(ty, rows, cols, tu, nt, xb, cols, n_x, xr, y1, rows, S.ACT_SWIGLU | S.SAME_X)
+    hip.gemm_grouped_gate_up(ty, rows, cols, tg, nt, ntd, xb, cols, n_x, xr, y2, rows, up_off)
+    a, b = down(hip, y1, np.float32, npos * rows), down(hip, y2, np.float32, npos * rows)
+    assert np.array_equal(a, b), np.abs(a - b).max()
+    # against the oracle through the gate and up results
+    want_g = np.zeros((npos, rows), dtype=np.float32)
+    want_u = np.zeros((npos, rows), dtype=np.float32)
+    for e, m0, c in spans:
+        for m in range(m0, m0 + c):
+            want_g[m] = O.matvec(ty, w[e * rows:(e + 1) * rows], rows, cols, x[xrow[m]])
+            want_u[m] = O.matvec(ty, w[(E + e) * rows:(E + e + 1) * rows], rows, cols, x[xrow[m]])
+    with np.errstate(over="ignore"):
+        want = want_g / (1 + np.exp(-want_g.astype(np.float64))) * want_u
+    assert max_rel_err(b.reshape(npos, rows), want) <= 2 * TOL
+    with pytest.raises(S.StrataError, match="a multiple of 64"):
+        hip.gemm_grouped_gate_up(ty, 200, cols, tg, nt, ntd, xb, cols, n_x, xr, y2, 200, up_off)
+    with pytest.raises(S.StrataError, match="Q8_0 has no fused"):
+        hip.gemm_grouped_gate_up(ggml.Q8_0, rows, cols, tg, nt, ntd, xb, cols, n_x, xr, y2, rows, up_off)
+
+
 @pytest.mark.parametrize("ty", [ggml.Q5_K, ggml.Q8_0])
 def test_gemm_dense(hip, ty):
     rows, cols, n = 200, 1024, 300
@@ -496,9 +535,11 @@ def test_moe_prefill_layer_matches_experts_multi(hip):
     want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, hs, ids_w, wts_w)
     got = run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits)
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+    # gate and up as one grouped GEMM: the same bits
+    assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True), got)
 
 
-def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits):
+def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=False):
     rb_gu, rb_d = ggml.row_bytes(ggml.Q5_K, H), ggml.row_bytes(ggml.Q6_K, F)
     g_b, u_b, d_b = up(hip, gate), up(hip, upw), up(hip, dn)
     hb, lb = up(hip, hs), up(hip, logits)
@@ -511,9 +552,12 @@ def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits):
     hip.moe_sort(ids, T, k, E, off, xrow, inv, [(int(g_b), F * rb_gu), (int(u_b), F * rb_gu), (int(d_b), H * rb_d)],
                  tiles, max_tiles, ntd, chunk=chunk)
     ge, ye = hip.alloc(T * k * F * 4), hip.alloc(T * k * H * 4)
-    hip.gemm_grouped(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, S.ACT_STORE)
-    hip.gemm_grouped(ggml.Q5_K, F, H, int(tiles) + max_tiles * 16, max_tiles, ntd, hb, H, T, xrow, ge, F,
-                     S.ACT_SWIGLU | S.SAME_X)
+    if fused:
+        hip.gemm_grouped_gate_up(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b))
+    else:
+        hip.gemm_grouped(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, S.ACT_STORE)
+        hip.gemm_grouped(ggml.Q5_K, F, H, int(tiles) + max_tiles * 16, max_tiles, ntd, hb, H, T, xrow, ge, F,
+                         S.ACT_SWIGLU | S.SAME_X)
     hip.gemm_grouped(ggml.Q6_K, H, F, int(tiles) + 2 * max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
                      S.ACT_STORE)
     x = hip.alloc(T * H * 4)
