@@ -221,8 +221,13 @@ constexpr int GEMV1_TILE = GEMV1_THREADS * 16 * GEMV1_CH;
 // Quantize x row xr (n values) into LDS (n int8, then n / 32 scales) with quant_xq's arithmetic (quant.hip): the
 // block's 256 threads take 8 values each, a group of 32 lanes one 256-value block.
 // This thread's 8 values v (positions i.., zeros past n) of one 2048-value chunk, quantized into LDS.
+// The staged x in LDS: value i at xpad(i) (16 bytes of padding after every 256, so the lanes of a wave reading
+// different super-blocks' slices hit different banks), the per-32 scales, and the per-16 sums of the int8 values.
+__device__ __forceinline__ int xpad(int i) { return i + 16 * (i >> 8); }
+__host__ __device__ constexpr uint32_t xpad_bytes(uint32_t ncp) { return ncp + ncp / 16; }
+
 template <bool Q32>
-__device__ __forceinline__ void quant8_lds(const float (&v)[8], int i, bool live, int8_t* q, float* d) {
+__device__ __forceinline__ void quant8_lds(const float (&v)[8], int i, bool live, int8_t* q, float* d, int* ss) {
     {
         float dd, mul;
         if constexpr (!Q32) {
@@ -255,19 +260,23 @@ __device__ __forceinline__ void quant8_lds(const float (&v)[8], int i, bool live
             dd = mx / 127.0f;
             mul = mx > 0.0f ? 127.0f / mx : 0.0f;
         }
-        if (live) {
-            uint32_t w[2] = {0, 0};
+        uint32_t w[2] = {0, 0};
 #pragma unroll
-            for (int j = 0; j < 8; j++) w[j >> 2] |= (uint32_t)((int)fminf(__builtin_rintf(mul * v[j]), 127.0f) & 255) << (8 * (j & 3));
-            *(uint2*)(q + i) = make_uint2(w[0], w[1]);
+        for (int j = 0; j < 8; j++) w[j >> 2] |= (uint32_t)((int)fminf(__builtin_rintf(mul * v[j]), 127.0f) & 255) << (8 * (j & 3));
+        // the 16-value group's sum: this lane's 8 and its neighbour's (lane ^ 1)
+        int s8 = sdot4((int)w[0], 0x01010101, sdot4((int)w[1], 0x01010101, 0));
+        s8 += xl32<0>(s8);
+        if (live) {
+            *(uint2*)(q + xpad(i)) = make_uint2(w[0], w[1]);
             if ((threadIdx.x & 3) == 0) d[i >> 5] = dd;
+            if ((threadIdx.x & 1) == 0) ss[i >> 4] = s8;
         }
     }
 }
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 template <bool Q32, bool SW>
-__device__ __forceinline__ void quant_row_lds(uint64_t xr, uint64_t ur, int n, int8_t* q, float* d) {
+__device__ __forceinline__ void quant_row_lds(uint64_t xr, uint64_t ur, int n, int8_t* q, float* d, int* ss) {
     for (int c0 = 0; c0 < n; c0 += 8 * (int)blockDim.x) {
         const int i = c0 + threadIdx.x * 8;
         const bool live = i < n;
@@ -285,26 +294,31 @@ __device__ __forceinline__ void quant_row_lds(uint64_t xr, uint64_t ur, int n, i
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = 0.0f;
         }
-        quant8_lds<Q32>(v, i, live, q, d);
+        quant8_lds<Q32>(v, i, live, q, d, ss);
     }
 }
 
 // x row xrow into the block's LDS copy (int8, then per-32 scales): copied from xq, or quantized from f32.
 template <bool Q32, bool SW>
-__device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl, float* xld) {
+__device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl, float* xld, int* xss) {
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     if (a.xq) {
         const uint64_t q = (uint64_t)(a.xq + (uint64_t)xrow * a.cols), d = (uint64_t)(a.xd + (uint64_t)xrow * (a.cols / 32));
-        for (int c = threadIdx.x; c < a.cols / 16; c += blockDim.x) *(v4u*)(xl + 16 * c) = *gptr<v4u>(q + 16 * c);
+        for (int c = threadIdx.x; c < a.cols / 16; c += blockDim.x) {
+            const v4u t = *gptr<v4u>(q + 16 * c);
+            *(v4u*)(xl + xpad(16 * c)) = t;
+            xss[c] = sdot4((int)t.x, 0x01010101, sdot4((int)t.y, 0x01010101, sdot4((int)t.z, 0x01010101, sdot4((int)t.w, 0x01010101, 0))));
+        }
         for (int c = threadIdx.x; c < a.cols / 32; c += blockDim.x) xld[c] = *gptr<float>(d + 4 * c);
     } else {
         quant_row_lds<Q32, SW>((uint64_t)(a.xf + (uint64_t)xrow * a.x_stride),
-                               SW ? (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) : 0, a.cols, xl, xld);
+                               SW ? (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) : 0, a.cols, xl, xld, xss);
     }
     // zeros up to whole super-blocks (Q8_0 rows may end inside one)
     const int n = a.cols, nup = (n + 255) & ~255;
-    for (int i = n + 4 * threadIdx.x; i < nup; i += 4 * blockDim.x) *(uint32_t*)(xl + i) = 0;
+    for (int i = n + 4 * threadIdx.x; i < nup; i += 4 * blockDim.x) *(uint32_t*)(xl + xpad(i)) = 0;
     for (int j = n / 32 + threadIdx.x; j < nup / 32; j += blockDim.x) xld[j] = 0.0f;
+    for (int j = n / 16 + threadIdx.x; j < nup / 16; j += blockDim.x) xss[j] = 0;
 }
 
 // The first tile's x row when it has at most 2048 values, requested before the tile's weights so that its arrival
@@ -334,11 +348,14 @@ __device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) 
     }
 }
 template <bool Q32, bool SW>
-__device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t* xl, float* xld) {
+__device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t* xl, float* xld, int* xss) {
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, n = a.cols;
     if (a.xq) {
-        if (tid < n / 16) *(v4u*)(xl + 16 * tid) = e.q;
+        if (tid < n / 16) {
+            *(v4u*)(xl + xpad(16 * tid)) = e.q;
+            xss[tid] = sdot4((int)e.q.x, 0x01010101, sdot4((int)e.q.y, 0x01010101, sdot4((int)e.q.z, 0x01010101, sdot4((int)e.q.w, 0x01010101, 0))));
+        }
         if (tid < n / 32) xld[tid] = e.d;
     } else {
         const bool live = 8 * tid < n;
@@ -352,28 +369,41 @@ __device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = 0.0f;
         }
-        quant8_lds<Q32>(v, 8 * tid, live, xl, xld);
+        quant8_lds<Q32>(v, 8 * tid, live, xl, xld, xss);
     }
     const int nup = (n + 255) & ~255;
-    for (int i = n + 4 * tid; i < nup; i += 4 * blockDim.x) *(uint32_t*)(xl + i) = 0;
+    for (int i = n + 4 * tid; i < nup; i += 4 * blockDim.x) *(uint32_t*)(xl + xpad(i)) = 0;
     for (int j = n / 32 + tid; j < nup / 32; j += blockDim.x) xld[j] = 0.0f;
+    for (int j = n / 16 + tid; j < nup / 16; j += blockDim.x) xss[j] = 0;
 }
 
 // This lane's 256-value slice (super-block sb) of the staged x into registers, with its per-16 sums.
-__device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const float* xld, XReg& x) {
+__device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const float* xld, const int* xss, XReg& x) {
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int c = 0; c < 16; c++) {
-        const v4u t = *(const v4u*)(xl + 256 * sb + 16 * c);
+        const v4u t = *(const v4u*)(xl + 272 * sb + 16 * c);
         x.w[4 * c] = t.x; x.w[4 * c + 1] = t.y; x.w[4 * c + 2] = t.z; x.w[4 * c + 3] = t.w;
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) x.ds[j] = xld[8 * sb + j];
 #pragma unroll
-    for (int g = 0; g < 16; g++)
-        x.sums[g] = sdot4((int)x.w[4 * g], 0x01010101, sdot4((int)x.w[4 * g + 1], 0x01010101,
-                    sdot4((int)x.w[4 * g + 2], 0x01010101, sdot4((int)x.w[4 * g + 3], 0x01010101, 0))));
+    for (int c = 0; c < 4; c++) {
+        const v4u t = *(const v4u*)(xss + 16 * sb + 4 * c);
+        x.sums[4 * c] = (int)t.x; x.sums[4 * c + 1] = (int)t.y; x.sums[4 * c + 2] = (int)t.z; x.sums[4 * c + 3] = (int)t.w;
+    }
 }
+
+#ifdef STRATA_GEMV1_TRACE
+// Debug builds: shader clock at the phases of the first tile of blocks 0..63 (read with strata_debug_gemv_trace).
+__device__ uint64_t g_gemv_trace[64][8];
+#define GTRACE(ph)                                                                                          \
+    do {                                                                                                    \
+        if (blockIdx.x < 64 && threadIdx.x == 0) g_gemv_trace[blockIdx.x][ph] = __builtin_amdgcn_s_memtime(); \
+    } while (0)
+#else
+#define GTRACE(ph) do {} while (0)
+#endif
 
 #ifdef STRATA_GEMV1_WPE
 #define GEMV1_ATTR __attribute__((amdgpu_waves_per_eu(STRATA_GEMV1_WPE)))
@@ -389,14 +419,11 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, cols = a.cols;
-    // LDS: [IqTables][x int8 (cols, whole super-blocks)][x scales][tile]
+    // LDS: [IqTables][x int8 (whole super-blocks, padded: xpad)][x scales][x per-16 sums][tile]
     const uint32_t ncp = (cols + 255) & ~255;
-#ifdef STRATA_GEMV1_XLDS
-    const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + ncp, o_ss = o_xd + ncp / 8, o_tile = o_ss + ncp / 4;
+    const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + xpad_bytes(ncp), o_ss = o_xd + ncp / 8,
+                   o_tile = o_ss + ncp / 4;
     int* xss = (int*)(smem + o_ss);
-#else
-    const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + ncp, o_tile = o_xd + ncp / 8;
-#endif
     IqTables* tab = (IqTables*)smem;
     if constexpr (IQ) load_iq_tables(tab);
     int8_t* xl = (int8_t*)(smem + o_x);
@@ -444,6 +471,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
         }
     };
 
+    GTRACE(0);
     int t = next_valid(blockIdx.x);
     if (t >= total) return;
     Span sp = span(t);
@@ -451,6 +479,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     XEarly xe;
     if (early) x_fetch<SW>(a, sp.xrow, xe);
     issue(sp);
+    GTRACE(1);
     // the tile after next is located while the next one is in flight
     int tn = next_valid(t + gridDim.x);
     Span spn = sp;
@@ -458,30 +487,25 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     const int G = a.G, wave = tid >> 6, lane = tid & 63, gl = lane & (G - 1);
     const int RPW = 64 / G, nsb = (cols + 255) >> 8;
     const bool has_sb = gl < nsb;
-#ifndef STRATA_GEMV1_XLDS
     XReg x;
-#endif
     int cur_xrow = -1;
     while (true) {
         __syncthreads();  // the previous tile's readers are done with the LDS tile
         if (sp.xrow != cur_xrow) {
-            if (early && cur_xrow < 0) x_put<Q32, SW>(a, xe, xl, xld);
-            else stage_x<Q32, SW>(a, sp.xrow, xl, xld);
+            if (early && cur_xrow < 0) x_put<Q32, SW>(a, xe, xl, xld, xss);
+            else stage_x<Q32, SW>(a, sp.xrow, xl, xld, xss);
+            GTRACE(6);
             __syncthreads();
-#ifdef STRATA_GEMV1_XLDS
-            for (int c = tid; c < (int)ncp / 16; c += GEMV1_THREADS) {
-                const v4u q = *(const v4u*)(xl + 16 * c);
-                xss[c] = sdot4((int)q.x, 0x01010101, sdot4((int)q.y, 0x01010101, sdot4((int)q.z, 0x01010101, sdot4((int)q.w, 0x01010101, 0))));
-            }
-#else
-            if (has_sb) load_x_slice(gl, xl, xld, x);
-#endif
+            GTRACE(7);
+            // every lane has its slice before the copy can change again: the next staging follows the loop's barrier
+            if (has_sb) load_x_slice(gl, xl, xld, xss, x);
             cur_xrow = sp.xrow;
-            __syncthreads();  // every lane has its slice before the LDS copy changes again
+            GTRACE(2);
         }
 #pragma unroll
         for (int i = 0; i < GEMV1_CH; i++) *(v4u*)(tile + 16 * (tid + GEMV1_THREADS * i)) = wv[i];
         __syncthreads();
+        GTRACE(3);
         const Span cs = sp;
         const bool more = tn < total;
         if (more) {
@@ -502,19 +526,22 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
             if (rr < cs.nr && has_sb) {
 #endif
                 const uint8_t* b = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb + gl * SBB;
-#ifdef STRATA_GEMV1_XLDS
-                const XLds xv{xl + 256 * gl, xld + 8 * gl, xss + 16 * gl};
-                acc = Q32 ? sb_dot_q32<T>(b, xv, tab, nv) : sb_dot_q8k<T>(b, xv, tab, nv);
-#else
                 acc = Q32 ? sb_dot_q32<T>(b, x, tab, nv) : sb_dot_q8k<T>(b, x, tab, nv);
-#endif
             }
             acc = group_sum(acc, G);
             if (rr < cs.nr && gl == 0) cs.Y[cs.r0 + rr] = acc;
         }
+        GTRACE(4);
         if (!more) break;
     }
+    GTRACE(5);
 }
+
+#ifdef STRATA_GEMV1_TRACE
+extern "C" int strata_debug_gemv_trace(uint64_t* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_gemv_trace), sizeof(g_gemv_trace)) == hipSuccess ? 0 : -1;
+}
+#endif
 
 template <int T, bool Q32, bool SW>
 static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
@@ -621,11 +648,7 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     bool iq = g.ty == IQ2_XXS || g.ty == IQ3_S;
     if (single) {
         const uint32_t ncp = (g.cols + 255) & ~255;
-#ifdef STRATA_GEMV1_XLDS
-        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + ncp + ncp / 8 + ncp / 4 + GEMV1_TILE + 16;
-#else
-        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + ncp + ncp / 8 + GEMV1_TILE + 16;
-#endif
+        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + xpad_bytes(ncp) + ncp / 8 + ncp / 4 + GEMV1_TILE + 16;
         switch (g.ty) {
         case Q8_0: return gemv1_t<Q8_0>(a, grid, smem1, s);
         case Q2_K: return gemv1_t<Q2_K>(a, grid, smem1, s);
