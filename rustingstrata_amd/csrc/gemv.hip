@@ -397,12 +397,18 @@ __device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const flo
 #ifdef STRATA_GEMV1_TRACE
 // Debug builds: shader clock at the phases of the first tile of blocks 0..63 (read with strata_debug_gemv_trace).
 __device__ uint64_t g_gemv_trace[64][8];
+__device__ uint64_t g_gemv_loop[32][4];
 #define GTRACE(ph)                                                                                          \
     do {                                                                                                    \
         if (blockIdx.x < 64 && threadIdx.x == 0) g_gemv_trace[blockIdx.x][ph] = __builtin_amdgcn_s_memtime(); \
     } while (0)
+#define LTRACE(ph)                                                                                          \
+    do {                                                                                                    \
+        if (blockIdx.x == 5 && threadIdx.x == 0 && ltile < 32) g_gemv_loop[ltile][ph] = __builtin_amdgcn_s_memtime(); \
+    } while (0)
 #else
 #define GTRACE(ph) do {} while (0)
+#define LTRACE(ph) do {} while (0)
 #endif
 
 #ifdef STRATA_GEMV1_WPE
@@ -489,8 +495,13 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     const bool has_sb = gl < nsb;
     XReg x;
     int cur_xrow = -1;
+#ifdef STRATA_GEMV1_TRACE
+    int ltile = 0;
+#endif
     while (true) {
+        LTRACE(0);
         __syncthreads();  // the previous tile's readers are done with the LDS tile
+        LTRACE(1);
         if (sp.xrow != cur_xrow) {
             if (early && cur_xrow < 0) x_put<Q32, SW>(a, xe, xl, xld, xss);
             else stage_x<Q32, SW>(a, sp.xrow, xl, xld, xss);
@@ -506,6 +517,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
         for (int i = 0; i < GEMV1_CH; i++) *(v4u*)(tile + 16 * (tid + GEMV1_THREADS * i)) = wv[i];
         __syncthreads();
         GTRACE(3);
+        LTRACE(2);
         const Span cs = sp;
         const bool more = tn < total;
         if (more) {
@@ -532,6 +544,10 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
             if (rr < cs.nr && gl == 0) cs.Y[cs.r0 + rr] = acc;
         }
         GTRACE(4);
+        LTRACE(3);
+#ifdef STRATA_GEMV1_TRACE
+        ltile++;
+#endif
         if (!more) break;
     }
     GTRACE(5);
@@ -540,6 +556,9 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
 #ifdef STRATA_GEMV1_TRACE
 extern "C" int strata_debug_gemv_trace(uint64_t* out) {
     return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_gemv_trace), sizeof(g_gemv_trace)) == hipSuccess ? 0 : -1;
+}
+extern "C" int strata_debug_gemv_loop(uint64_t* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_gemv_loop), sizeof(g_gemv_loop)) == hipSuccess ? 0 : -1;
 }
 #endif
 
