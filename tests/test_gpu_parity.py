@@ -697,3 +697,35 @@ def test_moe_gemv_from_gguf_slots(hip, tmp_path):
     for j, e in enumerate(ids):
         assert max_rel_err(gd[j], O.matvec(ggml.Q6_K, dn[e * H:(e + 1) * H], H, F, act[j])) <= TOL
 
+
+
+def test_moe_prefill_from_gguf_slots(hip, tmp_path):
+    """The prefill MoE block over experts uploaded in slots from a GGUF: moe_sort builds the tile lists with the slot
+    stride (gate at off[gate], down at off[down]), the fused gate/up GEMM finds up at off[up] - off[gate] from each
+    gate, then the down GEMM and the ordered combine; against cpu_moe::experts_multi."""
+    from rustingstrata_amd import gguf
+    from tests.test_gguf import moe_layer_file
+    E, H, F, T, k = 4, 512, 256, 40, 2
+    p = str(tmp_path / "moe.gguf")
+    gate, upw, dn = moe_layer_file(p, E, H, F)
+    g = gguf.Gguf(p)
+    buf, mats, slot = gguf.upload_experts(hip, g, 0)
+    hs = normal((T, H), seed=90)
+    logits = zipf_logits(T, E, seed=91)
+    ids_w, wts_w = O.route(logits, k)
+    want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, hs, ids_w, wts_w)
+    ids, wts = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
+    hip.router_topk(up(hip, logits), E, k, 0.0, ids, wts, T)
+    chunk = hip.gemm_block_positions()
+    max_tiles = T * k // chunk + E
+    off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
+    tiles, ntd = hip.alloc(2 * max_tiles * 16), hip.alloc(4)
+    hip.moe_sort(ids, T, k, E, off, xrow, inv, [(int(buf) + mats[0].off, slot), (int(buf) + mats[2].off, slot)],
+                 tiles, max_tiles, ntd, chunk=chunk)
+    ge, ye, x = hip.alloc(T * k * F * 4), hip.alloc(T * k * H * 4), hip.alloc(T * H * 4)
+    hb = up(hip, hs)
+    hip.gemm_grouped_gate_up(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, mats[1].off - mats[0].off)
+    hip.gemm_grouped(ggml.Q6_K, H, F, int(tiles) + max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H, S.ACT_STORE)
+    hip.moe_combine_seq(x, ye, wts, inv, k, 0, 0, H, T)
+    got = down(hip, x, np.float32, T * H).reshape(T, H)
+    assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
