@@ -236,10 +236,24 @@ def bench_moe_decode(hip, S, ggml, iters):
     for i in range(iters):
         token(i)
     hip.record(e1)
-    us = 1000 * hip.elapsed_ms(e0, e1) / iters
+    us_eager = 1000 * hip.elapsed_ms(e0, e1) / iters
+    us = us_eager
+    if USE_GRAPHS:
+        # 8 tokens a recorded graph (both weight copies, all four logit vectors), replayed the way the reference's
+        # decode replays CUDA graphs (src/cuda/mod.rs:868-888): host launch gaps do not count as GPU time
+        ng = 8
+        hip.graph("decode", lambda: [token(i) for i in range(ng)])
+        hip.sync()
+        reps = max(1, -(-iters // ng))
+        hip.record(e0)
+        for _ in range(reps):
+            hip.graph("decode", None)
+        hip.record(e1)
+        us = 1000 * hip.elapsed_ms(e0, e1) / (reps * ng)
+        hip.drop_graphs()
     bts = k * (2 * F * rb_gu + H * rb_d)
-    return {"us_per_token": round(us, 2), "expert_bytes": bts, "GB/s": round(bts / us / 1e3, 1),
-            "pct_peak": round(100 * bts / us / 1e3 / HBM_PEAK_GBS, 1)}
+    return {"us_per_token": round(us, 2), "us_per_token_eager": round(us_eager, 2), "expert_bytes": bts,
+            "GB/s": round(bts / us / 1e3, 1), "pct_peak": round(100 * bts / us / 1e3 / HBM_PEAK_GBS, 1)}
 
 
 def codebook_blocks(ggml, ty, rows, cols, seed):
@@ -411,6 +425,8 @@ def main():
                     help="only run the Q4_K lm-head GEMV and a 256 MB copy kernel 50 times each (for rocprofv3)")
     ap.add_argument("--profile-moe", action="store_true",
                     help="only run the configs[2] 4K-token MoE prefill layer (--moe-iters times, for rocprofv3)")
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="only run the configs[2] 1-token MoE decode layer 200 times, eagerly (for rocprofv3)")
     ap.add_argument("--eager", action="store_true", help="launch every op from the host (no recorded graphs)")
     args = ap.parse_args()
     global USE_GRAPHS
@@ -426,6 +442,10 @@ def main():
     log(f"[bench] {hip.device()}")
     if args.profile_gemv:
         profile_gemv(hip, S, ggml)
+        return
+    if args.profile_decode:
+        USE_GRAPHS = False
+        print(json.dumps({"moe_decode_1": bench_moe_decode(hip, S, ggml, 200)}), flush=True)
         return
     if args.profile_moe:
         print(json.dumps({"moe_prefill_4k": bench_moe(hip, S, ggml, 4096, args.moe_iters)}), flush=True)

@@ -42,10 +42,13 @@ def test_dequant_bit_exact(hip, ty):
 
 @pytest.mark.parametrize("name,ty", [("Q2_K", ggml.Q2_K), ("Q3_K", ggml.Q3_K), ("Q4_K", ggml.Q4_K), ("Q5_K", ggml.Q5_K),
                                      ("Q6_K", ggml.Q6_K), ("Q8_0", ggml.Q8_0), ("IQ4_XS", ggml.IQ4_XS),
-                                     ("ggml_q5_k", ggml.Q5_K), ("ggml_q8_0", ggml.Q8_0), ("ggml_iq2_xxs", ggml.IQ2_XXS)])
+                                     ("ggml_q5_k", ggml.Q5_K), ("ggml_q8_0", ggml.Q8_0), ("ggml_iq2_xxs", ggml.IQ2_XXS),
+                                     ("IQ3_S", ggml.IQ3_S)])
 def test_dequant_reference_fixtures(hip, name, ty):
     import os
     d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference")
+    if name == "IQ3_S":  # oracle-derived (the reference holds no IQ3_S vector): tests/golden/make_oracle_vectors.py
+        d = os.path.join(os.path.dirname(d), "oracle")
     raw = np.fromfile(os.path.join(d, name + (".blk" if name.startswith("ggml") else ".raw")), dtype=np.uint8)
     want = np.fromfile(os.path.join(d, name + ".f32"), dtype=np.float32)
     cols = ggml.block_elems(ty) * (raw.size // ggml.block_bytes(ty))
@@ -598,6 +601,31 @@ def test_moe_decode_layer_matches_experts(hip):
     assert np.array_equal(down(hip, g2, np.float32, 2 * k * F), down(hip, g, np.float32, 2 * k * F))
     hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, g2, int(g2) + k * F * 4, ye, x2, wh, 0, 0, 1)
     assert np.array_equal(down(hip, x2, np.float32, H), got)
+    # the whole token (route, gate/up, fused tail) recorded as a graph (the way the reference's decode replays CUDA
+    # graphs, src/cuda/mod.rs:868-888): each replay, with other logits and eager work in between, equals the eager
+    # token bit for bit
+    lb = up(hip, logits)
+
+    def token(xo):
+        hip.moe_route(lb, E, k, 0.0, table, ids, wts, slots, wh, 1)
+        hip.moe_gemv(ggml.Q5_K, F, H, gu, F * rb_gu, slots, k, hb, H, k, g2, pair=(E * F * rb_gu, k * F * 4))
+        hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, g2, int(g2) + k * F * 4, ye, xo, wh,
+                                    0, 0, 1)
+
+    x3 = hip.alloc(H * 4)
+    hip.graph("decode", lambda: token(x3))
+    for i in range(3):
+        hip.htod(zipf_logits(1, E, seed=90 + i), lb)
+        hip.htod(np.zeros(H, dtype=np.float32), x3)
+        hip.graph("decode", None)
+        got_g = down(hip, x3, np.float32, H)
+        x4 = hip.alloc(H * 4)
+        token(x4)
+        assert np.array_equal(got_g, down(hip, x4, np.float32, H)), i
+        iw, ww = O.route(zipf_logits(1, E, seed=90 + i), k)
+        want_i = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, h[None, :], iw, ww)[0]
+        assert max_rel_err(got_g, want_i) <= TOL, (i, max_rel_err(got_g, want_i))
+    hip.drop_graphs()
 
 
 @pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])

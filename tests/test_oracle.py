@@ -43,6 +43,25 @@ def test_dequant_matches_ggml_fixtures(name, ty):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+def test_iq3s_oracle_vectors_stable():
+    """tests/golden/oracle/IQ3_S.{raw,f32} (written by tests/golden/make_oracle_vectors.py; oracle-derived, not
+    reference-held): the oracle still reproduces them bit for bit, and every value is db * grid * sign with
+    db = d (1 + 2 sc) over the odd grid bytes 1..15 (src/quant/mod.rs:345-361)."""
+    d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "oracle")
+    raw = np.fromfile(os.path.join(d, "IQ3_S.raw"), dtype=np.uint8)
+    want = np.fromfile(os.path.join(d, "IQ3_S.f32"), dtype=np.float32)
+    got = O.dequant(ggml.IQ3_S, raw, want.size)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    blk = raw.reshape(-1, 110)
+    dd = blk[:, 0:2].copy().view(np.float16).astype(np.float32)[:, 0]
+    for b in range(blk.shape[0]):
+        for ib in range(8):
+            sc = (blk[b, 106 + ib // 2] >> (4 * (ib & 1))) & 15
+            db = np.float32(dd[b] * np.float32(1 + 2 * int(sc)))
+            q = np.abs(want[256 * b + 32 * ib:256 * b + 32 * ib + 32]) / db
+            assert np.all(np.isin(np.round(q), np.arange(1, 16, 2))), (b, ib)
+
+
 def test_iq3s_known_answer():
     """A hand-built IQ3_S block (layout src/quant/mod.rs:345-361): d = 0.5, sub-block 0 scale nibble 3 -> db = 3.5;
     qs[0] = 0 -> IQ3S_GRID[0] = 0x01010101 (four 1s); qs[1] = 5 with qh bit 1 set -> index 256 + 5; sign byte 0 of
