@@ -23,6 +23,10 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
     float v[ROUTE_R];
 #pragma unroll
     for (int r = 0; r < ROUTE_R; r++) { int i = lane + 64 * r; v[r] = i < n ? pr[i] : -INFINITY; }
+    // the slot table's entries, fetched with the logits (the chosen ones are read from these registers at the end)
+    int tv[ROUTE_R];
+#pragma unroll
+    for (int r = 0; r < ROUTE_R; r++) { int i = lane + 64 * r; tv[r] = table && i < n ? table[i] : -1; }
     if (sigmoid) {
 #pragma unroll
         for (int r = 0; r < ROUTE_R; r++) v[r] = 1.0f / (1.0f + exp_f32(-v[r]));  // ops::sigmoid
@@ -41,80 +45,84 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
 #pragma unroll
         for (int r = 0; r < ROUTE_R; r++) {
             int i = lane + 64 * r;
-            if (i < n) { v[r] = exp_f32(v[r] - m); se[wave][i] = v[r]; }
+            if (i < n) v[r] = exp_f32(v[r] - m);
+            se[wave][i] = i < n ? v[r] : 0.0f;  // entries past n add +0: the sum keeps its bits
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        // one lane adds in index order (the reference's sum), reading 4 values per LDS access
+        // one lane adds in index order (the reference's sum): 64 values a chunk read ahead into registers, 4 per LDS
+        // access, then added one by one
         float s = 0.0f;
         if (lane == 0) {
-            int i = 0;
-#pragma unroll 4
-            for (; i + 4 <= n; i += 4) {
-                const float4 q = *(const float4*)&se[wave][i];
-                s += q.x;
-                s += q.y;
-                s += q.z;
-                s += q.w;
+#pragma unroll
+            for (int c = 0; c < 64 * ROUTE_R; c += 64) {
+                float4 q[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) q[u] = *(const float4*)&se[wave][c + 4 * u];
+#pragma unroll
+                for (int u = 0; u < 16; u++) {
+                    s += q[u].x;
+                    s += q[u].y;
+                    s += q[u].z;
+                    s += q[u].w;
+                }
             }
-            for (; i < n; i++) s += se[wave][i];
         }
         s = __shfl(s, 0);
 #pragma unroll
         for (int r = 0; r < ROUTE_R; r++) v[r] = v[r] / s;
     }
     // ops::top_k: k rounds of the wave's largest value, ties to the lower index. v >= 0, so its bits order as it;
-    // key = (bits + 1) << 32 | ~index, 0 for taken or absent entries.
-    unsigned taken = 0;
+    // key = bits + 1, 0 for taken or absent entries. A round takes the largest key by 32-bit max steps, then the
+    // lowest index holding it from ballots in index order (entry r of lane l is index 64 r + l).
+    uint32_t key[ROUTE_R];
+#pragma unroll
+    for (int r = 0; r < ROUTE_R; r++) key[r] = lane + 64 * r < n ? __float_as_uint(v[r]) + 1u : 0u;
     int my_id = 0;
     float my_p = 0.0f;
     for (int j = 0; j < k; j++) {
-        uint64_t best = 0;
+        uint32_t best = key[0];
+#pragma unroll
+        for (int r = 1; r < ROUTE_R; r++) best = max(best, key[r]);
+        best = max(best, (uint32_t)xl32<0>((int)best));
+        best = max(best, (uint32_t)xl32<1>((int)best));
+        best = max(best, (uint32_t)xl32<2>((int)best));
+        best = max(best, (uint32_t)xl32<3>((int)best));
+        best = max(best, (uint32_t)xl32<4>((int)best));
+        best = max((uint32_t)__builtin_amdgcn_readlane((int)best, 0), (uint32_t)__builtin_amdgcn_readlane((int)best, 32));
+        int bi = 0;
 #pragma unroll
         for (int r = 0; r < ROUTE_R; r++) {
-            int i = lane + 64 * r;
-            if (i < n && !((taken >> r) & 1)) {
-                uint64_t key = (uint64_t)(__float_as_uint(v[r]) + 1u) << 32 | (uint32_t)~(uint32_t)i;
-                if (key > best) best = key;
+            const uint64_t m = __ballot(key[r] == best);
+            if (m) {
+                bi = 64 * r + (int)__builtin_ctzll(m);
+                break;
             }
         }
-        // the largest key within each 32 lanes (DPP and swizzle steps), then the larger of the two halves
-        auto step = [&](auto S) __attribute__((always_inline)) {
-            constexpr int st = decltype(S)::value;
-            const uint64_t other = (uint64_t)(uint32_t)xl32<st>((int)(best >> 32)) << 32 | (uint32_t)xl32<st>((int)best);
-            best = other > best ? other : best;
-        };
-        step(std::integral_constant<int, 0>{});
-        step(std::integral_constant<int, 1>{});
-        step(std::integral_constant<int, 2>{});
-        step(std::integral_constant<int, 3>{});
-        step(std::integral_constant<int, 4>{});
-        {
-            const uint64_t b0 = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(best >> 32), 0) << 32 |
-                                (uint32_t)__builtin_amdgcn_readlane((int)best, 0);
-            const uint64_t b1 = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(best >> 32), 32) << 32 |
-                                (uint32_t)__builtin_amdgcn_readlane((int)best, 32);
-            best = b0 > b1 ? b0 : b1;
-        }
-        int bi = (int)~(uint32_t)best;
-        float bv = __uint_as_float((uint32_t)(best >> 32) - 1u);
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == j) { my_id = bi; my_p = bv; }
+#pragma unroll
+        for (int r = 0; r < ROUTE_R; r++)
+            if (bi == 64 * r + lane) key[r] = 0u;
+        if (lane == j) { my_id = bi; my_p = __uint_as_float(best - 1u); }
     }
     // Weights: p / max(sum of the top k in rank order, 2^-14) (times extra_scale when not 0).
     float sum = 0.0f;
     for (int j = 0; j < k; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), j));
     float scale = 1.0f / fmaxf(sum, 6.103515625e-5f);
     if (extra_scale != 0.0f) scale *= extra_scale;
+    int slot = -1;  // table[my_id]: entry my_id >> 6 of lane my_id & 63
+#pragma unroll
+    for (int r = 0; r < ROUTE_R; r++) {
+        const int c = __shfl(tv[r], my_id & 63);
+        if ((my_id >> 6) == r) slot = c;
+    }
     if (lane < k) {
         int o = t * k + lane;
         float w = my_p * scale;
         ids[o] = my_id;
         wts[o] = w;
         if (table) {
-            int s = table[my_id];
-            slots[o] = s;
-            wh[o] = s >= 0 ? w : 0.0f;
+            slots[o] = slot;
+            wh[o] = slot >= 0 ? w : 0.0f;
         }
     }
 }
