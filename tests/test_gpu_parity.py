@@ -3,6 +3,8 @@
 Bars: dequant, quantized activations, routing ids, sort/gather indices bit-exact; fp32 outputs within max relative
 error 1e-3 (floor 1e-3 max|r|), the accumulation-order tolerance of the task.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -175,6 +177,22 @@ def test_gemv_matches_cpu_matvec(hip, ty, rows, cols):
     # and against the f64 dot of the dequantized weights with the same Q8_K activations
     wf = O.dequant(ty, w, rows * cols).reshape(rows, cols).astype(np.float64)
     assert rel_l2(got, wf @ seen_q8k(x)) < 1e-5
+
+
+@pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.Q8_0])
+@pytest.mark.parametrize("rows", [6144, 151936])
+def test_gemv_sweep_shapes(hip, ty, rows):
+    """configs[1] at full size (the fused-QKV-like and lm-head-like shapes, 2048 columns): every row against the
+    oracle's cpu_moe::matvec (tiles of many rows: a row past a tile's loaded bytes would show here)."""
+    cols = 2048
+    w = random_blocks(ty, rows, cols, seed=rows + ty)
+    x = normal(cols, seed=rows + ty + 1)
+    t = hip.upload_tensor(ty, w)
+    y = hip.alloc(rows * 4)
+    hip.gemv(t, up(hip, x), y)
+    got = down(hip, y, np.float32, rows)
+    want = O.matvec(ty, w, rows, cols, x, threads=min(16, os.cpu_count() or 1))
+    assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
 
 
 def test_gemv_per32_numerics(hip):
