@@ -371,6 +371,37 @@ def test_sort_bit_exact(hip, t, k, E, chunk):
             assert int(tl[m, i, 1]) == m0 | (c << 32)
 
 
+def test_empty_inputs_are_no_ops(hip):
+    """Zero rows, tokens, slots or tiles: every entry point returns cleanly and writes nothing (a sentinel stays), and
+    a sort of no pairs yields zero offsets and zero tiles, which a grouped GEMM then reads as no work."""
+    E, k, H, F = 8, 2, 512, 256
+    sentinel = np.full(64, 7.25, dtype=np.float32)
+    y = up(hip, sentinel)
+    b = hip.alloc(4096)
+    ty = ggml.Q4_K
+    w = up(hip, random_blocks(ty, 4, H, seed=5))
+    hip.dequant(S.GpuTensor(ty, 4, H, w), 0, y)
+    hip.quant_xq(b, H, H, 0, y)
+    hip.swiglu_q(b, b, H, 0, y)
+    hip.gemv(S.GpuTensor(ty, 0, H, w), b, y)
+    hip.moe_gemv(ty, F, H, w, 0, b, 0, b, H, 1, y)
+    hip.router_topk(b, E, k, 0.0, y, y, 0)
+    hip.moe_route(b, E, k, 0.0, b, y, y, y, y, 0)
+    hip.moe_combine_seq(y, b, b, b, k, 0, 0, H, 0)
+    hip.moe_combine(y, b, b, k, 0, 0, H, 0)
+    hip.gemm(ty, F, H, b, 0, b, H, 0, 0, y, F, S.ACT_STORE)
+    assert np.array_equal(down(hip, y, np.float32, 64), sentinel)
+    # a sort of no pairs, then the grouped GEMM over its (empty) tile list
+    off, xrow, inv = up(hip, np.full(E + 1, -1, np.int32)), hip.alloc(16), hip.alloc(16)
+    max_tiles = E
+    tiles, ntd, err = hip.alloc(max_tiles * 16), up(hip, np.array([-1], np.int32)), hip.alloc(4)
+    hip.moe_sort(b, 0, k, E, off, xrow, inv, [(int(w), 0)], tiles, max_tiles, ntd, err)
+    assert np.array_equal(down(hip, off, np.int32, E + 1), np.zeros(E + 1, np.int32))
+    assert down(hip, ntd, np.int32, 1)[0] == 0 and down(hip, err, np.int32, 1)[0] == 0
+    hip.gemm_grouped(ty, 64, H, tiles, max_tiles, ntd, b, H, 0, xrow, y, 64, S.ACT_STORE)
+    assert np.array_equal(down(hip, y, np.float32, 64), sentinel)
+
+
 def test_sort_counts_bad_ids(hip):
     ids = np.array([[0, 5], [9, 1]], dtype=np.int32)  # 9 is out of range for 6 experts
     E, t, k = 6, 2, 2
