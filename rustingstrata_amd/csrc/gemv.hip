@@ -321,10 +321,12 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl,
     for (int j = n / 16 + threadIdx.x; j < nup / 16; j += blockDim.x) xss[j] = 0;
 }
 
-// The first tile's x row when it has at most 2048 values, requested before the tile's weights so that its arrival
-// and quantization overlap the weights' flight: (f32 x) this thread's 8 values; (xq) its 16-byte chunk and scale.
+// The first tile's x row when it has at most 4096 values, requested before the tile's weights so that its arrival
+// and quantization overlap the weights' flight: (f32 x) this thread's 8 values of each half (XH values); (xq) its
+// 16-byte chunk and scale.
+constexpr int XH = 8 * GEMV1_THREADS;  // values of one half of an early x row
 struct XEarly {
-    v4f f0, f1, u0, u1;
+    v4f f0, f1, u0, u1, f2, f3, u2, u3;
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     v4u q;
     float d;
@@ -345,6 +347,15 @@ __device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) 
             e.u0 = *gptr<v4f>(ur);
             e.u1 = *gptr<v4f>(ur + 16);
         }
+        if (XH + 8 * tid < a.cols) {
+            e.f2 = *gptr<v4f>(xr + 4 * XH);
+            e.f3 = *gptr<v4f>(xr + 4 * XH + 16);
+            if constexpr (SW) {
+                const uint64_t ur = (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) + 32 * (uint64_t)tid;
+                e.u2 = *gptr<v4f>(ur + 4 * XH);
+                e.u3 = *gptr<v4f>(ur + 4 * XH + 16);
+            }
+        }
     }
 }
 template <bool Q32, bool SW>
@@ -358,18 +369,27 @@ __device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t
         }
         if (tid < n / 32) xld[tid] = e.d;
     } else {
-        const bool live = 8 * tid < n;
-        float v[8] = {e.f0.x, e.f0.y, e.f0.z, e.f0.w, e.f1.x, e.f1.y, e.f1.z, e.f1.w};
-        if constexpr (SW) {
-            const float u[8] = {e.u0.x, e.u0.y, e.u0.z, e.u0.w, e.u1.x, e.u1.y, e.u1.z, e.u1.w};
+        // each half of XH values present: every thread takes 8 values of it
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = silu_f32(v[j]) * u[j];
-        }
-        if (!live) {
+        for (int h = 0; h < 2; h++) {
+            if (XH * h < n) {
+                const int i = XH * h + 8 * tid;
+                const bool live = i < n;
+                const v4f a0 = h ? e.f2 : e.f0, a1 = h ? e.f3 : e.f1;
+                float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                if constexpr (SW) {
+                    const v4f b0 = h ? e.u2 : e.u0, b1 = h ? e.u3 : e.u1;
+                    const float u[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = 0.0f;
+                    for (int j = 0; j < 8; j++) v[j] = silu_f32(v[j]) * u[j];
+                }
+                if (!live) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) v[j] = 0.0f;
+                }
+                quant8_lds<Q32>(v, i, live, xl, xld, xss);
+            }
         }
-        quant8_lds<Q32>(v, 8 * tid, live, xl, xld, xss);
     }
     const int nup = (n + 255) & ~255;
     for (int i = n + 4 * tid; i < nup; i += 4 * blockDim.x) *(uint32_t*)(xl + xpad(i)) = 0;
@@ -481,7 +501,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     int t = next_valid(blockIdx.x);
     if (t >= total) return;
     Span sp = span(t);
-    const bool early = a.cols <= 8 * GEMV1_THREADS;
+    const bool early = a.cols <= 16 * GEMV1_THREADS;
     XEarly xe;
     if (early) x_fetch<SW>(a, sp.xrow, xe);
     issue(sp);

@@ -167,7 +167,7 @@ def gemv_case(hip, ty, rows, cols, seed):
 
 
 @pytest.mark.parametrize("ty", ggml.TYPES)
-@pytest.mark.parametrize("rows,cols", [(257, 2048), (64, 768), (33, 4096)])
+@pytest.mark.parametrize("rows,cols", [(257, 2048), (64, 768), (33, 4096), (40, 3072)])
 def test_gemv_matches_cpu_matvec(hip, ty, rows, cols):
     if ty == ggml.Q8_0 and cols == 768:
         cols = 736  # Q8_0 rows need only a multiple of 32
@@ -195,9 +195,10 @@ def test_gemv_sweep_shapes(hip, ty, rows):
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
 
 
-def test_gemv_per32_numerics(hip):
+@pytest.mark.parametrize("cols", [2048, 3072, 4096])
+def test_gemv_per32_numerics(hip, cols):
     """Reference GPU numerics (per-32 x scales): against f64 dequant times as_seen(x) (tests/kernels.rs:11-19,61)."""
-    ty, rows, cols = ggml.Q5_K, 100, 2048
+    ty, rows = ggml.Q5_K, 100
     hip.set_numerics(S.NUM_Q8_32)
     try:
         w, x, _, got = gemv_case(hip, ty, rows, cols, seed=9)
@@ -678,10 +679,12 @@ def test_moe_decode_layer_matches_experts(hip):
 
 
 @pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])
-def test_moe_down_swiglu_combine_matches_unfused(hip, numerics):
+@pytest.mark.parametrize("F", [768, 3072])
+def test_moe_down_swiglu_combine_matches_unfused(hip, numerics, F):
     """The fused decode tail (swiglu inside the down GEMV) gives the same bits as swiglu_q followed by
-    moe_down_combine (src/gpu_model.rs:3383-3412): same int8 x, same GEMV, same combine; 3 tokens, a shared expert."""
-    E, H, F, k, t = 16, 512, 768, 8, 3
+    moe_down_combine (src/gpu_model.rs:3383-3412): same int8 x, same GEMV, same combine; 3 tokens, a shared expert.
+    F = 3072: x rows past 2048 values (the second half of the early x fetch)."""
+    E, H, k, t = 16, 512, 8, 3
     _, _, dn = moe_weights(E, H, F, seed=60)
     rb_d = ggml.row_bytes(ggml.Q6_K, F)
     d_b = up(hip, dn)
