@@ -57,14 +57,35 @@ __device__ __forceinline__ float dpp_f(float v) {
 // Sum over aligned groups of g lanes (g a power of two), complete in the group's first lane: in-row steps by DPP
 // (xor 1, xor 2 by quad permutes, then + lane i + 4, + lane i + 8), wider ones by lane permutes. The additions pair
 // the same values in the same order as an xor butterfly.
-__device__ __forceinline__ float group_sum(float v, int g) {
-    if (g >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-    if (g >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-    if (g >= 8) v += dpp_f<0x104>(v);  // row_shl:4
-    if (g >= 16) v += dpp_f<0x108>(v); // row_shl:8
-    if (g >= 32) v += __shfl_xor(v, 16);
-    if (g >= 64) v += __shfl_xor(v, 32);
-    return v;
+// The row's super-block terms (lane p of a group of g holds term p) added in super-block order, as the CPU dots'
+// running sum does (src/cpu_moe.rs:319-377: sumf = 0, then sumf += each super-block's term); the sum is valid at the
+// group's last lane. Within a row of 16 lanes: g - 1 steps s = f + (s of the lane below) (row_shr:1), so after them
+// lane g - 1 holds f_{g-1} + (... + (f_1 + f_0)). Wider groups add the lanes' terms one by one through shuffles.
+// Terms are first made +0 from -0, as the CPU's sum starts from +0.
+template <int G>
+__device__ __forceinline__ float ordered_sum_row(float f) {
+    float s = f;
+#pragma unroll
+    for (int k = 1; k < G; k++) s = f + dpp_f<0x111>(s);  // row_shr:1
+    return s;
+}
+__device__ __forceinline__ float ordered_sum(float v, int g) {
+    const float f = v + 0.0f;
+    float s = f;
+    if (g == 8) {  // 2048 columns, the common case: one straight chain
+        s = ordered_sum_row<8>(f);
+    } else if (g == 4) {
+        s = ordered_sum_row<4>(f);
+    } else if (g == 2) {
+        s = ordered_sum_row<2>(f);
+    } else if (g == 16) {
+        s = ordered_sum_row<16>(f);
+    } else if (g > 16) {
+        const int base = (threadIdx.x & 63) & ~(g - 1);
+        s = 0.0f;
+        for (int j = 0; j < g; j++) s = s + __shfl(f, base + j);
+    }
+    return s;
 }
 
 template <int T, int NT, bool Q32>
@@ -189,8 +210,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
                 }
             }
 #pragma unroll
-            for (int u = 0; u < NT; u++) acc[u] = group_sum(acc[u], G);
-            if (rr < cs.nr && gl == 0) {
+            for (int u = 0; u < NT; u++) acc[u] = ordered_sum(acc[u], G);
+            if (rr < cs.nr && gl == G - 1) {
 #pragma unroll
                 for (int u = 0; u < NT; u++) cs.Y[(int64_t)u * a.y_stride + cs.r0 + rr] = acc[u];
             }
@@ -560,8 +581,8 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
                 const uint8_t* b = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb + gl * SBB;
                 acc = Q32 ? sb_dot_q32<T>(b, x, tab, nv) : sb_dot_q8k<T>(b, x, tab, nv);
             }
-            acc = group_sum(acc, G);
-            if (rr < cs.nr && gl == 0) cs.Y[cs.r0 + rr] = acc;
+            acc = ordered_sum(acc, G);
+            if (rr < cs.nr && gl == G - 1) cs.Y[cs.r0 + rr] = acc;
         }
         GTRACE(4);
         LTRACE(3);

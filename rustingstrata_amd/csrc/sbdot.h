@@ -146,9 +146,9 @@ __device__ __forceinline__ void sb_q6(const uint8_t* b, const X& x, int& isum, f
     isum = is;
 }
 
-// ---- Q8_0: 8 blocks of 32 with an f16 scale each (src/cpu_moe.rs:319-325): returns sum_b d_b * s_b ----
+// ---- Q8_0: 8 blocks of 32 with an f16 scale each (src/cpu_moe.rs:319-325): returns sum_b (d_b dx) s_b ----
 template <class X>
-__device__ __forceinline__ float sb_q8_0(const uint8_t* b, const X& x, int nb) {
+__device__ __forceinline__ float sb_q8_0(const uint8_t* b, const X& x, int nb, float dx) {
     float f = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
@@ -159,7 +159,7 @@ __device__ __forceinline__ float sb_q8_0(const uint8_t* b, const X& x, int nb) {
 #pragma unroll
         for (int i = 0; i < 8; i++) q[i] = align_bytes(w[i + 1], w[i], 2);
         const int s = dot16(q, x.q16(32 * k), x.q16(32 * k + 16));
-        f += f16_to_f32(w[0] & 0xFFFF) * (float)s;
+        f = f + (f16_to_f32(w[0] & 0xFFFF) * dx) * (float)s;
     }
     return f;
 }
@@ -184,7 +184,11 @@ __device__ __forceinline__ void sb_generic(const uint8_t* b, const X& x, const I
     msum = ms;
 }
 
-// The super-block's contribution, Q8_K numerics (one x scale for the whole super-block).
+// The super-block's contribution, Q8_K numerics (one x scale for the whole super-block), in the CPU dots' float
+// steps (src/cpu_moe.rs:319-377): (D dx) s - (M dx) m, each product rounded; Q8_0 adds its 32-blocks' (d dx) s in
+// order. Summed over a row's super-blocks in order (ordered_sum), the K-quant, IQ2_XXS and IQ3_S rows carry the CPU
+// dots' bits; Q8_0 (whose CPU sum runs over 32-blocks across super-blocks) and IQ4_XS (a float step per 32-value
+// sub-block, src/cpu_moe.rs:195-212) stay within rounding of them.
 template <int T, class X>
 __device__ __forceinline__ float sb_dot_q8k(const uint8_t* b, const X& x, const IqTables* tab, int nvals) {
     const float dx = x.d(0);
@@ -192,21 +196,21 @@ __device__ __forceinline__ float sb_dot_q8k(const uint8_t* b, const X& x, const 
         int is, ms;
         float D, M;
         sb_q45<T == Q5_K>(b, x, is, ms, D, M);
-        return dx * (D * (float)is - M * (float)ms);
+        return (D * dx) * (float)is - (M * dx) * (float)ms;
     } else if constexpr (T == Q6_K) {
         int is;
         float D;
         sb_q6(b, x, is, D);
-        return dx * (D * (float)is);
+        return (D * dx) * (float)is;
     } else if constexpr (T == Q8_0) {
-        return dx * sb_q8_0(b, x, nvals >> 5);
+        return sb_q8_0(b, x, nvals >> 5, dx);
     } else {
         int is, ms = 0;
         float D, M = 0.0f;
         sb_generic<T>(b, x, tab, is, ms, D, M);
-        float f = D * (float)is;
-        if constexpr (Fmt<T>::MIN) f -= M * (float)ms;
-        return dx * f;
+        float f = (D * dx) * (float)is;
+        if constexpr (Fmt<T>::MIN) f = f - (M * dx) * (float)ms;
+        return f;
     }
 }
 

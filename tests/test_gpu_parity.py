@@ -174,6 +174,9 @@ def test_gemv_matches_cpu_matvec(hip, ty, rows, cols):
     w, x, _, got = gemv_case(hip, ty, rows, cols, seed=7 * ty + cols)
     want = O.matvec(ty, w, rows, cols, x)
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+    if ty not in (ggml.Q8_0, ggml.IQ4_XS):
+        # the CPU dot's float steps and its super-block order: the same bits
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), int((got != want).sum())
     # and against the f64 dot of the dequantized weights with the same Q8_K activations
     wf = O.dequant(ty, w, rows * cols).reshape(rows, cols).astype(np.float64)
     assert rel_l2(got, wf @ seen_q8k(x)) < 1e-5
@@ -509,6 +512,10 @@ def test_gemm_tiles_match_cpu(hip, ty):
         for m in range(m0, m0 + c):
             want[m] = O.matvec(ty, we, rows, cols, x[xrow[m]])
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+    if ty != ggml.IQ4_XS:
+        # the CPU dots' float steps per super-block (per 32-block for Q8_0), in order: the same bits. IQ4_XS closes
+        # each 32-value sub-block in float on the CPU (src/cpu_moe.rs:195-212), here once per super-block.
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), int((got != want).sum())
     # act 1: y = silu(y) * (W x) with the same x (SAME_X), then act 2: y += W x
     hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_SWIGLU | S.SAME_X)
     got2 = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
@@ -590,6 +597,22 @@ def test_moe_prefill_layer_matches_experts_multi(hip):
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
     # gate and up as one grouped GEMM: the same bits
     assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True), got)
+
+
+def test_moe_prefill_layer_full_size(hip):
+    """configs[2] at its full size (128 experts, hidden 2048, intermediate 768, top-8, 4096 tokens, Zipf-skewed
+    routing): the device layer against cpu_moe::experts_multi on every token, and the fused gate/up launch equal to
+    the two-call sequence bit for bit."""
+    E, H, F, T, k = 128, 2048, 768, 4096, 8
+    gate, upw, dn = moe_weights(E, H, F, seed=140)
+    hs = normal((T, H), seed=141)
+    logits = zipf_logits(T, E, seed=142)
+    ids_w, wts_w = O.route(logits, k)
+    want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, hs, ids_w, wts_w,
+                           threads=min(16, os.cpu_count() or 1))
+    got = run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True)
+    assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+    assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits), got)
 
 
 def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=False):
