@@ -198,6 +198,24 @@ def test_gemv_sweep_shapes(hip, ty, rows):
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
 
 
+@pytest.mark.parametrize("ty", [ggml.Q2_K, ggml.Q3_K, ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S])
+def test_gemv_bits_over_random_shapes(hip, ty):
+    """The CPU dot's bits over seeded random shapes (1-300 rows, 256-8192 columns) and weight scales spanning
+    2^-14..2^4 (down to f16 subnormal-adjacent d): the per-super-block float steps and their order hold everywhere."""
+    rng = np.random.default_rng(500 + ty)
+    for case in range(6):
+        rows, cols = int(rng.integers(1, 301)), 256 * int(rng.integers(1, 33))
+        lo = float(2.0 ** rng.integers(-14, 4))
+        w = random_blocks(ty, rows, cols, seed=int(rng.integers(1 << 30)), scale=(lo, 2 * lo))
+        x = normal(cols, seed=int(rng.integers(1 << 30)), std=float(2.0 ** rng.integers(-6, 6)))
+        t = hip.upload_tensor(ty, w)
+        y = hip.alloc(rows * 4)
+        hip.gemv(t, up(hip, x), y)
+        got = down(hip, y, np.float32, rows)
+        want = O.matvec(ty, w, rows, cols, x)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (case, rows, cols, lo, int((got != want).sum()))
+
+
 @pytest.mark.parametrize("cols", [2048, 3072, 4096])
 def test_gemv_per32_numerics(hip, cols):
     """Reference GPU numerics (per-32 x scales): against f64 dequant times as_seen(x) (tests/kernels.rs:11-19,61)."""
