@@ -596,6 +596,24 @@ def test_gemm_dense(hip, ty):
     assert max_rel_err(got, want) <= TOL
 
 
+@pytest.mark.parametrize("ty", [ggml.Q2_K, ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ3_S, ggml.Q8_0])
+def test_gemm_dense_bits_over_random_shapes(hip, ty):
+    """gemm_dense against the CPU dot's bits over seeded random shapes: rows 1-400 (partial 128-row blocks), 256-4096
+    columns, 1-600 positions (partial 256-position blocks), weight scales 2^-12..2^2."""
+    rng = np.random.default_rng(700 + ty)
+    for case in range(3):
+        rows, cols, n = int(rng.integers(1, 401)), 256 * int(rng.integers(1, 17)), int(rng.integers(1, 601))
+        lo = float(2.0 ** rng.integers(-12, 2))
+        w = random_blocks(ty, rows, cols, seed=int(rng.integers(1 << 30)), scale=(lo, 2 * lo))
+        x = normal((n, cols), seed=int(rng.integers(1 << 30)))
+        t = hip.upload_tensor(ty, w)
+        y = hip.alloc(n * rows * 4)
+        hip.gemm_dense(t, n, up(hip, x), cols, y, rows, S.ACT_STORE)
+        got = down(hip, y, np.float32, n * rows).reshape(n, rows)
+        want = np.stack([O.matvec(ty, w, rows, cols, x[i]) for i in range(n)])
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (case, rows, cols, n, int((got != want).sum()))
+
+
 def moe_weights(E, H, F, seed):
     gate = random_blocks(ggml.Q5_K, E * F, H, seed=seed)
     upw = random_blocks(ggml.Q5_K, E * F, H, seed=seed + 1)
