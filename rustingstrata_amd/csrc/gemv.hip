@@ -347,7 +347,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl,
 // 16-byte chunk and scale.
 constexpr int XH = 8 * GEMV1_THREADS;  // values of one half of an early x row
 struct XEarly {
-    v4f f0, f1, u0, u1, f2, f3, u2, u3;
+    v4f f0, f1, u0, u1, f2, f3;
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     v4u q;
     float d;
@@ -368,15 +368,13 @@ __device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) 
             e.u0 = *gptr<v4f>(ur);
             e.u1 = *gptr<v4f>(ur + 16);
         }
-        if (XH + 8 * tid < a.cols) {
-            e.f2 = *gptr<v4f>(xr + 4 * XH);
-            e.f3 = *gptr<v4f>(xr + 4 * XH + 16);
-            if constexpr (SW) {
-                const uint64_t ur = (uint64_t)(a.xu + (uint64_t)xrow * a.x_stride) + 32 * (uint64_t)tid;
-                e.u2 = *gptr<v4f>(ur + 4 * XH);
-                e.u3 = *gptr<v4f>(ur + 4 * XH + 16);
+        // (the SwiGLU input takes the early path for its first half only: its second half's registers would be
+        // live across the weight loads of a kernel already at 256 VGPRs)
+        if constexpr (!SW)
+            if (XH + 8 * tid < a.cols) {
+                e.f2 = *gptr<v4f>(xr + 4 * XH);
+                e.f3 = *gptr<v4f>(xr + 4 * XH + 16);
             }
-        }
     }
 }
 template <bool Q32, bool SW>
@@ -392,14 +390,14 @@ __device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t
     } else {
         // each half of XH values present: every thread takes 8 values of it
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < (SW ? 1 : 2); h++) {
             if (XH * h < n) {
                 const int i = XH * h + 8 * tid;
                 const bool live = i < n;
                 const v4f a0 = h ? e.f2 : e.f0, a1 = h ? e.f3 : e.f1;
                 float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
                 if constexpr (SW) {
-                    const v4f b0 = h ? e.u2 : e.u0, b1 = h ? e.u3 : e.u1;
+                    const v4f b0 = e.u0, b1 = e.u1;
                     const float u[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
                     for (int j = 0; j < 8; j++) v[j] = silu_f32(v[j]) * u[j];
@@ -522,7 +520,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     int t = next_valid(blockIdx.x);
     if (t >= total) return;
     Span sp = span(t);
-    const bool early = a.cols <= 16 * GEMV1_THREADS;
+    const bool early = a.cols <= (SW ? 1 : 2) * XH;
     XEarly xe;
     if (early) x_fetch<SW>(a, sp.xrow, xe);
     issue(sp);
