@@ -73,11 +73,14 @@ void* strata_stream(strata_ctx* ctx);
  * strata_graph_begin starts recording the ops queued on the context's stream; strata_graph_end stops and returns an
  * executable graph; strata_graph_launch replays it on the stream. As in the trait, the recorded ops must read their
  * per-call values from device memory. Ops whose scratch would have to grow cannot be recorded (run them once
- * before recording). */
+ * before recording): they return an error while recording. Scratch that a later, larger eager call replaces stays
+ * allocated while any graph of the context exists (the graphs keep its address), and is freed when the last one is
+ * destroyed. A STRATA_SAME_X gemm inside a recording reuses only a quantization recorded in the same recording
+ * (strata_graph_begin forgets the cached X). */
 int strata_graph_begin(strata_ctx* ctx);
 int strata_graph_end(strata_ctx* ctx, void** graph);
 int strata_graph_launch(strata_ctx* ctx, void* graph);
-int strata_graph_destroy(void* graph);
+int strata_graph_destroy(strata_ctx* ctx, void* graph);
 
 /* ---- dequant and activation quantization ---- */
 

@@ -54,7 +54,7 @@ SIGNATURES = {
     "strata_graph_begin": [CTX],
     "strata_graph_end": [CTX, ctypes.POINTER(P)],
     "strata_graph_launch": [CTX, P],
-    "strata_graph_destroy": [P],
+    "strata_graph_destroy": [CTX, P],
     "strata_dequant": [CTX, TP, U64, U64],
     "strata_quant_xq": [CTX, U64, U64, U64, U64, U64],
     "strata_rms_norm": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float],
@@ -260,7 +260,7 @@ class HipBackend:
 
     def drop_graphs(self):
         for g in getattr(self, "_graphs", {}).values():
-            lib().strata_graph_destroy(g)
+            lib().strata_graph_destroy(self._ctx, g)
         self._graphs = {}
 
     # ---- ops ----

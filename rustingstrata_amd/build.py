@@ -29,9 +29,9 @@ def hipcc():
     return "hipcc"
 
 
-def _compile(src, build_dir=BUILD, defines=()):
+def _compile(src, build_dir=BUILD):
     obj = os.path.join(build_dir, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *FLAGS, *defines, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".cpp"):
         cmd = [hipcc(), "-x", "c++", "-O3", "-fPIC", "-std=c++17", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -40,11 +40,11 @@ def _compile(src, build_dir=BUILD, defines=()):
     return obj
 
 
-def build(verbose=False, out=OUT, build_dir=BUILD, defines=()):
-    """Compile and link; `defines` (-DNAME=VALUE) select tuning variants of the kernels."""
+def build(verbose=False, out=OUT, build_dir=BUILD):
+    """Compile every source and link the library."""
     os.makedirs(build_dir, exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, build_dir, defines), SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, build_dir), SOURCES))
     tmp = out + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp, *objs, "-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)

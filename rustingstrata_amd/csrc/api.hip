@@ -5,6 +5,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "kernels.h"
 #include "moe.h"
@@ -39,16 +40,22 @@ const char* type_name(int ty) {
     return "unknown";
 }
 
-// Device scratch that grows on demand. Growing waits for the stream first: queued kernels may still read it.
+// Device scratch that grows on demand. Growing waits for the stream first: queued kernels may still read it. A
+// recorded graph keeps the addresses it was recorded with, so a buffer replaced while any graph of the context
+// exists is retired, not freed, until the last graph is destroyed (or the context closes); while the stream is
+// recording, scratch cannot grow at all (the wait would end the recording).
 struct Scratch {
     void* p = nullptr;
     size_t n = 0;
-    hipError_t need(size_t bytes, hipStream_t s) {
+    std::vector<void*> retired;
+    hipError_t need(size_t bytes, hipStream_t s, bool recording, bool graphs_alive) {
         if (bytes <= n) return hipSuccess;
+        if (recording) return hipErrorStreamCaptureUnsupported;
         if (p) {
             hipError_t e = hipStreamSynchronize(s);
             if (e != hipSuccess) return e;
-            hipFree(p);
+            if (graphs_alive) retired.push_back(p);
+            else hipFree(p);
             p = nullptr;
             n = 0;
         }
@@ -58,7 +65,12 @@ struct Scratch {
         n = want;
         return hipSuccess;
     }
+    void free_retired() {
+        for (void* q : retired) hipFree(q);
+        retired.clear();
+    }
     void release() {
+        free_retired();
         if (p) hipFree(p);
         p = nullptr;
         n = 0;
@@ -77,6 +89,9 @@ struct strata_ctx {
     Scratch gx;                          // quantized x of the GEMM (kept for SAME_X)
     uint64_t gx_key[4] = {0, 0, 0, 0};   // x, x_stride, n_x, cols of gx's contents (all 0: none)
     Scratch misc;
+    bool recording = false;              // between strata_graph_begin and strata_graph_end
+    int graphs = 0;                      // executable graphs made by this context and not yet destroyed
+    hipError_t need(Scratch& s, size_t bytes) { return s.need(bytes, stream, recording, graphs > 0); }
 };
 
 namespace {
@@ -130,7 +145,7 @@ int check_align(int ty, uint64_t addr, const char* what) {
 
 // Quantize x (nt rows, x_stride apart) into the context's GEMV scratch; returns the scratch address.
 int quant_into_scratch(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t n, uint64_t nt, uint64_t* out) {
-    STRATA_HIP(c->xq.need(xq_bytes(n, nt), c->stream));
+    STRATA_HIP(c->need(c->xq, xq_bytes(n, nt)));
     STRATA_HIP(launch_quant_xq((const float*)x, x_stride, (int)n, (int)nt, (int8_t*)c->xq.p, c->numerics, c->stream));
     *out = (uint64_t)c->xq.p;
     return 0;
@@ -281,6 +296,10 @@ void* strata_stream(strata_ctx* c) { return c ? (void*)c->stream : nullptr; }
 int strata_graph_begin(strata_ctx* c) {
     if (check_ctx(c)) return -1;
     STRATA_HIP(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    // A SAME_X hit inside the recording must not lean on a quantization queued before it: the graph would replay
+    // against whatever the GEMM-X scratch holds at launch time.
+    c->gx_key[0] = c->gx_key[1] = c->gx_key[2] = c->gx_key[3] = 0;
+    c->recording = true;
     return 0;
 }
 
@@ -288,11 +307,13 @@ int strata_graph_end(strata_ctx* c, void** graph) {
     if (check_ctx(c)) return -1;
     if (!graph) return set_error("strata_graph_end: null out");
     hipGraph_t g = nullptr;
+    c->recording = false;
     STRATA_HIP(hipStreamEndCapture(c->stream, &g));
     hipGraphExec_t ex = nullptr;
     hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
     hipGraphDestroy(g);
     if (e != hipSuccess) return hip_error(e, "hipGraphInstantiate");
+    c->graphs++;
     *graph = (void*)ex;
     return 0;
 }
@@ -303,8 +324,16 @@ int strata_graph_launch(strata_ctx* c, void* graph) {
     return 0;
 }
 
-int strata_graph_destroy(void* graph) {
+int strata_graph_destroy(strata_ctx* c, void* graph) {
+    if (check_ctx(c)) return -1;
     STRATA_HIP(hipGraphExecDestroy((hipGraphExec_t)graph));
+    if (c->graphs > 0 && --c->graphs == 0) {
+        // No graph holds a retired scratch address any more.
+        STRATA_HIP(hipStreamSynchronize(c->stream));
+        c->xq.free_retired();
+        c->gx.free_retired();
+        c->misc.free_retired();
+    }
     return 0;
 }
 
@@ -330,7 +359,7 @@ int strata_rms_norm_q(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t w, 
     if (check_ctx(c)) return -1;
     if (!x || !w || !out) return set_error("rms_norm: null x, w or out");
     if (xq && n % 32) return set_error("rms_norm_q: " + std::to_string(n) + " values (a multiple of 32 to quantize)");
-    if (n > (1u << 30) || rows > (1u << 31)) return set_error("rms_norm: too large");
+    if (n > (1u << 30) || rows >= (1ull << 31)) return set_error("rms_norm: too large");
     STRATA_HIP(launch_rms_norm_q((float*)x, x_stride, (const float*)w, (float*)out, out_stride, (int)n, (int)rows, eps,
                                  (int8_t*)xq, (const float*)res, c->numerics, c->stream));
     return 0;
@@ -377,6 +406,7 @@ int strata_gemvq2(strata_ctx* c, const strata_tensor* a, const strata_tensor* b,
         return strata_gemvq(c, b, x, x_stride, xq, yb, b->rows, nt);
     }
     if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
+    if (a->rows > (1u << 30) || b->rows > (1u << 30)) return set_error("gemvq2: too many rows");
     if (check_gemv_cols(a->ty, a->cols) || check_align(a->ty, a->ptr, "gemvq2") || check_align(b->ty, b->ptr, "gemvq2")) return -1;
     if (!xq && nt > 1 && quant_into_scratch(c, x, x_stride, a->cols, nt, &xq)) return -1;
     GemvLaunch g;
@@ -507,7 +537,7 @@ int strata_moe_sort(strata_ctx* c, uint64_t ids, uint64_t t, uint64_t k, uint64_
     for (uint64_t m = 0; m < n_mats; m++) { s.bases[m] = bases[m]; s.strides[m] = strides[m]; }
     s.tiles = (uint64_t*)tiles; s.max_tiles = (int)max_tiles; s.n_tiles = (int*)n_tiles_dev; s.err = (int*)err_dev;
     s.chunk = (int)chunk;
-    STRATA_HIP(c->misc.need(sort_scratch_bytes((int)n_expert, (int)(t * k)), c->stream));
+    STRATA_HIP(c->need(c->misc, sort_scratch_bytes((int)n_expert, (int)(t * k))));
     s.scratch = (int*)c->misc.p;
     STRATA_HIP(launch_sort(s, c->stream));
     return 0;
@@ -519,7 +549,7 @@ static int gemm_x(strata_ctx* c, uint64_t cols, uint64_t n_x, uint64_t x, uint64
     bool hit = same && std::equal(key, key + 4, c->gx_key);
     if (!hit) {
         c->gx_key[0] = c->gx_key[1] = c->gx_key[2] = c->gx_key[3] = 0;
-        STRATA_HIP(c->gx.need(gemm_x_bytes(cols, n_x), c->stream));
+        STRATA_HIP(c->need(c->gx, gemm_x_bytes(cols, n_x)));
         STRATA_HIP(launch_gemm_quant_x((const float*)x, x_stride, (int)cols, (int)n_x, (uint8_t*)c->gx.p, c->numerics, c->stream));
         std::copy(key, key + 4, c->gx_key);
     }

@@ -82,18 +82,6 @@ __device__ __forceinline__ float silu_dev(float v) {
     return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-#ifdef STRATA_GEMM_TRACE
-// Debug builds: shader clock at the phases of the first steps of a few waves (read with strata_debug_gemm_trace).
-__device__ uint64_t g_gemm_trace[8][64][6];
-#define TRACE(ph)                                                                                         \
-    do {                                                                                                  \
-        const int tb_ = blockIdx.x == 0 ? 0 : blockIdx.x == 37 ? 1 : -1;                                  \
-        if (tb_ >= 0 && (wave == 0 || wave == 4) && lane == 0 && g < 64)                                  \
-            g_gemm_trace[tb_ * 2 + (wave >> 2)][g][ph] = __builtin_amdgcn_s_memtime();                    \
-    } while (0)
-#else
-#define TRACE(ph) do {} while (0)
-#endif
 
 // f(std::integral_constant<int, I>) for I = B .. E - 1: the index is a constant expression in the body, so register
 // arrays indexed by it stay in registers.
@@ -444,10 +432,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     advance();
     int s = 0;
     for (int g = 0; g < G; g++) {
-        TRACE(0);
         const bool nx = g + 1 < G;
         if (nx) load_dx(aL, sL);
-        TRACE(1);
         decode(rbeg, s, [&](int kk) __attribute__((always_inline)) {
 #pragma unroll
             for (int h = 0; h < XI / 4; h++)
@@ -455,23 +441,15 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         });
         __syncthreads();  // every wave has decoded: the raw buffer takes the next step's weights
         if (nx) load_w(iL, aL, sL);
-        TRACE(2);
-#ifdef STRATA_GEMM_ANALYZE_ROLE0
-        tiles(g, NTT);
-#else
         tiles(g, (cur.cnt + 15) >> 4);
-#endif
         if (s + 1 == nsb) store(cur, g);
-        TRACE(3);
         if (nx) store_dx(g + 1);
         cur = iL;
         rbeg = aL.rbeg;
         s = sL;
         advance();
         wait_loads();
-        TRACE(4);
         __syncthreads();
-        TRACE(5);
     }
 }
 
@@ -518,11 +496,6 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
     return hipGetLastError();
 }
 
-#ifdef STRATA_GEMM_TRACE
-extern "C" int strata_debug_gemm_trace(uint64_t* out) {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_gemm_trace), sizeof(g_gemm_trace)) == hipSuccess ? 0 : -1;
-}
-#endif
 
 // ---- Q8_0 (src/cuda/kernels.cu:380-388): blocks of 32 int8 values, each with its own f16 scale ----
 // The block scales are floats that differ within a super-block, so they cannot fold into integer planes; instead one

@@ -17,10 +17,7 @@
 namespace strata {
 
 constexpr int GEMV_THREADS = 256;
-#ifndef STRATA_GEMV_CH
-#define STRATA_GEMV_CH 6
-#endif
-constexpr int GEMV_CH = STRATA_GEMV_CH;                              // 16-byte chunks per thread per tile
+constexpr int GEMV_CH = 6;                              // 16-byte chunks per thread per tile
 constexpr int GEMV_TILE = GEMV_THREADS * 16 * GEMV_CH;               // 24 KB of weights per block
 uint64_t gemv_max_row_bytes() { return GEMV_TILE - 32; }
 
@@ -144,11 +141,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < GEMV_CH; i++) {
             const int c = tid + GEMV_THREADS * i;
-#ifdef STRATA_GEMV_PLAIN_LOADS
-            if (c < sp.nch) wv[i] = *gptr<v4u>(sp.g0 + 16 * (uint64_t)c);
-#else
             if (c < sp.nch) wv[i] = __builtin_nontemporal_load(gptr<v4u>(sp.g0 + 16 * (uint64_t)c));
-#endif
         }
     };
 
@@ -193,12 +186,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
             float acc[NT];
 #pragma unroll
             for (int u = 0; u < NT; u++) acc[u] = 0.0f;
-#ifdef STRATA_GEMV_NOCOMPUTE
-            if (rr < cs.nr) acc[0] = (float)tile[rr];
-            if (false) {
-#else
             if (rr < cs.nr) {
-#endif
                 const uint8_t* rowp = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb;
                 for (int sb = gl; sb < nsb; sb += G) {
 #pragma unroll
@@ -228,14 +216,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
 // that 256-value slice of x in registers for the whole launch (reloaded only when a MoE tile switches x rows) and
 // LDS carries nothing but the weight tiles. x arrives pre-quantized (xq) or as f32, quantized by each lane for its
 // own slice with quant_xq's arithmetic (the same bits).
-#ifndef STRATA_GEMV1_CH
-#define STRATA_GEMV1_CH 12
-#endif
-constexpr int GEMV1_CH = STRATA_GEMV1_CH;
-#ifndef STRATA_GEMV1_WAVES
-#define STRATA_GEMV1_WAVES 4
-#endif
-constexpr int GEMV1_WAVES = STRATA_GEMV1_WAVES;          // waves of a single-input GEMV block
+constexpr int GEMV1_CH = 12;
+constexpr int GEMV1_WAVES = 4;          // waves of a single-input GEMV block
 constexpr int GEMV1_THREADS = 64 * GEMV1_WAVES;
 constexpr int GEMV1_TILE = GEMV1_THREADS * 16 * GEMV1_CH;
 
@@ -433,32 +415,11 @@ __device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const flo
     }
 }
 
-#ifdef STRATA_GEMV1_TRACE
-// Debug builds: shader clock at the phases of the first tile of blocks 0..63 (read with strata_debug_gemv_trace).
-__device__ uint64_t g_gemv_trace[64][8];
-__device__ uint64_t g_gemv_loop[32][4];
-#define GTRACE(ph)                                                                                          \
-    do {                                                                                                    \
-        if (blockIdx.x < 64 && threadIdx.x == 0) g_gemv_trace[blockIdx.x][ph] = __builtin_amdgcn_s_memtime(); \
-    } while (0)
-#define LTRACE(ph)                                                                                          \
-    do {                                                                                                    \
-        if (blockIdx.x == 5 && threadIdx.x == 0 && ltile < 32) g_gemv_loop[ltile][ph] = __builtin_amdgcn_s_memtime(); \
-    } while (0)
-#else
-#define GTRACE(ph) do {} while (0)
-#define LTRACE(ph) do {} while (0)
-#endif
 
-#ifdef STRATA_GEMV1_WPE
-#define GEMV1_ATTR __attribute__((amdgpu_waves_per_eu(STRATA_GEMV1_WPE)))
-#else
-#define GEMV1_ATTR
-#endif
 // SW: x rows are silu(xf) * xu (the fused SwiGLU input of the down projection); a separate instantiation, so the
 // plain GEMV carries none of it.
 template <int T, bool Q32, bool SW>
-__global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArgs a) {
+__global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -516,7 +477,6 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
         }
     };
 
-    GTRACE(0);
     int t = next_valid(blockIdx.x);
     if (t >= total) return;
     Span sp = span(t);
@@ -524,7 +484,6 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     XEarly xe;
     if (early) x_fetch<SW>(a, sp.xrow, xe);
     issue(sp);
-    GTRACE(1);
     // the tile after next is located while the next one is in flight
     int tn = next_valid(t + gridDim.x);
     Span spn = sp;
@@ -534,29 +493,19 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
     const bool has_sb = gl < nsb;
     XReg x;
     int cur_xrow = -1;
-#ifdef STRATA_GEMV1_TRACE
-    int ltile = 0;
-#endif
     while (true) {
-        LTRACE(0);
         __syncthreads();  // the previous tile's readers are done with the LDS tile
-        LTRACE(1);
         if (sp.xrow != cur_xrow) {
             if (early && cur_xrow < 0) x_put<Q32, SW>(a, xe, xl, xld, xss);
             else stage_x<Q32, SW>(a, sp.xrow, xl, xld, xss);
-            GTRACE(6);
             __syncthreads();
-            GTRACE(7);
             // every lane has its slice before the copy can change again: the next staging follows the loop's barrier
             if (has_sb) load_x_slice(gl, xl, xld, xss, x);
             cur_xrow = sp.xrow;
-            GTRACE(2);
         }
 #pragma unroll
         for (int i = 0; i < GEMV1_CH; i++) *(v4u*)(tile + 16 * (tid + GEMV1_THREADS * i)) = wv[i];
         __syncthreads();
-        GTRACE(3);
-        LTRACE(2);
         const Span cs = sp;
         const bool more = tn < total;
         if (more) {
@@ -570,36 +519,17 @@ __global__ __launch_bounds__(GEMV1_THREADS) GEMV1_ATTR void gemv1_kernel(GemvArg
         for (int base = wave * RPW; base < cs.nr; base += GEMV1_WAVES * RPW) {
             const int rr = base + lane / G;
             float acc = 0.0f;
-#ifdef STRATA_GEMV1_NOCOMPUTE
-            if (rr < cs.nr && has_sb) acc = (float)tile[rr * a.rb + gl];
-            if (false) {
-#else
             if (rr < cs.nr && has_sb) {
-#endif
                 const uint8_t* b = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb + gl * SBB;
                 acc = Q32 ? sb_dot_q32<T>(b, x, tab, nv) : sb_dot_q8k<T>(b, x, tab, nv);
             }
             acc = ordered_sum(acc, G);
             if (rr < cs.nr && gl == G - 1) cs.Y[cs.r0 + rr] = acc;
         }
-        GTRACE(4);
-        LTRACE(3);
-#ifdef STRATA_GEMV1_TRACE
-        ltile++;
-#endif
         if (!more) break;
     }
-    GTRACE(5);
 }
 
-#ifdef STRATA_GEMV1_TRACE
-extern "C" int strata_debug_gemv_trace(uint64_t* out) {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_gemv_trace), sizeof(g_gemv_trace)) == hipSuccess ? 0 : -1;
-}
-extern "C" int strata_debug_gemv_loop(uint64_t* out) {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_gemv_loop), sizeof(g_gemv_loop)) == hipSuccess ? 0 : -1;
-}
-#endif
 
 template <int T, bool Q32, bool SW>
 static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {

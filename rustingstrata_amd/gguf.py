@@ -110,14 +110,11 @@ class Gguf:
             stem = name[:-len(tag)]
             for i in range(1, n):
                 shard = os.path.join(os.path.dirname(path), f"{stem}-{i + 1:05d}-of-{n:05d}.gguf")
-                other = Gguf.__new__(Gguf)
-                other.meta, other.tensors, other._maps = {}, {}, []
-                other._open_one(shard, i)
-                self._maps.extend(other._maps)
-                for k, t in other.tensors.items():
-                    if k in self.tensors:
+                before = set(self.tensors)
+                other = self._open_one(shard, i)
+                for k in other:
+                    if k in before:
                         raise GgufError(f"tensor {k} in two shards")
-                    self.tensors[k] = t
 
     def _open_one(self, path, file):
         with open(path, "rb") as f:
@@ -142,7 +139,7 @@ class Gguf:
             nd = c.u32()
             dims = [c.u64() for _ in range(nd)]
             ty, off = c.u32(), c.u64()
-            tensors[name] = TensorInfo(name, dims, ty, off, len(self._maps))
+            tensors[name] = TensorInfo(name, dims, ty, off, file)
         align = meta.get("general.alignment", 32)
         if not isinstance(align, int) or align <= 0:
             raise GgufError("invalid GGUF alignment")
@@ -155,8 +152,11 @@ class Gguf:
                 raise GgufError(f"{path}: GGUF truncated (tensor {t.name} lies past the end of the file; re-download it)")
         if file == 0:
             self.meta = meta
+        assert len(self._maps) == file, "shards are opened in order"
+        names = list(tensors)
         self.tensors.update(tensors)
         self._maps.append((mm, b, data))
+        return names
 
     def get(self, key):
         if key not in self.meta:

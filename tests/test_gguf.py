@@ -117,3 +117,21 @@ def test_slot_layout(tmp_path):
     assert slot == -(-(2 * gb + db) // 16) * 16
     with pytest.raises(gguf.GgufError, match="missing tensor blk.1.ffn_gate_exps.weight"):
         gguf.slot_layout(g, 1)
+
+
+def test_split_model_reads_each_shard(tmp_path):
+    """A split model (src/gguf.rs: open_one(path, i, ...)): a tensor of shard i reads shard i's bytes, at the same
+    offset as a tensor of shard 0, and a name in two shards is an error."""
+    a = np.arange(64, dtype=np.uint8)
+    b = np.arange(64, dtype=np.uint8)[::-1].copy()
+    c = np.full(64, 7, dtype=np.uint8)
+    meta = [("split.count", gguf.U16, 3)]
+    for i, (name, raw) in enumerate([("t0", a), ("t1", b), ("t2", c)]):
+        gguf.write_gguf(str(tmp_path / f"m-{i + 1:05d}-of-00003.gguf"), meta, [(name, [16], 0, raw.tobytes())])
+    g = gguf.Gguf(str(tmp_path / "m-00001-of-00003.gguf"))
+    assert [g.tensors[n].file for n in ("t0", "t1", "t2")] == [0, 1, 2]
+    assert np.array_equal(g.bytes("t0"), a) and np.array_equal(g.bytes("t1"), b) and np.array_equal(g.bytes("t2"), c)
+    g.close()
+    gguf.write_gguf(str(tmp_path / "m-00002-of-00003.gguf"), meta, [("t0", [16], 0, b.tobytes())])
+    with pytest.raises(gguf.GgufError, match="tensor t0 in two shards"):
+        gguf.Gguf(str(tmp_path / "m-00001-of-00003.gguf"))

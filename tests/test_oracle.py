@@ -261,3 +261,68 @@ def test_rms_norm_pinned():
     x64 = x.astype(np.float64)
     want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + eps) * w
     assert np.abs(O.rms_norm(x, w, eps) - want).max() / np.abs(want).max() < 1e-6
+
+
+def test_quant_xq32_known_answers():
+    """The reference GPU's per-32 quantization (src/cuda/kernels.cu:640-660): d = max|v| / 127, q = rn(v * (127 /
+    max|v|)) with ties to even (__float2int_rn), an all-zero group giving d = 0, q = 0. Hand-computed groups fail
+    the plausible slips: d = max / 128, id = 1 / d, ties away from zero, a missed extreme."""
+    x = np.zeros((2, 128), dtype=np.float32)
+    # group 0: max 127 -> d = 1, id = 1 exactly; exact .5 ties round to even
+    x[0, :8] = [127.0, -127.0, 2.5, 3.5, -2.5, 0.5, 1.5, -126.5]
+    # group 1: all zero
+    # group 2: max 0.3 (at the last element): 127 / 0.3 = 423.3333 in f32, while 1 / (0.3 / 127) = 423.33334; the
+    # value below lands on 1.49999.. with the first and on 1.5000.. with the second
+    x[0, 64] = np.float32(0.0035433070734143257)
+    x[0, 95] = np.float32(0.3)
+    # group 3: negative extreme -> -127, and a value of exactly half the maximum
+    x[0, 96], x[0, 97] = -8.0, 4.0
+    x[1, :32] = np.float32(0.25)          # row 1, group 0: all at the maximum -> 127 each, d = 0.25 / 127
+    q, d = O.quant_xq32(x)
+    assert q[0, :8].tolist() == [127, -127, 2, 4, -2, 0, 2, -126]
+    assert d[0, 0] == np.float32(1.0)
+    assert d[0, 1] == 0 and not q[0, 32:64].any()
+    assert q[0, 64] == 1 and q[0, 95] == 127
+    assert d[0, 2] == np.float32(np.float32(0.3) / np.float32(127.0))
+    assert q[0, 96] == -127 and q[0, 97] == 64 and d[0, 3] == np.float32(np.float32(8.0) / np.float32(127.0))
+    assert q[1, :32].tolist() == [127] * 32 and d[1, 0] == np.float32(np.float32(0.25) / np.float32(127.0))
+    assert not q[1, 32:].any() and not d[1, 1:].any()
+
+
+def test_quantize_q8k_ties_to_even():
+    """quantize_q8k rounds is * v with round_ties_even (src/cpu_moe.rs:39): a block whose first largest magnitude is
+    -127 has is = 1 exactly, so .5 values are exact ties; d = 1 / is = 1."""
+    x = np.zeros(256, dtype=np.float32)
+    x[:8] = [-127.0, 2.5, 3.5, -2.5, -3.5, 0.5, 126.5, 127.0]
+    d, qs, bs = O.quantize_q8k(x)
+    assert d[0] == np.float32(1.0)
+    assert qs[0, :8].tolist() == [-127, 2, 4, -2, -4, 0, 126, 127]
+    assert bs[0, 0] == sum([-127, 2, 4, -2, -4, 0, 126, 127])
+
+
+def test_iq3s_known_answer_all_qh_bits_and_sign_bytes():
+    """IQ3_S (src/quant/mod.rs:345-361), stated as the format defines it: the j-th of a sub-block's 8 grid indices
+    (j = 0..7, 4 values each) is qs[8 ib + j] plus 256 times bit j of qh[ib]; value e of the sub-block takes the sign
+    of bit e % 8 of signs[4 ib + e / 8]; db = d (1 + 2 sc[ib])."""
+    from tests.iq_tables import IQ3S_GRID
+    rng = np.random.default_rng(7)
+    b = np.zeros(110, dtype=np.uint8)
+    b[0:2] = np.array([0.25], dtype=np.float16).view(np.uint8)
+    b[2:66] = rng.integers(0, 256, 64, dtype=np.uint8)
+    b[66:74] = [0b1010_0110, 0b0101_1001, 0xFF, 0x00, 0b1000_0001, 0b0111_1110, 0b0011_1100, 0b1100_0011]
+    b[74:106] = rng.integers(0, 256, 32, dtype=np.uint8)
+    b[106:110] = [0x21, 0x43, 0x65, 0xF7]
+    y = O.dequant(ggml.IQ3_S, b, 256)
+    want = np.empty(256, dtype=np.float32)
+    d = np.float32(0.25)
+    for ib in range(8):
+        sc = (b[106 + ib // 2] >> (4 * (ib % 2))) & 15
+        db = np.float32(d * np.float32(1 + 2 * int(sc)))
+        for j in range(8):
+            idx = int(b[2 + 8 * ib + j]) + 256 * ((int(b[66 + ib]) >> j) & 1)
+            g = IQ3S_GRID[idx]
+            for c in range(4):
+                e = 4 * j + c
+                neg = (int(b[74 + 4 * ib + e // 8]) >> (e % 8)) & 1
+                want[32 * ib + e] = db * np.float32((g >> (8 * c)) & 255) * np.float32(-1.0 if neg else 1.0)
+    assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
