@@ -538,10 +538,10 @@ def test_gemm_tiles_match_cpu(hip, ty):
     hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_SWIGLU | S.SAME_X)
     got2 = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
     want2 = want / (1 + np.exp(-want.astype(np.float64))) * want
-    assert max_rel_err(got2, want2) <= 2 * TOL
+    assert max_rel_err(got2, want2) <= TOL
     hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_ADD | S.SAME_X)
     got3 = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
-    assert max_rel_err(got3, want2 + want) <= 2 * TOL
+    assert max_rel_err(got3, want2 + want) <= TOL
 
 
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
@@ -576,7 +576,7 @@ def test_gemm_gate_up_fused_matches_two_calls(hip, ty):
             want_u[m] = O.matvec(ty, w[(E + e) * rows:(E + e + 1) * rows], rows, cols, x[xrow[m]])
     with np.errstate(over="ignore"):
         want = want_g / (1 + np.exp(-want_g.astype(np.float64))) * want_u
-    assert max_rel_err(b.reshape(npos, rows), want) <= 2 * TOL
+    assert max_rel_err(b.reshape(npos, rows), want) <= TOL
     with pytest.raises(S.StrataError, match="a multiple of 64"):
         hip.gemm_grouped_gate_up(ty, 200, cols, tg, nt, ntd, xb, cols, n_x, xr, y2, 200, up_off)
     with pytest.raises(S.StrataError, match="Q8_0 has no fused"):
@@ -679,8 +679,8 @@ def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=False):
 
 def test_moe_decode_layer_matches_experts(hip):
     """The decode sequence of src/gpu_model.rs:3383-3412: moe_route -> paired gate/up moe_gemv -> swiglu_q ->
-    moe_down_combine, against cpu_moe::experts."""
-    E, H, F, k = 32, 2048, 768, 8
+    moe_down_combine, against cpu_moe::experts, at configs[2]'s shape (128 experts)."""
+    E, H, F, k = 128, 2048, 768, 8
     gate, upw, dn = moe_weights(E, H, F, seed=50)
     h = normal(H, seed=51)
     logits = zipf_logits(1, E, seed=52)
