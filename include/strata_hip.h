@@ -101,6 +101,13 @@ int strata_gemv(strata_ctx* ctx, const strata_tensor* w, uint64_t x, uint64_t y)
  * to strata_gemv per input. */
 int strata_gemvn(strata_ctx* ctx, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t y,
                  uint64_t y_stride, uint64_t nt);
+/* No counterpart in the reference: strata_gemvn for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). The same bits as strata_gemvn; the quantized
+ * x of the nt inputs goes to a fixed device array of 73728 bytes per GPU (4 inputs of 16384 values) instead of the
+ * context's growable scratch, so the call makes no allocation. Larger requests are rejected with an error. Every
+ * call on one GPU shares that array: calls that overlap on one GPU (other streams or contexts) race. */
+int strata_gemvn_noalloc(strata_ctx* ctx, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t y,
+                         uint64_t y_stride, uint64_t nt);
 /* Backend::gemvq (src/backend.rs:204): strata_gemvn reading x pre-quantized by strata_quant_xq at xq (0 =
  * quantize x itself). */
 int strata_gemvq(strata_ctx* ctx, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t xq, uint64_t y,

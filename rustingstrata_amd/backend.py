@@ -61,6 +61,7 @@ SIGNATURES = {
     "strata_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
     "strata_gemv": [CTX, TP, U64, U64],
     "strata_gemvn": [CTX, TP, U64, U64, U64, U64, U64],
+    "strata_gemvn_noalloc": [CTX, TP, U64, U64, U64, U64, U64],
     "strata_gemvq": [CTX, TP, U64, U64, U64, U64, U64, U64],
     "strata_gemvq2": [CTX, TP, TP, U64, U64, U64, U64, U64, U64],
     "strata_moe_gemv": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32, I64, I64, U64],
@@ -282,6 +283,9 @@ class HipBackend:
 
     def gemvn(self, w, x, x_stride, y, y_stride, nt):
         _check(lib().strata_gemvn(self._ctx, w._c(), int(x), x_stride, int(y), y_stride, nt))
+
+    def gemvn_noalloc(self, w, x, x_stride, y, y_stride, nt):
+        _check(lib().strata_gemvn_noalloc(self._ctx, w._c(), int(x), x_stride, int(y), y_stride, nt))
 
     def gemvq(self, w, x, x_stride, xq, y, y_stride, nt):
         _check(lib().strata_gemvq(self._ctx, w._c(), int(x), x_stride, int(xq), int(y), y_stride, nt))

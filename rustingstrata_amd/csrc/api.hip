@@ -77,6 +77,30 @@ struct Scratch {
     }
 };
 
+// Scratch of strata_gemvn_noalloc: the quantized x of up to 4 inputs of up to 16384 values (int8 values, then one
+// f32 scale per 32), in a file-scope device array so that the call allocates nothing. Each GPU holds its own copy
+// until the process ends; host code reaches it only through the address hipGetSymbolAddress returns for the device.
+constexpr size_t NOALLOC_SCRATCH_BYTES = 4 * (16384 + 16384 / 8);
+static __device__ __align__(256) int8_t scratch[NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static std::map<int, void*> g_scratch_ptr;  // device -> address of `scratch` on it
+
+// The device address of `scratch` on `device` (current), looked up once per device.
+hipError_t noalloc_scratch(int device, void** out) {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    auto it = g_scratch_ptr.find(device);
+    if (it != g_scratch_ptr.end()) {
+        *out = it->second;
+        return hipSuccess;
+    }
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = ptr;
+    *out = ptr;
+    return hipSuccess;
+}
+
 }  // namespace strata
 
 struct strata_ctx {
@@ -89,6 +113,7 @@ struct strata_ctx {
     Scratch gx;                          // quantized x of the GEMM (kept for SAME_X)
     uint64_t gx_key[4] = {0, 0, 0, 0};   // x, x_stride, n_x, cols of gx's contents (all 0: none)
     Scratch misc;
+    void* noalloc = nullptr;             // this device's address of the file-scope `scratch`
     bool recording = false;              // between strata_graph_begin and strata_graph_end
     int graphs = 0;                      // executable graphs made by this context and not yet destroyed
     hipError_t need(Scratch& s, size_t bytes) { return s.need(bytes, stream, recording, graphs > 0); }
@@ -173,6 +198,8 @@ int strata_open(int device, strata_ctx** out) {
     STRATA_HIP(hipSetDevice(device));
     strata_ctx* c = new strata_ctx();
     c->device = device;
+    e = noalloc_scratch(device, &c->noalloc);
+    if (e != hipSuccess) { delete c; return hip_error(e, "hipGetSymbolAddress(scratch)"); }
     e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
     if (e != hipSuccess) { delete c; return hip_error(e, "hipStreamCreate"); }
     *out = c;
@@ -395,6 +422,33 @@ int strata_gemv(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t y) {
 int strata_gemvn(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t y, uint64_t y_stride,
                  uint64_t nt) {
     return strata_gemvq(c, w, x, x_stride, 0, y, y_stride, nt);
+}
+
+int strata_gemvn_noalloc(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t y,
+                        uint64_t y_stride, uint64_t nt) {
+    if (check_ctx(c) || check_tensor(w, "gemvn_noalloc")) return -1;
+    if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
+    if (check_gemv_cols(w->ty, w->cols) || check_align(w->ty, w->ptr, "gemvn_noalloc")) return -1;
+    if (nt > 1 && xq_bytes(w->cols, nt) > NOALLOC_SCRATCH_BYTES)
+        return set_error("gemvn_noalloc: " + std::to_string(nt) + " inputs of " + std::to_string(w->cols) +
+                         " values need " + std::to_string(xq_bytes(w->cols, nt)) + " bytes of scratch (at most " +
+                         std::to_string(NOALLOC_SCRATCH_BYTES) + ")");
+    if (w->rows == 0) return 0;
+    if (w->rows > (1u << 30)) return set_error("gemv: too many rows");
+    uint64_t xq = 0;
+    if (nt > 1) {
+        // Every byte the GEMV reads is written here first, so the array needs no clearing between calls.
+        STRATA_HIP(launch_quant_xq((const float*)x, x_stride, (int)w->cols, (int)nt, (int8_t*)c->noalloc, c->numerics,
+                                   c->stream));
+        xq = (uint64_t)c->noalloc;
+    }
+    GemvLaunch g;
+    g.xf = (const float*)x; g.x_stride = x_stride;
+    g.ty = w->ty; g.w = (const uint8_t*)w->ptr; g.rows = (int)w->rows; g.cols = (int)w->cols;
+    g.nt = (int)nt; g.xq = (const int8_t*)xq; g.n_xrows = (int)nt; g.y = (float*)y; g.y_stride = (int)y_stride;
+    g.numerics = c->numerics;
+    STRATA_HIP(launch_gemv(g, c->stream));
+    return 0;
 }
 
 int strata_gemvq2(strata_ctx* c, const strata_tensor* a, const strata_tensor* b, uint64_t x, uint64_t x_stride,
