@@ -8,7 +8,8 @@
  *
  * Weight type ids are the GGUF ids of `GgmlType::from_u32` (src/quant/mod.rs:15-19): Q8_0 8, Q2_K 10, Q3_K 11,
  * Q4_K 12, Q5_K 13, Q6_K 14, IQ2_XXS 16, IQ3_S 21, IQ4_XS 23. Weights are the raw GGUF block bytes, rows of
- * `cols` values, row r at ptr + r * row_bytes (src/weights.rs:11-37), no repacking at upload. */
+ * `cols` values, row r at ptr + r * row_bytes (src/weights.rs:11-37), no repacking at upload. F32 (0) matrices, the
+ * form Backend::upload gives F32/F16 GGUF tensors (src/backend.rs:156-166), are accepted by gemv and gemm_dense. */
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -36,6 +37,9 @@ typedef struct {
 enum { STRATA_NUM_Q8K = 0, STRATA_NUM_Q8_32 = 1 };
 
 /* `gemm` act flags (src/backend.rs:187-191, SAME_X at src/backend.rs:91). */
+/* GGUF type id of float32 tensors. */
+enum { STRATA_F32 = 0 };
+
 enum { STRATA_ACT_STORE = 0, STRATA_ACT_SWIGLU = 1, STRATA_ACT_ADD = 2, STRATA_SAME_X = 4 };
 
 /* ---- context, memory and queue: backend::open and the memory methods of Backend ---- */
@@ -220,6 +224,76 @@ uint64_t strata_gemm_block_positions(void);
 int strata_int8_gemm(strata_ctx* ctx, int ty);
 /* Backend::prequant_gemm_x (src/backend.rs:197): quantize x (n rows) ahead, for a later gemm with STRATA_SAME_X. */
 int strata_prequant_gemm_x(strata_ctx* ctx, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride);
+
+/* ---- the decoder stack around the matmuls (src/backend.rs:232-410; the layer sequences of
+ *      src/gpu_model/prefill.rs:315-712 and src/gpu_model.rs:1950-2016) ----
+ * `step` arguments are device int32 arrays read at run time (so recorded graphs replay): prefill ops put token t of a
+ * call at position step[0] + t; decode attention reads token t's position from step[2 t]. KV caches are f16 rows of
+ * n_kv_head * head_dim values per position (Backend::kv_words: n words for n values). */
+
+/* Backend::kv_words (src/backend.rs:186): u16 words of an f16 cache for n values. */
+uint64_t strata_kv_words(uint64_t n);
+/* Backend::argmax_rows (src/backend.rs:246; kernels src/cuda/kernels.cu:1574-1592): out[r] = index of the largest
+ * value of row r (rows of n floats), the first on ties, under f32::total_cmp as ops::argmax (src/ops.rs:110-112). */
+int strata_argmax_rows(strata_ctx* ctx, uint64_t x, uint64_t n, uint64_t rows, uint64_t out);
+/* Backend::rope_pairs / rope_neox (src/backend.rs:250-254; ops::rope_neox src/ops.rs:36-45): in place on `heads`
+ * rows `stride` floats apart, `per` heads a token, token t at position step[0] + t; pairs (i, i + n_rot / 2) for
+ * lo <= i < hi turn by pos * base^(-2 i / n_rot) (f64 angle, f32 sine and cosine). */
+int strata_rope_pairs(strata_ctx* ctx, uint64_t x, uint64_t stride, uint64_t heads, uint64_t per, uint64_t n_rot,
+                      uint64_t step, float base, uint64_t lo, uint64_t hi);
+int strata_rope_neox(strata_ctx* ctx, uint64_t x, uint64_t stride, uint64_t heads, uint64_t per, uint64_t n_rot,
+                     uint64_t step, float base);
+/* Backend::rms_norm_rope (src/backend.rs:267): rms_norm of `rows` heads of n (x rows x_stride apart, out rows of n)
+ * with w, then rope_neox. n a multiple of 32 up to 512, n_rot <= n. */
+int strata_rms_norm_rope(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t n,
+                         uint64_t rows, float eps, uint64_t per, uint64_t n_rot, uint64_t step, float base);
+/* Backend::rms_norm_rope_kv (src/backend.rs:272; kernel src/cuda/kernels.cu:2196-2227): rms_norm_rope of the k heads,
+ * then the normed, roped k head and its v row (v rows of n like out) stored as f16 into kc / vc at cache row
+ * (position * per + head); kc = 0 stores nothing. */
+int strata_rms_norm_rope_kv(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t n,
+                            uint64_t rows, float eps, uint64_t per, uint64_t n_rot, uint64_t step, float base,
+                            uint64_t v, uint64_t kc, uint64_t vc);
+/* Backend::rms_norm_rope_qk (src/backend.rs:274-277): rms_norm_rope of the q heads (qrows rows of q, q_stride apart,
+ * into qo) and rms_norm_rope_kv of the k heads (rows of n), in one launch. */
+int strata_rms_norm_rope_qk(strata_ctx* ctx, uint64_t q, uint64_t q_stride, uint64_t qw, uint64_t qo, uint64_t qrows,
+                            uint64_t qper, uint64_t k, uint64_t kw, uint64_t ko, uint64_t krows, uint64_t kper, uint64_t n,
+                            float eps, uint64_t n_rot, uint64_t step, float base, uint64_t v, uint64_t kc, uint64_t vc);
+/* Backend::kv_store (src/backend.rs:380; kernel src/cuda/kernels.cu:2181-2186): t tokens of n values (k and v
+ * rows) into the f16 caches at positions step[0] ... */
+int strata_kv_store(strata_ctx* ctx, uint64_t k, uint64_t v, uint64_t kc, uint64_t vc, uint64_t n, uint64_t t,
+                    uint64_t step, uint64_t hd);
+/* Backend::attn_prefill / attn_prefill_m with qm = 0 (src/backend.rs:337-343; kernel src/cuda/kernels.cu:2787-3216):
+ * query row i of t (q rows of nh * hd floats, after norm and rope) at position step[0] + i attends to cached keys
+ * 0 .. step[0] + i (the last `win` only when win > 0); out rows of nh * hd = softmax(q k scale) V, times
+ * sigmoid(gate) when qg is not 0 (qg rows of nh * 2 hd, the gate at + hd per head), with a per-head sink logit when
+ * sink is not 0. head_dim 64 or 128, nh / nkv in 1, 2, 4, 8. A QSA mask (qm != 0) is an error here. */
+int strata_attn_prefill(strata_ctx* ctx, uint64_t q, uint64_t kc, uint64_t vc, uint64_t qg, uint64_t out, uint64_t step,
+                        uint64_t t, uint64_t nh, uint64_t nkv, uint64_t hd, float scale);
+int strata_attn_prefill_m(strata_ctx* ctx, uint64_t q, uint64_t kc, uint64_t vc, uint64_t qg, uint64_t out, uint64_t step,
+                          uint64_t t, uint64_t nh, uint64_t nkv, uint64_t hd, float scale, uint64_t qm, uint64_t mw,
+                          uint64_t sink, uint64_t win);
+/* Floats of the `part` buffer attn_decode needs per token. */
+uint64_t strata_attn_part_floats(uint64_t nh, uint64_t hd);
+/* Backend::attn_decode / attn_decode_gq (src/backend.rs:383-410; kernels src/cuda/kernels.cu:2123-2626): nt query
+ * tokens (rows of q, qg and out per token), token t over positions 0 ..= step[2 t] (the last `win` when win > 0),
+ * otherwise as strata_attn_prefill. part: nt * strata_attn_part_floats(nh, hd) floats of scratch. K / V loads are
+ * always shared across the GQA group here (gq_min is accepted and ignored). */
+int strata_attn_decode(strata_ctx* ctx, uint64_t q, uint64_t kc, uint64_t vc, uint64_t qg, uint64_t out, uint64_t part,
+                       uint64_t step, uint64_t nh, uint64_t nkv, uint64_t hd, float scale, uint64_t nt);
+int strata_attn_decode_gq(strata_ctx* ctx, uint64_t q, uint64_t kc, uint64_t vc, uint64_t qg, uint64_t out, uint64_t part,
+                          uint64_t step, uint64_t nh, uint64_t nkv, uint64_t hd, float scale, int gq_min, uint64_t nt,
+                          uint64_t sink, uint64_t win);
+/* Backend::add (src/backend.rs:282): x += y over n floats. */
+int strata_add(strata_ctx* ctx, uint64_t x, uint64_t y, uint64_t n);
+/* Backend::swiglu (src/backend.rs:284): g = silu(g) * u over n floats. */
+int strata_swiglu(strata_ctx* ctx, uint64_t g, uint64_t u, uint64_t n);
+/* Model::embed on the device (src/model.rs:334-339; the reference dequantizes token rows on the host): out[i] = row
+ * min(ids[i], rows - 1) of w as f32, for the n device int32 ids. No trait counterpart. */
+int strata_get_rows(strata_ctx* ctx, const strata_tensor* w, uint64_t ids, uint64_t n, uint64_t out);
+/* Synthetic weights on the device (no counterpart in the reference, whose tests build random tensors on the host,
+ * tests/kernels.rs:1473-1550): fill the tensor's blocks with seeded random bytes, every f16 scale field (d, and dmin
+ * where the type has one) set to a value in [lo, hi). The same seed gives the same bytes. */
+int strata_fill_blocks(strata_ctx* ctx, const strata_tensor* w, uint64_t seed, float lo, float hi);
 
 /* ---- weight quantizers (host) ----
  * The reference has none for these types (src/quant/mod.rs:1-2 only dequantizes). These make GGUF-valid blocks

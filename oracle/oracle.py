@@ -43,6 +43,9 @@ def lib():
             "or_silu": ([F], F),
             "or_rms_norm": ([P, P, F, I, P], None),
             "or_f16": ([ctypes.c_uint16], F),
+            "or_rope_neox": ([P, I, ctypes.c_long, F], None),
+            "or_argmax": ([P, I], I),
+            "or_attention": ([P, P, P, I, I, I, I, I, F, P, P, I, P, P], None),
         }
         for n, (a, r) in sig.items():
             f = getattr(l, n)
@@ -164,3 +167,32 @@ def rms_norm(x, w, eps):
 
 def silu(x):
     return lib().or_silu(float(x))
+
+
+def rope_neox(x, n_rot, pos, base):
+    """ops::rope_neox (src/ops.rs:36-45) on each row (one head) of x, at position pos; returns a copy."""
+    x = np.array(np.atleast_2d(x), dtype=np.float32, copy=True, order="C")
+    for r in range(x.shape[0]):
+        lib().or_rope_neox(_p(x[r]), n_rot, pos, base)
+    return x
+
+
+def argmax(x):
+    """ops::argmax (src/ops.rs:110-112): first index of the largest value under total_cmp."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return int(lib().or_argmax(_p(x), x.size))
+
+
+def attention(q, kc, vc, p0, p1, nh, nkv, hd, scale, sinks=None, gate=None, gate_stride=0):
+    """Model::attention's per-token attention (src/model.rs:771-793) over cells p0 .. p1 - 1: q [nh * hd], kc / vc
+    [positions, nkv * hd]; returns out [nh * hd]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    kc = np.ascontiguousarray(kc, dtype=np.float32)
+    vc = np.ascontiguousarray(vc, dtype=np.float32)
+    out = np.empty(nh * hd, dtype=np.float32)
+    sc = np.empty(max(p1 - p0, 1), dtype=np.float32)
+    sk = None if sinks is None else np.ascontiguousarray(sinks, dtype=np.float32)
+    g = None if gate is None else np.ascontiguousarray(gate, dtype=np.float32)
+    lib().or_attention(_p(q), _p(kc), _p(vc), p0, p1, nh, nkv, hd, ctypes.c_float(scale),
+                       None if sk is None else _p(sk), None if g is None else _p(g), gate_stride, _p(out), _p(sc))
+    return out

@@ -50,6 +50,15 @@ void or_experts_multi(int ty_gu, int ty_down, const uint8_t* gate, const uint8_t
 float or_silu(float x);
 void or_rms_norm(const float* x, const float* w, float eps, int n, float* out);
 
+/* ---- the decoder stack around the hot path (oracle/attention.c) ---- */
+/* ops::rope_neox, src/ops.rs:36-45, in place on one head. */
+void or_rope_neox(float* x, int n_rot, long pos, float base);
+/* ops::argmax, src/ops.rs:110-112. */
+int or_argmax(const float* x, int n);
+/* The attention of one token, Model::attention src/model.rs:771-793, over cells p0 .. p1 - 1. */
+void or_attention(const float* q, const float* kc, const float* vc, int p0, int p1, int nh, int nkv, int hd,
+                  float scale, const float* sinks, const float* gate, int gate_stride, float* out, float* sc);
+
 #ifdef __cplusplus
 }
 #endif

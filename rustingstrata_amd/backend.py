@@ -19,6 +19,7 @@ LIB_PATH = os.environ.get("STRATA_HIP_LIB") or os.path.join(os.path.dirname(os.p
 NUM_Q8K, NUM_Q8_32 = 0, 1
 ACT_STORE, ACT_SWIGLU, ACT_ADD, SAME_X = 0, 1, 2, 4
 GEMM_BM = 128  # positions per tile (src/backend.rs:16)
+F32_TYPE = 0   # GGUF type id of float32 matrices (gemv / gemm_dense accept them)
 
 
 class StrataError(RuntimeError):
@@ -88,9 +89,27 @@ SIGNATURES = {
     "strata_event_elapsed": [P, P, ctypes.POINTER(F32)],
     "strata_event_destroy": [P],
     "strata_copy_kernel": [CTX, U64, U64, U64],
+    "strata_kv_words": [U64],
+    "strata_argmax_rows": [CTX, U64, U64, U64, U64],
+    "strata_rope_pairs": [CTX, U64, U64, U64, U64, U64, U64, F32, U64, U64],
+    "strata_rope_neox": [CTX, U64, U64, U64, U64, U64, U64, F32],
+    "strata_rms_norm_rope": [CTX, U64, U64, U64, U64, U64, U64, F32, U64, U64, U64, F32],
+    "strata_rms_norm_rope_kv": [CTX, U64, U64, U64, U64, U64, U64, F32, U64, U64, U64, F32, U64, U64, U64],
+    "strata_rms_norm_rope_qk": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, F32, U64, U64, F32,
+                                U64, U64, U64],
+    "strata_kv_store": [CTX, U64, U64, U64, U64, U64, U64, U64, U64],
+    "strata_attn_prefill": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, F32],
+    "strata_attn_prefill_m": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, F32, U64, U64, U64, U64],
+    "strata_attn_part_floats": [U64, U64],
+    "strata_attn_decode": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, F32, U64],
+    "strata_attn_decode_gq": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, F32, I32, U64, U64, U64],
+    "strata_add": [CTX, U64, U64, U64],
+    "strata_swiglu": [CTX, U64, U64, U64],
+    "strata_get_rows": [CTX, TP, U64, U64, U64],
+    "strata_fill_blocks": [CTX, TP, U64, F32, F32],
 }
 _RESTYPES = {"strata_close": None, "strata_last_error": ctypes.c_char_p, "strata_stream": P, "strata_row_bytes": U64,
-             "strata_gemm_block_positions": U64}
+             "strata_gemm_block_positions": U64, "strata_kv_words": U64, "strata_attn_part_floats": U64}
 
 _lib = None
 
@@ -359,6 +378,66 @@ class HipBackend:
 
     def prequant_gemm_x(self, w, n, x, x_stride):
         _check(lib().strata_prequant_gemm_x(self._ctx, w._c(), n, int(x), x_stride))
+
+    # ---- the decoder stack (src/backend.rs:232-410) ----
+    def upload_f32(self, w):
+        """An F32 matrix (Backend::upload of an F32/F16 GGUF tensor, src/backend.rs:156-166) as a GpuTensor."""
+        w = np.ascontiguousarray(np.atleast_2d(w), dtype=np.float32)
+        return GpuTensor(F32_TYPE, w.shape[0], w.shape[1], self.upload(w))
+
+    @staticmethod
+    def kv_words(n):
+        return int(lib().strata_kv_words(n))
+
+    def argmax_rows(self, x, n, rows, out):
+        _check(lib().strata_argmax_rows(self._ctx, int(x), n, rows, int(out)))
+
+    def rope_pairs(self, x, stride, heads, per, n_rot, step, base, lo, hi):
+        _check(lib().strata_rope_pairs(self._ctx, int(x), stride, heads, per, n_rot, int(step), base, lo, hi))
+
+    def rope_neox(self, x, stride, heads, per, n_rot, step, base):
+        _check(lib().strata_rope_neox(self._ctx, int(x), stride, heads, per, n_rot, int(step), base))
+
+    def rms_norm_rope(self, x, x_stride, w, out, n, rows, eps, per, n_rot, step, base):
+        _check(lib().strata_rms_norm_rope(self._ctx, int(x), x_stride, int(w), int(out), n, rows, eps, per, n_rot,
+                                          int(step), base))
+
+    def rms_norm_rope_kv(self, x, x_stride, w, out, n, rows, eps, per, n_rot, step, base, v, kc, vc):
+        _check(lib().strata_rms_norm_rope_kv(self._ctx, int(x), x_stride, int(w), int(out), n, rows, eps, per, n_rot,
+                                             int(step), base, int(v), int(kc), int(vc)))
+
+    def rms_norm_rope_qk(self, q, q_stride, qw, qo, qrows, qper, k, kw, ko, krows, kper, n, eps, n_rot, step, base, v,
+                         kc, vc):
+        _check(lib().strata_rms_norm_rope_qk(self._ctx, int(q), q_stride, int(qw), int(qo), qrows, qper, int(k), int(kw),
+                                             int(ko), krows, kper, n, eps, n_rot, int(step), base, int(v), int(kc),
+                                             int(vc)))
+
+    def kv_store(self, k, v, kc, vc, n, t, step, hd):
+        _check(lib().strata_kv_store(self._ctx, int(k), int(v), int(kc), int(vc), n, t, int(step), hd))
+
+    def attn_prefill(self, q, kc, vc, qg, out, step, t, nh, nkv, hd, scale, sink=0, win=0):
+        _check(lib().strata_attn_prefill_m(self._ctx, int(q), int(kc), int(vc), int(qg), int(out), int(step), t, nh,
+                                           nkv, hd, scale, 0, 0, int(sink), win))
+
+    @staticmethod
+    def attn_part_floats(nh, hd):
+        return int(lib().strata_attn_part_floats(nh, hd))
+
+    def attn_decode(self, q, kc, vc, qg, out, part, step, nh, nkv, hd, scale, nt, sink=0, win=0):
+        _check(lib().strata_attn_decode_gq(self._ctx, int(q), int(kc), int(vc), int(qg), int(out), int(part), int(step),
+                                           nh, nkv, hd, scale, 0, nt, int(sink), win))
+
+    def add(self, x, y, n):
+        _check(lib().strata_add(self._ctx, int(x), int(y), n))
+
+    def swiglu(self, g, u, n):
+        _check(lib().strata_swiglu(self._ctx, int(g), int(u), n))
+
+    def get_rows(self, w, ids, n, out):
+        _check(lib().strata_get_rows(self._ctx, w._c(), int(ids), n, int(out)))
+
+    def fill_blocks(self, w, seed, lo, hi):
+        _check(lib().strata_fill_blocks(self._ctx, w._c(), seed, lo, hi))
 
     # ---- timing on the backend's stream ----
     def event(self):

@@ -10,6 +10,7 @@
 #include "kernels.h"
 #include "moe.h"
 #include "gemm.h"
+#include "decoder.h"
 #include "../../include/strata_hip.h"
 
 using namespace strata;
@@ -113,6 +114,7 @@ struct strata_ctx {
     Scratch gx;                          // quantized x of the GEMM (kept for SAME_X)
     uint64_t gx_key[4] = {0, 0, 0, 0};   // x, x_stride, n_x, cols of gx's contents (all 0: none)
     Scratch misc;
+    Scratch am;                          // argmax partials
     void* noalloc = nullptr;             // this device's address of the file-scope `scratch`
     bool recording = false;              // between strata_graph_begin and strata_graph_end
     int graphs = 0;                      // executable graphs made by this context and not yet destroyed
@@ -214,6 +216,7 @@ void strata_close(strata_ctx* c) {
     c->xq.release();
     c->gx.release();
     c->misc.release();
+    c->am.release();
     hipStreamDestroy(c->stream);
     delete c;
 }
@@ -360,6 +363,7 @@ int strata_graph_destroy(strata_ctx* c, void* graph) {
         c->xq.free_retired();
         c->gx.free_retired();
         c->misc.free_retired();
+        c->am.free_retired();
     }
     return 0;
 }
@@ -397,8 +401,25 @@ int strata_rms_norm(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t w, ui
     return strata_rms_norm_q(c, x, x_stride, w, out, out_stride, n, rows, eps, 0, 0);
 }
 
+// gemv / gemm_dense of an F32 matrix (the router's ffn_gate_inp): float dots, no activation quantization.
+static int gemv_f32(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t y, uint64_t y_stride,
+                    uint64_t nt, int act) {
+    if (nt < 1) return set_error("gemvn: " + std::to_string(nt) + " inputs");
+    if (w->cols == 0 || w->cols % 4) return set_error("F32 tensor with " + std::to_string(w->cols) + " columns: GEMV needs a multiple of 4");
+    if (w->rows == 0) return 0;
+    if (w->rows > (1u << 30) || w->cols > (1u << 30)) return set_error("gemv: too large");
+    if (x % 16 || (nt > 1 && x_stride % 4)) return set_error("F32 gemv: x rows must be 16-byte aligned");
+    STRATA_HIP(launch_gemv_f32((const float*)w->ptr, (int)w->rows, (int)w->cols, (const float*)x, x_stride, (float*)y,
+                               y_stride, (int)nt, act, c->stream));
+    return 0;
+}
+
 int strata_gemvq(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_stride, uint64_t xq, uint64_t y,
                  uint64_t y_stride, uint64_t nt) {
+    if (w && w->ty == STRATA_F32 && !check_ctx(c)) {
+        if (nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
+        return gemv_f32(c, w, x, x_stride, y, y_stride, nt, 0);
+    }
     if (check_ctx(c) || check_tensor(w, "gemv")) return -1;
     if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
     if (check_gemv_cols(w->ty, w->cols) || check_align(w->ty, w->ptr, "gemv")) return -1;
@@ -669,6 +690,18 @@ int strata_gemm_grouped_gate_up(strata_ctx* c, int ty, uint64_t rows, uint64_t c
 
 int strata_gemm_dense(strata_ctx* c, const strata_tensor* w, uint64_t n, uint64_t x, uint64_t x_stride, uint64_t y,
                       uint64_t y_stride, int act) {
+    if (w && w->ty == STRATA_F32) {
+        if (check_ctx(c)) return -1;
+        const int op = act & ~STRATA_SAME_X;
+        if (op < 0 || op > 2) return set_error("gemm: act " + std::to_string(act));
+        if (w->cols == 0 || w->cols % 4 || x % 16 || x_stride % 4)
+            return set_error("F32 gemm_dense: columns a multiple of 4 and x rows 16-byte aligned");
+        if (n == 0 || w->rows == 0) return 0;
+        if (n > (1u << 30) || w->rows > (1u << 30)) return set_error("gemm: too large");
+        STRATA_HIP(launch_gemm_f32((const float*)w->ptr, (int)w->rows, (int)w->cols, (const float*)x, x_stride, (float*)y,
+                                   y_stride, (int)n, op, c->stream));
+        return 0;
+    }
     if (check_tensor(w, "gemm_dense")) return -1;
     const uint64_t bp = gemm_block_positions();
     uint64_t nt = (n + bp - 1) / bp;
@@ -677,6 +710,173 @@ int strata_gemm_dense(strata_ctx* c, const strata_tensor* w, uint64_t n, uint64_
 }
 
 uint64_t strata_gemm_block_positions(void) { return gemm_block_positions(); }
+
+// ---- the decoder stack ----
+
+uint64_t strata_kv_words(uint64_t n) { return n; }
+
+int strata_argmax_rows(strata_ctx* c, uint64_t x, uint64_t n, uint64_t rows, uint64_t out) {
+    if (check_ctx(c)) return -1;
+    if (!rows) return 0;
+    if (n == 0 || n >= (1u << 31) || rows > 65535) return set_error("argmax_rows: " + std::to_string(rows) + " rows of " + std::to_string(n));
+    STRATA_HIP(c->need(c->am, argmax_part_bytes((int)rows)));
+    STRATA_HIP(launch_argmax_rows((const float*)x, (int)n, (int)rows, (uint64_t*)c->am.p, (int*)out, c->stream));
+    return 0;
+}
+
+static int check_rope(uint64_t n, uint64_t n_rot) {
+    if (n > 512 || n_rot > n || n_rot % 2 || n % 32 || n == 0)
+        return set_error("rms_norm_rope: head of " + std::to_string(n) + ", n_rot " + std::to_string(n_rot));
+    return 0;
+}
+
+int strata_rope_pairs(strata_ctx* c, uint64_t x, uint64_t stride, uint64_t heads, uint64_t per, uint64_t n_rot,
+                      uint64_t step, float base, uint64_t lo, uint64_t hi) {
+    if (check_ctx(c)) return -1;
+    if (!per || heads % per || n_rot % 2 || n_rot > stride || hi > n_rot / 2 || lo > hi)
+        return set_error("rope: " + std::to_string(heads) + " heads, " + std::to_string(per) + " per token, n_rot " +
+                         std::to_string(n_rot) + ", pairs " + std::to_string(lo) + ".." + std::to_string(hi));
+    if (heads >= (1u << 31)) return set_error("rope: too many heads");
+    STRATA_HIP(launch_rope_pairs((float*)x, stride, (int)heads, (int)per, (int)n_rot, (const int*)step, base, (int)lo,
+                                 (int)hi, c->stream));
+    return 0;
+}
+
+int strata_rope_neox(strata_ctx* c, uint64_t x, uint64_t stride, uint64_t heads, uint64_t per, uint64_t n_rot,
+                     uint64_t step, float base) {
+    return strata_rope_pairs(c, x, stride, heads, per, n_rot, step, base, 0, n_rot / 2);
+}
+
+int strata_rms_norm_rope_qk(strata_ctx* c, uint64_t q, uint64_t q_stride, uint64_t qw, uint64_t qo, uint64_t qrows,
+                            uint64_t qper, uint64_t k, uint64_t kw, uint64_t ko, uint64_t krows, uint64_t kper, uint64_t n,
+                            float eps, uint64_t n_rot, uint64_t step, float base, uint64_t v, uint64_t kc, uint64_t vc) {
+    if (check_ctx(c) || check_rope(n, n_rot)) return -1;
+    if ((qrows && (!qper || qrows % qper)) || (krows && (!kper || krows % kper)))
+        return set_error("rms_norm_rope: rows must be whole tokens of heads");
+    if (kc && (!v || !vc)) return set_error("rms_norm_rope_kv: null v or value cache");
+    if (qrows + krows >= (1u << 31)) return set_error("rms_norm_rope: too many rows");
+    NormRope a;
+    a.x = (const float*)k; a.x_stride = n; a.w = (const float*)kw; a.out = (float*)ko;
+    a.n = (int)n; a.rows = (int)krows; a.per = (int)(kper ? kper : 1);
+    a.v = (const float*)v; a.kc = (uint16_t*)kc; a.vc = (uint16_t*)vc;
+    a.qrows = (int)qrows; a.qx = (const float*)q; a.q_stride = q_stride; a.qw = (const float*)qw; a.qo = (float*)qo;
+    a.qper = (int)(qper ? qper : 1);
+    a.eps = eps; a.base = base; a.n_rot = (int)n_rot; a.step = (const int*)step;
+    STRATA_HIP(launch_norm_rope(a, c->stream));
+    return 0;
+}
+
+int strata_rms_norm_rope_kv(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t n,
+                            uint64_t rows, float eps, uint64_t per, uint64_t n_rot, uint64_t step, float base,
+                            uint64_t v, uint64_t kc, uint64_t vc) {
+    if (check_ctx(c) || check_rope(n, n_rot)) return -1;
+    if (!per || rows % per) return set_error("rms_norm_rope: rows must be whole tokens of heads");
+    if (kc && (!v || !vc)) return set_error("rms_norm_rope_kv: null v or value cache");
+    if (rows >= (1u << 31)) return set_error("rms_norm_rope: too many rows");
+    NormRope a;
+    a.x = (const float*)x; a.x_stride = x_stride; a.w = (const float*)w; a.out = (float*)out;
+    a.n = (int)n; a.rows = (int)rows; a.per = (int)per;
+    a.v = (const float*)v; a.kc = (uint16_t*)kc; a.vc = (uint16_t*)vc;
+    a.eps = eps; a.base = base; a.n_rot = (int)n_rot; a.step = (const int*)step;
+    STRATA_HIP(launch_norm_rope(a, c->stream));
+    return 0;
+}
+
+int strata_rms_norm_rope(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t n,
+                         uint64_t rows, float eps, uint64_t per, uint64_t n_rot, uint64_t step, float base) {
+    return strata_rms_norm_rope_kv(c, x, x_stride, w, out, n, rows, eps, per, n_rot, step, base, 0, 0, 0);
+}
+
+int strata_kv_store(strata_ctx* c, uint64_t k, uint64_t v, uint64_t kc, uint64_t vc, uint64_t n, uint64_t t,
+                    uint64_t step, uint64_t hd) {
+    if (check_ctx(c)) return -1;
+    (void)hd;  // f16 cache: the head size does not change the layout
+    if (n * t >= (1ull << 40)) return set_error("kv_store: too large");
+    STRATA_HIP(launch_kv_store((const float*)k, (const float*)v, (uint16_t*)kc, (uint16_t*)vc, (int)n, (int)t,
+                               (const int*)step, c->stream));
+    return 0;
+}
+
+static int check_attn(uint64_t nh, uint64_t nkv, uint64_t hd, const char* what) {
+    if (hd != 64 && hd != 128) return set_error(std::string(what) + ": head_dim " + std::to_string(hd) + " unsupported (64 or 128)");
+    if (!nkv || !nh || nh % nkv) return set_error(std::string(what) + ": " + std::to_string(nh) + " query heads over " + std::to_string(nkv) + " KV heads");
+    const uint64_t g = nh / nkv;
+    if (g != 1 && g != 2 && g != 4 && g != 8) return set_error(std::string(what) + ": GQA group of " + std::to_string(g) + " (1, 2, 4 or 8)");
+    return 0;
+}
+
+uint64_t strata_attn_part_floats(uint64_t nh, uint64_t hd) { return nh * ATT_SPLITS * (hd + 2); }
+
+int strata_attn_decode_gq(strata_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t qg, uint64_t out, uint64_t part,
+                          uint64_t step, uint64_t nh, uint64_t nkv, uint64_t hd, float scale, int gq_min, uint64_t nt,
+                          uint64_t sink, uint64_t win) {
+    if (check_ctx(c) || check_attn(nh, nkv, hd, "attention decode")) return -1;
+    (void)gq_min;  // every launch shares K / V loads across the GQA group
+    if (!nt) return 0;
+    if (!part) return set_error("attention decode: null part buffer");
+    if (nt > 65535 || win >= (1u << 31)) return set_error("attention decode: too large");
+    STRATA_HIP(launch_attn_decode((const float*)q, (const uint16_t*)kc, (const uint16_t*)vc, (const float*)qg,
+                                  (float*)out, (float*)part, (const int*)step, (int)nh, (int)nkv, (int)hd, scale, (int)nt,
+                                  (const float*)sink, (int)win, c->stream));
+    return 0;
+}
+
+int strata_attn_decode(strata_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t qg, uint64_t out, uint64_t part,
+                       uint64_t step, uint64_t nh, uint64_t nkv, uint64_t hd, float scale, uint64_t nt) {
+    return strata_attn_decode_gq(c, q, kc, vc, qg, out, part, step, nh, nkv, hd, scale, 0, nt, 0, 0);
+}
+
+int strata_attn_prefill_m(strata_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t qg, uint64_t out, uint64_t step,
+                          uint64_t t, uint64_t nh, uint64_t nkv, uint64_t hd, float scale, uint64_t qm, uint64_t mw,
+                          uint64_t sink, uint64_t win) {
+    if (check_ctx(c) || check_attn(nh, nkv, hd, "attention prefill")) return -1;
+    if (qm || mw) return set_error("attention prefill: QSA block masks are not supported by this backend");
+    if (!t) return 0;
+    if (t >= (1u << 24) || win >= (1u << 31)) return set_error("attention prefill: too large");
+    if (q % 16 || out % 16 || (qg && qg % 16)) return set_error("attention prefill: q, out and qg must be 16-byte aligned");
+    STRATA_HIP(launch_attn_prefill((const float*)q, (const uint16_t*)kc, (const uint16_t*)vc, (const float*)qg,
+                                   (float*)out, (const int*)step, (int)t, (int)nh, (int)nkv, (int)hd, scale,
+                                   (const float*)sink, (int)win, c->stream));
+    return 0;
+}
+
+int strata_attn_prefill(strata_ctx* c, uint64_t q, uint64_t kc, uint64_t vc, uint64_t qg, uint64_t out, uint64_t step,
+                        uint64_t t, uint64_t nh, uint64_t nkv, uint64_t hd, float scale) {
+    return strata_attn_prefill_m(c, q, kc, vc, qg, out, step, t, nh, nkv, hd, scale, 0, 0, 0, 0);
+}
+
+int strata_add(strata_ctx* c, uint64_t x, uint64_t y, uint64_t n) {
+    if (check_ctx(c)) return -1;
+    STRATA_HIP(launch_add((float*)x, (const float*)y, n, c->stream));
+    return 0;
+}
+
+int strata_swiglu(strata_ctx* c, uint64_t g, uint64_t u, uint64_t n) {
+    if (check_ctx(c)) return -1;
+    STRATA_HIP(launch_swiglu((float*)g, (const float*)u, n, c->stream));
+    return 0;
+}
+
+int strata_get_rows(strata_ctx* c, const strata_tensor* w, uint64_t ids, uint64_t n, uint64_t out) {
+    if (check_ctx(c) || check_tensor(w, "get_rows")) return -1;
+    uint64_t b = w->ty == Q8_0 ? 32 : 256;
+    if (w->cols % b || w->cols == 0) return set_error(std::string(type_name(w->ty)) + " tensor with " + std::to_string(w->cols) + " columns: get_rows needs a multiple of " + std::to_string(b));
+    if (!n) return 0;
+    if (!w->rows) return set_error("get_rows: empty tensor");
+    if (n * (w->cols / 32) >= (1ull << 40) || n >= (1u << 31)) return set_error("get_rows: too large");
+    STRATA_HIP(launch_get_rows(w->ty, (const uint8_t*)w->ptr, w->rows, w->cols, (const int*)ids, (int)n, (float*)out,
+                               c->stream));
+    return 0;
+}
+
+int strata_fill_blocks(strata_ctx* c, const strata_tensor* w, uint64_t seed, float lo, float hi) {
+    if (check_ctx(c) || check_tensor(w, "fill_blocks")) return -1;
+    if (w->cols % block_elems(w->ty)) return set_error("fill_blocks: columns not whole blocks");
+    const uint64_t nb = w->rows * (w->cols / block_elems(w->ty));
+    if (w->ptr % 4) return set_error("fill_blocks: the tensor must be 4-byte aligned");
+    STRATA_HIP(launch_fill_blocks(w->ty, (uint8_t*)w->ptr, nb, seed, lo, hi, c->stream));
+    return 0;
+}
 
 int strata_int8_gemm(strata_ctx* c, int ty) {
     (void)c;

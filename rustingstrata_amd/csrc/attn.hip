@@ -1,0 +1,439 @@
+// Attention over the f16 KV cache (Backend::attn_prefill_m and Backend::attn_decode_gq, src/backend.rs:337-343,
+// 383-410; reference kernels src/cuda/kernels.cu:2123-2626 decode and 2787-3216 prefill). Cache rows: position p,
+// KV head g at (p nkv + g) hd halves. Query head h reads KV head h / (nh / nkv). Output head h of token t:
+// softmax(q . k scale) V over its positions, with an optional per-head sink logit (one more logit that takes mass and
+// adds nothing) and an optional gate (times sigmoid(qg[t, h 2 hd + hd + d])), as Model::attention
+// (src/model.rs:771-793) computes it.
+//
+// Prefill runs on f16 MFMA (v_mfma_f32_16x16x32_f16) without giving up f32 accuracy: q is split into f16 hi + lo
+// parts (q = hi + lo to 2^-22 relative) and so are the softmax weights, each product pair summed in f32, while K and V
+// are exact in f16 (the cache format). Both are scaled by powers of two first so that no part is a subnormal f16. Scores are computed transposed (S^T = K Q^T: keys on the MFMA rows), so the
+// softmax weights leave the score MFMA in exactly the register layout the P V MFMA takes as its B operand, and V sits
+// in LDS transposed ([dim][key]) for the A operand. Decode splits a token's positions over blocks (each serving all
+// query heads of one KV head) and merges the partial softmax sums in a second launch.
+#include <climits>
+
+#include "decoder.h"
+
+namespace strata {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(uint16_t b) {
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Positions of token t: base .. end (inclusive); a sliding window keeps the last `win`.
+__device__ __forceinline__ void att_range(const int* step, int t, int win, int& base, int& n_pos) {
+    const int end = step[2 * t];
+    base = win > 0 ? max(end + 1 - win, 0) : 0;
+    n_pos = end + 1 - base;
+}
+
+// ---------------- decode ----------------
+// grid (nkv, ATT_SPLITS, nt), 256 threads. Block (g, s, t) serves the G = nh / nkv query heads of KV head g over the
+// s-th share of token t's positions, in chunks of 64: wave w scores positions 16 w .. 16 w + 15 of the chunk for all G
+// heads (4 lanes a position, each a quarter of the head dims, summed by two xor steps), waves then run the online
+// softmax of heads w, w + 4, .. over the chunk, and thread i adds p V for head i / (256 / G) and 4 or more dims from
+// the chunk's V rows staged in LDS. The block leaves [acc (hd) | max | sum] per head in part.
+template <int HD, int G>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                          const uint16_t* __restrict__ vc, float* __restrict__ part,
+                                                          const int* step, int nh, int nkv, float scale, int win) {
+    // TPH threads per head in the P V step, DPT dims each (threads past the head's dims idle when HD < TPH)
+    constexpr int C = 64, QD = HD / 4, TPH = 256 / G, DPT = HD >= TPH ? HD / TPH : 1;
+    static_assert(HD % DPT == 0 && G <= 16, "head layout");
+    __shared__ float sq[G][HD];
+    __shared__ float ss[G][C];
+    __shared__ float salpha[G];
+    __shared__ __align__(16) uint16_t sv[C][HD];
+    const int g = blockIdx.x, split = blockIdx.y, t = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int h0 = g * G, ns = gridDim.y;
+    int base, n_pos;
+    att_range(step, t, win, base, n_pos);
+    const int per_s = (((n_pos + ns - 1) / ns) + C - 1) / C * C;
+    const int p0 = split * per_s, p1 = min(n_pos, p0 + per_s);
+    float* pp = part + ((uint64_t)(t * nh + h0) * ns + split) * (HD + 2);
+    const uint64_t pstride = (uint64_t)ns * (HD + 2);  // between heads
+    if (p0 >= n_pos) {
+        for (int i = tid; i < G * (HD + 2); i += 256) {
+            const int hh = i / (HD + 2), d = i % (HD + 2);
+            pp[hh * pstride + d] = d == HD ? -INFINITY : 0.0f;
+        }
+        return;
+    }
+    for (int i = tid; i < G * HD; i += 256) sq[i / HD][i % HD] = q[(uint64_t)t * nh * HD + h0 * HD + i];
+    const uint64_t kvd = (uint64_t)nkv * HD;
+    // running max and sum of head wave + 4 j (the softmax waves)
+    float mrun[(G + 3) / 4], lrun[(G + 3) / 4];
+#pragma unroll
+    for (int j = 0; j < (G + 3) / 4; j++) { mrun[j] = -INFINITY; lrun[j] = 0.0f; }
+    const int hh = tid / TPH, d0 = (tid % TPH) * DPT;
+    const bool pv = d0 < HD;
+    float acc[DPT];
+#pragma unroll
+    for (int i = 0; i < DPT; i++) acc[i] = 0.0f;
+    __syncthreads();
+    for (int c0 = p0; c0 < p1; c0 += C) {
+        const int nc = min(C, p1 - c0);
+        // V rows of the chunk into LDS (16 bytes a thread a round; rows past the chunk as zeros)
+        for (int i = tid; i < C * HD / 8; i += 256) {
+            const int r = i / (HD / 8), c = (i % (HD / 8)) * 8;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (r < nc) v = *(const uint4*)(vc + (uint64_t)(base + c0 + r) * kvd + g * HD + c);
+            *(uint4*)&sv[r][c] = v;
+        }
+        // scores: position 16 wave + lane / 4, dims QD (lane % 4) ..
+        {
+            const int r = 16 * wave + (lane >> 2), qq = lane & 3;
+            float s[G];
+#pragma unroll
+            for (int i = 0; i < G; i++) s[i] = 0.0f;
+            if (r < nc) {
+                const uint16_t* kr = kc + (uint64_t)(base + c0 + r) * kvd + g * HD + qq * QD;
+#pragma unroll
+                for (int c = 0; c < QD; c += 8) {
+                    const uint4 kv = *(const uint4*)(kr + c);
+                    const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float kf = h2f((uint16_t)(w4[e >> 1] >> (16 * (e & 1))));
+#pragma unroll
+                        for (int i = 0; i < G; i++) s[i] += sq[i][qq * QD + c + e] * kf;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < G; i++) {
+                float v = s[i];
+                v += __shfl_xor(v, 1, 64);
+                v += __shfl_xor(v, 2, 64);
+                if (qq == 0) ss[i][r] = r < nc ? v * scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // online softmax: wave w runs heads w, w + 4, ... over the chunk (lane = position)
+#pragma unroll
+        for (int j = 0; j < (G + 3) / 4; j++) {
+            const int h = wave + 4 * j;
+            if (h < G) {
+                const float s = ss[h][lane];
+                float mx = s;
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+                const float mnew = fmaxf(mrun[j], mx);
+                const float p = s == -INFINITY ? 0.0f : expf(s - mnew);
+                float sum = p;
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+                const float alpha = mrun[j] == -INFINITY ? 0.0f : expf(mrun[j] - mnew);
+                lrun[j] = lrun[j] * alpha + sum;
+                mrun[j] = mnew;
+                ss[h][lane] = p;
+                if (lane == 0) salpha[h] = alpha;
+            }
+        }
+        __syncthreads();
+        if (pv) {
+            const float alpha = salpha[hh];
+#pragma unroll
+            for (int i = 0; i < DPT; i++) acc[i] *= alpha;
+            for (int r = 0; r < nc; r++) {
+                const float p = ss[hh][r];
+#pragma unroll
+                for (int i = 0; i < DPT; i++) acc[i] += p * h2f(sv[r][d0 + i]);
+            }
+        }
+        __syncthreads();  // ss, salpha and sv are rewritten by the next chunk
+    }
+    if (pv)
+#pragma unroll
+        for (int i = 0; i < DPT; i++) pp[hh * pstride + d0 + i] = acc[i];
+#pragma unroll
+    for (int j = 0; j < (G + 3) / 4; j++) {
+        const int h = wave + 4 * j;
+        if (h < G && lane == 0) {
+            pp[h * pstride + HD] = mrun[j];
+            pp[h * pstride + HD + 1] = lrun[j];
+        }
+    }
+}
+
+// grid (nh, nt), HD threads: out = sum_s acc_s e^(m_s - M) / (sum_s l_s e^(m_s - M) + e^(sink - M)) (sigmoid gate).
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qg,
+                                                        float* __restrict__ out, int nh, int ns,
+                                                        const float* __restrict__ sink) {
+    const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+    const float* pp = part + (uint64_t)(t * nh + h) * ns * (HD + 2);
+    const float sk = sink ? sink[h] : -INFINITY;
+    float M = sk;
+    for (int s = 0; s < ns; s++) M = fmaxf(M, pp[s * (HD + 2) + HD]);
+    float den = sk == -INFINITY ? 0.0f : expf(sk - M), o = 0.0f;
+    for (int s = 0; s < ns; s++) {
+        const float m = pp[s * (HD + 2) + HD];
+        if (m == -INFINITY) continue;
+        const float e = expf(m - M);
+        den += pp[s * (HD + 2) + HD + 1] * e;
+        o += pp[s * (HD + 2) + d] * e;
+    }
+    float r = den > 0.0f ? o / den : 0.0f;
+    if (qg) r *= sigmoid_f(qg[(uint64_t)t * nh * 2 * HD + h * 2 * HD + HD + d]);
+    out[(uint64_t)t * nh * HD + h * HD + d] = r;
+}
+
+template <int HD, int G>
+static void decode_t(const float* q, const uint16_t* kc, const uint16_t* vc, float* part, const int* step, int nh,
+                     int nkv, float scale, int nt, int win, hipStream_t s) {
+    attn_decode_kernel<HD, G><<<dim3((unsigned)nkv, ATT_SPLITS, (unsigned)nt), dim3(256), 0, s>>>(q, kc, vc, part, step, nh,
+                                                                                              nkv, scale, win);
+}
+
+hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                              float* part, const int* step, int nh, int nkv, int hd, float scale, int nt,
+                              const float* sink, int win, hipStream_t s) {
+    if (nt <= 0) return hipSuccess;
+    const int G = nh / nkv;
+#define DEC(HD_, G_) if (hd == HD_ && G == G_) decode_t<HD_, G_>(q, kc, vc, part, step, nh, nkv, scale, nt, win, s); else
+    DEC(128, 1) DEC(128, 2) DEC(128, 4) DEC(128, 8) DEC(128, 16) DEC(64, 1) DEC(64, 2) DEC(64, 4) DEC(64, 8) DEC(64, 16)
+    return hipErrorInvalidValue;
+#undef DEC
+    if (hd == 128) attn_merge_kernel<128><<<dim3((unsigned)nh, (unsigned)nt), dim3(128), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink);
+    else attn_merge_kernel<64><<<dim3((unsigned)nh, (unsigned)nt), dim3(64), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink);
+    return hipGetLastError();
+}
+
+// ---------------- prefill ----------------
+// grid (ceil(t / 32), nkv), G waves: wave w is query head g G + w over the block's 32 query rows (two 16-query MFMA
+// columns j), so every K/V tile in LDS serves the whole GQA group. Query row i sits at position step[0] + q0 + i and
+// sees keys base(i) .. step[0] + q0 + i (base 0, or the sliding window's start). Per tile of 64 keys:
+//   S^T (16 keys x 16 queries, 4 key sub-tiles kt) = sum over dims of K (A: key row, 8 dims a lane) with Q^T hi and lo
+//   (B: query column, the same 8 dims); lane holds keys 16 kt + 4 (l / 16) + i of query 16 j + l % 16.
+//   Online softmax per query column (the lane's 16 values, then across the 4 lane groups).
+//   O^T (16 dims x 16 queries, 8 dim tiles dt) += V^T (A: dim row, 8 keys) P^T hi and lo (B: the lane's own p values:
+//   keys 4 (l / 16) + i of sub-tiles 2 c and 2 c + 1 make the 8 K-elements of k-step c, and V^T's A fragment reads
+//   the same keys).
+constexpr int PF_BQ = 32, PF_BK = 64;
+
+template <int HD> struct PfLayout {
+    static constexpr int KP = HD + 8;          // halves per K row in LDS (16-byte pad: rows start in spread banks)
+    static constexpr int VP = PF_BK + 4;       // halves per V^T row (8-byte pad)
+    static constexpr int KBYTES = PF_BK * KP * 2;
+    static constexpr int VBYTES = HD * VP * 2;
+};
+
+template <int HD, int G>
+__global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                              const uint16_t* __restrict__ vc, const float* __restrict__ qg,
+                                                              float* __restrict__ out, const int* step, int T, int nh,
+                                                              int nkv, float scale, const float* __restrict__ sink,
+                                                              int win) {
+    using L = PfLayout<HD>;
+    constexpr int KS = HD / 32, DT = HD / 16, NTH = 64 * G;
+    __shared__ __align__(16) uint16_t ks[PF_BK * L::KP];
+    __shared__ __align__(16) uint16_t vs[HD * L::VP];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int q0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * PF_BQ;  // heaviest tiles first
+    const int g = blockIdx.y, h = g * G + wave, pos0 = step[0];
+    const uint64_t kvd = (uint64_t)nkv * HD;
+    const int qlast = min(q0 + PF_BQ, T) - 1;  // last live query row of the block
+    const int last = pos0 + qlast;             // last key any of them sees
+    const int first = win > 0 ? max(pos0 + q0 + 1 - win, 0) : 0;
+    // Q^T fragments (B operand): query 16 j + l16, dims 32 ks + 8 lg .. + 7, split into f16 hi and lo after scaling
+    // the query by a power of two that puts its largest value in [2^13, 2^14): the lo parts then stay normal f16
+    // numbers (no subnormal precision loss) and the hi parts cannot overflow. usc[j] undoes it (times `scale`).
+    h8 qh[2][KS], ql[2][KS];
+    float usc[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int row = q0 + 16 * j + l16;
+        const float* qr = q + (uint64_t)row * nh * HD + h * HD;
+        float v[KS][8];
+        float mx = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            if (row < T) {
+                const float4 a = *(const float4*)(qr + 32 * k + 8 * lg), b = *(const float4*)(qr + 32 * k + 8 * lg + 4);
+                v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
+                v[k][4] = b.x; v[k][5] = b.y; v[k][6] = b.z; v[k][7] = b.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[k][e] = 0.0f;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[k][e]));
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        int ex = 0;
+        if (mx > 0.0f) (void)frexpf(mx, &ex);  // mx < 2^ex
+        const float up = ldexpf(1.0f, 14 - ex);
+        usc[j] = ldexpf(scale, ex - 14);
+#pragma unroll
+        for (int k = 0; k < KS; k++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float x = v[k][e] * up;
+                const _Float16 hi = (_Float16)x;
+                qh[j][k][e] = hi;
+                ql[j][k][e] = (_Float16)(x - (float)hi);
+            }
+    }
+    f4 o[2][DT];
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int d = 0; d < DT; d++) o[j][d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    const int qpos[2] = {pos0 + q0 + l16, pos0 + q0 + 16 + l16};  // the lane's query position per column j
+    for (int k0 = first / PF_BK * PF_BK; k0 <= last; k0 += PF_BK) {
+        __syncthreads();  // the previous tile's readers are done
+        // K tile [key][dim] and V tile transposed [dim][key]; keys past `last` as zeros (finite: p = 0 times them)
+        for (int i = tid; i < PF_BK * HD / 8; i += NTH) {
+            const int key = i % PF_BK, c = (i / PF_BK) * 8, kp = k0 + key;
+            uint4 kv = make_uint4(0, 0, 0, 0), vv = kv;
+            if (kp <= last) {
+                kv = *(const uint4*)(kc + (uint64_t)kp * kvd + g * HD + c);
+                vv = *(const uint4*)(vc + (uint64_t)kp * kvd + g * HD + c);
+            }
+            *(uint4*)&ks[key * L::KP + c] = kv;
+            const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) vs[(c + e) * L::VP + key] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+        }
+        __syncthreads();
+        // S^T
+        f4 s[2][4];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            h8 kf[KS];
+#pragma unroll
+            for (int k = 0; k < KS; k++) kf[k] = *(const h8*)&ks[(16 * kt + l16) * L::KP + 32 * k + 8 * lg];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                f4 c = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k = 0; k < KS; k++) {
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[k], qh[j][k], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[k], ql[j][k], c, 0, 0, 0);
+                }
+                s[j][kt] = c;
+            }
+        }
+        // online softmax per query column; mask keys outside first .. qpos
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int qp = qpos[j], lo = win > 0 ? qp + 1 - win : INT_MIN;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int kp = k0 + 16 * kt + 4 * lg + i;
+                    float v = s[j][kt][i] * usc[j];
+                    if (kp > qp || kp < lo) v = -INFINITY;
+                    s[j][kt][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mnew = fmaxf(m[j], mx);
+            const float alpha = m[j] == -INFINITY ? 0.0f : expf(m[j] - mnew);
+            float sum = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float p = s[j][kt][i] == -INFINITY ? 0.0f : expf(s[j][kt][i] - mnew);
+                    s[j][kt][i] = p;
+                    sum += p;
+                }
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            l[j] = l[j] * alpha + sum;
+            m[j] = mnew;
+#pragma unroll
+            for (int d = 0; d < DT; d++) o[j][d] *= alpha;
+        }
+        // O^T += V^T P^T
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            h8 ph[2], pl[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    // p in [0, 1] times 2^14: the lo parts stay normal down to p ~ 2^-17
+                    const float p = s[j][2 * c + (e >> 2)][e & 3] * 16384.0f;
+                    const _Float16 hi = (_Float16)p;
+                    ph[j][e] = hi;
+                    pl[j][e] = (_Float16)(p - (float)hi);
+                }
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+                const uint16_t* vr = &vs[(16 * d + l16) * L::VP + 32 * c + 4 * lg];
+                const uint2 a0 = *(const uint2*)vr, a1 = *(const uint2*)(vr + 16);
+                h8 vf;
+                const uint32_t w4[4] = {a0.x, a0.y, a1.x, a1.y};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint16_t b = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+                    _Float16 hv;
+                    __builtin_memcpy(&hv, &b, 2);
+                    vf[e] = hv;
+                }
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    o[j][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[j], o[j][d], 0, 0, 0);
+                    o[j][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[j], o[j][d], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // out[row, h HD + 16 dt + 4 lg + i] for query row q0 + 16 j + l16
+    const float sk = sink ? sink[h] : -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int row = q0 + 16 * j + l16;
+        if (row >= T) continue;
+        const float M = fmaxf(m[j], sk);
+        const float sc = m[j] == -INFINITY ? 0.0f : expf(m[j] - M);
+        const float den = l[j] * sc + (sk == -INFINITY ? 0.0f : expf(sk - M));
+        const float inv = den > 0.0f ? sc / den * (1.0f / 16384.0f) : 0.0f;  // O carries the weights' 2^14
+        float* orow = out + (uint64_t)row * nh * HD + h * HD;
+        const float* gate = qg ? qg + (uint64_t)row * nh * 2 * HD + h * 2 * HD + HD : nullptr;
+#pragma unroll
+        for (int d = 0; d < DT; d++) {
+            const int col = 16 * d + 4 * lg;
+            float4 r = make_float4(o[j][d][0] * inv, o[j][d][1] * inv, o[j][d][2] * inv, o[j][d][3] * inv);
+            if (gate) {
+                r.x *= sigmoid_f(gate[col]); r.y *= sigmoid_f(gate[col + 1]);
+                r.z *= sigmoid_f(gate[col + 2]); r.w *= sigmoid_f(gate[col + 3]);
+            }
+            *(float4*)(orow + col) = r;
+        }
+    }
+}
+
+hipError_t launch_attn_prefill(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                               const int* step, int t, int nh, int nkv, int hd, float scale, const float* sink, int win,
+                               hipStream_t s) {
+    if (t <= 0) return hipSuccess;
+    const int G = nh / nkv;
+    const dim3 grid((unsigned)((t + PF_BQ - 1) / PF_BQ), (unsigned)nkv);
+#define PF(HD_, G_)                                                                                               \
+    if (hd == HD_ && G == G_)                                                                                     \
+        attn_prefill_kernel<HD_, G_><<<grid, dim3(64 * G_), 0, s>>>(q, kc, vc, qg, out, step, t, nh, nkv, scale,  \
+                                                                     sink, win);                                  \
+    else
+    PF(128, 1) PF(128, 2) PF(128, 4) PF(128, 8) PF(64, 1) PF(64, 2) PF(64, 4) PF(64, 8)
+    return hipErrorInvalidValue;
+#undef PF
+    return hipGetLastError();
+}
+
+}  // namespace strata

@@ -1,0 +1,49 @@
+// Launchers of the decoder-stack kernels around the quantized matmuls (decoder.hip, attn.hip): norms with rope and
+// the KV cache store, argmax, float-weight matmuls, embedding rows, attention. Arguments are checked in api.hip.
+#pragma once
+#include "common.h"
+
+namespace strata {
+
+// rms_norm_rope over `rows` heads of n: head b (token b / per, position step[0] + b / per) from x + b x_stride into
+// out + b n, normed with w then NEOX-roped on its first n_rot values; with
+// kc, also stored with its v row (v + b n) into the f16 caches at row (position per + b % per). q rows first: the
+// first qrows heads come from qx (q_stride, qw, qo, qper) and are never stored.
+struct NormRope {
+    const float* x = nullptr; uint64_t x_stride = 0; const float* w = nullptr; float* out = nullptr;
+    int n = 0, rows = 0, per = 1;
+    const float* v = nullptr; uint16_t* kc = nullptr; uint16_t* vc = nullptr;
+    int qrows = 0; const float* qx = nullptr; uint64_t q_stride = 0; const float* qw = nullptr; float* qo = nullptr;
+    int qper = 1;
+    float eps = 0, base = 0; int n_rot = 0; const int* step = nullptr;
+};
+hipError_t launch_norm_rope(const NormRope& a, hipStream_t s);
+hipError_t launch_rope_pairs(float* x, uint64_t stride, int heads, int per, int n_rot, const int* step, float base,
+                             int lo, int hi, hipStream_t s);
+hipError_t launch_kv_store(const float* k, const float* v, uint16_t* kc, uint16_t* vc, int n, int t, const int* step,
+                           hipStream_t s);
+// part: at least argmax_part_bytes(rows) bytes of scratch.
+uint64_t argmax_part_bytes(int rows);
+hipError_t launch_argmax_rows(const float* x, int n, int rows, uint64_t* part, int* out, hipStream_t s);
+hipError_t launch_add(float* x, const float* y, uint64_t n, hipStream_t s);
+hipError_t launch_swiglu(float* g, const float* u, uint64_t n, hipStream_t s);
+hipError_t launch_get_rows(int ty, const uint8_t* w, uint64_t rows, uint64_t cols, const int* ids, int n, float* out,
+                           hipStream_t s);
+// y[t * y_stride + r] = W[r] . x[t * x_stride] for an f32 matrix W (rows x cols), t < nt; act 2 adds to y.
+hipError_t launch_gemv_f32(const float* w, int rows, int cols, const float* x, uint64_t x_stride, float* y,
+                           uint64_t y_stride, int nt, int act, hipStream_t s);
+// gemm_dense with f32 weights: y[m * y_stride + r] (op) W[r] . x[m * x_stride], m < n; act 0 store, 1 SwiGLU, 2 add.
+hipError_t launch_gemm_f32(const float* w, int rows, int cols, const float* x, uint64_t x_stride, float* y,
+                           uint64_t y_stride, int n, int act, hipStream_t s);
+hipError_t launch_fill_blocks(int ty, uint8_t* w, uint64_t n_blocks, uint64_t seed, float lo, float hi, hipStream_t s);
+
+// Attention (attn.hip). Caches: f16 rows of nkv * hd values per position.
+constexpr int ATT_SPLITS = 64;  // position splits of a decode token (part rows per head)
+hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                              float* part, const int* step, int nh, int nkv, int hd, float scale, int nt,
+                              const float* sink, int win, hipStream_t s);
+hipError_t launch_attn_prefill(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
+                               const int* step, int t, int nh, int nkv, int hd, float scale, const float* sink, int win,
+                               hipStream_t s);
+
+}  // namespace strata

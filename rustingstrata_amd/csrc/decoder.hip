@@ -1,0 +1,394 @@
+// The decoder stack around the quantized matmuls: per-head RMS norm with NEOX rope and the f16 KV-cache store
+// (Backend::rms_norm_rope_kv / rms_norm_rope_qk / rope_pairs / kv_store, src/backend.rs:250-277,380), argmax over
+// logit rows (Backend::argmax_rows, :246), x += y and SwiGLU (:282-284), float-weight matmuls (the router's F32
+// weights through gemv / gemm_dense), embedding rows (Model::embed, src/model.rs:334-339, on the device) and seeded
+// synthetic GGUF blocks.
+#include "decoder.h"
+#include "formats.h"
+
+namespace strata {
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
+    _Float16 h = (_Float16)v;  // round to nearest even, as __float2half_rn
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__device__ __forceinline__ float wave_sum_xor(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ---- rms_norm + rope (+ KV store) ----
+// One wave per head, n <= 512, the head staged in LDS. The sum of squares runs in index order on one lane (n adds per
+// head, a small part of the launch), and out = x * (1 / sqrt(ss / n + eps)) * w in the reference's operation order,
+// so the normed head has the CPU's bits (src/ops.rs:3-7; kernel
+// src/cuda/kernels.cu:2196-2227). The rope turns pair (i, i + n_rot / 2) by theta = pos * base^(-2 i / n_rot), theta
+// in f64 and its sine and cosine rounded to f32 as ops::rope_neox does (src/ops.rs:36-45).
+constexpr int NR_WAVES = 4;
+
+__global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
+    __shared__ float sh[NR_WAVES][512];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int b = (int)blockIdx.x * NR_WAVES + wave - a.qrows;
+    if (b >= a.rows) return;
+    const float* x = a.x;
+    uint64_t xs = a.x_stride;
+    const float* w = a.w;
+    float* out = a.out;
+    int per = a.per;
+    bool store = a.kc != nullptr;
+    if (b < 0) {
+        b += a.qrows;
+        x = a.qx; xs = a.q_stride; w = a.qw; out = a.qo; per = a.qper; store = false;
+    }
+    const int n = a.n, tok = b / per, pos = a.step[0] + tok;
+    const float* xr = x + (uint64_t)b * xs;
+    float* o = out + (uint64_t)b * n;
+    float* s = sh[wave];
+    // the sum of squares in index order by one lane, as ops::rms_norm's iterator sum: the same bits as the CPU
+    for (int i = lane; i < n; i += 64) s[i] = xr[i];
+    __builtin_amdgcn_wave_barrier();
+    float ss = 0.0f;
+    if (lane == 0)
+        for (int i = 0; i < n; i++) ss += s[i] * s[i];
+    ss = __shfl(ss, 0, 64);
+    const float sc = 1.0f / sqrtf(ss / (float)n + a.eps);
+    for (int i = lane; i < n; i += 64) s[i] = s[i] * sc * w[i];
+    __builtin_amdgcn_wave_barrier();
+    const int half = a.n_rot / 2;
+    for (int i = lane; i < half; i += 64) {
+        const double theta = (double)pos * pow((double)a.base, -2.0 * (double)i / (double)a.n_rot);
+        const float sn = (float)sin(theta), c = (float)cos(theta);
+        const float p = s[i], q = s[i + half];
+        s[i] = p * c - q * sn;
+        s[i + half] = p * sn + q * c;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < n; i += 64) o[i] = s[i];
+    if (store) {
+        const float* vr = a.v + (uint64_t)b * n;
+        const uint64_t e = ((uint64_t)pos * per + b % per) * n;
+        for (int i = lane; i < n; i += 64) {
+            a.kc[e + i] = f32_to_f16_bits(s[i]);
+            a.vc[e + i] = f32_to_f16_bits(vr[i]);
+        }
+    }
+}
+
+// rope_neox of pairs lo .. hi - 1 only (Backend::rope_pairs, src/backend.rs:254; kernel src/cuda/kernels.cu:1596-1610),
+// in place on `heads` rows `stride` floats apart, head b of token b / per at position step[0] + b / per.
+__global__ __launch_bounds__(64 * NR_WAVES) void rope_pairs_kernel(float* x, uint64_t stride, int heads, int per,
+                                                                   int n_rot, const int* step, float base, int lo, int hi) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = (int)blockIdx.x * NR_WAVES + wave;
+    if (b >= heads) return;
+    const int pos = step[0] + b / per, half = n_rot / 2;
+    float* h = x + (uint64_t)b * stride;
+    for (int i = lane; i < half; i += 64) {
+        if (i < lo || i >= hi) continue;
+        const double theta = (double)pos * pow((double)base, -2.0 * (double)i / (double)n_rot);
+        const float sn = (float)sin(theta), c = (float)cos(theta);
+        const float p = h[i], q = h[i + half];
+        h[i] = p * c - q * sn;
+        h[i + half] = p * sn + q * c;
+    }
+}
+
+hipError_t launch_norm_rope(const NormRope& a, hipStream_t s) {
+    const int total = a.qrows + a.rows;
+    if (total <= 0) return hipSuccess;
+    norm_rope_kernel<<<dim3((unsigned)((total + NR_WAVES - 1) / NR_WAVES)), dim3(64 * NR_WAVES), 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_pairs(float* x, uint64_t stride, int heads, int per, int n_rot, const int* step, float base,
+                             int lo, int hi, hipStream_t s) {
+    if (heads <= 0 || hi <= lo) return hipSuccess;
+    rope_pairs_kernel<<<dim3((unsigned)((heads + NR_WAVES - 1) / NR_WAVES)), dim3(64 * NR_WAVES), 0, s>>>(
+        x, stride, heads, per, n_rot, step, base, lo, hi);
+    return hipGetLastError();
+}
+
+// kv_store (src/cuda/kernels.cu:2181-2186): value i of the t tokens' rows of n goes to cache element step[0] n + i.
+__global__ __launch_bounds__(256) void kv_store_kernel(const float* k, const float* v, uint16_t* kc, uint16_t* vc,
+                                                       uint64_t n, uint64_t total, const int* step) {
+    const uint64_t base = (uint64_t)step[0] * n;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256) {
+        kc[base + i] = f32_to_f16_bits(k[i]);
+        vc[base + i] = f32_to_f16_bits(v[i]);
+    }
+}
+
+hipError_t launch_kv_store(const float* k, const float* v, uint16_t* kc, uint16_t* vc, int n, int t, const int* step,
+                           hipStream_t s) {
+    const uint64_t total = (uint64_t)n * t;
+    if (!total) return hipSuccess;
+    const uint64_t blocks = std::min<uint64_t>((total + 255) / 256, 4096);
+    kv_store_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(k, v, kc, vc, (uint64_t)n, total, step);
+    return hipGetLastError();
+}
+
+// ---- argmax ----
+// ops::argmax's order (src/ops.rs:110-112): the largest value under f32::total_cmp, the first index on ties. A value
+// and its index pack into one 64-bit key whose unsigned maximum is that choice: the total-order image of the bits
+// above, ~index below.
+constexpr int AMAX_PARTS = 64;
+
+__device__ __forceinline__ uint64_t amax_key(float v, int i) {
+    const int32_t b = __float_as_int(v);
+    const uint32_t u = (uint32_t)(b ^ (int32_t)((uint32_t)(b >> 31) >> 1)) ^ 0x80000000u;
+    return ((uint64_t)u << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)k, o, 64), hi = __shfl_xor((uint32_t)(k >> 32), o, 64);
+        const uint64_t other = ((uint64_t)hi << 32) | lo;
+        k = other > k ? other : k;
+    }
+    return k;
+}
+
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float* x, int n, uint64_t* part) {
+    __shared__ uint64_t sk[4];
+    const float* xr = x + (uint64_t)blockIdx.y * n;
+    uint64_t best = 0;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += AMAX_PARTS * 256) {
+        const uint64_t k = amax_key(xr[i], i);
+        best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = sk[0];
+        for (int w = 1; w < 4; w++) b = sk[w] > b ? sk[w] : b;
+        part[(uint64_t)blockIdx.y * AMAX_PARTS + blockIdx.x] = b;
+    }
+}
+
+__global__ __launch_bounds__(64) void argmax_final_kernel(const uint64_t* part, int* out) {
+    const uint64_t k = wave_max_u64(part[(uint64_t)blockIdx.x * AMAX_PARTS + threadIdx.x]);
+    if (threadIdx.x == 0) out[blockIdx.x] = (int)(0xFFFFFFFFu - (uint32_t)k);
+}
+
+uint64_t argmax_part_bytes(int rows) { return (uint64_t)rows * AMAX_PARTS * 8; }
+
+hipError_t launch_argmax_rows(const float* x, int n, int rows, uint64_t* part, int* out, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    argmax_part_kernel<<<dim3(AMAX_PARTS, (unsigned)rows), dim3(256), 0, s>>>(x, n, part);
+    argmax_final_kernel<<<dim3((unsigned)rows), dim3(64), 0, s>>>(part, out);
+    return hipGetLastError();
+}
+
+// ---- elementwise ----
+__global__ __launch_bounds__(256) void add_kernel(float* x, const float* y, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) x[i] = x[i] + y[i];
+}
+__global__ __launch_bounds__(256) void swiglu_kernel(float* g, const float* u, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256)
+        g[i] = silu_f32(g[i]) * u[i];
+}
+static unsigned ew_blocks(uint64_t n) { return (unsigned)std::min<uint64_t>((n + 255) / 256, 8192); }
+
+hipError_t launch_add(float* x, const float* y, uint64_t n, hipStream_t s) {
+    if (!n) return hipSuccess;
+    add_kernel<<<dim3(ew_blocks(n)), dim3(256), 0, s>>>(x, y, n);
+    return hipGetLastError();
+}
+hipError_t launch_swiglu(float* g, const float* u, uint64_t n, hipStream_t s) {
+    if (!n) return hipSuccess;
+    swiglu_kernel<<<dim3(ew_blocks(n)), dim3(256), 0, s>>>(g, u, n);
+    return hipGetLastError();
+}
+
+// ---- embedding rows: out[i] = dequant(row min(ids[i], rows - 1)) (Model::embed, src/model.rs:334-339) ----
+template <int T>
+__global__ __launch_bounds__(256) void get_rows_kernel(const uint8_t* __restrict__ w, uint64_t rb, uint64_t rows,
+                                                       int cols, const int* ids, uint64_t groups, float* __restrict__ out) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= groups) return;
+    const int gpr = cols / 32;
+    const uint64_t r = i / gpr;
+    const int g = (int)(i % gpr);
+    const int id = ids[r];
+    const uint64_t src = id < 0 ? 0 : (uint64_t)id >= rows ? rows - 1 : (uint64_t)id;
+    const uint8_t* sb = w + src * rb + (uint64_t)(g / 8) * sb_bytes(T);
+    float v[32];
+    dequant32<T>(sb, g % 8, v);
+    float4* o = (float4*)(out + r * cols + 32 * g);
+#pragma unroll
+    for (int j = 0; j < 8; j++) o[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+}
+
+template <int T>
+static hipError_t get_rows_t(const uint8_t* w, uint64_t rows, uint64_t cols, const int* ids, int n, float* out,
+                             hipStream_t s) {
+    const uint64_t groups = (uint64_t)n * (cols / 32);
+    if (!groups) return hipSuccess;
+    get_rows_kernel<T><<<dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, s>>>(w, row_bytes(T, cols), rows,
+                                                                                   (int)cols, ids, groups, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_get_rows(int ty, const uint8_t* w, uint64_t rows, uint64_t cols, const int* ids, int n, float* out,
+                           hipStream_t s) {
+    switch (ty) {
+    case Q8_0: return get_rows_t<Q8_0>(w, rows, cols, ids, n, out, s);
+    case Q2_K: return get_rows_t<Q2_K>(w, rows, cols, ids, n, out, s);
+    case Q3_K: return get_rows_t<Q3_K>(w, rows, cols, ids, n, out, s);
+    case Q4_K: return get_rows_t<Q4_K>(w, rows, cols, ids, n, out, s);
+    case Q5_K: return get_rows_t<Q5_K>(w, rows, cols, ids, n, out, s);
+    case Q6_K: return get_rows_t<Q6_K>(w, rows, cols, ids, n, out, s);
+    case IQ2_XXS: return get_rows_t<IQ2_XXS>(w, rows, cols, ids, n, out, s);
+    case IQ3_S: return get_rows_t<IQ3_S>(w, rows, cols, ids, n, out, s);
+    case IQ4_XS: return get_rows_t<IQ4_XS>(w, rows, cols, ids, n, out, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+// ---- f32-weight GEMV: one wave per weight row, every input of the launch on that row ----
+constexpr int GF_NT = 4;
+__global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__ w, int rows, int cols,
+                                                       const float* __restrict__ x, uint64_t x_stride, float* y,
+                                                       uint64_t y_stride, int nt, int act) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float4* wr = (const float4*)(w + (uint64_t)r * cols);
+    float acc[GF_NT] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = lane; c < cols / 4; c += 64) {
+        const float4 wv = wr[c];
+#pragma unroll
+        for (int t = 0; t < GF_NT; t++) {
+            if (t < nt) {
+                const float4 xv = ((const float4*)(x + t * x_stride))[c];
+                acc[t] += wv.x * xv.x + wv.y * xv.y + wv.z * xv.z + wv.w * xv.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < GF_NT; t++) {
+        if (t < nt) {
+            const float v = wave_sum_xor(acc[t]);
+            if (lane == 0) {
+                float* yo = y + t * y_stride + r;
+                *yo = act == 2 ? *yo + v : v;
+            }
+        }
+    }
+}
+
+hipError_t launch_gemv_f32(const float* w, int rows, int cols, const float* x, uint64_t x_stride, float* y,
+                           uint64_t y_stride, int nt, int act, hipStream_t s) {
+    if (!rows || !nt) return hipSuccess;
+    for (int t0 = 0; t0 < nt; t0 += GF_NT) {
+        const int n = std::min(GF_NT, nt - t0);
+        gemv_f32_kernel<<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s>>>(w, rows, cols, x + t0 * x_stride, x_stride,
+                                                                                y + t0 * y_stride, y_stride, n, act);
+    }
+    return hipGetLastError();
+}
+
+// ---- f32-weight GEMM (gemm_dense of a float matrix): 64 positions x 64 weight rows a block, K in steps of 16 ----
+__global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ w, int rows, int cols,
+                                                       const float* __restrict__ x, uint64_t x_stride, float* y,
+                                                       uint64_t y_stride, int n, int act) {
+    __shared__ float xs[16][64 + 4], ws[16][64 + 4];
+    const int m0 = blockIdx.x * 64, r0 = blockIdx.y * 64, tid = threadIdx.x;
+    const int tm = tid >> 4, tr = tid & 15;  // this thread's outputs: positions m0 + tm + 16 i, rows r0 + tr + 16 j
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < cols; k0 += 16) {
+        // each thread loads 4 of the 1024 values of each tile: row (tid / 4) of the tile, k k0 + 4 (tid % 4) ..
+        const int lr = tid >> 2, lk = 4 * (tid & 3);
+        float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), wv = xv;
+        if (m0 + lr < n && k0 + lk < cols) xv = *(const float4*)(x + (uint64_t)(m0 + lr) * x_stride + k0 + lk);
+        if (r0 + lr < rows && k0 + lk < cols) wv = *(const float4*)(w + (uint64_t)(r0 + lr) * cols + k0 + lk);
+        __syncthreads();
+        xs[lk][lr] = xv.x; xs[lk + 1][lr] = xv.y; xs[lk + 2][lr] = xv.z; xs[lk + 3][lr] = xv.w;
+        ws[lk][lr] = wv.x; ws[lk + 1][lr] = wv.y; ws[lk + 2][lr] = wv.z; ws[lk + 3][lr] = wv.w;
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) { a[i] = xs[k][tm + 16 * i]; b[i] = ws[k][tr + 16 * i]; }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int m = m0 + tm + 16 * i;
+        if (m >= n) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = r0 + tr + 16 * j;
+            if (r >= rows) continue;
+            float* yo = y + (uint64_t)m * y_stride + r;
+            const float v = acc[i][j];
+            *yo = act == 0 ? v : act == 1 ? silu_f32(*yo) * v : *yo + v;
+        }
+    }
+}
+
+hipError_t launch_gemm_f32(const float* w, int rows, int cols, const float* x, uint64_t x_stride, float* y,
+                           uint64_t y_stride, int n, int act, hipStream_t s) {
+    if (!rows || !n) return hipSuccess;
+    gemm_f32_kernel<<<dim3((unsigned)((n + 63) / 64), (unsigned)((rows + 63) / 64)), dim3(256), 0, s>>>(
+        w, rows, cols, x, x_stride, y, y_stride, n, act);
+    return hipGetLastError();
+}
+
+// ---- synthetic weights: random block bytes with every f16 scale field in [lo, hi) (the reference's random_tensor
+// design, tests/kernels.rs:1473-1550), from a counter-based hash of (seed, position) ----
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void fill_bytes_kernel(uint8_t* w, uint64_t bytes, uint64_t seed) {
+    const uint64_t words = bytes / 4;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < (bytes + 3) / 4; i += (uint64_t)gridDim.x * 256) {
+        const uint32_t r = (uint32_t)mix64(seed * 0x9E3779B97F4A7C15ull + i);
+        if (i < words) {
+            ((uint32_t*)w)[i] = r;
+        } else {
+            for (uint64_t b = 4 * i; b < bytes; b++) w[b] = (uint8_t)(r >> (8 * (b - 4 * i)));
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void fill_scales_kernel(uint8_t* w, uint64_t n_blocks, int bb, int f0, int f1,
+                                                          uint64_t seed, float lo, float hi) {
+    for (uint64_t b = (uint64_t)blockIdx.x * 256 + threadIdx.x; b < n_blocks; b += (uint64_t)gridDim.x * 256) {
+        const uint64_t r = mix64(~seed * 0xD1B54A32D192ED03ull + b);
+        const float u0 = (float)(uint32_t)r * 2.3283064365386963e-10f, u1 = (float)(uint32_t)(r >> 32) * 2.3283064365386963e-10f;
+        *(uint16_t*)(w + b * bb + f0) = f32_to_f16_bits(lo + (hi - lo) * u0);
+        if (f1 >= 0) *(uint16_t*)(w + b * bb + f1) = f32_to_f16_bits(lo + (hi - lo) * u1);
+    }
+}
+
+hipError_t launch_fill_blocks(int ty, uint8_t* w, uint64_t n_blocks, uint64_t seed, float lo, float hi, hipStream_t s) {
+    if (!n_blocks) return hipSuccess;
+    const int bb = block_bytes(ty);
+    int f0 = 0, f1 = -1;  // offsets of the f16 scale fields in a block (d, and dmin where the type has one)
+    switch (ty) {
+    case Q2_K: f0 = 80; f1 = 82; break;
+    case Q3_K: f0 = 108; break;
+    case Q4_K: case Q5_K: f0 = 0; f1 = 2; break;
+    case Q6_K: f0 = 208; break;
+    default: f0 = 0; break;
+    }
+    const uint64_t bytes = n_blocks * (uint64_t)bb;
+    fill_bytes_kernel<<<dim3(ew_blocks((bytes + 3) / 4)), dim3(256), 0, s>>>(w, bytes, seed);
+    fill_scales_kernel<<<dim3(ew_blocks(n_blocks)), dim3(256), 0, s>>>(w, n_blocks, bb, f0, f1, seed, lo, hi);
+    return hipGetLastError();
+}
+
+}  // namespace strata

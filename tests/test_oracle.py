@@ -326,3 +326,72 @@ def test_iq3s_known_answer_all_qh_bits_and_sign_bytes():
                 neg = (int(b[74 + 4 * ib + e // 8]) >> (e % 8)) & 1
                 want[32 * ib + e] = db * np.float32((g >> (8 * c)) & 255) * np.float32(-1.0 if neg else 1.0)
     assert np.array_equal(y.view(np.uint32), want.view(np.uint32))
+
+
+# ---- the decoder stack's CPU functions (oracle/attention.c) ----
+
+def test_rope_neox_closed_forms():
+    """ops::rope_neox (src/ops.rs:36-45): position 0 is the identity; pair (i, i + n_rot / 2) turns by
+    theta_i = pos * base^(-2 i / n_rot) (i = 0: theta = pos exactly; i = 1 checked against f64 numpy); each pair keeps
+    its length; dims past n_rot are untouched; turning by p1 then p2 is turning by p1 + p2 (to rounding)."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, 128)).astype(np.float32)
+    assert np.array_equal(O.rope_neox(x, 128, 0, 1e6), x)
+    y = O.rope_neox(x, 128, 37, 1e6)
+    c, s = np.float32(np.cos(37.0)), np.float32(np.sin(37.0))
+    assert np.array_equal(y[:, 0], (x[:, 0] * c - x[:, 64] * s).astype(np.float32))
+    th1 = 37.0 * 1e6 ** (-2.0 / 128)
+    assert np.allclose(y[:, 1], x[:, 1] * np.cos(th1) - x[:, 65] * np.sin(th1), rtol=0, atol=1e-5)
+    assert np.allclose(y[:, 65], x[:, 1] * np.sin(th1) + x[:, 65] * np.cos(th1), rtol=0, atol=1e-5)
+    for i in range(64):
+        assert np.allclose(np.hypot(y[:, i], y[:, i + 64]), np.hypot(x[:, i], x[:, i + 64]), rtol=1e-5)
+    # partial rotation: n_rot 64 leaves dims 64.. alone and pairs (i, i + 32)
+    z = O.rope_neox(x, 64, 5, 1e4)
+    assert np.array_equal(z[:, 64:], x[:, 64:])
+    assert np.allclose(np.hypot(z[:, 3], z[:, 35]), np.hypot(x[:, 3], x[:, 35]), rtol=1e-5)
+    assert np.allclose(O.rope_neox(O.rope_neox(x, 128, 300, 1e6), 128, 1000, 1e6), O.rope_neox(x, 128, 1300, 1e6),
+                       atol=5e-5)
+
+
+def test_argmax_total_order():
+    """ops::argmax (src/ops.rs:110-112): first index on ties; under total_cmp +0 is above -0 and a positive NaN above
+    everything."""
+    assert O.argmax(np.array([1, 5, 5, 2], np.float32)) == 1
+    assert O.argmax(np.array([-0.0, 0.0, -0.0], np.float32)) == 1
+    assert O.argmax(np.array([np.inf, np.nan, 3], np.float32)) == 1
+    assert O.argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
+    x = np.random.default_rng(1).standard_normal(151936).astype(np.float32)
+    assert O.argmax(x) == int(np.argmax(x))
+
+
+def test_attention_known_answers():
+    """Model::attention (src/model.rs:771-793): one cell gives its V row exactly; the GQA map sends query head i to
+    KV head i / (nh / nkv) (distinct constant V rows per KV head); a large sink logit takes all the mass; the gate
+    multiplies by sigmoid; in general the output is the f64 softmax-weighted mean of V."""
+    rng = np.random.default_rng(4)
+    nh, nkv, hd, P = 8, 2, 16, 9
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    kc = rng.standard_normal((P, nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((P, nkv * hd)).astype(np.float32)
+    one = O.attention(q, kc, vc, 4, 5, nh, nkv, hd, 0.25)
+    for i in range(nh):
+        g = i // (nh // nkv)
+        assert np.array_equal(one[i * hd:(i + 1) * hd], vc[4, g * hd:(g + 1) * hd])
+    vconst = np.concatenate([np.full((P, hd), -3.0), np.full((P, hd), 7.0)], axis=1).astype(np.float32)
+    o = O.attention(q, kc, vconst, 0, P, nh, nkv, hd, 0.25).reshape(nh, hd)
+    assert np.allclose(o[:4], -3.0, atol=1e-5) and np.allclose(o[4:], 7.0, atol=1e-5)
+    o = O.attention(q, kc, vc, 0, P, nh, nkv, hd, 0.25, sinks=np.full(nh, 80.0, np.float32))
+    assert np.abs(o).max() < 1e-20
+    gate = rng.standard_normal(nh * 2 * hd).astype(np.float32)
+    plain = O.attention(q, kc, vc, 2, P, nh, nkv, hd, 0.25)
+    gated = O.attention(q, kc, vc, 2, P, nh, nkv, hd, 0.25, gate=gate[hd:], gate_stride=2 * hd)
+    sig = 1 / (1 + np.exp(-gate.reshape(nh, 2 * hd)[:, hd:].astype(np.float64)))
+    assert np.allclose(gated, plain * sig.reshape(-1), rtol=1e-6, atol=1e-7)
+    # f64 brute force
+    want = np.empty((nh, hd))
+    for i in range(nh):
+        g = i // (nh // nkv)
+        s = kc[2:, g * hd:(g + 1) * hd].astype(np.float64) @ q[i * hd:(i + 1) * hd].astype(np.float64) * 0.25
+        p = np.exp(s - s.max())
+        want[i] = p @ vc[2:, g * hd:(g + 1) * hd].astype(np.float64) / p.sum()
+    assert np.allclose(plain.reshape(nh, hd), want, rtol=1e-5, atol=1e-6)
