@@ -1,0 +1,275 @@
+"""The Qwen3-MoE decoder stack on this backend: the layer sequences of the reference's GpuModel for an attention +
+routed-MoE model (chunked prefill, src/gpu_model/prefill.rs:315-712; one decode token, src/gpu_model.rs:1950-2016,
+3100-3419), driven through the C ABI with every expert resident in HBM (no CPU offload, no mailbox).
+
+Config 5 of the build is the Qwen3-30B-A3B shape (48 layers, hidden 2048, 32 query heads and 4 KV heads of 128,
+128 experts, top-8, expert intermediate 768, vocabulary 151936) with a UD-Q2_K_XL-like type mix: Q2_K gate/up and
+Q3_K down experts, Q6_K attention, Q8_0 token embeddings and output head, F32 norms and router. `Weights.random`
+builds such a model from a seed on the device (random blocks with realistic scale fields); `Weights.from_host`
+takes host arrays (tests build small models with them and check the device stack against the CPU oracle).
+
+Per prefill chunk of t tokens at position pos (step[0] = pos):
+    x = embed(tokens)
+    per layer: h = rms_norm(x) ; q, k, v = gemm_dense(h) (k and v reuse q's int8 X) ; rms_norm_rope_qk (q/k norms,
+    NEOX rope, f16 KV store) ; attn_prefill (causal) ; x += gemm_dense(o, attn) ; h = rms_norm(x) ;
+    logits = gemm_dense(router F32, h) ; router_topk ; moe_sort (on the device) ; gate/up grouped GEMM with the
+    SwiGLU epilogue ; down grouped GEMM ; x += moe_combine_seq.
+Per decode token (recorded once as a graph and replayed; the step buffer carries the position):
+    x = embed(token) ; per layer: h, hq = rms_norm_q(x (+= mix)) ; q = gemvq ; k, v = gemvq2 ; rms_norm_rope_qk ;
+    attn_decode ; mix = gemvq(o) ; h, hq = rms_norm_q(x += mix) ; logits = gemv(router) ; moe_route ; paired
+    gate/up moe_gemv ; moe_down_swiglu_combine (x += sum w y) ; then rms_norm, output gemv, argmax_rows.
+"""
+import numpy as np
+
+from . import ggml
+from .backend import ACT_ADD, ACT_STORE, SAME_X, GpuTensor, StrataError
+
+
+class Config:
+    def __init__(self, n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, head_dim=128, n_expert=128, n_expert_used=8,
+                 n_ff_exp=768, n_vocab=151936, rope_base=1e6, eps=1e-6, ty_attn=ggml.Q6_K, ty_gate_up=ggml.Q2_K,
+                 ty_down=ggml.Q3_K, ty_embd=ggml.Q8_0, ty_out=ggml.Q8_0):
+        self.n_layer, self.n_embd, self.n_head, self.n_head_kv, self.head_dim = n_layer, n_embd, n_head, n_head_kv, head_dim
+        self.n_expert, self.n_expert_used, self.n_ff_exp, self.n_vocab = n_expert, n_expert_used, n_ff_exp, n_vocab
+        self.rope_base, self.eps = rope_base, eps
+        self.ty_attn, self.ty_gate_up, self.ty_down, self.ty_embd, self.ty_out = ty_attn, ty_gate_up, ty_down, ty_embd, ty_out
+
+    @classmethod
+    def qwen3_30b_a3b(cls, n_layer=48):
+        return cls(n_layer=n_layer)
+
+
+# f16 scale ranges for random blocks whose values have a standard deviation near 0.02 (N(0, 0.02)-like weights):
+# Q8_0 d q (q uniform int8, sd ~74 d); Q6_K d sc (q - 32) (sd ~1370 d); Q2_K d sc q - dmin m (sd ~12 d);
+# Q3_K d (sc - 32) q3 (sd ~42 d).
+SCALE = {ggml.Q8_0: (2.2e-4, 3.2e-4), ggml.Q6_K: (1.2e-5, 1.8e-5), ggml.Q2_K: (1.4e-3, 2.0e-3),
+         ggml.Q3_K: (4.0e-4, 5.5e-4), ggml.Q4_K: (1.0e-3, 1.6e-3), ggml.Q5_K: (5e-4, 8e-4)}
+
+
+class Layer:
+    __slots__ = ("attn_norm", "q", "k", "v", "q_norm", "k_norm", "o", "ffn_norm", "router", "gate_up", "down",
+                 "e_gu", "e_down", "up_off", "kc", "vc")
+
+
+class Weights:
+    """Device tensors of the model. A layer's routed experts are the GGUF expert-stacked tensors (expert e of a matrix
+    at e * rows * row_bytes): gate then up in one buffer (so the up matrix of every expert sits a fixed offset after
+    its gate matrix, the pairing the fused gate/up kernels take), down in another."""
+
+    def __init__(self, hip, cfg):
+        self.hip, self.cfg = hip, cfg
+        self.layers = []
+
+    def strides(self):
+        c = self.cfg
+        return (ggml.row_bytes(c.ty_gate_up, c.n_embd) * c.n_ff_exp, ggml.row_bytes(c.ty_down, c.n_ff_exp) * c.n_embd)
+
+    def _quant(self, ty, rows, cols, seed, buf=None):
+        t = GpuTensor(ty, rows, cols, buf if buf is not None else self.hip.alloc(rows * ggml.row_bytes(ty, cols)))
+        lo, hi = SCALE[ty]
+        self.hip.fill_blocks(t, seed, lo, hi)
+        return t
+
+    @classmethod
+    def random(cls, hip, cfg, seed=0):
+        """A random-init model of cfg's shapes, built on the device from `seed` (the same seed, the same bytes)."""
+        w = cls(hip, cfg)
+        c = cfg
+        rng = np.random.default_rng(seed)
+        s = seed * 1000003
+        w.embd = w._quant(c.ty_embd, c.n_vocab, c.n_embd, s + 1)
+        w.output = w._quant(c.ty_out, c.n_vocab, c.n_embd, s + 2)
+        w.output_norm = hip.upload((1.0 + 0.1 * rng.standard_normal(c.n_embd)).astype(np.float32))
+        e_gu, e_down = w.strides()
+        for il in range(c.n_layer):
+            ly = Layer()
+            b = s + 100 * (il + 1)
+            ly.attn_norm = hip.upload((1.0 + 0.1 * rng.standard_normal(c.n_embd)).astype(np.float32))
+            ly.ffn_norm = hip.upload((1.0 + 0.1 * rng.standard_normal(c.n_embd)).astype(np.float32))
+            ly.q_norm = hip.upload((1.0 + 0.1 * rng.standard_normal(c.head_dim)).astype(np.float32))
+            ly.k_norm = hip.upload((1.0 + 0.1 * rng.standard_normal(c.head_dim)).astype(np.float32))
+            ly.q = w._quant(c.ty_attn, c.n_head * c.head_dim, c.n_embd, b + 1)
+            ly.k = w._quant(c.ty_attn, c.n_head_kv * c.head_dim, c.n_embd, b + 2)
+            ly.v = w._quant(c.ty_attn, c.n_head_kv * c.head_dim, c.n_embd, b + 3)
+            ly.o = w._quant(c.ty_attn, c.n_embd, c.n_head * c.head_dim, b + 4)
+            ly.router = hip.upload_f32((0.02 * rng.standard_normal((c.n_expert, c.n_embd))).astype(np.float32))
+            # gate and up stacks: 2 * n_expert matrices of n_ff_exp rows, one fill
+            ly.gate_up = w._quant(c.ty_gate_up, 2 * c.n_expert * c.n_ff_exp, c.n_embd, b + 5).buf
+            ly.down = w._quant(c.ty_down, c.n_expert * c.n_embd, c.n_ff_exp, b + 6).buf
+            ly.e_gu, ly.e_down, ly.up_off = e_gu, e_down, c.n_expert * e_gu
+            w.layers.append(ly)
+        return w
+
+    @classmethod
+    def from_host(cls, hip, cfg, embd, output, output_norm, layers):
+        """Upload host weights: layers = [dict(attn_norm, q, k, v, q_norm, k_norm, o, ffn_norm, router (f32
+        [n_expert, n_embd]), gate, up, down (expert-stacked block bytes, expert e at e * rows * row_bytes))]."""
+        w = cls(hip, cfg)
+        c = cfg
+        w.embd = hip.upload_tensor(c.ty_embd, embd)
+        w.output = hip.upload_tensor(c.ty_out, output)
+        w.output_norm = hip.upload(np.asarray(output_norm, np.float32))
+        e_gu, e_down = w.strides()
+        for L in layers:
+            ly = Layer()
+            ly.attn_norm = hip.upload(np.asarray(L["attn_norm"], np.float32))
+            ly.ffn_norm = hip.upload(np.asarray(L["ffn_norm"], np.float32))
+            ly.q_norm = hip.upload(np.asarray(L["q_norm"], np.float32))
+            ly.k_norm = hip.upload(np.asarray(L["k_norm"], np.float32))
+            ly.q, ly.k, ly.v, ly.o = (hip.upload_tensor(c.ty_attn, L[n]) for n in ("q", "k", "v", "o"))
+            ly.router = hip.upload_f32(L["router"])
+            ly.gate_up = hip.upload(np.concatenate([np.ascontiguousarray(L["gate"]).reshape(-1),
+                                                    np.ascontiguousarray(L["up"]).reshape(-1)]))
+            ly.down = hip.upload(np.ascontiguousarray(L["down"]).reshape(-1))
+            ly.e_gu, ly.e_down, ly.up_off = e_gu, e_down, c.n_expert * e_gu
+            w.layers.append(ly)
+        return w
+
+
+class Model:
+    """GpuModel for the Qwen3-MoE stack: KV caches for `ctx` positions, prefill chunks of up to `chunk` tokens."""
+
+    def __init__(self, hip, weights, ctx=4096 + 256, chunk=2048):
+        self.hip, self.w, self.c = hip, weights, weights.cfg
+        c = self.c
+        self.ctx, self.chunk = ctx, chunk
+        self.pos = 0
+        kv = c.n_head_kv * c.head_dim
+        for ly in weights.layers:
+            ly.kc = hip.alloc(ctx * hip.kv_words(kv) * 2)
+            ly.vc = hip.alloc(ctx * hip.kv_words(kv) * 2)
+        self.step = hip.alloc(8)
+        H, nh, hd, E, k, F = c.n_embd, c.n_head, c.head_dim, c.n_expert, c.n_expert_used, c.n_ff_exp
+        n = chunk
+        A = hip.alloc
+        # prefill buffers (rows of the chunk)
+        self.x = A(n * H * 4)
+        self.h = A(n * H * 4)
+        self.qa = A(n * nh * hd * 4)
+        self.qb = A(n * nh * hd * 4)
+        self.kraw, self.kk, self.vv = A(n * kv * 4), A(n * kv * 4), A(n * kv * 4)
+        self.att = A(n * nh * hd * 4)
+        self.rl = A(n * E * 4)
+        self.ids, self.wts = A(n * k * 4), A(n * k * 4)
+        self.off, self.xrow, self.inv = A((E + 1) * 4), A(n * k * 4), A(n * k * 4)
+        self.tchunk = hip.gemm_block_positions()
+        self.max_tiles = n * k // self.tchunk + E
+        self.tiles, self.ntd, self.err = A(2 * self.max_tiles * 16), A(4), A(4)
+        self.ge, self.ye = A(n * k * F * 4), A(n * k * H * 4)
+        self.tok_in = A(n * 4)
+        # decode buffers
+        self.hq = A(H + H // 8)
+        self.mix = A(H * 4)
+        self.dq, self.dk, self.dv = A(nh * hd * 4), A(kv * 4), A(kv * 4)
+        self.dqo, self.dko = A(nh * hd * 4), A(kv * 4)
+        self.datt = A(nh * hd * 4)
+        self.part = A(hip.attn_part_floats(nh, hd) * 4)
+        self.dl = A(E * 4)
+        self.dids, self.dwts, self.dslots, self.dwh = A(k * 4), A(k * 4), A(k * 4), A(k * 4)
+        self.table = hip.upload(np.arange(E, dtype=np.int32))
+        self.g2 = A(2 * k * F * 4)
+        self.ye1 = A(k * H * 4)
+        self.logits = A(c.n_vocab * 4)
+        self.tok = A(4)
+
+    def reset(self):
+        self.pos = 0
+
+    def _set_step(self, pos):
+        self.hip.htod(np.array([pos, 0], dtype=np.int32), self.step)
+
+    # ---- prefill (src/gpu_model/prefill.rs:315-712) ----
+    def prefill_chunk(self, tokens, layer_hook=None):
+        """One chunk; layer_hook(il, x) (if given) runs after each layer with the chunk's hidden rows (a debugging and
+        test probe, like the reference's STRATA_NAN_TRACE; it may read x, which syncs)."""
+        hip, c, w = self.hip, self.c, self.w
+        t = len(tokens)
+        if t > self.chunk or t == 0:
+            raise StrataError(f"prefill chunk of {t} tokens (1 to {self.chunk})")
+        if self.pos + t > self.ctx:
+            raise StrataError(f"context full ({self.ctx} tokens)")
+        H, nh, nkv, hd, E, k, F = c.n_embd, c.n_head, c.n_head_kv, c.head_dim, c.n_expert, c.n_expert_used, c.n_ff_exp
+        kv = nkv * hd
+        hip.htod(np.asarray(tokens, dtype=np.int32), self.tok_in)
+        self._set_step(self.pos)
+        hip.get_rows(w.embd, self.tok_in, t, self.x)
+        scale = 1.0 / np.sqrt(hd)
+        if layer_hook:
+            layer_hook(-1, self.x)
+        for il, ly in enumerate(w.layers):
+            hip.rms_norm(self.x, H, ly.attn_norm, self.h, H, H, t, c.eps)
+            hip.gemm_dense(ly.q, t, self.h, H, self.qa, nh * hd, ACT_STORE)
+            hip.gemm_dense(ly.k, t, self.h, H, self.kraw, kv, ACT_STORE | SAME_X)
+            hip.gemm_dense(ly.v, t, self.h, H, self.vv, kv, ACT_STORE | SAME_X)
+            hip.rms_norm_rope_qk(self.qa, hd, ly.q_norm, self.qb, t * nh, nh, self.kraw, ly.k_norm, self.kk, t * nkv,
+                                 nkv, hd, c.eps, hd, self.step, c.rope_base, self.vv, ly.kc, ly.vc)
+            hip.attn_prefill(self.qb, ly.kc, ly.vc, 0, self.att, self.step, t, nh, nkv, hd, scale)
+            hip.gemm_dense(ly.o, t, self.att, nh * hd, self.x, H, ACT_ADD)
+            hip.rms_norm(self.x, H, ly.ffn_norm, self.h, H, H, t, c.eps)
+            hip.gemm_dense(ly.router, t, self.h, H, self.rl, E, ACT_STORE)
+            hip.router_topk(self.rl, E, k, 0.0, self.ids, self.wts, t)
+            hip.moe_sort(self.ids, t, k, E, self.off, self.xrow, self.inv,
+                         [(int(ly.gate_up), ly.e_gu), (int(ly.down), ly.e_down)], self.tiles, self.max_tiles,
+                         self.ntd, err_dev=self.err, chunk=self.tchunk)
+            hip.gemm_grouped_gate_up(c.ty_gate_up, F, H, self.tiles, self.max_tiles, self.ntd, self.h, H, t, self.xrow,
+                                     self.ge, F, ly.up_off)
+            hip.gemm_grouped(c.ty_down, H, F, int(self.tiles) + self.max_tiles * 16, self.max_tiles, self.ntd, self.ge,
+                             F, t * k, 0, self.ye, H, ACT_STORE)
+            hip.moe_combine_seq(self.x, self.ye, self.wts, self.inv, k, 0, 0, H, t)
+            if layer_hook:
+                layer_hook(il, self.x)
+        self.pos += t
+        self.last_row = t - 1
+
+    def prefill(self, tokens, layer_hook=None):
+        """Chunked prefill (prefill_with, src/gpu_model/prefill.rs:135-163): the logits of the last token, and its
+        greedy choice, on the device (logits, tok)."""
+        for i in range(0, len(tokens), self.chunk):
+            self.prefill_chunk(tokens[i:i + self.chunk], layer_hook)
+        hip, c = self.hip, self.c
+        H = c.n_embd
+        last = int(self.x) + 4 * self.last_row * H
+        hip.rms_norm(last, H, self.w.output_norm, self.h, H, H, 1, c.eps)
+        hip.gemv(self.w.output, self.h, self.logits)
+        hip.argmax_rows(self.logits, c.n_vocab, 1, self.tok)
+        # the decode's hidden state starts from the last token's row (x row 0 of the decode buffers)
+        return self.logits, self.tok
+
+    # ---- decode (src/gpu_model.rs:1950-2016, 3100-3419) ----
+    def _decode_ops(self):
+        hip, c, w = self.hip, self.c, self.w
+        H, nh, nkv, hd, E, k, F = c.n_embd, c.n_head, c.n_head_kv, c.head_dim, c.n_expert, c.n_expert_used, c.n_ff_exp
+        kv = nkv * hd
+        x = self.x  # row 0
+        hip.get_rows(w.embd, self.tok, 1, x)
+        for ly in w.layers:
+            hip.rms_norm_q(x, H, ly.attn_norm, self.h, H, H, 1, c.eps, xq=self.hq)
+            hip.gemvq(ly.q, self.h, H, self.hq, self.dq, nh * hd, 1)
+            hip.gemvq2(ly.k, ly.v, self.h, H, self.hq, self.dk, self.dv, 1)
+            hip.rms_norm_rope_qk(self.dq, hd, ly.q_norm, self.dqo, nh, nh, self.dk, ly.k_norm, self.dko, nkv, nkv, hd,
+                                 c.eps, hd, self.step, c.rope_base, self.dv, ly.kc, ly.vc)
+            hip.attn_decode(self.dqo, ly.kc, ly.vc, 0, self.datt, self.part, self.step, nh, nkv, hd,
+                            float(1.0 / np.sqrt(hd)), 1)
+            hip.gemv(ly.o, self.datt, self.mix)
+            hip.rms_norm_q(x, H, ly.ffn_norm, self.h, H, H, 1, c.eps, xq=self.hq, res=self.mix)
+            hip.gemv(ly.router, self.h, self.dl)
+            hip.moe_route(self.dl, E, k, 0.0, self.table, self.dids, self.dwts, self.dslots, self.dwh, 1)
+            hip.moe_gemv(c.ty_gate_up, F, H, ly.gate_up, ly.e_gu, self.dslots, k, self.h, H, k, self.g2,
+                         pair=(ly.up_off, k * F * 4), xq=self.hq)
+            hip.moe_down_swiglu_combine(c.ty_down, H, F, ly.down, ly.e_down, self.dslots, k, self.g2,
+                                        int(self.g2) + k * F * 4, self.ye1, x, self.dwh, 0, 0, 1)
+        hip.rms_norm(x, H, w.output_norm, self.h, H, H, 1, c.eps)
+        hip.gemv(w.output, self.h, self.logits)
+        hip.argmax_rows(self.logits, c.n_vocab, 1, self.tok)
+
+    def decode_step(self, graph=True):
+        """One greedy token from the token in self.tok at position self.pos: the decode ops (recorded once as a graph
+        and replayed) leave the next token in self.tok and its logits in self.logits."""
+        if self.pos >= self.ctx:
+            raise StrataError(f"context full ({self.ctx} tokens)")
+        self._set_step(self.pos)
+        if graph:
+            self.hip.graph(("decode", id(self)), self._decode_ops)
+        else:
+            self._decode_ops()
+        self.pos += 1
