@@ -331,6 +331,50 @@ def bench_codebook(hip, S, ggml, iters):
     return out
 
 
+def bench_stack(hip, S, ggml, n_prompt=4096, n_decode=128, chunk=2048, n_layer=48):
+    """the 48-layer Qwen3-30B-A3B-shaped stack, random-init on the device (Q2_K gate/up and Q3_K down
+    experts, Q6_K attention, Q8_0 embeddings and output head), every expert resident. A uniform-random prompt of 4096
+    token ids is prefilled in chunks of `chunk`, then 128 greedy tokens are decoded (each a recorded-graph replay
+    after the first; the host writes the position before each token, the next token stays on the device)."""
+    from rustingstrata_amd.qwen3moe import Config, Model, Weights
+    c = Config.qwen3_30b_a3b(n_layer=n_layer)
+    t0 = time.time()
+    w = Weights.random(hip, c, seed=5)
+    hip.sync()
+    build_s = time.time() - t0
+    m = Model(hip, w, ctx=n_prompt + n_decode + 64, chunk=chunk)
+    prompt = np.random.default_rng(6).integers(0, c.n_vocab, n_prompt).tolist()
+    # warm-up: one short prefill and a few decode tokens (graph recorded), then the caches are reused from position 0
+    m.prefill(prompt[:chunk])
+    for _ in range(3):
+        m.decode_step(graph=USE_GRAPHS)
+    hip.sync()
+    m.reset()
+    e0, e1, e2 = hip.event(), hip.event(), hip.event()
+    hip.record(e0)
+    m.prefill(prompt)
+    hip.record(e1)
+    pre_ms = hip.elapsed_ms(e0, e1)
+    t1 = time.time()
+    for _ in range(n_decode):
+        m.decode_step(graph=USE_GRAPHS)
+    hip.record(e2)
+    dec_ms = hip.elapsed_ms(e1, e2)
+    wall_dec = time.time() - t1
+    toks = hip.get(m.tok, np.int32, 1)
+    hip.drop_graphs()
+    wbytes = sum(t.bytes() for t in [w.embd, w.output]) + sum(
+        ly.q.bytes() + ly.k.bytes() + ly.v.bytes() + ly.o.bytes() for ly in w.layers) + n_layer * (
+        2 * c.n_expert * w.strides()[0] + c.n_expert * w.strides()[1])
+    return {"layers": n_layer, "prompt_tokens": n_prompt, "chunk": chunk,
+            "prefill_ms": round(pre_ms, 2), "prefill_tok_per_s": round(n_prompt / (pre_ms / 1e3), 1),
+            "decode_tokens": n_decode, "decode_ms_per_token": round(dec_ms / n_decode, 3),
+            "decode_tok_per_s": round(n_decode / (dec_ms / 1e3), 1),
+            "decode_wall_tok_per_s": round(n_decode / wall_dec, 1), "weight_bytes": int(wbytes),
+            "weights_build_s": round(build_s, 2), "last_token": int(toks[0]),
+            "types": "experts Q2_K gate/up + Q3_K down, attention Q6_K, embeddings and output Q8_0, router F32"}
+
+
 def cpu_baseline(shapes, budget_s=12.0):
     """The oracle's C restatement of cpu_moe::matvec (Q8_K activations, scalar dots compiled with gcc -O3
     -march=x86-64-v3, threads over 32-row chunks like rayon's par_chunks_mut(32)) over the same GEMV sweep."""
@@ -428,6 +472,8 @@ def main():
     ap.add_argument("--profile-decode", action="store_true",
                     help="only run the configs[2] 1-token MoE decode layer 200 times, eagerly (for rocprofv3)")
     ap.add_argument("--eager", action="store_true", help="launch every op from the host (no recorded graphs)")
+    ap.add_argument("--no-stack", action="store_true", help="skip the configs[4] 48-layer stack")
+    ap.add_argument("--stack-only", action="store_true", help="only run the configs[4] 48-layer stack")
     args = ap.parse_args()
     global USE_GRAPHS
     USE_GRAPHS = not args.eager
@@ -449,6 +495,9 @@ def main():
         return
     if args.profile_moe:
         print(json.dumps({"moe_prefill_4k": bench_moe(hip, S, ggml, 4096, args.moe_iters)}), flush=True)
+        return
+    if args.stack_only:
+        print(json.dumps({"stack_config4": bench_stack(hip, S, ggml)}), flush=True)
         return
     shapes, ms_step, gbs, per_shape, steps = bench_gemv(hip, S, ggml, args.steps, args.warmup)
     log(f"[bench] GEMV sweep: {gbs:.1f} GB/s, {ms_step:.3f} ms/step")
@@ -475,6 +524,9 @@ def main():
         log(f"[bench] MoE decode: {extra['moe_decode_1']}")
         extra["codebook_experts"] = bench_codebook(hip, S, ggml, 100)
         log(f"[bench] configs[3] codebook experts: {extra['codebook_experts']}")
+    if not args.no_stack:
+        extra["stack_config4"] = bench_stack(hip, S, ggml)
+        log(f"[bench] configs[4] 48-layer stack: {extra['stack_config4']}")
     cpu = None if args.no_cpu else cpu_baseline(shapes)
     out = {
         "metric": "Q-GEMV achieved HBM GB/s (% peak); MoE grouped-GEMM prefill tok/s at 4K",

@@ -35,162 +35,201 @@ __device__ __forceinline__ void att_range(const int* step, int t, int win, int& 
 }
 
 // ---------------- decode ----------------
-// grid (nkv, ATT_SPLITS, nt), 256 threads. Block (g, s, t) serves the G = nh / nkv query heads of KV head g over the
-// s-th share of token t's positions, in chunks of 64: wave w scores positions 16 w .. 16 w + 15 of the chunk for all G
-// heads (4 lanes a position, each a quarter of the head dims, summed by two xor steps), waves then run the online
-// softmax of heads w, w + 4, .. over the chunk, and thread i adds p V for head i / (256 / G) and 4 or more dims from
-// the chunk's V rows staged in LDS. The block leaves [acc (hd) | max | sum] per head in part.
+// grid (ATT_SPLITS, nkv, nt), one wave a block. Wave (s, g, t) serves the G = nh / nkv query heads of KV head g over
+// the s-th share of token t's positions, in chunks of 64 positions with no block barrier:
+//   scores: lane r holds position r of the chunk, reads its K row into registers and dots it with the G query heads
+//     (in LDS, read as broadcasts); the online softmax of each head is a wave reduction;
+//   P V: the weights go through LDS, lane l owns dims l, l + 64, ... and adds p V over the chunk's V rows (one
+//     coalesced row read a position, all rows of the chunk in flight together).
+// The wave leaves [acc (hd) | max | sum] per head in part; attn_merge_kernel combines the splits.
 template <int HD, int G>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                          const uint16_t* __restrict__ vc, float* __restrict__ part,
-                                                          const int* step, int nh, int nkv, float scale, int win) {
-    // TPH threads per head in the P V step, DPT dims each (threads past the head's dims idle when HD < TPH)
-    constexpr int C = 64, QD = HD / 4, TPH = 256 / G, DPT = HD >= TPH ? HD / TPH : 1;
-    static_assert(HD % DPT == 0 && G <= 16, "head layout");
-    __shared__ float sq[G][HD];
-    __shared__ float ss[G][C];
-    __shared__ float salpha[G];
-    __shared__ __align__(16) uint16_t sv[C][HD];
-    const int g = blockIdx.x, split = blockIdx.y, t = blockIdx.z, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int h0 = g * G, ns = gridDim.y;
+__global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                         const uint16_t* __restrict__ vc, float* __restrict__ part,
+                                                         const int* step, int nh, int nkv, float scale, int win) {
+    constexpr int C = 64, DL = HD / 64, GP = (G + 3) / 4 * 4;  // positions a chunk; dims a lane in P V; padded G
+    __shared__ __align__(16) float sq[G][HD];
+    __shared__ __align__(16) float sp[C][GP];
+    const int split = blockIdx.x, g = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+    const int h0 = g * G, ns = gridDim.x;
     int base, n_pos;
     att_range(step, t, win, base, n_pos);
-    const int per_s = (((n_pos + ns - 1) / ns) + C - 1) / C * C;
+    const int per_s = max((n_pos + ns - 1) / ns, 16);  // at least 16 positions a split: few waves for short contexts
     const int p0 = split * per_s, p1 = min(n_pos, p0 + per_s);
     float* pp = part + ((uint64_t)(t * nh + h0) * ns + split) * (HD + 2);
     const uint64_t pstride = (uint64_t)ns * (HD + 2);  // between heads
     if (p0 >= n_pos) {
-        for (int i = tid; i < G * (HD + 2); i += 256) {
+        for (int i = lane; i < G * (HD + 2); i += 64) {
             const int hh = i / (HD + 2), d = i % (HD + 2);
             pp[hh * pstride + d] = d == HD ? -INFINITY : 0.0f;
         }
         return;
     }
-    for (int i = tid; i < G * HD; i += 256) sq[i / HD][i % HD] = q[(uint64_t)t * nh * HD + h0 * HD + i];
+    for (int i = lane; i < G * HD / 4; i += 64)
+        ((float4*)&sq[0][0])[i] = *(const float4*)(q + (uint64_t)t * nh * HD + h0 * HD + 4 * i);
     const uint64_t kvd = (uint64_t)nkv * HD;
-    // running max and sum of head wave + 4 j (the softmax waves)
-    float mrun[(G + 3) / 4], lrun[(G + 3) / 4];
+    float m[G], l[G], acc[G][DL];
 #pragma unroll
-    for (int j = 0; j < (G + 3) / 4; j++) { mrun[j] = -INFINITY; lrun[j] = 0.0f; }
-    const int hh = tid / TPH, d0 = (tid % TPH) * DPT;
-    const bool pv = d0 < HD;
-    float acc[DPT];
+    for (int i = 0; i < G; i++) {
+        m[i] = -INFINITY;
+        l[i] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < DPT; i++) acc[i] = 0.0f;
-    __syncthreads();
+        for (int d = 0; d < DL; d++) acc[i][d] = 0.0f;
+    }
+    __builtin_amdgcn_wave_barrier();
     for (int c0 = p0; c0 < p1; c0 += C) {
         const int nc = min(C, p1 - c0);
-        // V rows of the chunk into LDS (16 bytes a thread a round; rows past the chunk as zeros)
-        for (int i = tid; i < C * HD / 8; i += 256) {
-            const int r = i / (HD / 8), c = (i % (HD / 8)) * 8;
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (r < nc) v = *(const uint4*)(vc + (uint64_t)(base + c0 + r) * kvd + g * HD + c);
-            *(uint4*)&sv[r][c] = v;
-        }
-        // scores: position 16 wave + lane / 4, dims QD (lane % 4) ..
-        {
-            const int r = 16 * wave + (lane >> 2), qq = lane & 3;
-            float s[G];
+        // scores of position c0 + lane
+        float s[G];
 #pragma unroll
-            for (int i = 0; i < G; i++) s[i] = 0.0f;
-            if (r < nc) {
-                const uint16_t* kr = kc + (uint64_t)(base + c0 + r) * kvd + g * HD + qq * QD;
+        for (int i = 0; i < G; i++) s[i] = 0.0f;
+        if (lane < nc) {
+            const uint4* kr = (const uint4*)(kc + (uint64_t)(base + c0 + lane) * kvd + g * HD);
+            uint4 kv[HD / 8];
 #pragma unroll
-                for (int c = 0; c < QD; c += 8) {
-                    const uint4 kv = *(const uint4*)(kr + c);
-                    const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+            for (int c = 0; c < HD / 8; c++) kv[c] = kr[c];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        const float kf = h2f((uint16_t)(w4[e >> 1] >> (16 * (e & 1))));
+            for (int c = 0; c < HD / 8; c++) {
+                const uint32_t w4[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
 #pragma unroll
-                        for (int i = 0; i < G; i++) s[i] += sq[i][qq * QD + c + e] * kf;
+                for (int e4 = 0; e4 < 2; e4++) {
+                    float kf[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) kf[e] = h2f((uint16_t)(w4[(4 * e4 + e) >> 1] >> (16 * (e & 1))));
+#pragma unroll
+                    for (int i = 0; i < G; i++) {
+                        const float4 qv = *(const float4*)&sq[i][8 * c + 4 * e4];
+                        s[i] += qv.x * kf[0];
+                        s[i] += qv.y * kf[1];
+                        s[i] += qv.z * kf[2];
+                        s[i] += qv.w * kf[3];
                     }
                 }
             }
+        }
+        // online softmax per head over the chunk
+        float alpha[G];
 #pragma unroll
-            for (int i = 0; i < G; i++) {
-                float v = s[i];
-                v += __shfl_xor(v, 1, 64);
-                v += __shfl_xor(v, 2, 64);
-                if (qq == 0) ss[i][r] = r < nc ? v * scale : -INFINITY;
+        for (int i = 0; i < G; i++) {
+            const float v = lane < nc ? s[i] * scale : -INFINITY;
+            float mx = v;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+            const float mnew = fmaxf(m[i], mx);
+            const float p = v == -INFINITY ? 0.0f : expf(v - mnew);
+            float sum = p;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+            alpha[i] = m[i] == -INFINITY ? 0.0f : expf(m[i] - mnew);
+            l[i] = l[i] * alpha[i] + sum;
+            m[i] = mnew;
+            sp[lane][i] = p;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // P V: lane owns dims DL lane .. DL lane + DL - 1; every row of the chunk is loaded (rows past nc repeat the
+        // last one and weigh 0), 16 rows in flight at a time
+#pragma unroll
+        for (int i = 0; i < G; i++)
+#pragma unroll
+            for (int d = 0; d < DL; d++) acc[i][d] *= alpha[i];
+        const uint16_t* vr = vc + (uint64_t)(base + c0) * kvd + g * HD + DL * lane;
+        for (int r0 = 0; r0 < nc; r0 += 16) {
+            uint32_t vv[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint64_t off = (uint64_t)min(r0 + r, nc - 1) * kvd;
+                vv[r] = DL == 2 ? *(const uint32_t*)(vr + off) : (uint32_t)vr[off];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float pv[GP];
+#pragma unroll
+                for (int i = 0; i < GP; i += 4) {
+                    const float4 p4 = *(const float4*)&sp[min(r0 + r, C - 1)][i];
+                    pv[i] = p4.x; pv[i + 1] = p4.y; pv[i + 2] = p4.z; pv[i + 3] = p4.w;
+                }
+#pragma unroll
+                for (int d = 0; d < DL; d++) {
+                    const float vf = h2f((uint16_t)(vv[r] >> (16 * d)));
+#pragma unroll
+                    for (int i = 0; i < G; i++) acc[i][d] += pv[i] * vf;
+                }
             }
         }
-        __syncthreads();
-        // online softmax: wave w runs heads w, w + 4, ... over the chunk (lane = position)
-#pragma unroll
-        for (int j = 0; j < (G + 3) / 4; j++) {
-            const int h = wave + 4 * j;
-            if (h < G) {
-                const float s = ss[h][lane];
-                float mx = s;
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-                const float mnew = fmaxf(mrun[j], mx);
-                const float p = s == -INFINITY ? 0.0f : expf(s - mnew);
-                float sum = p;
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
-                const float alpha = mrun[j] == -INFINITY ? 0.0f : expf(mrun[j] - mnew);
-                lrun[j] = lrun[j] * alpha + sum;
-                mrun[j] = mnew;
-                ss[h][lane] = p;
-                if (lane == 0) salpha[h] = alpha;
-            }
-        }
-        __syncthreads();
-        if (pv) {
-            const float alpha = salpha[hh];
-#pragma unroll
-            for (int i = 0; i < DPT; i++) acc[i] *= alpha;
-            for (int r = 0; r < nc; r++) {
-                const float p = ss[hh][r];
-#pragma unroll
-                for (int i = 0; i < DPT; i++) acc[i] += p * h2f(sv[r][d0 + i]);
-            }
-        }
-        __syncthreads();  // ss, salpha and sv are rewritten by the next chunk
+        __builtin_amdgcn_wave_barrier();  // sp is rewritten by the next chunk
     }
-    if (pv)
 #pragma unroll
-        for (int i = 0; i < DPT; i++) pp[hh * pstride + d0 + i] = acc[i];
+    for (int i = 0; i < G; i++) {
 #pragma unroll
-    for (int j = 0; j < (G + 3) / 4; j++) {
-        const int h = wave + 4 * j;
-        if (h < G && lane == 0) {
-            pp[h * pstride + HD] = mrun[j];
-            pp[h * pstride + HD + 1] = lrun[j];
+        for (int d = 0; d < DL; d++) pp[i * pstride + DL * lane + d] = acc[i][d];
+        if (lane == 0) {
+            pp[i * pstride + HD] = m[i];
+            pp[i * pstride + HD + 1] = l[i];
         }
     }
 }
 
-// grid (nh, nt), HD threads: out = sum_s acc_s e^(m_s - M) / (sum_s l_s e^(m_s - M) + e^(sink - M)) (sigmoid gate).
+// grid (nh, nt), one wave: out = sum_s acc_s e^(m_s - M) / (sum_s l_s e^(m_s - M) + e^(sink - M)) (sigmoid gate).
+// Lanes weigh the splits (two a lane); each lane then sums the splits of its dims, 16 loads in flight at a time.
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qg,
+__global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qg,
                                                         float* __restrict__ out, int nh, int ns,
                                                         const float* __restrict__ sink) {
-    const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+    constexpr int DL = HD / 64, SL = ATT_SPLITS / 64;  // dims a lane; splits a lane
+    __shared__ float se[ATT_SPLITS];
+    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const float* pp = part + (uint64_t)(t * nh + h) * ns * (HD + 2);
     const float sk = sink ? sink[h] : -INFINITY;
-    float M = sk;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, pp[s * (HD + 2) + HD]);
-    float den = sk == -INFINITY ? 0.0f : expf(sk - M), o = 0.0f;
-    for (int s = 0; s < ns; s++) {
-        const float m = pp[s * (HD + 2) + HD];
-        if (m == -INFINITY) continue;
-        const float e = expf(m - M);
-        den += pp[s * (HD + 2) + HD + 1] * e;
-        o += pp[s * (HD + 2) + d] * e;
+    float ms[SL], M = sk;
+#pragma unroll
+    for (int j = 0; j < SL; j++) {
+        const int s = lane + 64 * j;
+        ms[j] = s < ns ? pp[s * (HD + 2) + HD] : -INFINITY;
+        M = fmaxf(M, ms[j]);
     }
-    float r = den > 0.0f ? o / den : 0.0f;
-    if (qg) r *= sigmoid_f(qg[(uint64_t)t * nh * 2 * HD + h * 2 * HD + HD + d]);
-    out[(uint64_t)t * nh * HD + h * HD + d] = r;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    float den = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SL; j++) {
+        const int s = lane + 64 * j;
+        const float e = ms[j] == -INFINITY ? 0.0f : expf(ms[j] - M);
+        if (s < ns) den += pp[s * (HD + 2) + HD + 1] * e;
+        se[s] = e;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
+    if (sk != -INFINITY) den += expf(sk - M);
+    __builtin_amdgcn_wave_barrier();
+    float o[DL];
+#pragma unroll
+    for (int d = 0; d < DL; d++) o[d] = 0.0f;
+    for (int s0 = 0; s0 < ns; s0 += 16) {
+        float a[16][DL];
+#pragma unroll
+        for (int s = 0; s < 16; s++)
+#pragma unroll
+            for (int d = 0; d < DL; d++) a[s][d] = pp[min(s0 + s, ns - 1) * (HD + 2) + DL * lane + d];
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            const float es = s0 + s < ns ? se[s0 + s] : 0.0f;
+#pragma unroll
+            for (int d = 0; d < DL; d++) o[d] += a[s][d] * es;
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < DL; d++) {
+        const int dd = DL * lane + d;
+        float r = den > 0.0f ? o[d] / den : 0.0f;
+        if (qg) r *= sigmoid_f(qg[(uint64_t)t * nh * 2 * HD + h * 2 * HD + HD + dd]);
+        out[(uint64_t)t * nh * HD + h * HD + dd] = r;
+    }
 }
 
 template <int HD, int G>
 static void decode_t(const float* q, const uint16_t* kc, const uint16_t* vc, float* part, const int* step, int nh,
                      int nkv, float scale, int nt, int win, hipStream_t s) {
-    attn_decode_kernel<HD, G><<<dim3((unsigned)nkv, ATT_SPLITS, (unsigned)nt), dim3(256), 0, s>>>(q, kc, vc, part, step, nh,
-                                                                                              nkv, scale, win);
+    attn_decode_kernel<HD, G><<<dim3(ATT_SPLITS, (unsigned)nkv, (unsigned)nt), dim3(64), 0, s>>>(q, kc, vc, part, step,
+                                                                                            nh, nkv, scale, win);
 }
 
 hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
@@ -199,10 +238,10 @@ hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t
     if (nt <= 0) return hipSuccess;
     const int G = nh / nkv;
 #define DEC(HD_, G_) if (hd == HD_ && G == G_) decode_t<HD_, G_>(q, kc, vc, part, step, nh, nkv, scale, nt, win, s); else
-    DEC(128, 1) DEC(128, 2) DEC(128, 4) DEC(128, 8) DEC(128, 16) DEC(64, 1) DEC(64, 2) DEC(64, 4) DEC(64, 8) DEC(64, 16)
+    DEC(128, 1) DEC(128, 2) DEC(128, 4) DEC(128, 8) DEC(64, 1) DEC(64, 2) DEC(64, 4) DEC(64, 8)
     return hipErrorInvalidValue;
 #undef DEC
-    if (hd == 128) attn_merge_kernel<128><<<dim3((unsigned)nh, (unsigned)nt), dim3(128), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink);
+    if (hd == 128) attn_merge_kernel<128><<<dim3((unsigned)nh, (unsigned)nt), dim3(64), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink);
     else attn_merge_kernel<64><<<dim3((unsigned)nh, (unsigned)nt), dim3(64), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink);
     return hipGetLastError();
 }

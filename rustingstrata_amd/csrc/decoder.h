@@ -38,7 +38,7 @@ hipError_t launch_gemm_f32(const float* w, int rows, int cols, const float* x, u
 hipError_t launch_fill_blocks(int ty, uint8_t* w, uint64_t n_blocks, uint64_t seed, float lo, float hi, hipStream_t s);
 
 // Attention (attn.hip). Caches: f16 rows of nkv * hd values per position.
-constexpr int ATT_SPLITS = 64;  // position splits of a decode token (part rows per head)
+constexpr int ATT_SPLITS = 128;  // position splits of a decode token (part rows per head)
 hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
                               float* part, const int* step, int nh, int nkv, int hd, float scale, int nt,
                               const float* sink, int win, hipStream_t s);

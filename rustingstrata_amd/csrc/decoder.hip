@@ -292,41 +292,46 @@ hipError_t launch_gemv_f32(const float* w, int rows, int cols, const float* x, u
     return hipGetLastError();
 }
 
-// ---- f32-weight GEMM (gemm_dense of a float matrix): 64 positions x 64 weight rows a block, K in steps of 16 ----
+// ---- f32-weight GEMM (gemm_dense of a float matrix): 32 positions x 32 weight rows a block (so a 2048-token chunk
+// times the 128 router rows fills 256 blocks), K in steps of 32 through LDS, the next step's values loaded into
+// registers while this one is summed. Each output's dot runs over k in index order with a multiply then an add, as
+// Tensor::matvec's f32 iterator sum (src/weights.rs:29-37): the CPU's bits. ----
+constexpr int GF_T = 32, GF_K = 32;
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ w, int rows, int cols,
                                                        const float* __restrict__ x, uint64_t x_stride, float* y,
                                                        uint64_t y_stride, int n, int act) {
-    __shared__ float xs[16][64 + 4], ws[16][64 + 4];
-    const int m0 = blockIdx.x * 64, r0 = blockIdx.y * 64, tid = threadIdx.x;
-    const int tm = tid >> 4, tr = tid & 15;  // this thread's outputs: positions m0 + tm + 16 i, rows r0 + tr + 16 j
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < cols; k0 += 16) {
-        // each thread loads 4 of the 1024 values of each tile: row (tid / 4) of the tile, k k0 + 4 (tid % 4) ..
-        const int lr = tid >> 2, lk = 4 * (tid & 3);
-        float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), wv = xv;
+    __shared__ float xs[GF_K][GF_T + 1], ws[GF_K][GF_T + 1];
+    const int m0 = blockIdx.x * GF_T, r0 = blockIdx.y * GF_T, tid = threadIdx.x;
+    const int tm = tid >> 4, tr = tid & 15;  // outputs: positions m0 + tm + 16 i, rows r0 + tr + 16 j (i, j < 2)
+    const int lr = tid >> 3, lk = 4 * (tid & 7);  // loads: row lr of each tile, k k0 + lk .. + 3
+    float acc[2][2] = {};
+    auto load = [&](int k0, float4& xv, float4& wv) {
+        xv = make_float4(0.f, 0.f, 0.f, 0.f);
+        wv = xv;
         if (m0 + lr < n && k0 + lk < cols) xv = *(const float4*)(x + (uint64_t)(m0 + lr) * x_stride + k0 + lk);
         if (r0 + lr < rows && k0 + lk < cols) wv = *(const float4*)(w + (uint64_t)(r0 + lr) * cols + k0 + lk);
+    };
+    float4 xv, wv;
+    load(0, xv, wv);
+    for (int k0 = 0; k0 < cols; k0 += GF_K) {
         __syncthreads();
         xs[lk][lr] = xv.x; xs[lk + 1][lr] = xv.y; xs[lk + 2][lr] = xv.z; xs[lk + 3][lr] = xv.w;
         ws[lk][lr] = wv.x; ws[lk + 1][lr] = wv.y; ws[lk + 2][lr] = wv.z; ws[lk + 3][lr] = wv.w;
         __syncthreads();
+        if (k0 + GF_K < cols) load(k0 + GF_K, xv, wv);
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) { a[i] = xs[k][tm + 16 * i]; b[i] = ws[k][tr + 16 * i]; }
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] += a[i] * b[j];
+        for (int k = 0; k < GF_K; k++) {
+            const float a0 = xs[k][tm], a1 = xs[k][tm + 16], b0 = ws[k][tr], b1 = ws[k][tr + 16];
+            acc[0][0] += a0 * b0; acc[0][1] += a0 * b1;
+            acc[1][0] += a1 * b0; acc[1][1] += a1 * b1;
         }
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 2; i++) {
         const int m = m0 + tm + 16 * i;
         if (m >= n) continue;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < 2; j++) {
             const int r = r0 + tr + 16 * j;
             if (r >= rows) continue;
             float* yo = y + (uint64_t)m * y_stride + r;
@@ -339,7 +344,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 hipError_t launch_gemm_f32(const float* w, int rows, int cols, const float* x, uint64_t x_stride, float* y,
                            uint64_t y_stride, int n, int act, hipStream_t s) {
     if (!rows || !n) return hipSuccess;
-    gemm_f32_kernel<<<dim3((unsigned)((n + 63) / 64), (unsigned)((rows + 63) / 64)), dim3(256), 0, s>>>(
+    gemm_f32_kernel<<<dim3((unsigned)((n + GF_T - 1) / GF_T), (unsigned)((rows + GF_T - 1) / GF_T)), dim3(256), 0, s>>>(
         w, rows, cols, x, x_stride, y, y_stride, n, act);
     return hipGetLastError();
 }
