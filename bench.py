@@ -143,15 +143,18 @@ def bench_gemv(hip, S, ggml, steps, warmup):
     return shapes, ms / steps, total_bytes / (ms / 1e3) / 1e9, per_shape, steps
 
 
-def bench_moe(hip, S, ggml, T, iters):
-    """E=128, top-8, H=2048, I=768; gate/up Q5_K, down Q6_K; Zipf-skewed routing; T tokens."""
+def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
+    """E=128, top-8, H=2048, I=768; gate/up Q5_K, down Q6_K (or the given types, e.g. configs[4]'s
+    Q2_K / Q3_K experts); Zipf-skewed routing; T tokens."""
     E, H, F, k = 128, 2048, 768, 8
+    ty_gu = ggml.Q5_K if ty_gu is None else ty_gu
+    ty_d = ggml.Q6_K if ty_d is None else ty_d
     rng = np.random.default_rng(11)
-    rb_gu, rb_d = ggml.row_bytes(ggml.Q5_K, H), ggml.row_bytes(ggml.Q6_K, F)
+    rb_gu, rb_d = ggml.row_bytes(ty_gu, H), ggml.row_bytes(ty_d, F)
     uniq = 8  # distinct experts quantized; the 128 repeat them
-    gate = S.quantize_rows(ggml.Q5_K, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32))
-    upw = S.quantize_rows(ggml.Q5_K, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32))
-    dn = S.quantize_rows(ggml.Q6_K, (rng.standard_normal((uniq * H, F)) * 0.02).astype(np.float32))
+    gate = S.quantize_rows(ty_gu, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32))
+    upw = S.quantize_rows(ty_gu, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32))
+    dn = S.quantize_rows(ty_d, (rng.standard_normal((uniq * H, F)) * 0.02).astype(np.float32))
     rep = E // uniq
     g_b, u_b, d_b = hip.upload(np.tile(gate, (rep, 1))), hip.upload(np.tile(upw, (rep, 1))), hip.upload(np.tile(dn, (rep, 1)))
     perm = rng.permutation(E) + 1
@@ -174,8 +177,8 @@ def bench_moe(hip, S, ggml, T, iters):
         if timed:
             hip.record(ev[1])
         # gate and up in one grouped GEMM: ge = silu(W_gate x) * (W_up x) (the bits of the two-call sequence)
-        hip.gemm_grouped_gate_up(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b))
-        hip.gemm_grouped(ggml.Q6_K, H, F, int(tiles) + max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
+        hip.gemm_grouped_gate_up(ty_gu, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b))
+        hip.gemm_grouped(ty_d, H, F, int(tiles) + max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
                          S.ACT_STORE)
         if timed:
             hip.record(ev[2])
@@ -196,7 +199,9 @@ def bench_moe(hip, S, ggml, T, iters):
     return {"tokens": T, "ms_layer": round(tot, 4), "tok_per_s": round(T / (tot / 1e3), 1),
             "grouped_gemm_ms": round(gemm, 4), "int8_TOPS": round(ops / (gemm / 1e3) / 1e12, 1),
             "mfma_frac": round(ops / (gemm / 1e3) / 1e12 / INT8_PEAK_TOPS, 4), "ops": ops,
-            "routing": "Zipf(1.1)-biased N(0,1) logits, softmax top-8"}
+            "types": f"gate/up {ggml.NAMES[ty_gu]}, down {ggml.NAMES[ty_d]}",
+            "routing": "N(0,1) logits + 8 * rank^-1.1 over a seeded expert permutation (Zipf s=1.1, scale 8), "
+                       "softmax top-8, seed 11"}
 
 
 def bench_moe_decode(hip, S, ggml, iters):
@@ -516,10 +521,27 @@ def main():
                                       "pct_peak": round(100 * by1 / us1 / 1e3 / HBM_PEAK_GBS, 1)}
     hip.drop_graphs()
     log(f"[bench] configs[0] Q4_K 4096x4096: {extra['config0_q4k_4096x4096']}")
+    # configs[4]'s expert types as decode GEMVs (the Q8_0 lm head is in the sweep)
+    ud = {}
+    for name, rows, cols in (("Q2_K", 6144, 2048), ("Q2_K", 2048, 2048), ("Q3_K", 6144, 2048), ("Q3_K", 2048, 2048),
+                             ("Q2_K", 151936, 2048), ("Q3_K", 151936, 2048)):
+        ty = ggml.BY_NAME[name]
+        bl = synth_weights(S, ggml, ty, rows, cols, seed=77 + rows + ty)
+        rr = Rotated(hip, S, ty, bl, rows, cols)
+        us = 1000 * time_gemv(hip, rr, xb, yb, 200)
+        by = bl.nbytes + 4 * cols + 4 * rows
+        ud[f"{name} {rows}x{cols}"] = {"us": round(us, 2), "GB/s": round(by / us / 1e3, 1),
+                                       "pct_peak": round(100 * by / us / 1e3 / HBM_PEAK_GBS, 1)}
+        hip.drop_graphs()
+        del rr
+    extra["gemv_config4_types"] = ud
+    log(f"[bench] configs[4] types GEMV: {ud}")
     if not args.no_moe:
         extra["moe_prefill_4k"] = bench_moe(hip, S, ggml, 4096, args.moe_iters)
         log(f"[bench] MoE prefill 4K: {extra['moe_prefill_4k']}")
         extra["moe_prefill_512"] = bench_moe(hip, S, ggml, 512, args.moe_iters)
+        extra["moe_prefill_4k_q2k_q3k"] = bench_moe(hip, S, ggml, 4096, args.moe_iters, ggml.Q2_K, ggml.Q3_K)
+        log(f"[bench] MoE prefill 4K, Q2_K/Q3_K experts: {extra['moe_prefill_4k_q2k_q3k']}")
         extra["moe_decode_1"] = bench_moe_decode(hip, S, ggml, 200)
         log(f"[bench] MoE decode: {extra['moe_decode_1']}")
         extra["codebook_experts"] = bench_codebook(hip, S, ggml, 100)
