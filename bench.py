@@ -380,51 +380,87 @@ def bench_stack(hip, S, ggml, n_prompt=4096, n_decode=128, chunk=2048, n_layer=4
             "types": "experts Q2_K gate/up + Q3_K down, attention Q6_K, embeddings and output Q8_0, router F32"}
 
 
-def cpu_baseline(shapes, budget_s=12.0):
-    """The oracle's C restatement of cpu_moe::matvec (Q8_K activations, scalar dots compiled with gcc -O3
-    -march=x86-64-v3, threads over 32-row chunks like rayon's par_chunks_mut(32)) over the same GEMV sweep."""
+def cpu_info():
+    """This host's CPU model, logical CPUs and the CPU share this process may use."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    share = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = min(share or 1, int(omp)) if omp and omp.isdigit() else (share or 1)
+    return {"model": model, "nproc": os.cpu_count(), "affinity": share, "omp_num_threads": omp, "threads": threads}
+
+
+def cpu_baseline(shapes, budget_s=10.0):
+    """The reference CPU path restated in C (oracle/): cpu_moe::matvec over the same GEMV sweep with the AVX2 dots the
+    reference dispatches to on x86-64-v3 (src/cpu_moe.rs:1364-1391), threads over 32-row chunks like rayon's
+    par_chunks_mut(32); beside it the scalar dots, one thread, and the configs[0] GEMV and configs[2] MoE layer."""
     from oracle import oracle as O
+    info = cpu_info()
+    threads = info["threads"]
     x = np.random.default_rng(7).standard_normal(2048).astype(np.float32)
-    threads = min(16, os.cpu_count() or 1)
-    t0, reps, nbytes = time.time(), 0, 0
-    while True:
-        for s in shapes:
-            O.matvec(s["ty"], s["host"], s["rows"], s["cols"], x, threads=threads)
-            nbytes += s["bytes"]
-        reps += 1
-        if time.time() - t0 >= budget_s:
-            break
-    dt = time.time() - t0
-    out = {"value": round(nbytes / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-           "sample": f"{reps} pass(es) of the full 12-GEMV sweep in {dt:.1f} s with {threads} threads "
-                     "(C restatement of cpu_moe::matvec)"}
-    # one thread (tests/cpu_moe.rs:50-66 report both): the 6144-row shapes, about 2 s
-    small = [s for s in shapes if s["rows"] == 6144]
-    t0, nbytes = time.time(), 0
-    while time.time() - t0 < 2.0:
-        for s in small:
-            O.matvec(s["ty"], s["host"], s["rows"], s["cols"], x, threads=1)
-            nbytes += s["bytes"]
-    out["one_thread_GB/s"] = round(nbytes / (time.time() - t0) / 1e9, 2)
-    # configs[2] on the CPU: cpu_moe::experts_multi over 64 tokens of the MoE layer (E=128, top-8, Q5_K gate/up,
-    # Q6_K down; 16 distinct experts repeated), about 3-6 s
-    E, H, F, k, T = 128, 2048, 768, 8, 64
-    rng = np.random.default_rng(13)
-    import rustingstrata_amd as S
-    from rustingstrata_amd import ggml
-    uniq = 16
-    gate = np.tile(S.quantize_rows(ggml.Q5_K, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32)), (E // uniq, 1))
-    up = np.tile(S.quantize_rows(ggml.Q5_K, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32)), (E // uniq, 1))
-    dn = np.tile(S.quantize_rows(ggml.Q6_K, (rng.standard_normal((uniq * H, F)) * 0.02).astype(np.float32)), (E // uniq, 1))
-    perm = rng.permutation(E) + 1
-    logits = (rng.standard_normal((T, E)) + 8.0 * perm.astype(np.float64) ** -1.1).astype(np.float32)
-    hs = rng.standard_normal((T, H)).astype(np.float32)
-    ids, wts = O.route(logits, k)
-    t0 = time.time()
-    O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, up, dn, H, F, hs, ids, wts, threads=threads)
-    dt = time.time() - t0
-    out["moe_layer"] = {"tok_per_s": round(T / dt, 1), "ms_per_token": round(1000 * dt / T, 3), "tokens": T,
-                        "cores": threads, "sample": "cpu_moe::experts_multi restated in C, 64 tokens of configs[2]"}
+
+    def sweep_rate(budget, nthreads, sel=None):
+        t0, reps, nbytes = time.time(), 0, 0
+        while True:
+            for s in (sel or shapes):
+                O.matvec(s["ty"], s["host"], s["rows"], s["cols"], x, threads=nthreads)
+                nbytes += s["bytes"]
+            reps += 1
+            if time.time() - t0 >= budget:
+                break
+        dt = time.time() - t0
+        return nbytes / dt / 1e9, reps, dt
+
+    O.set_avx2(True)
+    try:
+        gbs, reps, dt = sweep_rate(budget_s, threads)
+        out = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port", "variant": "avx2",
+               "cpu": info,
+               "sample": f"{reps} pass(es) of the full 12-GEMV sweep in {dt:.1f} s, {threads} threads, AVX2 dots "
+                         "(C restatement of cpu_moe::matvec and its x86-64-v3 kernels)"}
+        small = [s for s in shapes if s["rows"] == 6144]
+        out["one_thread_GB/s"] = round(sweep_rate(2.0, 1, small)[0], 2)
+        # configs[0]: Q4_K 4096 x 4096
+        import rustingstrata_amd as S
+        from rustingstrata_amd import ggml
+        w0 = synth_weights(S, ggml, ggml.Q4_K, 4096, 4096, seed=999)
+        x0 = np.random.default_rng(8).standard_normal(4096).astype(np.float32)
+        t0, n0 = time.time(), 0
+        while time.time() - t0 < 1.0:
+            O.matvec(ggml.Q4_K, w0, 4096, 4096, x0, threads=threads)
+            n0 += 1
+        us0 = 1e6 * (time.time() - t0) / n0
+        out["config0_q4k_4096x4096"] = {"us": round(us0, 1), "GB/s": round((w0.nbytes + 32768) / us0 / 1e3, 2),
+                                        "threads": threads}
+        # configs[2] on the CPU: cpu_moe::experts_multi over 64 tokens of the MoE layer (E=128, top-8, Q5_K gate/up,
+        # Q6_K down; 16 distinct experts repeated)
+        E, H, F, k, T = 128, 2048, 768, 8, 64
+        rng = np.random.default_rng(13)
+        uniq = 16
+        gate = np.tile(S.quantize_rows(ggml.Q5_K, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32)), (E // uniq, 1))
+        up = np.tile(S.quantize_rows(ggml.Q5_K, (rng.standard_normal((uniq * F, H)) * 0.02).astype(np.float32)), (E // uniq, 1))
+        dn = np.tile(S.quantize_rows(ggml.Q6_K, (rng.standard_normal((uniq * H, F)) * 0.02).astype(np.float32)), (E // uniq, 1))
+        perm = rng.permutation(E) + 1
+        logits = (rng.standard_normal((T, E)) + 8.0 * perm.astype(np.float64) ** -1.1).astype(np.float32)
+        hs = rng.standard_normal((T, H)).astype(np.float32)
+        ids, wts = O.route(logits, k)
+        t0 = time.time()
+        O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, up, dn, H, F, hs, ids, wts, threads=threads)
+        dt = time.time() - t0
+        out["moe_layer"] = {"tok_per_s": round(T / dt, 1), "ms_per_token": round(1000 * dt / T, 3), "tokens": T,
+                            "cores": threads, "variant": "avx2",
+                            "sample": "cpu_moe::experts_multi restated in C, 64 tokens of configs[2] (routing: N(0,1) "
+                                      "logits + 8 * rank^-1.1 over a seeded expert permutation, seed 13)"}
+    finally:
+        O.set_avx2(False)
+    # the scalar dots beside it (the reference's STRATA_SCALAR path)
+    out["scalar_GB/s"] = round(sweep_rate(3.0, threads)[0], 2)
     return out
 
 

@@ -44,6 +44,7 @@ def lib():
             "or_rms_norm": ([P, P, F, I, P], None),
             "or_f16": ([ctypes.c_uint16], F),
             "or_rope_neox": ([P, I, ctypes.c_long, F], None),
+            "or_set_avx2": ([I], None),
             "or_argmax": ([P, I], I),
             "or_attention": ([P, P, P, I, I, I, I, I, F, P, P, I, P, P], None),
         }
@@ -56,6 +57,12 @@ def lib():
 
 def _p(a):
     return a.ctypes.data
+
+
+def set_avx2(on):
+    """Select the AVX2 dots (the reference's timed x86-64-v3 path) for int_dot / matvec / experts_multi, or the
+    scalar ones (the default, the parity checker)."""
+    lib().or_set_avx2(1 if on else 0)
 
 
 def dequant(ty, blocks, n):

@@ -458,7 +458,14 @@ static float dot_iq4xs(const uint8_t* row, size_t cols, const or_q8k* xq) { /* c
     return sumf;
 }
 
+static int g_avx2 = 0;
+void or_set_avx2(int on) { g_avx2 = on; }
+
 float or_int_dot(int ty, const uint8_t* row, size_t cols, const or_q8k* xq) {
+    if (g_avx2) {
+        or_dot_fn f = or_avx2_dot(ty);
+        if (f) return f(row, cols, xq);
+    }
     switch (ty) {
     case Q8_0: return dot_q8_0(row, cols, xq);
     case Q2_K: return dot_q2k(row, cols, xq);

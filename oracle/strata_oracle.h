@@ -25,8 +25,15 @@ float or_f16(uint16_t h);
 int or_dequant_row(int ty, const uint8_t* src, size_t n, float* dst);
 /* quantize_q8k, src/cpu_moe.rs:28-46: ceil(n / 256) blocks, a short tail zero-padded. */
 void or_quantize_q8k(const float* x, size_t n, or_q8k* out);
-/* int_dot's scalar kernels, src/cpu_moe.rs:74-377 (dispatch 1364-1391, scalar branch 1390). */
+/* int_dot's scalar kernels, src/cpu_moe.rs:74-377 (dispatch 1364-1391, scalar branch 1390); with or_set_avx2(1) the
+ * AVX2 kernels of oracle/cpu_avx2.c (branch 1389) for the types that have one. */
 float or_int_dot(int ty, const uint8_t* row, size_t cols, const or_q8k* xq);
+typedef float (*or_dot_fn)(const uint8_t* row, size_t cols, const or_q8k* xq);
+/* The AVX2 dot of a type (Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_0), or null. */
+or_dot_fn or_avx2_dot(int ty);
+/* Select the dots or_int_dot (and so or_matvec and or_experts_multi) runs: 0 scalar (the default, the parity
+ * checker), 1 AVX2 where available (the reference's timed path on x86-64-v3). Process-wide. */
+void or_set_avx2(int on);
 /* cpu_moe::matvec, src/cpu_moe.rs:1405-1420: threads over chunks of 32 rows (rayon par_chunks_mut(32)).
  * threads <= 0: all available. */
 void or_matvec(int ty, const uint8_t* w, size_t rows, size_t cols, const float* x, float* y, int threads);

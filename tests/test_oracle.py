@@ -395,3 +395,25 @@ def test_attention_known_answers():
         p = np.exp(s - s.max())
         want[i] = p @ vc[2:, g * hd:(g + 1) * hd].astype(np.float64) / p.sum()
     assert np.allclose(plain.reshape(nh, hd), want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("ty", [ggml.Q2_K, ggml.Q3_K, ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.Q8_0])
+def test_avx2_dots_match_scalar(ty):
+    """The AVX2 dots (the timed CPU baseline, src/cpu_moe.rs:757-981) compute the same integer super-block sums as the
+    scalar dots and close them in 8 f32 lanes: within f32 rounding of the scalar results (1e-5 relative), and equal
+    to the f64 dot of dequant(w) with dequant(Q8_K(x))."""
+    n, rows = 2048, 64
+    w = random_blocks(ty, rows, n, seed=90 + ty)
+    x = xs(n) * 3
+    try:
+        O.set_avx2(False)
+        scalar = O.matvec(ty, w, rows, n, x, threads=1)
+        O.set_avx2(True)
+        fast = O.matvec(ty, w, rows, n, x, threads=1)
+    finally:
+        O.set_avx2(False)
+    assert np.allclose(fast, scalar, rtol=1e-5, atol=1e-6 * np.abs(scalar).max()), np.abs(fast - scalar).max()
+    d, qs, _ = O.quantize_q8k(x)
+    seen = (d[:, None] * qs.astype(np.float32)).reshape(-1).astype(np.float64)
+    wf = O.dequant(ty, w, rows * n).reshape(rows, n).astype(np.float64)
+    assert np.allclose(fast, wf @ seen, rtol=1e-5, atol=1e-5 * np.abs(wf @ seen).max())
