@@ -868,3 +868,38 @@ def test_moe_prefill_from_gguf_slots(hip, tmp_path):
     hip.moe_combine_seq(x, ye, wts, inv, k, 0, 0, H, T)
     got = down(hip, x, np.float32, T * H).reshape(T, H)
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+
+
+@pytest.mark.parametrize("t", [1, 3])
+def test_down_combine_equals_two_launches(hip, t):
+    """moe_down_combine (src/backend.rs:436-442): the same x bits as moe_gemv followed by moe_combine, with a slot not
+    resident (id -1, weight 0) and a slot of weight 0, over repeated calls; and against the oracle."""
+    E, H, F, k = 16, 2048, 768, 8
+    dn = random_blocks(ggml.Q6_K, E * H, F, seed=71)
+    rb = ggml.row_bytes(ggml.Q6_K, F)
+    db = up(hip, dn)
+    rng = np.random.default_rng(72)
+    slots = np.stack([rng.choice(E, k, replace=False) for _ in range(t)]).astype(np.int32)
+    slots[0, 3] = -1
+    wh = rng.uniform(0.05, 0.3, (t, k)).astype(np.float32)
+    wh[0, 3] = 0.0
+    wh[-1, 5] = 0.0
+    h = normal((t * k, F), seed=73)
+    x0 = normal((t, H), seed=74)
+    sb, whb, hb = up(hip, slots), up(hip, wh), up(hip, h)
+    ye1, ye2 = hip.alloc(t * k * H * 4), hip.alloc(t * k * H * 4)
+    xa, xb = up(hip, x0), up(hip, x0)
+    for rep in range(3):
+        hip.moe_down_combine(ggml.Q6_K, H, F, db, H * rb, sb, k, hb, ye1, 0, xa, whb, 0, 0, t)
+        hip.moe_gemv(ggml.Q6_K, H, F, db, H * rb, sb, t * k, hb, F, 1, ye2)
+        hip.moe_combine(xb, ye2, whb, k, 0, 0, H, t)
+        ga, gb = hip.get(xa, np.float32, t * H), hip.get(xb, np.float32, t * H)
+        assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), (rep, int((ga != gb).sum()))
+    # and against the oracle: x0 + 3 * sum_j w_j W_j h_j (three calls)
+    want = x0.astype(np.float64).copy()
+    for tt in range(t):
+        for j in range(k):
+            if slots[tt, j] >= 0 and wh[tt, j] != 0:
+                y = O.matvec(ggml.Q6_K, dn[slots[tt, j] * H:(slots[tt, j] + 1) * H], H, F, h[tt * k + j])
+                want[tt] += 3 * wh[tt, j] * y
+    assert max_rel_err(ga.reshape(t, H), want) <= TOL
