@@ -14,6 +14,7 @@
 #include <climits>
 
 #include "decoder.h"
+#include "xlane.h"
 
 namespace strata {
 
@@ -27,6 +28,27 @@ __device__ __forceinline__ float h2f(uint16_t b) {
 }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Maximum and sum over the 64 lanes of a wave, returned to every lane: DPP and swizzle steps within each half, then
+// the two halves' results through scalar lane reads (no LDS round trip per step).
+__device__ __forceinline__ float wave_max64(float v) {
+    v = fmaxf(v, xl32f<0>(v));
+    v = fmaxf(v, xl32f<1>(v));
+    v = fmaxf(v, xl32f<2>(v));
+    v = fmaxf(v, xl32f<3>(v));
+    v = fmaxf(v, xl32f<4>(v));
+    return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+}
+__device__ __forceinline__ float wave_sum64(float v) {
+    v += xl32f<0>(v);
+    v += xl32f<1>(v);
+    v += xl32f<2>(v);
+    v += xl32f<3>(v);
+    v += xl32f<4>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+           __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+}
+
 // Positions of token t: base .. end (inclusive); a sliding window keeps the last `win`.
 __device__ __forceinline__ void att_range(const int* step, int t, int win, int& base, int& n_pos) {
     const int end = step[2 * t];
@@ -35,35 +57,38 @@ __device__ __forceinline__ void att_range(const int* step, int t, int win, int& 
 }
 
 // ---------------- decode ----------------
+// Positions a split of a token with n_pos positions: at least 16, so short contexts use few waves.
+__device__ __forceinline__ int split_len(int n_pos, int ns) { return max((n_pos + ns - 1) / ns, 16); }
+
 // grid (ATT_SPLITS, nkv, nt), one wave a block. Wave (s, g, t) serves the G = nh / nkv query heads of KV head g over
 // the s-th share of token t's positions, in chunks of 64 positions with no block barrier:
-//   scores: lane r holds position r of the chunk, reads its K row into registers and dots it with the G query heads
-//     (in LDS, read as broadcasts); the online softmax of each head is a wave reduction;
-//   P V: the weights go through LDS, lane l owns dims l, l + 64, ... and adds p V over the chunk's V rows (one
-//     coalesced row read a position, all rows of the chunk in flight together).
+//   the chunk's K and V rows come into LDS by coalesced 16-byte loads, all in flight together (one memory round
+//     trip a chunk);
+//   scores: lane r holds position r of the chunk and dots its K row with the G query heads (read as broadcasts);
+//     the online softmax of each head is a wave reduction;
+//   P V: the weights go through LDS, lane l owns 2 (or 1) consecutive dims and adds p V over the chunk's rows.
+// The loops over dims and positions stay rolled (a few unrolled steps): the code stays small enough for the
+// instruction cache, which a fully unrolled body (a few thousand instructions) did not.
 // The wave leaves [acc (hd) | max | sum] per head in part; attn_merge_kernel combines the splits.
 template <int HD, int G>
 __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                          const uint16_t* __restrict__ vc, float* __restrict__ part,
                                                          const int* step, int nh, int nkv, float scale, int win) {
     constexpr int C = 64, DL = HD / 64, GP = (G + 3) / 4 * 4;  // positions a chunk; dims a lane in P V; padded G
+    constexpr int KP = HD + 8;                                  // halves per staged K row (16-byte pad: spread banks)
     __shared__ __align__(16) float sq[G][HD];
     __shared__ __align__(16) float sp[C][GP];
+    __shared__ __align__(16) uint16_t sk[C * KP];
+    __shared__ __align__(16) uint16_t sv[C * HD];
     const int split = blockIdx.x, g = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
     const int h0 = g * G, ns = gridDim.x;
     int base, n_pos;
     att_range(step, t, win, base, n_pos);
-    const int per_s = max((n_pos + ns - 1) / ns, 16);  // at least 16 positions a split: few waves for short contexts
+    const int per_s = split_len(n_pos, ns);
     const int p0 = split * per_s, p1 = min(n_pos, p0 + per_s);
     float* pp = part + ((uint64_t)(t * nh + h0) * ns + split) * (HD + 2);
     const uint64_t pstride = (uint64_t)ns * (HD + 2);  // between heads
-    if (p0 >= n_pos) {
-        for (int i = lane; i < G * (HD + 2); i += 64) {
-            const int hh = i / (HD + 2), d = i % (HD + 2);
-            pp[hh * pstride + d] = d == HD ? -INFINITY : 0.0f;
-        }
-        return;
-    }
+    if (p0 >= n_pos) return;  // past the token's positions: the merge reads only the splits that have some
     for (int i = lane; i < G * HD / 4; i += 64)
         ((float4*)&sq[0][0])[i] = *(const float4*)(q + (uint64_t)t * nh * HD + h0 * HD + 4 * i);
     const uint64_t kvd = (uint64_t)nkv * HD;
@@ -75,35 +100,50 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
 #pragma unroll
         for (int d = 0; d < DL; d++) acc[i][d] = 0.0f;
     }
-    __builtin_amdgcn_wave_barrier();
     for (int c0 = p0; c0 < p1; c0 += C) {
         const int nc = min(C, p1 - c0);
-        // scores of position c0 + lane
+        // the chunk's K and V rows into LDS with coalesced 16-byte loads, all in flight together (rows past nc repeat
+        // row nc - 1; their weights are 0)
+        {
+            constexpr int PER = C * HD / 8 / 64;  // 16-byte pieces a lane of each of K and V
+            uint4 kb[PER], vb[PER];
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int i = lane + 64 * j, r = i / (HD / 8), c = (i % (HD / 8)) * 8;
+                const uint64_t off = (uint64_t)(base + c0 + min(r, nc - 1)) * kvd + g * HD + c;
+                kb[j] = *(const uint4*)(kc + off);
+                vb[j] = *(const uint4*)(vc + off);
+            }
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                const int i = lane + 64 * j, r = i / (HD / 8), c = (i % (HD / 8)) * 8;
+                *(uint4*)&sk[r * KP + c] = kb[j];
+                *(uint4*)&sv[r * HD + c] = vb[j];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        // scores of position c0 + lane: its K row from LDS, the G query heads as broadcasts
         float s[G];
 #pragma unroll
         for (int i = 0; i < G; i++) s[i] = 0.0f;
-        if (lane < nc) {
-            const uint4* kr = (const uint4*)(kc + (uint64_t)(base + c0 + lane) * kvd + g * HD);
-            uint4 kv[HD / 8];
+#pragma unroll 2
+        for (int c = 0; c < HD / 8; c++) {
+            const uint4 kv = *(const uint4*)&sk[lane * KP + 8 * c];
+            const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+            float kf[8];
 #pragma unroll
-            for (int c = 0; c < HD / 8; c++) kv[c] = kr[c];
+            for (int e = 0; e < 8; e++) kf[e] = h2f((uint16_t)(w4[e >> 1] >> (16 * (e & 1))));
 #pragma unroll
-            for (int c = 0; c < HD / 8; c++) {
-                const uint32_t w4[4] = {kv[c].x, kv[c].y, kv[c].z, kv[c].w};
-#pragma unroll
-                for (int e4 = 0; e4 < 2; e4++) {
-                    float kf[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) kf[e] = h2f((uint16_t)(w4[(4 * e4 + e) >> 1] >> (16 * (e & 1))));
-#pragma unroll
-                    for (int i = 0; i < G; i++) {
-                        const float4 qv = *(const float4*)&sq[i][8 * c + 4 * e4];
-                        s[i] += qv.x * kf[0];
-                        s[i] += qv.y * kf[1];
-                        s[i] += qv.z * kf[2];
-                        s[i] += qv.w * kf[3];
-                    }
-                }
+            for (int i = 0; i < G; i++) {
+                const float4 qa = *(const float4*)&sq[i][8 * c], qb = *(const float4*)&sq[i][8 * c + 4];
+                s[i] += qa.x * kf[0];
+                s[i] += qa.y * kf[1];
+                s[i] += qa.z * kf[2];
+                s[i] += qa.w * kf[3];
+                s[i] += qb.x * kf[4];
+                s[i] += qb.y * kf[5];
+                s[i] += qb.z * kf[6];
+                s[i] += qb.w * kf[7];
             }
         }
         // online softmax per head over the chunk
@@ -111,51 +151,37 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
 #pragma unroll
         for (int i = 0; i < G; i++) {
             const float v = lane < nc ? s[i] * scale : -INFINITY;
-            float mx = v;
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-            const float mnew = fmaxf(m[i], mx);
+            const float mnew = fmaxf(m[i], wave_max64(v));
             const float p = v == -INFINITY ? 0.0f : expf(v - mnew);
-            float sum = p;
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+            const float sum = wave_sum64(p);
             alpha[i] = m[i] == -INFINITY ? 0.0f : expf(m[i] - mnew);
             l[i] = l[i] * alpha[i] + sum;
             m[i] = mnew;
             sp[lane][i] = p;
         }
         __builtin_amdgcn_wave_barrier();
-        // P V: lane owns dims DL lane .. DL lane + DL - 1; every row of the chunk is loaded (rows past nc repeat the
-        // last one and weigh 0), 16 rows in flight at a time
+        // P V: lane owns dims DL lane .. DL lane + DL - 1
 #pragma unroll
         for (int i = 0; i < G; i++)
 #pragma unroll
             for (int d = 0; d < DL; d++) acc[i][d] *= alpha[i];
-        const uint16_t* vr = vc + (uint64_t)(base + c0) * kvd + g * HD + DL * lane;
-        for (int r0 = 0; r0 < nc; r0 += 16) {
-            uint32_t vv[16];
+#pragma unroll 4
+        for (int r = 0; r < nc; r++) {
+            float pv[GP];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint64_t off = (uint64_t)min(r0 + r, nc - 1) * kvd;
-                vv[r] = DL == 2 ? *(const uint32_t*)(vr + off) : (uint32_t)vr[off];
+            for (int i = 0; i < GP; i += 4) {
+                const float4 p4 = *(const float4*)&sp[r][i];
+                pv[i] = p4.x; pv[i + 1] = p4.y; pv[i + 2] = p4.z; pv[i + 3] = p4.w;
             }
+            const uint32_t vw = DL == 2 ? *(const uint32_t*)&sv[r * HD + 2 * lane] : (uint32_t)sv[r * HD + lane];
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float pv[GP];
+            for (int d = 0; d < DL; d++) {
+                const float vf = h2f((uint16_t)(vw >> (16 * d)));
 #pragma unroll
-                for (int i = 0; i < GP; i += 4) {
-                    const float4 p4 = *(const float4*)&sp[min(r0 + r, C - 1)][i];
-                    pv[i] = p4.x; pv[i + 1] = p4.y; pv[i + 2] = p4.z; pv[i + 3] = p4.w;
-                }
-#pragma unroll
-                for (int d = 0; d < DL; d++) {
-                    const float vf = h2f((uint16_t)(vv[r] >> (16 * d)));
-#pragma unroll
-                    for (int i = 0; i < G; i++) acc[i][d] += pv[i] * vf;
-                }
+                for (int i = 0; i < G; i++) acc[i][d] += pv[i] * vf;
             }
         }
-        __builtin_amdgcn_wave_barrier();  // sp is rewritten by the next chunk
+        __builtin_amdgcn_wave_barrier();  // sp, sk and sv are rewritten by the next chunk
     }
 #pragma unroll
     for (int i = 0; i < G; i++) {
@@ -168,58 +194,61 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
     }
 }
 
-// grid (nh, nt), one wave: out = sum_s acc_s e^(m_s - M) / (sum_s l_s e^(m_s - M) + e^(sink - M)) (sigmoid gate).
-// Lanes weigh the splits (two a lane); each lane then sums the splits of its dims, 16 loads in flight at a time.
+// grid (nh, nt), 4 waves: out = sum_s acc_s e^(m_s - M) / (sum_s l_s e^(m_s - M) + e^(sink - M)) (sigmoid gate).
+// Wave w takes splits w, w + 4, ..: their weights (a lane each), then the weighted sum of their partial rows (lane =
+// dims), all of its loads in flight together; the 4 wave sums are added in wave order through LDS.
 template <int HD>
-__global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qg,
-                                                        float* __restrict__ out, int nh, int ns,
-                                                        const float* __restrict__ sink) {
-    constexpr int DL = HD / 64, SL = ATT_SPLITS / 64;  // dims a lane; splits a lane
-    __shared__ float se[ATT_SPLITS];
-    const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qg,
+                                                         float* __restrict__ out, int nh, int ns,
+                                                         const float* __restrict__ sink, const int* step, int win) {
+    constexpr int DL = HD / 64, SW = ATT_SPLITS / 4;  // dims a lane; splits a wave
+    __shared__ float sm[4], sd[4], so[4][HD];
+    const int h = blockIdx.x, t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const float* pp = part + (uint64_t)(t * nh + h) * ns * (HD + 2);
+    {
+        // the splits that hold positions (the decode leaves the others unwritten)
+        int base, n_pos;
+        att_range(step, t, win, base, n_pos);
+        const int per_s = split_len(n_pos, ns);
+        ns = min(ns, (n_pos + per_s - 1) / per_s);
+    }
     const float sk = sink ? sink[h] : -INFINITY;
-    float ms[SL], M = sk;
+    // this wave's splits: s = wave + 4 i, i < SW (lane i < SW holds split i's max and sum)
+    const int sl = wave + 4 * lane;
+    const float ms = lane < SW && sl < ns ? pp[sl * (HD + 2) + HD] : -INFINITY;
+    const float ls = lane < SW && sl < ns ? pp[sl * (HD + 2) + HD + 1] : 0.0f;
+    float a[SW][DL];
 #pragma unroll
-    for (int j = 0; j < SL; j++) {
-        const int s = lane + 64 * j;
-        ms[j] = s < ns ? pp[s * (HD + 2) + HD] : -INFINITY;
-        M = fmaxf(M, ms[j]);
-    }
+    for (int i = 0; i < SW; i++)
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    float den = 0.0f;
-#pragma unroll
-    for (int j = 0; j < SL; j++) {
-        const int s = lane + 64 * j;
-        const float e = ms[j] == -INFINITY ? 0.0f : expf(ms[j] - M);
-        if (s < ns) den += pp[s * (HD + 2) + HD + 1] * e;
-        se[s] = e;
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
-    if (sk != -INFINITY) den += expf(sk - M);
-    __builtin_amdgcn_wave_barrier();
+        for (int d = 0; d < DL; d++) a[i][d] = pp[min(wave + 4 * i, ns - 1) * (HD + 2) + DL * lane + d];
+    float M = wave_max64(ms);
+    if (lane == 0) sm[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])), sk);
+    const float e = ms == -INFINITY ? 0.0f : expf(ms - M);
+    const float den = wave_sum64(ls * e);
     float o[DL];
 #pragma unroll
     for (int d = 0; d < DL; d++) o[d] = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += 16) {
-        float a[16][DL];
 #pragma unroll
-        for (int s = 0; s < 16; s++)
+    for (int i = 0; i < SW; i++) {
+        const float es = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), i));
 #pragma unroll
-            for (int d = 0; d < DL; d++) a[s][d] = pp[min(s0 + s, ns - 1) * (HD + 2) + DL * lane + d];
-#pragma unroll
-        for (int s = 0; s < 16; s++) {
-            const float es = s0 + s < ns ? se[s0 + s] : 0.0f;
-#pragma unroll
-            for (int d = 0; d < DL; d++) o[d] += a[s][d] * es;
-        }
+        for (int d = 0; d < DL; d++) o[d] += a[i][d] * es;
     }
+    if (lane == 0) sd[wave] = den;
+#pragma unroll
+    for (int d = 0; d < DL; d++) so[wave][DL * lane + d] = o[d];
+    __syncthreads();
+    if (wave) return;
+    float dt = sd[0] + sd[1] + sd[2] + sd[3];
+    if (sk != -INFINITY) dt += expf(sk - M);
 #pragma unroll
     for (int d = 0; d < DL; d++) {
         const int dd = DL * lane + d;
-        float r = den > 0.0f ? o[d] / den : 0.0f;
+        const float ov = so[0][dd] + so[1][dd] + so[2][dd] + so[3][dd];
+        float r = dt > 0.0f ? ov / dt : 0.0f;
         if (qg) r *= sigmoid_f(qg[(uint64_t)t * nh * 2 * HD + h * 2 * HD + HD + dd]);
         out[(uint64_t)t * nh * HD + h * HD + dd] = r;
     }
@@ -241,8 +270,8 @@ hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t
     DEC(128, 1) DEC(128, 2) DEC(128, 4) DEC(128, 8) DEC(64, 1) DEC(64, 2) DEC(64, 4) DEC(64, 8)
     return hipErrorInvalidValue;
 #undef DEC
-    if (hd == 128) attn_merge_kernel<128><<<dim3((unsigned)nh, (unsigned)nt), dim3(64), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink);
-    else attn_merge_kernel<64><<<dim3((unsigned)nh, (unsigned)nt), dim3(64), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink);
+    if (hd == 128) attn_merge_kernel<128><<<dim3((unsigned)nh, (unsigned)nt), dim3(256), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink, step, win);
+    else attn_merge_kernel<64><<<dim3((unsigned)nh, (unsigned)nt), dim3(256), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink, step, win);
     return hipGetLastError();
 }
 

@@ -30,7 +30,7 @@ __device__ __forceinline__ float wave_sum_xor(float v) {
 constexpr int NR_WAVES = 4;
 
 __global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
-    __shared__ float sh[NR_WAVES][512];
+    __shared__ __align__(16) float sh[NR_WAVES][512];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     int b = (int)blockIdx.x * NR_WAVES + wave - a.qrows;
     if (b >= a.rows) return;
@@ -53,7 +53,11 @@ __global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
     __builtin_amdgcn_wave_barrier();
     float ss = 0.0f;
     if (lane == 0)
-        for (int i = 0; i < n; i++) ss += s[i] * s[i];
+        for (int i = 0; i < n; i += 8) {  // 8 values a read pair, added one by one in index order
+            const float4 p = *(const float4*)&s[i], q = *(const float4*)&s[i + 4];
+            ss += p.x * p.x; ss += p.y * p.y; ss += p.z * p.z; ss += p.w * p.w;
+            ss += q.x * q.x; ss += q.y * q.y; ss += q.z * q.z; ss += q.w * q.w;
+        }
     ss = __shfl(ss, 0, 64);
     const float sc = 1.0f / sqrtf(ss / (float)n + a.eps);
     for (int i = lane; i < n; i += 64) s[i] = s[i] * sc * w[i];

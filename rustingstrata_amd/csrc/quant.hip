@@ -135,14 +135,66 @@ __global__ __launch_bounds__(256) void quant_xq_kernel(const float* __restrict__
 // rms_norm_q (Backend::rms_norm_q, src/backend.rs:232-235; ops::rms_norm src/ops.rs:3-7): per row, x += res first
 // (when res is not null, in place), then out = x * (1 / sqrt(mean(x^2) + eps)) * w, and (when xq is not null) out
 // quantized as quant_xq does into xq ([rows x n int8][rows x n / 32 f32]). One block of 256 threads per row; the sum
-// of squares is a fixed tree (per-thread strided sums, DPP within 32 lanes, then the 8 half-waves in order).
+// of squares is a fixed tree (per-thread sums, DPP within 32 lanes, then the 8 half-waves in order). Rows of up to 2048
+// values (a multiple of 8, 16-byte aligned rows) take one memory round trip: each thread keeps its 8 consecutive
+// values in registers from the loads to the quantization.
 __global__ __launch_bounds__(256) void rms_norm_q_kernel(float* x, uint64_t x_stride, const float* __restrict__ w,
                                                          float* out, uint64_t out_stride, int n, float eps,
-                                                         int8_t* xq, const float* __restrict__ res, int rows, int mode) {
+                                                         int8_t* xq, const float* __restrict__ res, int rows, int mode,
+                                                         int vec) {
     __shared__ float part[8];
     const int r = blockIdx.x, tid = threadIdx.x;
     float* xr = x + (uint64_t)r * x_stride;
     float* o = out + (uint64_t)r * out_stride;
+    if (vec && n <= 2048 && n % 8 == 0) {
+        // one memory round trip: thread tid holds values 8 tid .. 8 tid + 7 (with res and w loaded beside them) from
+        // the sum of squares to the quantization
+        const int i = 8 * tid;
+        const bool live = i < n;
+        float v[8], wv[8];
+        if (live) {
+            const float4 a = *(const float4*)(xr + i), b = *(const float4*)(xr + i + 4);
+            const float4 c = *(const float4*)(w + i), d = *(const float4*)(w + i + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+            wv[0] = c.x; wv[1] = c.y; wv[2] = c.z; wv[3] = c.w; wv[4] = d.x; wv[5] = d.y; wv[6] = d.z; wv[7] = d.w;
+            if (res) {
+                const float* rr = res + (uint64_t)r * x_stride;
+                const float4 e = *(const float4*)(rr + i), f = *(const float4*)(rr + i + 4);
+                const float ev[8] = {e.x, e.y, e.z, e.w, f.x, f.y, f.z, f.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = v[j] + ev[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = wv[j] = 0.0f;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) s += v[j] * v[j];
+        s += xl32f<0>(s);
+        s += xl32f<1>(s);
+        s += xl32f<2>(s);
+        s += xl32f<3>(s);
+        s += xl32f<4>(s);
+        if ((tid & 31) == 0) part[tid >> 5] = s;
+        if (res && live) {
+            *(float4*)(xr + i) = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4*)(xr + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 8; h++) tot += part[h];
+        const float sc = 1.0f / sqrtf(tot / (float)n + eps);
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = live ? v[j] * sc * wv[j] : 0.0f;
+        if (live) {
+            *(float4*)(o + i) = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4*)(o + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        if (xq) quant8_group(v, i, live, mode, xq + (uint64_t)r * n, (float*)(xq + (uint64_t)rows * n) + (uint64_t)r * (n / 32));
+        return;
+    }
     float s = 0.0f;
     if (res) {
         const float* rr = res + (uint64_t)r * x_stride;
@@ -182,7 +234,10 @@ __global__ __launch_bounds__(256) void rms_norm_q_kernel(float* x, uint64_t x_st
 hipError_t launch_rms_norm_q(float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride, int n, int rows,
                              float eps, int8_t* xq, const float* res, int mode, hipStream_t s) {
     if (!n || !rows) return hipSuccess;
-    rms_norm_q_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, x_stride, w, out, out_stride, n, eps, xq, res, rows, mode);
+    const int vec = ((uintptr_t)x | (uintptr_t)w | (uintptr_t)out | (uintptr_t)res) % 16 == 0 && x_stride % 4 == 0 &&
+                    out_stride % 4 == 0;
+    rms_norm_q_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, x_stride, w, out, out_stride, n, eps, xq, res, rows, mode,
+                                                                 vec);
     return hipGetLastError();
 }
 
