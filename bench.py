@@ -143,6 +143,48 @@ def bench_gemv(hip, S, ggml, steps, warmup):
     return shapes, ms / steps, total_bytes / (ms / 1e3) / 1e9, per_shape, steps
 
 
+def bench_floor(hip, shapes, per_shape, iters=400):
+    """The launch and read floors the small GEMVs are measured against: an empty kernel, and a plain streaming read
+    of each small sweep shape's weight bytes (e.g. 2048x2048 Q4_K = 2.36 MB, 6144x2048 Q5_K = 8.65 MB), each replayed
+    from a recorded graph and read from copies rotated past the Infinity Cache like the GEMV sweep's; the GEMV's time
+    over the read's is `gemv_over_read`."""
+    out = {}
+    sink = hip.alloc(256)
+    empty = hip.alloc(16)
+    e0, e1 = hip.event(), hip.event()
+    hip.graph("floor_empty", lambda: [hip.read_kernel(empty, 0, sink) for _ in range(100)])
+    hip.graph("floor_empty", None)
+    hip.sync()
+    hip.record(e0)
+    for _ in range(iters // 100):
+        hip.graph("floor_empty", None)
+    hip.record(e1)
+    out["empty_kernel_us"] = round(1000 * hip.elapsed_ms(e0, e1) / (100 * (iters // 100)), 3)
+    for s in shapes:
+        if s["rows"] > 8192:
+            continue
+        key = f'{s["name"]} {s["rows"]}x{s["cols"]}'
+        nbytes = int(s["host"].nbytes)
+        stride = (nbytes + 255) & ~255
+        n = max(2, -(-ROTATE_BYTES // nbytes) + 1)
+        pool = hip.alloc(n * stride)
+        hip.graph(("floor", nbytes), lambda: [hip.read_kernel(int(pool) + i * stride, nbytes, sink) for i in range(n)])
+        hip.graph(("floor", nbytes), None)
+        hip.sync()
+        reps = max(1, -(-iters // n))
+        hip.record(e0)
+        for _ in range(reps):
+            hip.graph(("floor", nbytes), None)
+        hip.record(e1)
+        us = 1000 * hip.elapsed_ms(e0, e1) / (reps * n)
+        out[f"read {key} bytes"] = {"bytes": nbytes, "us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1),
+                                    "gemv_over_read": round(per_shape[key]["us"] / us, 2)}
+        hip.drop_graphs()
+        del pool
+    hip.drop_graphs()
+    return out
+
+
 def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
     """E=128, top-8, H=2048, I=768; gate/up Q5_K, down Q6_K (or the given types, e.g. configs[4]'s
     Q2_K / Q3_K experts); Zipf-skewed routing; T tokens."""
@@ -514,6 +556,7 @@ def main():
                     help="only run the configs[2] 1-token MoE decode layer 200 times, eagerly (for rocprofv3)")
     ap.add_argument("--eager", action="store_true", help="launch every op from the host (no recorded graphs)")
     ap.add_argument("--no-stack", action="store_true", help="skip the configs[4] 48-layer stack")
+    ap.add_argument("--floor-only", action="store_true", help="only the GEMV sweep and its launch / read floors")
     ap.add_argument("--stack-only", action="store_true", help="only run the configs[4] 48-layer stack")
     args = ap.parse_args()
     global USE_GRAPHS
@@ -542,6 +585,9 @@ def main():
         return
     shapes, ms_step, gbs, per_shape, steps = bench_gemv(hip, S, ggml, args.steps, args.warmup)
     log(f"[bench] GEMV sweep: {gbs:.1f} GB/s, {ms_step:.3f} ms/step")
+    if args.floor_only:
+        print(json.dumps({"per_shape": per_shape, "floor": bench_floor(hip, shapes, per_shape)}), flush=True)
+        return
     xb = hip.upload(np.random.default_rng(7).standard_normal(2048).astype(np.float32))
     yb = hip.alloc(151936 * 4)
     roof = roofline_q4k_lmhead(hip, shapes, xb, yb)
@@ -572,6 +618,8 @@ def main():
         del rr
     extra["gemv_config4_types"] = ud
     log(f"[bench] configs[4] types GEMV: {ud}")
+    extra["floor"] = bench_floor(hip, shapes, per_shape)
+    log(f"[bench] launch / read floors: {extra['floor']}")
     if not args.no_moe:
         extra["moe_prefill_4k"] = bench_moe(hip, S, ggml, 4096, args.moe_iters)
         log(f"[bench] MoE prefill 4K: {extra['moe_prefill_4k']}")

@@ -314,6 +314,9 @@ int strata_event_destroy(void* ev);
 /* A plain streaming copy kernel (16-byte loads and stores) of `bytes` (a multiple of 16) from src to dst: the known-size
  * reference against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are scaled. */
 int strata_copy_kernel(strata_ctx* ctx, uint64_t src, uint64_t dst, uint64_t bytes);
+/* A plain streaming read of `bytes` (a multiple of 16) from src, 16-byte loads (sink: 256 bytes the kernel may write,
+ * so the loads are not dropped); bytes = 0 is an empty launch. The floor a GEMV of the same bytes is compared with. */
+int strata_read_kernel(strata_ctx* ctx, uint64_t src, uint64_t bytes, uint64_t sink);
 
 #ifdef __cplusplus
 }

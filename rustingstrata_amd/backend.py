@@ -89,6 +89,7 @@ SIGNATURES = {
     "strata_event_elapsed": [P, P, ctypes.POINTER(F32)],
     "strata_event_destroy": [P],
     "strata_copy_kernel": [CTX, U64, U64, U64],
+    "strata_read_kernel": [CTX, U64, U64, U64],
     "strata_kv_words": [U64],
     "strata_argmax_rows": [CTX, U64, U64, U64, U64],
     "strata_rope_pairs": [CTX, U64, U64, U64, U64, U64, U64, F32, U64, U64],
@@ -450,6 +451,9 @@ class HipBackend:
 
     def copy_kernel(self, src, dst, nbytes):
         _check(lib().strata_copy_kernel(self._ctx, int(src), int(dst), nbytes))
+
+    def read_kernel(self, src, nbytes, sink):
+        _check(lib().strata_read_kernel(self._ctx, int(src), nbytes, int(sink)))
 
     @staticmethod
     def elapsed_ms(e0, e1):

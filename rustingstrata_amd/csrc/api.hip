@@ -919,6 +919,14 @@ int strata_copy_kernel(strata_ctx* c, uint64_t src, uint64_t dst, uint64_t bytes
     return 0;
 }
 
+int strata_read_kernel(strata_ctx* c, uint64_t src, uint64_t bytes, uint64_t sink) {
+    if (check_ctx(c)) return -1;
+    if (bytes % 16) return set_error("read_kernel: bytes must be a multiple of 16");
+    if (!sink) return set_error("read_kernel: null sink (256 bytes)");
+    STRATA_HIP(launch_read((const void*)src, bytes, (uint32_t*)sink, c->stream));
+    return 0;
+}
+
 int strata_event_destroy(void* ev) {
     STRATA_HIP(hipEventDestroy((hipEvent_t)ev));
     return 0;

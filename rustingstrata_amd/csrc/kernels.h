@@ -39,6 +39,8 @@ struct GemvLaunch {
 hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s);
 // Streaming copy of `bytes` (multiple of 16), the reference kernel for HBM byte counters.
 hipError_t launch_copy(const void* src, void* dst, uint64_t bytes, hipStream_t s);
+// Streaming read of `bytes` (multiple of 16; 0: an empty launch), the floor a GEMV of the same bytes is measured against.
+hipError_t launch_read(const void* src, uint64_t bytes, uint32_t* sink, hipStream_t s);
 // Largest row size (bytes) launch_gemv accepts.
 uint64_t gemv_max_row_bytes();
 
