@@ -39,6 +39,8 @@ struct GemvArgs {
     const float* xf;     // single-input kernel: x as f32 (quantized in-lane) when xq is null
     const float* xu;     // with xf: x = silu(xf) * xu, rows x_stride floats apart (swiglu_q fused), or null
     uint64_t x_stride;   // floats between the f32 x rows
+    int quarter;         // single-input kernel: every tile fits one pass of a wave (at most 64 / G rows), and the four
+                         // waves each take one quarter of every super-block (sb_quarter / sb_close)
 };
 
 // LDS layout: [IqTables (IQ types)][x int8: nt * cols][x scales: nt * cols / 32 f32][x sums: nt * cols / 16
@@ -418,8 +420,12 @@ __device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const flo
 
 // SW: x rows are silu(xf) * xu (the fused SwiGLU input of the down projection); a separate instantiation, so the
 // plain GEMV carries none of it.
-template <int T, bool Q32, bool SW>
+// MODE: bit 0 SW (x rows are silu(xf) * xu), bit 1 the quarter split (GemvArgs::quarter), bit 2 one plain matrix
+// (no expert ids, no pair: tile t is row tile t and every tile is valid, with none of the general indexing's
+// divisions, tens of instructions each).
+template <int T, bool Q32, int MODE>
 __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
+    constexpr bool SW = MODE & 1, QU = MODE & 2, plain = MODE & 4;
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -428,16 +434,20 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     // LDS: [IqTables][x int8 (whole super-blocks, padded: xpad)][x scales][x per-16 sums][tile]
     const uint32_t ncp = (cols + 255) & ~255;
     const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + xpad_bytes(ncp), o_ss = o_xd + ncp / 8,
-                   o_tile = o_ss + ncp / 4;
+                   o_tile = o_ss + ncp / 4, o_part = o_tile + GEMV1_TILE + 16;
     int* xss = (int*)(smem + o_ss);
     IqTables* tab = (IqTables*)smem;
     if constexpr (IQ) load_iq_tables(tab);
     int8_t* xl = (int8_t*)(smem + o_x);
     float* xld = (float*)(smem + o_xd);
     uint8_t* tile = smem + o_tile;
+    uint32_t* qpart = (uint32_t*)(smem + o_part);  // quarter split: waves 1-3's outputs, 2 words a lane
 
     const int total = a.ntr * a.nslots * a.nz;
+    // one plain matrix (no slots, no pair, no expert ids): tile t is row tile t, and every tile is valid; the
+    // divisions below (tens of instructions each) stay off that path
     auto valid = [&](int t) {
+        if constexpr (plain) return true;
         const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
         if (rt * a.R >= (z ? a.rows2 : a.rows)) return false;
         return !a.ids || sload(a.ids + slot) >= 0;  // a slot not routed here leaves its output untouched
@@ -449,19 +459,27 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     struct Span { float* Y; int r0, nr, xrow; uint64_t beg, g0; int nch; };
     auto span = [&](int t) {
         Span sp;
-        const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
-        const int rows = z ? a.rows2 : a.rows;
-        sp.r0 = rt * a.R;
-        sp.nr = min(a.R, rows - sp.r0);
-        const uint8_t* W = a.w + (z ? a.w2 : 0);
-        sp.Y = (float*)((uint8_t*)a.y + (z ? a.y2 : 0));
-        sp.xrow = 0;
-        if (a.ids) {
-            W += (int64_t)sload(a.ids + slot) * a.stride;
-            sp.xrow = slot / a.xg;
-            sp.Y += (int64_t)slot * rows;
+        if constexpr (plain) {
+            sp.r0 = t * a.R;
+            sp.nr = min(a.R, a.rows - sp.r0);
+            sp.Y = a.y;
+            sp.xrow = 0;
+            sp.beg = (uint64_t)(a.w + (uint64_t)sp.r0 * a.rb);
+        } else {
+            const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
+            const int rows = z ? a.rows2 : a.rows;
+            sp.r0 = rt * a.R;
+            sp.nr = min(a.R, rows - sp.r0);
+            const uint8_t* W = a.w + (z ? a.w2 : 0);
+            sp.Y = (float*)((uint8_t*)a.y + (z ? a.y2 : 0));
+            sp.xrow = 0;
+            if (a.ids) {
+                W += (int64_t)sload(a.ids + slot) * a.stride;
+                sp.xrow = slot / a.xg;
+                sp.Y += (int64_t)slot * rows;
+            }
+            sp.beg = (uint64_t)(W + (uint64_t)sp.r0 * a.rb);
         }
-        sp.beg = (uint64_t)(W + (uint64_t)sp.r0 * a.rb);
         sp.g0 = sp.beg & ~(uint64_t)15;
         sp.nch = (int)((((sp.beg + (uint64_t)sp.nr * a.rb) + 15) & ~(uint64_t)15) - sp.g0) >> 4;
         return sp;
@@ -500,11 +518,12 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
             else stage_x<Q32, SW>(a, sp.xrow, xl, xld, xss);
             __syncthreads();
             // every lane has its slice before the copy can change again: the next staging follows the loop's barrier
-            if (has_sb) load_x_slice(gl, xl, xld, xss, x);
+            if (has_sb && !QU) load_x_slice(gl, xl, xld, xss, x);
             cur_xrow = sp.xrow;
         }
 #pragma unroll
-        for (int i = 0; i < GEMV1_CH; i++) *(v4u*)(tile + 16 * (tid + GEMV1_THREADS * i)) = wv[i];
+        for (int i = 0; i < GEMV1_CH; i++)
+            *(v4u*)(tile + 16 * (tid + GEMV1_THREADS * i)) = wv[i];
         __syncthreads();
         const Span cs = sp;
         const bool more = tn < total;
@@ -516,6 +535,41 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
             if (tn < total) spn = span(tn);
         }
         const int nv = min(256, cols - 256 * gl);
+        if constexpr (QU) {
+            // row lane / G of the tile, super-block gl, quarter `wave`; wave 0 closes the four quarters
+            const int rr = lane / G;
+            const bool live = rr < cs.nr && has_sb;
+            uint32_t o0 = 0, o1 = 0;
+            float D = 0.0f, M = 0.0f;
+            if (live) {
+                const uint8_t* b = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb + gl * SBB;
+                const XLds xv{xl + xpad(256 * gl), xld + 8 * gl, xss + 16 * gl};
+                switch (wave) {
+                case 0: sb_quarter<T, Q32, 0>(b, xv, tab, nv, o0, o1, D, M); break;
+                case 1: sb_quarter<T, Q32, 1>(b, xv, tab, nv, o0, o1, D, M); break;
+                case 2: sb_quarter<T, Q32, 2>(b, xv, tab, nv, o0, o1, D, M); break;
+                default: sb_quarter<T, Q32, 3>(b, xv, tab, nv, o0, o1, D, M); break;
+                }
+            }
+            if (wave) *(uint2*)(qpart + 128 * (wave - 1) + 2 * lane) = make_uint2(o0, o1);
+            __syncthreads();
+            if (wave == 0) {
+                uint32_t o[8];
+                o[0] = o0;
+                o[1] = o1;
+#pragma unroll
+                for (int w = 1; w < 4; w++) {
+                    const uint2 v = *(const uint2*)(qpart + 128 * (w - 1) + 2 * lane);
+                    o[2 * w] = v.x;
+                    o[2 * w + 1] = v.y;
+                }
+                float acc = live ? sb_close<T, Q32>(o, D, M, xld[8 * gl], nv) : 0.0f;
+                acc = ordered_sum(acc, G);
+                if (rr < cs.nr && gl == G - 1) cs.Y[cs.r0 + rr] = acc;
+            }
+            if (!more) break;
+            continue;
+        }
         for (int base = wave * RPW; base < cs.nr; base += GEMV1_WAVES * RPW) {
             const int rr = base + lane / G;
             float acc = 0.0f;
@@ -531,7 +585,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
 }
 
 
-template <int T, bool Q32, bool SW>
+template <int T, bool Q32, int MODE>
 static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
     static int ncu = 0, per_cu = 0;
     static size_t cached_smem = 0;
@@ -542,20 +596,27 @@ static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, 
     }
     if (cached_smem != smem) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv1_kernel<T, Q32, SW>, GEMV1_THREADS, smem) != hipSuccess || n < 1) n = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv1_kernel<T, Q32, MODE>, GEMV1_THREADS, smem) != hipSuccess || n < 1) n = 1;
         per_cu = n;
         cached_smem = smem;
     }
     long long blocks = (long long)per_cu * ncu;
     if (blocks > tiles) blocks = tiles;
-    gemv1_kernel<T, Q32, SW><<<dim3((unsigned)blocks), GEMV1_THREADS, smem, s>>>(a);
+    gemv1_kernel<T, Q32, MODE><<<dim3((unsigned)blocks), GEMV1_THREADS, smem, s>>>(a);
     return hipGetLastError();
 }
 
 template <int T>
 static hipError_t gemv1_t(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
-    if (a.xu) return a.per32 ? gemv1_launch<T, true, true>(a, tiles, smem, s) : gemv1_launch<T, false, true>(a, tiles, smem, s);
-    return a.per32 ? gemv1_launch<T, true, false>(a, tiles, smem, s) : gemv1_launch<T, false, false>(a, tiles, smem, s);
+    const int mode = (a.xu ? 1 : 0) | (a.quarter ? 2 : 0) | (!a.xu && !a.ids && a.nz == 1 ? 4 : 0);
+    switch (mode) {
+    case 0: return a.per32 ? gemv1_launch<T, true, 0>(a, tiles, smem, s) : gemv1_launch<T, false, 0>(a, tiles, smem, s);
+    case 1: return a.per32 ? gemv1_launch<T, true, 1>(a, tiles, smem, s) : gemv1_launch<T, false, 1>(a, tiles, smem, s);
+    case 2: return a.per32 ? gemv1_launch<T, true, 2>(a, tiles, smem, s) : gemv1_launch<T, false, 2>(a, tiles, smem, s);
+    case 3: return a.per32 ? gemv1_launch<T, true, 3>(a, tiles, smem, s) : gemv1_launch<T, false, 3>(a, tiles, smem, s);
+    case 4: return a.per32 ? gemv1_launch<T, true, 4>(a, tiles, smem, s) : gemv1_launch<T, false, 4>(a, tiles, smem, s);
+    default: return a.per32 ? gemv1_launch<T, true, 6>(a, tiles, smem, s) : gemv1_launch<T, false, 6>(a, tiles, smem, s);
+    }
 }
 
 template <int T, int NT, bool Q32>
@@ -640,7 +701,9 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     bool iq = g.ty == IQ2_XXS || g.ty == IQ3_S;
     if (single) {
         const uint32_t ncp = (g.cols + 255) & ~255;
-        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + xpad_bytes(ncp) + ncp / 8 + ncp / 4 + GEMV1_TILE + 16;
+        a.quarter = a.R <= 64 / a.G;
+        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + xpad_bytes(ncp) + ncp / 8 + ncp / 4 + GEMV1_TILE + 16 +
+                             (a.quarter ? 3 * 64 * 8 : 0);
         switch (g.ty) {
         case Q8_0: return gemv1_t<Q8_0>(a, grid, smem1, s);
         case Q2_K: return gemv1_t<Q2_K>(a, grid, smem1, s);

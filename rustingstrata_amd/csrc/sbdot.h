@@ -67,7 +67,9 @@ __device__ __forceinline__ void words_a2(const uint8_t* p, uint32_t* out) {
 }
 
 // ---- Q4_K / Q5_K: 8 sub-blocks of 32, 6-bit scales and mins (src/cpu_moe.rs:327-358) ----
-template <bool Q5, class X>
+// Quarters [P0, P1) of the super-block (quarter p: values 64p .. 64p + 63, sub-blocks 2p and 2p + 1); all four for
+// the whole dot.
+template <bool Q5, int P0, int P1, class X>
 __device__ __forceinline__ void sb_q45(const uint8_t* b, const X& x, int& isum, int& msum, float& D, float& M) {
     const uint4 h = *(const uint4*)b;
     D = f16_to_f32(h.x & 0xFFFF);
@@ -81,7 +83,7 @@ __device__ __forceinline__ void sb_q45(const uint8_t* b, const X& x, int& isum, 
     const uint8_t* qs = b + (Q5 ? 48 : 16);
     int is = 0;
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
+    for (int p = P0; p < P1; p++) {
         const uint4 w0 = *(const uint4*)(qs + 32 * p), w1 = *(const uint4*)(qs + 32 * p + 16);
         uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
         uint32_t lo[8], hi[8];
@@ -108,12 +110,13 @@ __device__ __forceinline__ void sb_q45(const uint8_t* b, const X& x, int& isum, 
     // min term: sum_j m_j * (sum of x over sub-block j)
     int ms = 0;
 #pragma unroll
-    for (int j = 0; j < 8; j++) ms += __mul24((int)byte_of(j < 4 ? m_lo : m_hi, j & 3), x.s(2 * j) + x.s(2 * j + 1));
+    for (int j = 2 * P0; j < 2 * P1; j++) ms += __mul24((int)byte_of(j < 4 ? m_lo : m_hi, j & 3), x.s(2 * j) + x.s(2 * j + 1));
     msum = ms;
 }
 
 // ---- Q6_K: 16 groups of 16, int8 scales, values q - 32 (src/cpu_moe.rs:360-377) ----
-template <class X>
+// Quarters [P0, P1): quarter 2n + (qd >> 1) is half n's passes qd (values 128n + 32qd .. + 31) for its two qd.
+template <int P0, int P1, class X>
 __device__ __forceinline__ void sb_q6(const uint8_t* b, const X& x, int& isum, float& D) {
     uint32_t sc[4];
     words_a2<4>(b + 192, sc);
@@ -121,6 +124,7 @@ __device__ __forceinline__ void sb_q6(const uint8_t* b, const X& x, int& isum, f
     int is = 0;
 #pragma unroll
     for (int n = 0; n < 2; n++) {
+        if (2 * n + 1 < P0 || 2 * n >= P1) continue;
         // half n: 64 bytes of low nibbles (ql[l] = words 0..7, ql[l + 32] = words 8..15), 32 bytes of high bits
         uint32_t ql[16], qh[8];
         words_a2<16>(b + 64 * n, ql);
@@ -129,6 +133,7 @@ __device__ __forceinline__ void sb_q6(const uint8_t* b, const X& x, int& isum, f
         for (int qd = 0; qd < 4; qd++)
 #pragma unroll
             for (int a = 0; a < 2; a++) {
+                if (2 * n + (qd >> 1) < P0 || 2 * n + (qd >> 1) >= P1) continue;
                 uint32_t v[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -147,30 +152,36 @@ __device__ __forceinline__ void sb_q6(const uint8_t* b, const X& x, int& isum, f
 }
 
 // ---- Q8_0: 8 blocks of 32 with an f16 scale each (src/cpu_moe.rs:319-325): returns sum_b (d_b dx) s_b ----
+// The (d_b dx) s_b of block k (one term of the sum).
+template <class X>
+__device__ __forceinline__ float q8_0_term(const uint8_t* b, const X& x, int k, float dx) {
+    uint32_t w[9];
+    words_a2<9>(b + 34 * k, w);  // d (low half of w[0]) then 32 int8
+    uint32_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) q[i] = align_bytes(w[i + 1], w[i], 2);
+    const int s = dot16(q, x.q16(32 * k), x.q16(32 * k + 16));
+    return (f16_to_f32(w[0] & 0xFFFF) * dx) * (float)s;
+}
 template <class X>
 __device__ __forceinline__ float sb_q8_0(const uint8_t* b, const X& x, int nb, float dx) {
     float f = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         if (k >= nb) break;  // a partial last super-block (Q8_0 rows are multiples of 32 values)
-        uint32_t w[9];
-        words_a2<9>(b + 34 * k, w);  // d (low half of w[0]) then 32 int8
-        uint32_t q[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) q[i] = align_bytes(w[i + 1], w[i], 2);
-        const int s = dot16(q, x.q16(32 * k), x.q16(32 * k + 16));
-        f = f + (f16_to_f32(w[0] & 0xFFFF) * dx) * (float)s;
+        f = f + q8_0_term(b, x, k, dx);
     }
     return f;
 }
 
 // ---- generic: any type through task<T> (8 tasks of 32 values) ----
-template <int T, class X>
+// Tasks [K0, K1).
+template <int T, int K0, int K1, class X>
 __device__ __forceinline__ void sb_generic(const uint8_t* b, const X& x, const IqTables* tab, int& isum, int& msum,
                                            float& D, float& M) {
     int is = 0, ms = 0;
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int k = K0; k < K1; k++) {
         Task t;
         task<T>(b, k, tab, t);
         int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x.q16(t.o0)), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x.q16(t.o1));
@@ -195,19 +206,19 @@ __device__ __forceinline__ float sb_dot_q8k(const uint8_t* b, const X& x, const 
     if constexpr (T == Q4_K || T == Q5_K) {
         int is, ms;
         float D, M;
-        sb_q45<T == Q5_K>(b, x, is, ms, D, M);
+        sb_q45<T == Q5_K, 0, 4>(b, x, is, ms, D, M);
         return (D * dx) * (float)is - (M * dx) * (float)ms;
     } else if constexpr (T == Q6_K) {
         int is;
         float D;
-        sb_q6(b, x, is, D);
+        sb_q6<0, 4>(b, x, is, D);
         return (D * dx) * (float)is;
     } else if constexpr (T == Q8_0) {
         return sb_q8_0(b, x, nvals >> 5, dx);
     } else {
         int is, ms = 0;
         float D, M = 0.0f;
-        sb_generic<T>(b, x, tab, is, ms, D, M);
+        sb_generic<T, 0, 8>(b, x, tab, is, ms, D, M);
         float f = (D * dx) * (float)is;
         if constexpr (Fmt<T>::MIN) f = f - (M * dx) * (float)ms;
         return f;
@@ -216,22 +227,84 @@ __device__ __forceinline__ float sb_dot_q8k(const uint8_t* b, const X& x, const 
 
 // The same under per-32 x scales (the reference GPU's default numerics): every 32-group has its own dx, so each task
 // closes in float.
+// Task k's term of that sum.
+template <int T, class X>
+__device__ __forceinline__ float q32_term(const uint8_t* b, const X& x, const IqTables* tab, int k) {
+    Task t;
+    task<T>(b, k, tab, t);
+    int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x.q16(t.o0)), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x.q16(t.o1));
+    const int a0 = x.s(t.o0 >> 4), a1 = x.s(t.o1 >> 4);
+    if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * a0; s1 -= Fmt<T>::BIAS * a1; }
+    float f0 = t.D * (float)__mul24(t.sc0, s0), f1 = t.D * (float)__mul24(t.sc1, s1);
+    if constexpr (Fmt<T>::MIN) { f0 -= t.M * (float)__mul24(t.m0, a0); f1 -= t.M * (float)__mul24(t.m1, a1); }
+    return x.d(t.o0 >> 5) * f0 + x.d(t.o1 >> 5) * f1;
+}
 template <int T, class X>
 __device__ __forceinline__ float sb_dot_q32(const uint8_t* b, const X& x, const IqTables* tab, int nvals) {
     float f = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         if (32 * k >= nvals) break;  // a partial last super-block (Q8_0 only)
-        Task t;
-        task<T>(b, k, tab, t);
-        int s0 = dot4w(t.q[0], t.q[1], t.q[2], t.q[3], x.q16(t.o0)), s1 = dot4w(t.q[4], t.q[5], t.q[6], t.q[7], x.q16(t.o1));
-        const int a0 = x.s(t.o0 >> 4), a1 = x.s(t.o1 >> 4);
-        if constexpr (Fmt<T>::BIAS != 0) { s0 -= Fmt<T>::BIAS * a0; s1 -= Fmt<T>::BIAS * a1; }
-        float f0 = t.D * (float)__mul24(t.sc0, s0), f1 = t.D * (float)__mul24(t.sc1, s1);
-        if constexpr (Fmt<T>::MIN) { f0 -= t.M * (float)__mul24(t.m0, a0); f1 -= t.M * (float)__mul24(t.m1, a1); }
-        f += x.d(t.o0 >> 5) * f0 + x.d(t.o1 >> 5) * f1;
+        f += q32_term<T>(b, x, tab, k);
     }
     return f;
+}
+
+// ---- quarter split: four waves take one quarter (values 64W .. 64W + 63) each of the same super-blocks, and wave 0
+// closes them with the super-block's float steps (sb_close) in the order sb_dot_q8k / sb_dot_q32 take them, so the
+// result carries the same bits. Integer numerics (Q8_K, all types but Q8_0): o0, o1 = the quarter's exact integer
+// sums (scale-weighted products, min-weighted x sums); float steps (per-32 scales, or Q8_0): o0, o1 = the float
+// terms of its two 32-value tasks 2W and 2W + 1, added in task order by the close. D and M: the super-block scales
+// (set by quarter 0).
+template <int T, bool Q32>
+constexpr bool quarter_ints() { return !Q32 && T != Q8_0; }
+
+template <int T, bool Q32, int W, class X>
+__device__ __forceinline__ void sb_quarter(const uint8_t* b, const X& x, const IqTables* tab, int nvals, uint32_t& o0,
+                                           uint32_t& o1, float& D, float& M) {
+    if constexpr (!quarter_ints<T, Q32>()) {
+        float t0 = 0.0f, t1 = 0.0f;
+        if constexpr (Q32) {
+            if (64 * W < nvals) t0 = q32_term<T>(b, x, tab, 2 * W);
+            if (64 * W + 32 < nvals) t1 = q32_term<T>(b, x, tab, 2 * W + 1);
+        } else {
+            const float dx = x.d(0);
+            if (64 * W < nvals) t0 = q8_0_term(b, x, 2 * W, dx);
+            if (64 * W + 32 < nvals) t1 = q8_0_term(b, x, 2 * W + 1, dx);
+        }
+        o0 = __float_as_uint(t0);
+        o1 = __float_as_uint(t1);
+    } else {
+        int is = 0, ms = 0;
+        if constexpr (T == Q4_K || T == Q5_K) {
+            sb_q45<T == Q5_K, W, W + 1>(b, x, is, ms, D, M);
+        } else if constexpr (T == Q6_K) {
+            sb_q6<W, W + 1>(b, x, is, D);
+        } else {
+            sb_generic<T, 2 * W, 2 * W + 2>(b, x, tab, is, ms, D, M);
+        }
+        o0 = (uint32_t)is;
+        o1 = (uint32_t)ms;
+    }
+}
+
+// o[2W], o[2W + 1]: quarter W's outputs; D, M from quarter 0; dx: x's scale (Q8_K numerics).
+template <int T, bool Q32>
+__device__ __forceinline__ float sb_close(const uint32_t (&o)[8], float D, float M, float dx, int nvals) {
+    if constexpr (!quarter_ints<T, Q32>()) {
+        float f = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            if (32 * k >= nvals) break;
+            f += __uint_as_float(o[k]);
+        }
+        return f;
+    } else {
+        const int is = (int)(o[0] + o[2] + o[4] + o[6]), ms = (int)(o[1] + o[3] + o[5] + o[7]);
+        float f = (D * dx) * (float)is;
+        if constexpr (Fmt<T>::MIN) f = f - (M * dx) * (float)ms;
+        return f;
+    }
 }
 
 }  // namespace strata

@@ -903,3 +903,23 @@ def test_down_combine_equals_two_launches(hip, t):
                 y = O.matvec(ggml.Q6_K, dn[slots[tt, j] * H:(slots[tt, j] + 1) * H], H, F, h[tt * k + j])
                 want[tt] += 3 * wh[tt, j] * y
     assert max_rel_err(ga.reshape(t, H), want) <= TOL
+
+
+
+def test_moe_gemv_one_slot_not_resident(hip):
+    """A single MoE slot whose id is -1 leaves its output untouched (the one-slot launch is not a plain matrix);
+    with a resident id it is that expert's matvec."""
+    ty, rows, cols, E = ggml.Q4_K, 64, 512, 3
+    rb = ggml.row_bytes(ty, cols)
+    wblk = random_blocks(ty, E * rows, cols, seed=91)
+    wb = up(hip, wblk)
+    x = normal(cols, seed=92)
+    xb = up(hip, x)
+    for e in (-1, 2):
+        y = up(hip, np.full(rows, 3.5, np.float32))
+        hip.moe_gemv(ty, rows, cols, wb, rows * rb, up(hip, np.array([e], np.int32)), 1, xb, cols, 1, y)
+        got = down(hip, y, np.float32, rows)
+        if e < 0:
+            assert np.all(got == np.float32(3.5))
+        else:
+            assert max_rel_err(got, O.matvec(ty, wblk[e * rows:(e + 1) * rows], rows, cols, x)) <= TOL
