@@ -39,6 +39,8 @@ struct GemvArgs {
     const float* xf;     // single-input kernel: x as f32 (quantized in-lane) when xq is null
     const float* xu;     // with xf: x = silu(xf) * xu, rows x_stride floats apart (swiglu_q fused), or null
     uint64_t x_stride;   // floats between the f32 x rows
+    uint32_t ntr_m, ns_m; // magic multipliers and shifts dividing by ntr and nslots (fdiv)
+    int ntr_s, ns_s;
     int quarter;         // single-input kernel: every tile fits one pass of a wave (at most 64 / G rows), and the four
                          // waves each take one quarter of every super-block (sb_quarter / sb_close)
 };
@@ -420,6 +422,15 @@ __device__ __forceinline__ void load_x_slice(int sb, const int8_t* xl, const flo
 
 // SW: x rows are silu(xf) * xu (the fused SwiGLU input of the down projection); a separate instantiation, so the
 // plain GEMV carries none of it.
+// n / d for 0 <= n < 2^31 and d >= 1, from m and s of magic(d) (Granlund and Montgomery, "Division by invariant
+// integers using multiplication", 1994: s = ceil(log2 d), m = floor(2^32 (2^s - d) / d) + 1).
+__device__ __forceinline__ int fdiv(int n, uint32_t m, int s) { return (int)((__umulhi((uint32_t)n, m) + (uint32_t)n) >> s); }
+static void magic(uint32_t d, uint32_t& m, int& s) {
+    s = 0;
+    while ((1ull << s) < d) s++;
+    m = (uint32_t)((((1ull << s) - d) << 32) / d + 1);
+}
+
 // MODE: bit 0 SW (x rows are silu(xf) * xu), bit 1 the quarter split (GemvArgs::quarter), bit 2 one plain matrix
 // (no expert ids, no pair: tile t is row tile t and every tile is valid, with none of the general indexing's
 // divisions, tens of instructions each).
@@ -448,7 +459,8 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     // divisions below (tens of instructions each) stay off that path
     auto valid = [&](int t) {
         if constexpr (plain) return true;
-        const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
+        const int rest = fdiv(t, a.ntr_m, a.ntr_s), rt = t - rest * a.ntr, z = fdiv(rest, a.ns_m, a.ns_s),
+                  slot = rest - z * a.nslots;
         if (rt * a.R >= (z ? a.rows2 : a.rows)) return false;
         return !a.ids || sload(a.ids + slot) >= 0;  // a slot not routed here leaves its output untouched
     };
@@ -466,7 +478,8 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
             sp.xrow = 0;
             sp.beg = (uint64_t)(a.w + (uint64_t)sp.r0 * a.rb);
         } else {
-            const int rt = t % a.ntr, rest = t / a.ntr, slot = rest % a.nslots, z = rest / a.nslots;
+            const int rest = fdiv(t, a.ntr_m, a.ntr_s), rt = t - rest * a.ntr, z = fdiv(rest, a.ns_m, a.ns_s),
+                      slot = rest - z * a.nslots;
             const int rows = z ? a.rows2 : a.rows;
             sp.r0 = rt * a.R;
             sp.nr = min(a.R, rows - sp.r0);
@@ -697,6 +710,8 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     a.ntr = (maxrows + a.R - 1) / a.R;
     a.nslots = nslots;
     a.nz = nz;
+    magic((uint32_t)a.ntr, a.ntr_m, a.ntr_s);
+    magic((uint32_t)a.nslots, a.ns_m, a.ns_s);
     const long long grid = (long long)a.ntr * nslots * nz;  // tiles
     bool iq = g.ty == IQ2_XXS || g.ty == IQ3_S;
     if (single) {
