@@ -159,7 +159,9 @@ int strata_swiglu_q(strata_ctx* ctx, uint64_t g, uint64_t u, uint64_t n, uint64_
 int strata_moe_combine(strata_ctx* ctx, uint64_t x, uint64_t ye, uint64_t w, uint64_t k, uint64_t sh, uint64_t sg,
                        uint64_t n, uint64_t t);
 /* Backend::moe_down_combine with mb = 0 (src/backend.rs:436-442): moe_gemv of the down experts (k slots per token,
- * x = h rows of cols, pre-quantized at xq when not 0) into ye, then moe_combine of ye into x with weights wh. */
+ * x = h rows of cols, pre-quantized at xq when not 0) into ye, then moe_combine of ye into x with weights wh. With
+ * xq and cols a multiple of 256 both run as one launch whose blocks each hold all k slots of some output rows (ye
+ * is then not written); otherwise ye is the experts' outputs. Either way x gets the same bits. */
 int strata_moe_down_combine(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
                             uint64_t slots, uint64_t k, uint64_t h, uint64_t ye, uint64_t xq, uint64_t x, uint64_t wh,
                             uint64_t sh, uint64_t sg, uint64_t t);

@@ -568,9 +568,34 @@ int strata_moe_combine(strata_ctx* c, uint64_t x, uint64_t ye, uint64_t w, uint6
     return 0;
 }
 
+// The down GEMV and the combine as one launch where the fused layout takes the shape (1: done, 0: not taken, -1:
+// error); x rows from xq.
+static int down_combine_fused(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
+                              uint64_t slots, uint64_t k, uint64_t xq, uint64_t x, uint64_t wh, uint64_t sh, uint64_t sg,
+                              uint64_t t) {
+    if (check_ctx(c) || check_type(ty)) return -1;
+    if (check_gemv_cols(ty, cols) || check_align(ty, w, "moe_down_combine") || check_align(ty, stride, "moe_down_combine stride")) return -1;
+    if (!t || !rows || !k) return 1;
+    if (rows > (1u << 30) || k > 256 || t > 65535 || !slots || !wh || !x) return 0;
+    DownCombineLaunch d;
+    d.ty = ty; d.numerics = c->numerics; d.w = (const uint8_t*)w; d.stride = (int64_t)stride;
+    d.rows = (int)rows; d.cols = (int)cols; d.k = (int)k; d.t = (int)t;
+    d.slots = (const int*)slots; d.wh = (const float*)wh;
+    d.xq = (const int8_t*)xq;
+    d.x = (float*)x; d.sh = (const float*)sh; d.sg = (const float*)sg;
+    const hipError_t e = launch_down_combine(d, c->stream);
+    if (e == hipErrorNotSupported) return 0;
+    STRATA_HIP(e);
+    return 1;
+}
+
 int strata_moe_down_combine(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
                             uint64_t slots, uint64_t k, uint64_t h, uint64_t ye, uint64_t xq, uint64_t x, uint64_t wh,
                             uint64_t sh, uint64_t sg, uint64_t t) {
+    if (xq) {
+        const int r = down_combine_fused(c, ty, rows, cols, w, stride, slots, k, xq, x, wh, sh, sg, t);
+        if (r) return r < 0 ? -1 : 0;
+    }
     if (strata_moe_gemv(c, ty, rows, cols, w, stride, slots, t * k, h, cols, 1, ye, 0, 0, 0, xq)) return -1;
     return strata_moe_combine(c, x, ye, wh, k, sh, sg, rows, t);
 }
@@ -580,6 +605,7 @@ int strata_moe_down_swiglu_combine(strata_ctx* c, int ty, uint64_t rows, uint64_
                                    uint64_t wh, uint64_t sh, uint64_t sg, uint64_t t) {
     if (check_ctx(c)) return -1;
     if (!g || !u) return set_error("moe_down_swiglu_combine: null g or u");
+    // (the one-launch layout would quantize every slot's SwiGLU in every block: slower than two launches)
     if (moe_gemv_impl(c, ty, rows, cols, w, stride, slots, t * k, g, cols, 1, ye, 0, 0, 0, 0, u)) return -1;
     return strata_moe_combine(c, x, ye, wh, k, sh, sg, rows, t);
 }

@@ -748,4 +748,224 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     return hipErrorInvalidValue;
 }
 
+// ---- moe_down_combine in one launch ----
+// Block (row block rb, token tk) of 1024 threads: rows r0 = rb R .. of all k slots of the token. Its 16 waves are 4
+// groups of 4; group q takes pairs (slot, row) 16 q .. 16 q + 15 (64 / G pairs a wave pass, G lanes a pair, one
+// super-block a lane) and its 4 waves one quarter each of every super-block (sb_quarter; the group's wave 0 closes
+// them), so R = 4 (64 / G) / k rows. x of all k slots (quantized by quant_xq) is staged once per block as one
+// flattened vector, every slot's rows padded like the single-input kernel's. Each
+// (slot, row) dot lands in LDS and the first R threads then add the slots' weighted outputs to x in slot order,
+// plus the shared expert, as combine_kernel does (src/cuda/kernels.cu:2742-2773).
+constexpr int DC_THREADS = 1024;
+struct DcArgs {
+    const uint8_t* w;
+    int64_t stride;       // bytes between experts
+    const int* slots;     // t k expert slots (-1: not resident)
+    const float* wh;      // t k combine weights
+    const int8_t* xq;     // x pre-quantized (quant_xq layout of t k rows; row tk k + j for slot j of token tk)
+    const float* xd;
+    float* x;             // t rows of `rows` floats: x += combine
+    const float* sh;      // shared expert output (t rows of `rows`) or null, gated by sigmoid(sg[tk]) when sg
+    const float* sg;
+    int rows, cols, k, R, G, nsb, nch;  // nch: 16-byte chunks a slot's span may take (its LDS pitch / 16)
+    uint64_t rb;
+    uint32_t nch_m;
+    int nch_s;
+};
+
+__device__ __forceinline__ float dc_sigmoid(float v) { return 1.0f / (1.0f + (float)exp(-(double)v)); }
+
+template <int T, bool Q32>
+__global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(DcArgs a) {
+    constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
+    constexpr int SBB = sb_bytes(T);
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, tk = blockIdx.y;
+    const int k = a.k, cols = a.cols, n = k * cols, R = a.R, G = a.G;
+    const int r0 = blockIdx.x * R, nr = min(R, a.rows - r0);
+    // LDS: [IqTables][x: n int8 (padded)][n / 32 scales][n / 16 sums][tile: k spans of 16 nch bytes][parts][ye]
+    const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + xpad_bytes(n), o_ss = o_xd + n / 8,
+                   o_tile = o_ss + n / 4, o_part = o_tile + 16 * a.nch * k, o_ye = o_part + 4 * 3 * 64 * 8,
+                   o_sl = o_ye + 4 * k * R;
+    IqTables* tab = (IqTables*)smem;
+    if constexpr (IQ) load_iq_tables(tab);
+    int8_t* xl = (int8_t*)(smem + o_x);
+    float* xld = (float*)(smem + o_xd);
+    int* xss = (int*)(smem + o_ss);
+    uint8_t* tile = smem + o_tile;
+    uint32_t* part = (uint32_t*)(smem + o_part);
+    float* ye = (float*)(smem + o_ye);
+    int* sslot = (int*)(smem + o_sl);
+    float* swh = (float*)(sslot + k);
+
+    // Requested first, none of them depending on anything of this launch: the token's slots and combine weights,
+    // the combine's x and shared-expert values of this thread's row, and this thread's first chunk of x.
+    if (tid < k) {
+        sslot[tid] = a.slots[(uint64_t)tk * k + tid];
+        swh[tid] = a.wh[(uint64_t)tk * k + tid];
+    }
+    const uint64_t orow = (uint64_t)tk * a.rows + r0 + tid;
+    float xo = 0.0f, sho = 0.0f, sgv = 0.0f;
+    if (tid < nr) {
+        xo = a.x[orow];
+        if (a.sh) sho = a.sh[orow];
+        if (a.sg) sgv = a.sg[tk];
+    }
+    v4u xq0{};
+    float xd0 = 0.0f;
+    if (tid < n / 16) {
+        const int i = 16 * tid, j = i / cols, cc = i - j * cols;
+        xq0 = *gptr<v4u>((uint64_t)(a.xq + ((uint64_t)tk * k + j) * cols + cc));
+    }
+    if (tid < n / 32) {
+        const int i = 32 * tid, j = i / cols, cc = i - j * cols;
+        xd0 = *gptr<float>((uint64_t)(a.xd + ((uint64_t)tk * k + j) * (cols / 32) + cc / 32));
+    }
+    __syncthreads();  // the slots
+
+    // the k spans' loads: chunk c of the flattened list is chunk c - j nch of slot j's span (rows r0 .. of its
+    // expert, from the 16-byte-aligned cover); chunks past a span's end and spans of slots not resident are skipped
+    constexpr int DC_CH = 8;  // loads a thread (k nch <= DC_CH DC_THREADS, checked on the host)
+    v4u wv[DC_CH];
+#pragma unroll
+    for (int i = 0; i < DC_CH; i++) {
+        const int c = tid + DC_THREADS * i;
+        const int j = fdiv(c, a.nch_m, a.nch_s), cc = c - j * a.nch;
+        if (j < k) {
+            const int e = sslot[j];
+            if (e >= 0) {
+                const uint64_t beg = (uint64_t)(a.w + e * a.stride + (uint64_t)r0 * a.rb), g0 = beg & ~(uint64_t)15;
+                const int nch = (int)((((beg + (uint64_t)nr * a.rb) + 15) & ~(uint64_t)15) - g0) >> 4;
+                if (cc < nch) wv[i] = __builtin_nontemporal_load(gptr<v4u>(g0 + 16 * (uint64_t)cc));
+            }
+        }
+    }
+    // x of the k slots, flattened: value v of slot j at j cols + v
+    {
+        for (int c = tid; c < n / 16; c += DC_THREADS) {
+            const int i = 16 * c, j = i / cols, cc = i - j * cols;
+            const v4u q = c == tid ? xq0 : *gptr<v4u>((uint64_t)(a.xq + ((uint64_t)tk * k + j) * cols + cc));
+            *(v4u*)(xl + xpad(i)) = q;
+            xss[c] = sdot4((int)q.x, 0x01010101, sdot4((int)q.y, 0x01010101, sdot4((int)q.z, 0x01010101, sdot4((int)q.w, 0x01010101, 0))));
+        }
+        for (int c = tid; c < n / 32; c += DC_THREADS) {
+            const int i = 32 * c, j = i / cols, cc = i - j * cols;
+            xld[c] = c == tid ? xd0 : *gptr<float>((uint64_t)(a.xd + ((uint64_t)tk * k + j) * (cols / 32) + cc / 32));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < DC_CH; i++) {
+        const int c = tid + DC_THREADS * i;
+        const int j = fdiv(c, a.nch_m, a.nch_s);
+        if (j < k) *(v4u*)(tile + 16 * c) = wv[i];
+    }
+    __syncthreads();
+
+    // pair p = 16 q + lane / G of group q = wave / 4: slot p / R, row p % R; quarter wave % 4 of super-block lane % G
+    const int grp = wave >> 2, qw = wave & 3, gl = lane & (G - 1);
+    const int p = grp * (64 / G) + lane / G, j = p / R, rr = p - j * R;
+    int e = -1;
+    if (j < k) e = sslot[j];
+    const bool live = j < k && e >= 0 && rr < nr && gl < a.nsb;
+    const int nv = min(256, cols - 256 * gl);
+    uint32_t o0 = 0, o1 = 0;
+    float D = 0.0f, M = 0.0f;
+    if (live) {
+        const uint64_t beg = (uint64_t)(a.w + e * a.stride + (uint64_t)r0 * a.rb);
+        const uint8_t* b = tile + 16 * a.nch * j + (beg & 15) + (uint64_t)rr * a.rb + gl * SBB;
+        const int sb = j * a.nsb + gl;
+        const XLds xv{xl + xpad(256 * sb), xld + 8 * sb, xss + 16 * sb};
+        switch (qw) {
+        case 0: sb_quarter<T, Q32, 0>(b, xv, tab, nv, o0, o1, D, M); break;
+        case 1: sb_quarter<T, Q32, 1>(b, xv, tab, nv, o0, o1, D, M); break;
+        case 2: sb_quarter<T, Q32, 2>(b, xv, tab, nv, o0, o1, D, M); break;
+        default: sb_quarter<T, Q32, 3>(b, xv, tab, nv, o0, o1, D, M); break;
+        }
+    }
+    if (qw) *(uint2*)(part + ((grp * 3 + qw - 1) * 64 + lane) * 2) = make_uint2(o0, o1);
+    __syncthreads();
+    if (qw == 0) {
+        uint32_t o[8];
+        o[0] = o0;
+        o[1] = o1;
+#pragma unroll
+        for (int w = 1; w < 4; w++) {
+            const uint2 v = *(const uint2*)(part + ((grp * 3 + w - 1) * 64 + lane) * 2);
+            o[2 * w] = v.x;
+            o[2 * w + 1] = v.y;
+        }
+        const int sb = j * a.nsb + gl;
+        float acc = live ? sb_close<T, Q32>(o, D, M, live ? xld[8 * sb] : 0.0f, nv) : 0.0f;
+        acc = ordered_sum(acc, G);
+        if (j < k && rr < R && gl == G - 1) ye[j * R + rr] = acc;
+    }
+    __syncthreads();
+    // the combine of each row: the slots' weighted outputs in slot order (a slot of weight 0 or not resident adds
+    // nothing), then the shared expert
+    if (tid < nr) {
+        float y = 0.0f;
+        for (int jj = 0; jj < k; jj++) {
+            const float wj = swh[jj];
+            if (wj != 0.0f && sslot[jj] >= 0) y += wj * ye[jj * R + tid];
+        }
+        if (a.sh) y += (a.sg ? dc_sigmoid(sgv) : 1.0f) * sho;
+        a.x[orow] = xo + y;
+    }
+}
+
+template <int T, bool Q32>
+static hipError_t dc_launch(const DcArgs& a, int t, size_t smem, hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        if (hipFuncSetAttribute((const void*)moe_down_combine_kernel<T, Q32>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return hipErrorInvalidValue;
+        attr = true;
+    }
+    moe_down_combine_kernel<T, Q32><<<dim3((unsigned)((a.rows + a.R - 1) / a.R), (unsigned)t), DC_THREADS, smem, s>>>(a);
+    return hipGetLastError();
+}
+template <int T>
+static hipError_t dc_t(const DcArgs& a, bool q32, int t, size_t smem, hipStream_t s) {
+    return q32 ? dc_launch<T, true>(a, t, smem, s) : dc_launch<T, false>(a, t, smem, s);
+}
+
+hipError_t launch_down_combine(const DownCombineLaunch& g, hipStream_t s) {
+    DcArgs a{};
+    a.w = g.w; a.stride = g.stride; a.slots = g.slots; a.wh = g.wh;
+    a.xq = g.xq;
+    a.xd = g.xq ? (const float*)(g.xq + (uint64_t)g.t * g.k * g.cols) : nullptr;
+    a.x = g.x; a.sh = g.sh; a.sg = g.sg;
+    a.rows = g.rows; a.cols = g.cols; a.k = g.k;
+    a.rb = row_bytes(g.ty, g.cols);
+    a.nsb = g.cols / 256;
+    a.G = 1;
+    while (a.G < a.nsb) a.G <<= 1;
+    const int pairs = 4 * (64 / a.G);
+    a.R = pairs / g.k;
+    a.nch = (int)((a.R * a.rb + 15) / 16 + 1);
+    magic((uint32_t)a.nch, a.nch_m, a.nch_s);
+    const bool iq = g.ty == IQ2_XXS || g.ty == IQ3_S;
+    const uint32_t n = (uint32_t)(g.k * g.cols);
+    const size_t smem = (iq ? up16(sizeof(IqTables)) : 0) + xpad_bytes(n) + n / 8 + n / 4 + 16 * (size_t)a.nch * g.k +
+                        4 * 3 * 64 * 8 + 4 * (size_t)g.k * a.R + 8 * (size_t)g.k;
+    // shapes this layout does not take: the caller's two launches
+    if (!g.xq || g.cols % 256 || a.G > 64 || a.R < 1 || g.k * a.nch > 8 * DC_THREADS || smem > 160 * 1024 ||
+        g.t < 1 || g.t > 65535)
+        return hipErrorNotSupported;
+    const bool q32 = g.numerics == STRATA_NUM_Q8_32;
+    switch (g.ty) {
+    case Q8_0: return dc_t<Q8_0>(a, q32, g.t, smem, s);
+    case Q2_K: return dc_t<Q2_K>(a, q32, g.t, smem, s);
+    case Q3_K: return dc_t<Q3_K>(a, q32, g.t, smem, s);
+    case Q4_K: return dc_t<Q4_K>(a, q32, g.t, smem, s);
+    case Q5_K: return dc_t<Q5_K>(a, q32, g.t, smem, s);
+    case Q6_K: return dc_t<Q6_K>(a, q32, g.t, smem, s);
+    case IQ2_XXS: return dc_t<IQ2_XXS>(a, q32, g.t, smem, s);
+    case IQ3_S: return dc_t<IQ3_S>(a, q32, g.t, smem, s);
+    case IQ4_XS: return dc_t<IQ4_XS>(a, q32, g.t, smem, s);
+    }
+    return hipErrorInvalidValue;
+}
+
 }  // namespace strata

@@ -37,6 +37,22 @@ struct GemvLaunch {
     int rows2 = 0;
 };
 hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s);
+// moe_down_combine as one launch: x[tk] += sum_j wh[tk k + j] W_{slots[j]} x_j (slots in order) + the shared expert,
+// x_j row tk k + j of xq. hipErrorNotSupported: a shape the fused layout does not take (cols not a multiple of 256,
+// too many slots for its rows), for the caller's two launches.
+struct DownCombineLaunch {
+    int ty = 0, numerics = 0;
+    const uint8_t* w = nullptr;
+    int64_t stride = 0;
+    int rows = 0, cols = 0, k = 1, t = 1;
+    const int* slots = nullptr;
+    const float* wh = nullptr;
+    const int8_t* xq = nullptr;
+    float* x = nullptr;
+    const float* sh = nullptr;
+    const float* sg = nullptr;
+};
+hipError_t launch_down_combine(const DownCombineLaunch& g, hipStream_t s);
 // Streaming copy of `bytes` (multiple of 16), the reference kernel for HBM byte counters.
 hipError_t launch_copy(const void* src, void* dst, uint64_t bytes, hipStream_t s);
 // Streaming read of `bytes` (multiple of 16; 0: an empty launch), the floor a GEMV of the same bytes is measured against.

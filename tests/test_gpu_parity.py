@@ -740,16 +740,20 @@ def test_moe_decode_layer_matches_experts(hip):
 @pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])
 @pytest.mark.parametrize("F", [768, 3072])
 def test_moe_down_swiglu_combine_matches_unfused(hip, numerics, F):
-    """The fused decode tail (swiglu inside the down GEMV) gives the same bits as swiglu_q followed by
-    moe_down_combine (src/gpu_model.rs:3383-3412): same int8 x, same GEMV, same combine; 3 tokens, a shared expert.
-    F = 3072: x rows past 2048 values (the second half of the early x fetch)."""
+    """The fused decode tail gives the same x bits as swiglu_q, the down moe_gemv and moe_combine as three launches
+    (src/gpu_model.rs:3383-3412), with x quantized inside (moe_down_swiglu_combine) or from xq (moe_down_combine);
+    3 tokens, a shared expert, a slot not resident and a slot of weight 0. F = 3072: 16 lanes a row, 2 rows a block."""
     E, H, k, t = 16, 512, 8, 3
     _, _, dn = moe_weights(E, H, F, seed=60)
     rb_d = ggml.row_bytes(ggml.Q6_K, F)
     d_b = up(hip, dn)
     rng = np.random.default_rng(61)
-    slots = up(hip, rng.integers(0, E, t * k).astype(np.int32))
-    wh = up(hip, rng.random(t * k).astype(np.float32))
+    sl = rng.integers(0, E, t * k).astype(np.int32)
+    sl[4] = -1
+    w = rng.random(t * k).astype(np.float32)
+    w[4] = 0.0
+    w[13] = 0.0
+    slots, wh = up(hip, sl), up(hip, w)
     gu = rng.standard_normal((2, t * k, F)).astype(np.float32) * 3
     g = up(hip, gu)
     u = int(g) + t * k * F * 4
@@ -758,18 +762,58 @@ def test_moe_down_swiglu_combine_matches_unfused(hip, numerics, F):
     old = hip.numerics()
     hip.set_numerics(numerics)
     try:
-        xa, xb = up(hip, x0), up(hip, x0)
+        xa, xb, xc = up(hip, x0), up(hip, x0), up(hip, x0)
         ya, yb = hip.alloc(t * k * H * 4), hip.alloc(t * k * H * 4)
         aq = hip.alloc(t * k * (F + F // 8))
         aqr = hip.swiglu_q(g, u, F, t * k, aq)
-        hip.moe_down_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, 0, ya, aqr, xa, wh, sh, sg, t)
-        hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, g, u, yb, xb, wh, sh, sg, t)
+        hip.moe_gemv(ggml.Q6_K, H, F, d_b, H * rb_d, slots, t * k, 0, F, 1, ya, xq=aqr)
+        hip.moe_combine(xa, ya, wh, k, sh, sg, H, t)
+        hip.moe_down_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, 0, yb, aqr, xb, wh, sh, sg, t)
+        hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, g, u, yb, xc, wh, sh, sg, t)
     finally:
         hip.set_numerics(old)
-    assert np.array_equal(down(hip, ya, np.float32, t * k * H), down(hip, yb, np.float32, t * k * H))
-    assert np.array_equal(down(hip, xa, np.float32, t * H), down(hip, xb, np.float32, t * H))
+    ga = down(hip, xa, np.float32, t * H)
+    assert np.array_equal(ga, down(hip, xb, np.float32, t * H))
+    assert np.array_equal(ga, down(hip, xc, np.float32, t * H))
     with pytest.raises(S.StrataError, match="null g or u"):
         hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d_b, H * rb_d, slots, k, g, 0, yb, xb, wh, 0, 0, t)
+
+
+@pytest.mark.parametrize("ty", ggml.TYPES)
+@pytest.mark.parametrize("k,F,t", [(8, 768, 1), (4, 512, 2), (6, 1024, 1), (16, 256, 2)])
+def test_down_combine_one_launch_all_types(hip, ty, k, F, t):
+    """moe_down_combine as one launch (every slot of a block's rows in the block) against moe_gemv + moe_combine
+    bit for bit, for every type, slot counts that do and do not divide the block's pairs (k = 6: 10 rows a block),
+    a partial last row block (H = 1000), a slot not resident; and against the oracle."""
+    E, H = 5, 1000
+    rb = ggml.row_bytes(ty, F)
+    dn = random_blocks(ty, E * H, F, seed=300 + ty)
+    d_b = up(hip, dn)
+    rng = np.random.default_rng(301)
+    sl = rng.integers(0, E, t * k).astype(np.int32)
+    sl[1] = -1
+    w = rng.uniform(0.1, 0.5, t * k).astype(np.float32)
+    w[1] = 0.0
+    slots, wh = up(hip, sl), up(hip, w)
+    h = normal((t * k, F), seed=302)
+    hb = up(hip, h)
+    xq = hip.alloc(t * k * (F + F // 8))
+    hip.quant_xq(hb, F, F, t * k, xq)
+    x0 = normal((t, H), seed=303)
+    xa, xb = up(hip, x0), up(hip, x0)
+    ya, yb = hip.alloc(t * k * H * 4), hip.alloc(t * k * H * 4)
+    hip.moe_gemv(ty, H, F, d_b, H * rb, slots, t * k, hb, F, 1, ya, xq=xq)
+    hip.moe_combine(xa, ya, wh, k, 0, 0, H, t)
+    hip.moe_down_combine(ty, H, F, d_b, H * rb, slots, k, hb, yb, xq, xb, wh, 0, 0, t)
+    ga, gb = down(hip, xa, np.float32, t * H), down(hip, xb, np.float32, t * H)
+    assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), int((ga != gb).sum())
+    want = x0.astype(np.float64).copy()
+    for tt in range(t):
+        for j in range(k):
+            e = sl[tt * k + j]
+            if e >= 0 and w[tt * k + j] != 0:
+                want[tt] += w[tt * k + j] * O.matvec(ty, dn[e * H:(e + 1) * H], H, F, h[tt * k + j])
+    assert max_rel_err(gb.reshape(t, H), want) <= TOL
 
 
 def test_errors_do_not_launch(hip):
