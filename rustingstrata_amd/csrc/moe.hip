@@ -1,16 +1,12 @@
 // MoE routing, the stable sort of (token, expert) pairs with its tile lists, and the combines.
 #include "moe.h"
+#include "route.h"
 #include "xlane.h"
 
 namespace strata {
 
-// exp for the router and SwiGLU: exp in double, rounded once to f32. This is the correctly rounded f32 exp except
-// in vanishingly rare cases, and so agrees with the host libm expf the reference calls (src/ops.rs:14-24) wherever
-// that one is correctly rounded.
-__device__ __forceinline__ float exp_f32(float x) { return (float)exp((double)x); }
-
-// ---- routing: one wave64 per token (Model::route src/model.rs:837-851; topk_warp src/cuda/kernels.cu:2633-2686) ----
-// ROUTE_R logits per lane (n <= 64 ROUTE_R): an instantiation per 1, 2, 4, 8, so a 128-expert router scans 2 a lane.
+// ---- routing (Model::route src/model.rs:837-851; topk_warp src/cuda/kernels.cu:2633-2686) ----
+// One wave64 per token, ROUTE_R logits per lane (n <= 64 ROUTE_R): an instantiation per 1, 2, 4, 8.
 template <int ROUTE_R>
 __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p, int n, int k, float extra_scale,
                                                     const int* __restrict__ table, int* ids, float* wts, int* slots,
@@ -19,106 +15,12 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + wave;
     if (t >= T) return;  // whole waves only
-    const float* pr = p + (uint64_t)t * n;
-    float v[ROUTE_R];
-#pragma unroll
-    for (int r = 0; r < ROUTE_R; r++) { int i = lane + 64 * r; v[r] = i < n ? pr[i] : -INFINITY; }
-    // the slot table's entries, fetched with the logits (the chosen ones are read from these registers at the end)
-    int tv[ROUTE_R];
-#pragma unroll
-    for (int r = 0; r < ROUTE_R; r++) { int i = lane + 64 * r; tv[r] = table && i < n ? table[i] : -1; }
-    if (sigmoid) {
-#pragma unroll
-        for (int r = 0; r < ROUTE_R; r++) v[r] = 1.0f / (1.0f + exp_f32(-v[r]));  // ops::sigmoid
-    } else {
-        // ops::softmax: m = max, v = exp(v - m), s = the sum in index order, v /= s.
-        float m = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < ROUTE_R; r++) m = fmaxf(m, v[r]);
-        m = fmaxf(m, xl32f<0>(m));
-        m = fmaxf(m, xl32f<1>(m));
-        m = fmaxf(m, xl32f<2>(m));
-        m = fmaxf(m, xl32f<3>(m));
-        m = fmaxf(m, xl32f<4>(m));
-        m = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0)),
-                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32)));
-#pragma unroll
-        for (int r = 0; r < ROUTE_R; r++) {
-            int i = lane + 64 * r;
-            if (i < n) v[r] = exp_f32(v[r] - m);
-            se[wave][i] = i < n ? v[r] : 0.0f;  // entries past n add +0: the sum keeps its bits
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        // one lane adds in index order (the reference's sum): 64 values a chunk read ahead into registers, 4 per LDS
-        // access, then added one by one
-        float s = 0.0f;
-        if (lane == 0) {
-#pragma unroll
-            for (int c = 0; c < 64 * ROUTE_R; c += 64) {
-                float4 q[16];
-#pragma unroll
-                for (int u = 0; u < 16; u++) q[u] = *(const float4*)&se[wave][c + 4 * u];
-#pragma unroll
-                for (int u = 0; u < 16; u++) {
-                    s += q[u].x;
-                    s += q[u].y;
-                    s += q[u].z;
-                    s += q[u].w;
-                }
-            }
-        }
-        s = __shfl(s, 0);
-#pragma unroll
-        for (int r = 0; r < ROUTE_R; r++) v[r] = v[r] / s;
-    }
-    // ops::top_k: k rounds of the wave's largest value, ties to the lower index. v >= 0, so its bits order as it;
-    // key = bits + 1, 0 for taken or absent entries. A round takes the largest key by 32-bit max steps, then the
-    // lowest index holding it from ballots in index order (entry r of lane l is index 64 r + l).
-    uint32_t key[ROUTE_R];
-#pragma unroll
-    for (int r = 0; r < ROUTE_R; r++) key[r] = lane + 64 * r < n ? __float_as_uint(v[r]) + 1u : 0u;
-    int my_id = 0;
-    float my_p = 0.0f;
-    for (int j = 0; j < k; j++) {
-        uint32_t best = key[0];
-#pragma unroll
-        for (int r = 1; r < ROUTE_R; r++) best = max(best, key[r]);
-        best = max(best, (uint32_t)xl32<0>((int)best));
-        best = max(best, (uint32_t)xl32<1>((int)best));
-        best = max(best, (uint32_t)xl32<2>((int)best));
-        best = max(best, (uint32_t)xl32<3>((int)best));
-        best = max(best, (uint32_t)xl32<4>((int)best));
-        best = max((uint32_t)__builtin_amdgcn_readlane((int)best, 0), (uint32_t)__builtin_amdgcn_readlane((int)best, 32));
-        int bi = 0;
-#pragma unroll
-        for (int r = 0; r < ROUTE_R; r++) {
-            const uint64_t m = __ballot(key[r] == best);
-            if (m) {
-                bi = 64 * r + (int)__builtin_ctzll(m);
-                break;
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < ROUTE_R; r++)
-            if (bi == 64 * r + lane) key[r] = 0u;
-        if (lane == j) { my_id = bi; my_p = __uint_as_float(best - 1u); }
-    }
-    // Weights: p / max(sum of the top k in rank order, 2^-14) (times extra_scale when not 0).
-    float sum = 0.0f;
-    for (int j = 0; j < k; j++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_p), j));
-    float scale = 1.0f / fmaxf(sum, 6.103515625e-5f);
-    if (extra_scale != 0.0f) scale *= extra_scale;
-    int slot = -1;  // table[my_id]: entry my_id >> 6 of lane my_id & 63
-#pragma unroll
-    for (int r = 0; r < ROUTE_R; r++) {
-        const int c = __shfl(tv[r], my_id & 63);
-        if ((my_id >> 6) == r) slot = c;
-    }
+    int id, slot;
+    float w;
+    route_wave<ROUTE_R>(p + (uint64_t)t * n, n, k, extra_scale, table, sigmoid, se[wave], id, w, slot);
     if (lane < k) {
-        int o = t * k + lane;
-        float w = my_p * scale;
-        ids[o] = my_id;
+        const int o = t * k + lane;
+        ids[o] = id;
         wts[o] = w;
         if (table) {
             slots[o] = slot;
@@ -127,9 +29,34 @@ __global__ __launch_bounds__(256) void route_kernel(const float* __restrict__ p,
     }
 }
 
+// A 256-thread block per token (n <= 128: few tokens, where the route's latency is the cost).
+__global__ __launch_bounds__(256) void route_block_kernel(const float* __restrict__ p, int n, int k, float extra_scale,
+                                                          const int* __restrict__ table, int* ids, float* wts,
+                                                          int* slots, float* wh, int sigmoid) {
+    __shared__ RouteLds L;
+    const int t = blockIdx.x;
+    int id, slot;
+    float w;
+    route_block4(p + (uint64_t)t * n, n, k, extra_scale, table, sigmoid, &L, id, w, slot);
+    if (threadIdx.x < k) {
+        const int o = t * k + threadIdx.x;
+        ids[o] = id;
+        wts[o] = w;
+        if (table) {
+            slots[o] = slot;
+            wh[o] = slot >= 0 ? w : 0.0f;
+        }
+    }
+}
+
+constexpr int ROUTE_BLOCK_MAX_T = 16;  // tokens up to which each gets a block of its own
 hipError_t launch_route(const float* p, int n, int k, float extra_scale, const int* table, int* ids, float* wts,
                         int* slots, float* wh, int t, int sigmoid, hipStream_t s) {
     const dim3 grid((unsigned)((t + 3) / 4)), block(256);
+    if (n <= 128 && k <= 32 && t <= ROUTE_BLOCK_MAX_T) {
+        route_block_kernel<<<dim3((unsigned)t), block, 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, sigmoid);
+        return hipGetLastError();
+    }
     if (n <= 64) route_kernel<1><<<grid, block, 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);
     else if (n <= 128) route_kernel<2><<<grid, block, 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);
     else if (n <= 256) route_kernel<4><<<grid, block, 0, s>>>(p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid);

@@ -967,3 +967,55 @@ def test_moe_gemv_one_slot_not_resident(hip):
             assert np.all(got == np.float32(3.5))
         else:
             assert max_rel_err(got, O.matvec(ty, wblk[e * rows:(e + 1) * rows], rows, cols, x)) <= TOL
+
+
+def _division_tie_logits(count, seed):
+    """Router logit rows (128 experts) in which two experts among the top 8 have different exp(v - max) that the
+    softmax's division by the sum rounds to one p: the tie the reference breaks by index (ops::top_k), which the
+    ranking of the unnormalised values would order the other way when the larger one has the higher index."""
+    rng = np.random.default_rng(seed)
+    rows, flips = [], 0
+    while len(rows) < count:
+        v = (rng.standard_normal(128) * 0.3).astype(np.float32)
+        order = np.argsort(-v)
+        a, b = order[rng.integers(1, 7)], order[rng.integers(9, 40)]
+        m = v.max()
+        ea = np.float32(np.exp(np.float64(np.float32(v[a] - m))))
+        x, target = v[a], np.nextafter(ea, np.float32(0))
+        for _ in range(50):
+            x = np.nextafter(x, np.float32(-np.inf))
+            eb = np.float32(np.exp(np.float64(np.float32(x - m))))
+            if eb <= target:
+                break
+        if eb != target:
+            continue
+        v[b] = x
+        e = np.exp((v - m).astype(np.float32).astype(np.float64)).astype(np.float32)
+        p = (e / np.cumsum(e, dtype=np.float32)[-1]).astype(np.float32)
+        if e[a] != e[b] and p[a] == p[b]:
+            rows.append(v)
+            flips += int(b < a)
+    return np.stack(rows), flips
+
+
+def test_route_division_ties(hip):
+    """The per-token route (a block per token for up to 16 tokens) on rows with a tie made by the softmax's division
+    (some with the larger e at the higher index, which the ranking of e alone would get wrong), and sigmoid rows:
+    ids bit-exact with ops::top_k's, weights to 1e-6, slots and wh from the table."""
+    logits, flips = _division_tie_logits(12, seed=7)
+    assert flips >= 3  # cases where the tie reverses the order of the unnormalised values
+    n, k, t = 128, 8, logits.shape[0]
+    for lg, sig in [(logits, False), (zipf_logits(5, 100, seed=8), True), (zipf_logits(16, 128, seed=9), False)]:
+        tt = lg.shape[0]
+        table = np.arange(lg.shape[1], dtype=np.int32)
+        table[::5] = -1
+        bufs = [hip.alloc(tt * k * 4) for _ in range(4)]
+        hip.moe_route(up(hip, lg), lg.shape[1], k, 0.0, up(hip, table), *bufs, tt, sig)
+        ids, wts, slots, wh = [down(hip, b, dt, tt * k) for b, dt in
+                               zip(bufs, (np.int32, np.float32, np.int32, np.float32))]
+        wi, ww = O.route(lg, k, sigmoid=sig)
+        assert np.array_equal(ids, wi.reshape(-1))
+        assert np.abs(wts - ww.reshape(-1)).max() <= 1e-6
+        assert np.array_equal(slots, table[ids])
+        assert np.array_equal(wh, np.where(slots >= 0, wts, 0.0).astype(np.float32))
+    assert t == 12
