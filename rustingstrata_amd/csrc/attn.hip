@@ -49,6 +49,9 @@ __device__ __forceinline__ float wave_sum64(float v) {
            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
+// Word i (0..3, a constant) of v.
+__device__ __forceinline__ uint32_t u4c(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+
 // Positions of token t: base .. end (inclusive); a sliding window keeps the last `win`.
 __device__ __forceinline__ void att_range(const int* step, int t, int win, int& base, int& n_pos) {
     const int end = step[2 * t];
@@ -57,139 +60,204 @@ __device__ __forceinline__ void att_range(const int* step, int t, int win, int& 
 }
 
 // ---------------- decode ----------------
-// Positions a split of a token with n_pos positions: at least 16, so short contexts use few waves.
-__device__ __forceinline__ int split_len(int n_pos, int ns) { return max((n_pos + ns - 1) / ns, 16); }
+// Positions a split of a token with n_pos positions: at least one chunk of 64, so short contexts use few waves.
+__device__ __forceinline__ int split_len(int n_pos, int ns) { return max((n_pos + ns - 1) / ns, 64); }
+
+// Layout of the K tile ([key][dim]) and the V tile transposed ([dim][key]) in LDS, 64 keys.
+template <int HD> struct PfLayout {
+    static constexpr int KP = HD + 8;          // halves per K row in LDS (16-byte pad: rows start in spread banks)
+    static constexpr int VP = 64 + 4;          // halves per V^T row (8-byte pad)
+};
 
 // grid (ATT_SPLITS, nkv, nt), one wave a block. Wave (s, g, t) serves the G = nh / nkv query heads of KV head g over
-// the s-th share of token t's positions, in chunks of 64 positions with no block barrier:
-//   the chunk's K and V rows come into LDS by coalesced 16-byte loads, all in flight together (one memory round
-//     trip a chunk);
-//   scores: lane r holds position r of the chunk and dots its K row with the G query heads (read as broadcasts);
-//     the online softmax of each head is a wave reduction;
-//   P V: the weights go through LDS, lane l owns 2 (or 1) consecutive dims and adds p V over the chunk's rows.
-// The loops over dims and positions stay rolled (a few unrolled steps): the code stays small enough for the
-// instruction cache, which a fully unrolled body (a few thousand instructions) did not.
+// the s-th share of token t's positions, 64 keys a chunk, on f16 MFMA (v_mfma_f32_16x16x32_f16) with f32 accuracy:
+// the G heads are the MFMA's 16 columns (padded), so
+//   S^T (16 keys x 16 heads, 4 key sub-tiles kt) = K (A: key row, 8 dims a lane) Q^T (B: head column; q split into
+//   f16 hi and lo after scaling it by a power of two that puts its largest value in [2^13, 2^14));
+//   the online softmax of a head runs over the lane's 16 values and its 4 lane groups;
+//   O^T (16 dims x 16 heads, DT dim tiles) += V^T (A: dim row, 8 keys) P^T (B: the lane's own weights, times 2^14,
+//   split hi and lo), the keys of each K-step the same in both operands.
+// K and V rows arrive by 16-byte loads, all in flight together (one memory round trip a chunk; lane l loads keys
+// 4 (l % 16) .. + 3, dims HD / 4 (l / 16) .. of each), K stored as is, V transposed 4 keys a write.
 // The wave leaves [acc (hd) | max | sum] per head in part; attn_merge_kernel combines the splits.
 template <int HD, int G>
 __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                          const uint16_t* __restrict__ vc, float* __restrict__ part,
                                                          const int* step, int nh, int nkv, float scale, int win) {
-    constexpr int C = 64, DL = HD / 64, GP = (G + 3) / 4 * 4;  // positions a chunk; dims a lane in P V; padded G
-    constexpr int KP = HD + 8;                                  // halves per staged K row (16-byte pad: spread banks)
-    __shared__ __align__(16) float sq[G][HD];
-    __shared__ __align__(16) float sp[C][GP];
-    __shared__ __align__(16) uint16_t sk[C * KP];
-    __shared__ __align__(16) uint16_t sv[C * HD];
-    const int split = blockIdx.x, g = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+    using L = PfLayout<HD>;
+    constexpr int KS = HD / 32, DT = HD / 16, DW = HD / 4, NL = DW / 8;  // dims a lane loads; 16-byte loads a key
+    __shared__ __align__(16) uint16_t ks[64 * L::KP];
+    __shared__ __align__(16) uint16_t vs[HD * L::VP];
+    const int split = blockIdx.x, g = blockIdx.y, t = blockIdx.z, lane = threadIdx.x, l16 = lane & 15, lg = lane >> 4;
     const int h0 = g * G, ns = gridDim.x;
+    const uint64_t kvd = (uint64_t)nkv * HD;
+    // the query first (it does not depend on the position), then the first chunk's K and V rows as soon as the
+    // position is known, so the round trips overlap
+    f4 qv[2 * KS];  // dims 32 k + 8 lg .. + 3 and + 4 .. + 7
+    {
+        const float* qr = q + (uint64_t)t * nh * HD + (uint64_t)(h0 + l16) * HD;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            qv[2 * k] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+            qv[2 * k + 1] = qv[2 * k];
+            if (l16 < G) {
+                qv[2 * k] = *(const f4*)(qr + 32 * k + 8 * lg);
+                qv[2 * k + 1] = *(const f4*)(qr + 32 * k + 8 * lg + 4);
+            }
+        }
+    }
     int base, n_pos;
     att_range(step, t, win, base, n_pos);
     const int per_s = split_len(n_pos, ns);
     const int p0 = split * per_s, p1 = min(n_pos, p0 + per_s);
-    float* pp = part + ((uint64_t)(t * nh + h0) * ns + split) * (HD + 2);
-    const uint64_t pstride = (uint64_t)ns * (HD + 2);  // between heads
     if (p0 >= n_pos) return;  // past the token's positions: the merge reads only the splits that have some
-    for (int i = lane; i < G * HD / 4; i += 64)
-        ((float4*)&sq[0][0])[i] = *(const float4*)(q + (uint64_t)t * nh * HD + h0 * HD + 4 * i);
-    const uint64_t kvd = (uint64_t)nkv * HD;
-    float m[G], l[G], acc[G][DL];
+    // Q^T fragments: head h0 + l16 (zero past G), dims 32 k + 8 lg .. + 7; usc undoes the scaling (times `scale`)
+    h8 qh[KS], ql[KS];
+    float usc = 0.0f;
+    f4 o[DT];
 #pragma unroll
-    for (int i = 0; i < G; i++) {
-        m[i] = -INFINITY;
-        l[i] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < DL; d++) acc[i][d] = 0.0f;
-    }
-    for (int c0 = p0; c0 < p1; c0 += C) {
-        const int nc = min(C, p1 - c0);
-        // the chunk's K and V rows into LDS with coalesced 16-byte loads, all in flight together (rows past nc repeat
-        // row nc - 1; their weights are 0)
+    for (int d = 0; d < DT; d++) o[d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    for (int c0 = p0; c0 < p1; c0 += 64) {
+        const int nc = min(64, p1 - c0);
         {
-            constexpr int PER = C * HD / 8 / 64;  // 16-byte pieces a lane of each of K and V
-            uint4 kb[PER], vb[PER];
+            // the chunk's K and V rows into registers (keys past nc repeat key nc - 1: finite, and their weights
+            // are 0)
+            uint4 kb[4][NL], vb[4][NL];
 #pragma unroll
-            for (int j = 0; j < PER; j++) {
-                const int i = lane + 64 * j, r = i / (HD / 8), c = (i % (HD / 8)) * 8;
-                const uint64_t off = (uint64_t)(base + c0 + min(r, nc - 1)) * kvd + g * HD + c;
-                kb[j] = *(const uint4*)(kc + off);
-                vb[j] = *(const uint4*)(vc + off);
+            for (int kk = 0; kk < 4; kk++) {
+                const uint64_t off = (uint64_t)(base + c0 + min(4 * l16 + kk, nc - 1)) * kvd + g * HD + DW * lg;
+#pragma unroll
+                for (int j = 0; j < NL; j++) {
+                    kb[kk][j] = *(const uint4*)(kc + off + 8 * j);
+                    vb[kk][j] = *(const uint4*)(vc + off + 8 * j);
+                }
+            }
+            if (c0 == p0) {
+                // the query's fragments while the first chunk's rows are in flight: scaled by the power of two
+                // that puts its largest value in [2^13, 2^14), so the lo parts stay normal f16 numbers
+                float mx = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 2 * KS; k++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) mx = fmaxf(mx, fabsf(qv[k][e]));
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                int ex = 0;
+                if (mx > 0.0f) (void)frexpf(mx, &ex);  // mx < 2^ex
+                const float up = ldexpf(1.0f, 14 - ex);
+                usc = ldexpf(scale, ex - 14);
+#pragma unroll
+                for (int k = 0; k < KS; k++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float x = qv[2 * k + (e >> 2)][e & 3] * up;
+                        const _Float16 hi = (_Float16)x;
+                        qh[k][e] = hi;
+                        ql[k][e] = (_Float16)(x - (float)hi);
+                    }
             }
 #pragma unroll
-            for (int j = 0; j < PER; j++) {
-                const int i = lane + 64 * j, r = i / (HD / 8), c = (i % (HD / 8)) * 8;
-                *(uint4*)&sk[r * KP + c] = kb[j];
-                *(uint4*)&sv[r * HD + c] = vb[j];
-            }
+            for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+                for (int j = 0; j < NL; j++) *(uint4*)&ks[(4 * l16 + kk) * L::KP + DW * lg + 8 * j] = kb[kk][j];
+#pragma unroll
+            for (int j = 0; j < NL; j++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int sh = 16 * (e & 1);
+                    const uint32_t a0 = (u4c(vb[0][j], e >> 1) >> sh) & 0xFFFFu, a1 = (u4c(vb[1][j], e >> 1) >> sh) & 0xFFFFu;
+                    const uint32_t a2 = (u4c(vb[2][j], e >> 1) >> sh) & 0xFFFFu, a3 = (u4c(vb[3][j], e >> 1) >> sh) & 0xFFFFu;
+                    *(uint2*)&vs[(DW * lg + 8 * j + e) * L::VP + 4 * l16] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
+                }
         }
         __builtin_amdgcn_wave_barrier();
-        // scores of position c0 + lane: its K row from LDS, the G query heads as broadcasts
-        float s[G];
+        // S^T: lane holds keys 16 kt + 4 lg + i of head l16
+        f4 s[4];
 #pragma unroll
-        for (int i = 0; i < G; i++) s[i] = 0.0f;
-#pragma unroll 2
-        for (int c = 0; c < HD / 8; c++) {
-            const uint4 kv = *(const uint4*)&sk[lane * KP + 8 * c];
-            const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
-            float kf[8];
+        for (int kt = 0; kt < 4; kt++) {
+            f4 c = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int e = 0; e < 8; e++) kf[e] = h2f((uint16_t)(w4[e >> 1] >> (16 * (e & 1))));
+            for (int k = 0; k < KS; k++) {
+                const h8 kf = *(const h8*)&ks[(16 * kt + l16) * L::KP + 32 * k + 8 * lg];
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[k], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[k], c, 0, 0, 0);
+            }
+            s[kt] = c;
+        }
+        // online softmax of head l16 over the chunk
+        float mx = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < G; i++) {
-                const float4 qa = *(const float4*)&sq[i][8 * c], qb = *(const float4*)&sq[i][8 * c + 4];
-                s[i] += qa.x * kf[0];
-                s[i] += qa.y * kf[1];
-                s[i] += qa.z * kf[2];
-                s[i] += qa.w * kf[3];
-                s[i] += qb.x * kf[4];
-                s[i] += qb.y * kf[5];
-                s[i] += qb.z * kf[6];
-                s[i] += qb.w * kf[7];
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v = s[kt][i] * usc;
+                if (16 * kt + 4 * lg + i >= nc) v = -INFINITY;
+                s[kt][i] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m, mx);
+        const float alpha = m == -INFINITY ? 0.0f : expf(m - mnew);
+        float sum = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float p = s[kt][i] == -INFINITY ? 0.0f : expf(s[kt][i] - mnew);
+                s[kt][i] = p;
+                sum += p;
+            }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        l = l * alpha + sum;
+        m = mnew;
+#pragma unroll
+        for (int d = 0; d < DT; d++) o[d] *= alpha;
+        // O^T += V^T P^T: K-step c takes keys 32 c + 16 (e / 4) + 4 lg + e % 4 as its K-element e
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            h8 ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                // p in [0, 1] times 2^14: the lo parts stay normal down to p ~ 2^-17
+                const float p = s[2 * c + (e >> 2)][e & 3] * 16384.0f;
+                const _Float16 hi = (_Float16)p;
+                ph[e] = hi;
+                pl[e] = (_Float16)(p - (float)hi);
+            }
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+                const uint16_t* vr = &vs[(16 * d + l16) * L::VP + 32 * c + 4 * lg];
+                const uint2 a0 = *(const uint2*)vr, a1 = *(const uint2*)(vr + 16);
+                h8 vf;
+                const uint32_t w4[4] = {a0.x, a0.y, a1.x, a1.y};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint16_t b = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+                    _Float16 hv;
+                    __builtin_memcpy(&hv, &b, 2);
+                    vf[e] = hv;
+                }
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
             }
         }
-        // online softmax per head over the chunk
-        float alpha[G];
-#pragma unroll
-        for (int i = 0; i < G; i++) {
-            const float v = lane < nc ? s[i] * scale : -INFINITY;
-            const float mnew = fmaxf(m[i], wave_max64(v));
-            const float p = v == -INFINITY ? 0.0f : expf(v - mnew);
-            const float sum = wave_sum64(p);
-            alpha[i] = m[i] == -INFINITY ? 0.0f : expf(m[i] - mnew);
-            l[i] = l[i] * alpha[i] + sum;
-            m[i] = mnew;
-            sp[lane][i] = p;
-        }
-        __builtin_amdgcn_wave_barrier();
-        // P V: lane owns dims DL lane .. DL lane + DL - 1
-#pragma unroll
-        for (int i = 0; i < G; i++)
-#pragma unroll
-            for (int d = 0; d < DL; d++) acc[i][d] *= alpha[i];
-#pragma unroll 4
-        for (int r = 0; r < nc; r++) {
-            float pv[GP];
-#pragma unroll
-            for (int i = 0; i < GP; i += 4) {
-                const float4 p4 = *(const float4*)&sp[r][i];
-                pv[i] = p4.x; pv[i + 1] = p4.y; pv[i + 2] = p4.z; pv[i + 3] = p4.w;
-            }
-            const uint32_t vw = DL == 2 ? *(const uint32_t*)&sv[r * HD + 2 * lane] : (uint32_t)sv[r * HD + lane];
-#pragma unroll
-            for (int d = 0; d < DL; d++) {
-                const float vf = h2f((uint16_t)(vw >> (16 * d)));
-#pragma unroll
-                for (int i = 0; i < G; i++) acc[i][d] += pv[i] * vf;
-            }
-        }
-        __builtin_amdgcn_wave_barrier();  // sp, sk and sv are rewritten by the next chunk
+        __builtin_amdgcn_wave_barrier();  // ks and vs are rewritten by the next chunk
     }
+    // partials of head h0 + l16: dims 16 d + 4 lg + i (the weights' 2^14 taken out), max and sum
+    if (l16 < G) {
+        float* pp = part + ((uint64_t)(t * nh + h0 + l16) * ns + split) * (HD + 2);
 #pragma unroll
-    for (int i = 0; i < G; i++) {
+        for (int d = 0; d < DT; d++) {
+            const float r = 1.0f / 16384.0f;
 #pragma unroll
-        for (int d = 0; d < DL; d++) pp[i * pstride + DL * lane + d] = acc[i][d];
-        if (lane == 0) {
-            pp[i * pstride + HD] = m[i];
-            pp[i * pstride + HD + 1] = l[i];
+            for (int i = 0; i < 4; i++) pp[16 * d + 4 * lg + i] = o[d][i] * r;
+        }
+        if (lg == 0) {
+            pp[HD] = m;
+            pp[HD + 1] = l;
         }
     }
 }
@@ -285,14 +353,7 @@ hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t
 //   O^T (16 dims x 16 queries, 8 dim tiles dt) += V^T (A: dim row, 8 keys) P^T hi and lo (B: the lane's own p values:
 //   keys 4 (l / 16) + i of sub-tiles 2 c and 2 c + 1 make the 8 K-elements of k-step c, and V^T's A fragment reads
 //   the same keys).
-constexpr int PF_BQ = 32, PF_BK = 64;
-
-template <int HD> struct PfLayout {
-    static constexpr int KP = HD + 8;          // halves per K row in LDS (16-byte pad: rows start in spread banks)
-    static constexpr int VP = PF_BK + 4;       // halves per V^T row (8-byte pad)
-    static constexpr int KBYTES = PF_BK * KP * 2;
-    static constexpr int VBYTES = HD * VP * 2;
-};
+constexpr int PF_BQ = 32, PF_BK = 64;  // query rows, keys a tile (PfLayout's 64)
 
 template <int HD, int G>
 __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
