@@ -296,50 +296,70 @@ hipError_t launch_gemv_f32(const float* w, int rows, int cols, const float* x, u
     return hipGetLastError();
 }
 
-// ---- f32-weight GEMM (gemm_dense of a float matrix): 32 positions x 32 weight rows a block (so a 2048-token chunk
-// times the 128 router rows fills 256 blocks), K in steps of 32 through LDS, the next step's values loaded into
-// registers while this one is summed. Each output's dot runs over k in index order with a multiply then an add, as
-// Tensor::matvec's f32 iterator sum (src/weights.rs:29-37): the CPU's bits. ----
-constexpr int GF_T = 32, GF_K = 32;
+// ---- f32-weight GEMM (gemm_dense of a float matrix): each output's dot runs over k in index order with a multiply
+// then an add, as Tensor::matvec's f32 iterator sum (src/weights.rs:29-37): the CPU's bits. That makes every output
+// one dependent chain of 2 cols instructions, so the kernel is built for VALU throughput with two waves a SIMD: a
+// block of 4 waves takes 64 positions (a lane each) x 8 weight rows (2 a wave, 2 chains a lane); per step of 64 k the
+// block stages x transposed ([k][position]: a lane's reads hit distinct banks) and the 8 rows' weights in LDS, and a
+// lane reads its x value once per k and the weights as wave-wide broadcasts (one 16-byte read for 4 k of a row). ----
+constexpr int GF_M = 64, GF_RW = 2, GF_R = 4 * GF_RW, GF_K = 64;  // GF_RW rows (chains) a wave
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ w, int rows, int cols,
                                                        const float* __restrict__ x, uint64_t x_stride, float* y,
                                                        uint64_t y_stride, int n, int act) {
-    __shared__ float xs[GF_K][GF_T + 1], ws[GF_K][GF_T + 1];
-    const int m0 = blockIdx.x * GF_T, r0 = blockIdx.y * GF_T, tid = threadIdx.x;
-    const int tm = tid >> 4, tr = tid & 15;  // outputs: positions m0 + tm + 16 i, rows r0 + tr + 16 j (i, j < 2)
-    const int lr = tid >> 3, lk = 4 * (tid & 7);  // loads: row lr of each tile, k k0 + lk .. + 3
-    float acc[2][2] = {};
-    auto load = [&](int k0, float4& xv, float4& wv) {
-        xv = make_float4(0.f, 0.f, 0.f, 0.f);
-        wv = xv;
-        if (m0 + lr < n && k0 + lk < cols) xv = *(const float4*)(x + (uint64_t)(m0 + lr) * x_stride + k0 + lk);
-        if (r0 + lr < rows && k0 + lk < cols) wv = *(const float4*)(w + (uint64_t)(r0 + lr) * cols + k0 + lk);
+    __shared__ __align__(16) float xs[GF_K][GF_M + 1];  // (+1: the staging writes spread over banks)
+    __shared__ __align__(16) float ws[GF_R][GF_K];
+    const int m0 = blockIdx.x * GF_M, r0 = blockIdx.y * GF_R, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // staging: x rows m0 + tid / KQ + SP i (i < NP), k k0 + 4 (tid % KQ) .. + 3; w row r0 + tid / KQ (< GF_R)
+    constexpr int KQ = GF_K / 4, SP = 256 / KQ, NP = GF_M / SP;
+    static_assert(GF_R <= SP, "one pass stages the weight rows");
+    const int sm = tid / KQ, sk = 4 * (tid % KQ);
+    float acc[GF_RW] = {};
+    float4 xv[NP], wv;
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < NP; i++) {
+            const int m = m0 + sm + SP * i;
+            xv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (m < n && k0 + sk < cols) xv[i] = *(const float4*)(x + (uint64_t)m * x_stride + k0 + sk);
+        }
+        wv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (sm < GF_R && r0 + sm < rows && k0 + sk < cols) wv = *(const float4*)(w + (uint64_t)(r0 + sm) * cols + k0 + sk);
     };
-    float4 xv, wv;
-    load(0, xv, wv);
+    load(0);
     for (int k0 = 0; k0 < cols; k0 += GF_K) {
         __syncthreads();
-        xs[lk][lr] = xv.x; xs[lk + 1][lr] = xv.y; xs[lk + 2][lr] = xv.z; xs[lk + 3][lr] = xv.w;
-        ws[lk][lr] = wv.x; ws[lk + 1][lr] = wv.y; ws[lk + 2][lr] = wv.z; ws[lk + 3][lr] = wv.w;
-        __syncthreads();
-        if (k0 + GF_K < cols) load(k0 + GF_K, xv, wv);
 #pragma unroll
-        for (int k = 0; k < GF_K; k++) {
-            const float a0 = xs[k][tm], a1 = xs[k][tm + 16], b0 = ws[k][tr], b1 = ws[k][tr + 16];
-            acc[0][0] += a0 * b0; acc[0][1] += a0 * b1;
-            acc[1][0] += a1 * b0; acc[1][1] += a1 * b1;
+        for (int i = 0; i < NP; i++) {
+            const int m = sm + SP * i;
+            xs[sk][m] = xv[i].x; xs[sk + 1][m] = xv[i].y; xs[sk + 2][m] = xv[i].z; xs[sk + 3][m] = xv[i].w;
+        }
+        if (sm < GF_R) *(float4*)&ws[sm][sk] = wv;
+        __syncthreads();
+        if (k0 + GF_K < cols) load(k0 + GF_K);
+        const int kn = min(GF_K, cols - k0);
+        const float* wr = &ws[GF_RW * wave][0];
+        // the whole step unrolled (cols % 4 == 0; a shorter last step ends early), so its LDS reads run ahead
+#pragma unroll
+        for (int k = 0; k < GF_K; k += 4) {
+            if (k >= kn) break;
+            const float a[4] = {xs[k][lane], xs[k + 1][lane], xs[k + 2][lane], xs[k + 3][lane]};
+            float4 wj[GF_RW];
+#pragma unroll
+            for (int j = 0; j < GF_RW; j++) wj[j] = *(const float4*)(wr + j * GF_K + k);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int j = 0; j < GF_RW; j++) acc[j] += a[e] * (e == 0 ? wj[j].x : e == 1 ? wj[j].y : e == 2 ? wj[j].z : wj[j].w);
         }
     }
+    const int m = m0 + lane;
+    if (m < n) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int m = m0 + tm + 16 * i;
-        if (m >= n) continue;
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int r = r0 + tr + 16 * j;
+        for (int j = 0; j < GF_RW; j++) {
+            const int r = r0 + GF_RW * wave + j;
             if (r >= rows) continue;
             float* yo = y + (uint64_t)m * y_stride + r;
-            const float v = acc[i][j];
+            const float v = acc[j];
             *yo = act == 0 ? v : act == 1 ? silu_f32(*yo) * v : *yo + v;
         }
     }
@@ -348,7 +368,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 hipError_t launch_gemm_f32(const float* w, int rows, int cols, const float* x, uint64_t x_stride, float* y,
                            uint64_t y_stride, int n, int act, hipStream_t s) {
     if (!rows || !n) return hipSuccess;
-    gemm_f32_kernel<<<dim3((unsigned)((n + GF_T - 1) / GF_T), (unsigned)((rows + GF_T - 1) / GF_T)), dim3(256), 0, s>>>(
+    gemm_f32_kernel<<<dim3((unsigned)((n + GF_M - 1) / GF_M), (unsigned)((rows + GF_R - 1) / GF_R)), dim3(256), 0, s>>>(
         w, rows, cols, x, x_stride, y, y_stride, n, act);
     return hipGetLastError();
 }
