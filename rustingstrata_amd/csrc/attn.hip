@@ -49,6 +49,12 @@ __device__ __forceinline__ float wave_sum64(float v) {
            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
+// 2^x by the hardware's v_exp_f32 (within 1 ulp; 2^-inf = 0). The softmaxes work in log2 units: scores times log2(e)
+// (one rounding, relative 2^-24 of the exponent, so about |s| 2^-24 ln 2 of each weight: ~1e-7 for the scores that
+// carry the weight), then exp2 of the difference from the running maximum.
+constexpr float LOG2E = 1.44269504088896341f;
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Word i (0..3, a constant) of v.
 __device__ __forceinline__ uint32_t u4c(const uint4& v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
 
@@ -79,7 +85,7 @@ template <int HD> struct PfLayout {
 //   split hi and lo), the keys of each K-step the same in both operands.
 // K and V rows arrive by 16-byte loads, all in flight together (one memory round trip a chunk; lane l loads keys
 // 4 (l % 16) .. + 3, dims HD / 4 (l / 16) .. of each), K stored as is, V transposed 4 keys a write.
-// The wave leaves [acc (hd) | max | sum] per head in part; attn_merge_kernel combines the splits.
+// The wave leaves [acc (hd) | max | sum] per head in part (max in log2 units); attn_merge_kernel combines the splits.
 template <int HD, int G>
 __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                          const uint16_t* __restrict__ vc, float* __restrict__ part,
@@ -146,7 +152,7 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
                 int ex = 0;
                 if (mx > 0.0f) (void)frexpf(mx, &ex);  // mx < 2^ex
                 const float up = ldexpf(1.0f, 14 - ex);
-                usc = ldexpf(scale, ex - 14);
+                usc = ldexpf(scale * LOG2E, ex - 14);  // scores in log2 units: the softmax's exps are exp2s
 #pragma unroll
                 for (int k = 0; k < KS; k++)
 #pragma unroll
@@ -199,13 +205,13 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mnew = fmaxf(m, mx);
-        const float alpha = m == -INFINITY ? 0.0f : expf(m - mnew);
+        const float alpha = m == -INFINITY ? 0.0f : exp2_hw(m - mnew);
         float sum = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float p = s[kt][i] == -INFINITY ? 0.0f : expf(s[kt][i] - mnew);
+                const float p = exp2_hw(s[kt][i] - mnew);  // exp2(-inf) = 0 (every chunk has a key: mnew is finite)
                 s[kt][i] = p;
                 sum += p;
             }
@@ -231,15 +237,7 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
             for (int d = 0; d < DT; d++) {
                 const uint16_t* vr = &vs[(16 * d + l16) * L::VP + 32 * c + 4 * lg];
                 const uint2 a0 = *(const uint2*)vr, a1 = *(const uint2*)(vr + 16);
-                h8 vf;
-                const uint32_t w4[4] = {a0.x, a0.y, a1.x, a1.y};
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const uint16_t b = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
-                    _Float16 hv;
-                    __builtin_memcpy(&hv, &b, 2);
-                    vf[e] = hv;
-                }
+                const h8 vf = __builtin_bit_cast(h8, make_uint4(a0.x, a0.y, a1.x, a1.y));
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
             }
@@ -262,7 +260,8 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
     }
 }
 
-// grid (nh, nt), 4 waves: out = sum_s acc_s e^(m_s - M) / (sum_s l_s e^(m_s - M) + e^(sink - M)) (sigmoid gate).
+// grid (nh, nt), 4 waves: out = sum_s acc_s 2^(m_s - M) / (sum_s l_s 2^(m_s - M) + 2^(sink log2(e) - M)) (sigmoid
+// gate), the maxima in log2 units.
 // Wave w takes splits w, w + 4, ..: their weights (a lane each), then the weighted sum of their partial rows (lane =
 // dims), all of its loads in flight together; the 4 wave sums are added in wave order through LDS.
 template <int HD>
@@ -280,7 +279,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
         const int per_s = split_len(n_pos, ns);
         ns = min(ns, (n_pos + per_s - 1) / per_s);
     }
-    const float sk = sink ? sink[h] : -INFINITY;
+    const float sk = sink ? sink[h] * LOG2E : -INFINITY;  // the splits' maxima are in log2 units
     // this wave's splits: s = wave + 4 i, i < SW (lane i < SW holds split i's max and sum)
     const int sl = wave + 4 * lane;
     const float ms = lane < SW && sl < ns ? pp[sl * (HD + 2) + HD] : -INFINITY;
@@ -294,7 +293,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
     if (lane == 0) sm[wave] = M;
     __syncthreads();
     M = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])), sk);
-    const float e = ms == -INFINITY ? 0.0f : expf(ms - M);
+    const float e = ms == -INFINITY ? 0.0f : exp2_hw(ms - M);
     const float den = wave_sum64(ls * e);
     float o[DL];
 #pragma unroll
@@ -311,7 +310,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
     __syncthreads();
     if (wave) return;
     float dt = sd[0] + sd[1] + sd[2] + sd[3];
-    if (sk != -INFINITY) dt += expf(sk - M);
+    if (sk != -INFINITY) dt += exp2_hw(sk - M);
 #pragma unroll
     for (int d = 0; d < DL; d++) {
         const int dd = DL * lane + d;
@@ -401,7 +400,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
         int ex = 0;
         if (mx > 0.0f) (void)frexpf(mx, &ex);  // mx < 2^ex
         const float up = ldexpf(1.0f, 14 - ex);
-        usc[j] = ldexpf(scale, ex - 14);
+        usc[j] = ldexpf(scale * LOG2E, ex - 14);  // scores in log2 units: the softmax's exps are exp2s
 #pragma unroll
         for (int k = 0; k < KS; k++)
 #pragma unroll
@@ -419,22 +418,37 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
         for (int d = 0; d < DT; d++) o[j][d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
     const int qpos[2] = {pos0 + q0 + l16, pos0 + q0 + 16 + l16};  // the lane's query position per column j
-    for (int k0 = first / PF_BK * PF_BK; k0 <= last; k0 += PF_BK) {
-        __syncthreads();  // the previous tile's readers are done
-        // K tile [key][dim] and V tile transposed [dim][key]; keys past `last` as zeros (finite: p = 0 times them)
-        for (int i = tid; i < PF_BK * HD / 8; i += NTH) {
-            const int key = i % PF_BK, c = (i / PF_BK) * 8, kp = k0 + key;
-            uint4 kv = make_uint4(0, 0, 0, 0), vv = kv;
+    // K tile [key][dim] and V tile transposed [dim][key], chunk i = tid + NTH u of a tile: key i % 64, dims
+    // 8 (i / 64) ..; the next tile's chunks are loaded into registers while this one is computed. Keys past `last`
+    // are zeros (finite: p = 0 times them).
+    constexpr int NPT = PF_BK * HD / 8 / NTH;  // 16-byte chunks a thread of each of K and V
+    uint4 kr[NPT], vr4[NPT];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < NPT; u++) {
+            const int i = tid + NTH * u, key = i % PF_BK, c = (i / PF_BK) * 8, kp = k0 + key;
+            kr[u] = make_uint4(0, 0, 0, 0);
+            vr4[u] = kr[u];
             if (kp <= last) {
-                kv = *(const uint4*)(kc + (uint64_t)kp * kvd + g * HD + c);
-                vv = *(const uint4*)(vc + (uint64_t)kp * kvd + g * HD + c);
+                kr[u] = *(const uint4*)(kc + (uint64_t)kp * kvd + g * HD + c);
+                vr4[u] = *(const uint4*)(vc + (uint64_t)kp * kvd + g * HD + c);
             }
-            *(uint4*)&ks[key * L::KP + c] = kv;
-            const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+        }
+    };
+    const int kbeg = first / PF_BK * PF_BK;
+    fetch(kbeg);
+    for (int k0 = kbeg; k0 <= last; k0 += PF_BK) {
+        __syncthreads();  // the previous tile's readers are done
+#pragma unroll
+        for (int u = 0; u < NPT; u++) {
+            const int i = tid + NTH * u, key = i % PF_BK, c = (i / PF_BK) * 8;
+            *(uint4*)&ks[key * L::KP + c] = kr[u];
+            const uint32_t w4[4] = {vr4[u].x, vr4[u].y, vr4[u].z, vr4[u].w};
 #pragma unroll
             for (int e = 0; e < 8; e++) vs[(c + e) * L::VP + key] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
         }
         __syncthreads();
+        if (k0 + PF_BK <= last) fetch(k0 + PF_BK);
         // S^T
         f4 s[2][4];
 #pragma unroll
@@ -453,7 +467,8 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
                 s[j][kt] = c;
             }
         }
-        // online softmax per query column; mask keys outside first .. qpos
+        // online softmax per query column; keys outside first .. qpos masked, on the tiles that have such keys
+        const bool edge = k0 + PF_BK - 1 > pos0 + q0 || (win > 0 && k0 < pos0 + qlast + 1 - win);
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int qp = qpos[j], lo = win > 0 ? qp + 1 - win : INT_MIN;
@@ -464,20 +479,21 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
                 for (int i = 0; i < 4; i++) {
                     const int kp = k0 + 16 * kt + 4 * lg + i;
                     float v = s[j][kt][i] * usc[j];
-                    if (kp > qp || kp < lo) v = -INFINITY;
+                    if (edge && (kp > qp || kp < lo)) v = -INFINITY;
                     s[j][kt][i] = v;
                     mx = fmaxf(mx, v);
                 }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float mnew = fmaxf(m[j], mx);
-            const float alpha = m[j] == -INFINITY ? 0.0f : expf(m[j] - mnew);
+            const float alpha = m[j] == -INFINITY ? 0.0f : exp2_hw(m[j] - mnew);
+            const float mref = mnew == -INFINITY ? 0.0f : mnew;  // a column with no key yet: every p is 0
             float sum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float p = s[j][kt][i] == -INFINITY ? 0.0f : expf(s[j][kt][i] - mnew);
+                    const float p = exp2_hw(s[j][kt][i] - mref);  // exp2(-inf) = 0
                     s[j][kt][i] = p;
                     sum += p;
                 }
@@ -485,8 +501,9 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
             sum += __shfl_xor(sum, 32, 64);
             l[j] = l[j] * alpha + sum;
             m[j] = mnew;
+            if (__ballot(alpha != 1.0f))  // the running maximum moved for some column of the wave
 #pragma unroll
-            for (int d = 0; d < DT; d++) o[j][d] *= alpha;
+                for (int d = 0; d < DT; d++) o[j][d] *= alpha;
         }
         // O^T += V^T P^T
 #pragma unroll
@@ -506,15 +523,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
             for (int d = 0; d < DT; d++) {
                 const uint16_t* vr = &vs[(16 * d + l16) * L::VP + 32 * c + 4 * lg];
                 const uint2 a0 = *(const uint2*)vr, a1 = *(const uint2*)(vr + 16);
-                h8 vf;
-                const uint32_t w4[4] = {a0.x, a0.y, a1.x, a1.y};
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const uint16_t b = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
-                    _Float16 hv;
-                    __builtin_memcpy(&hv, &b, 2);
-                    vf[e] = hv;
-                }
+                const h8 vf = __builtin_bit_cast(h8, make_uint4(a0.x, a0.y, a1.x, a1.y));
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     o[j][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[j], o[j][d], 0, 0, 0);
@@ -524,14 +533,14 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
         }
     }
     // out[row, h HD + 16 dt + 4 lg + i] for query row q0 + 16 j + l16
-    const float sk = sink ? sink[h] : -INFINITY;
+    const float sk = sink ? sink[h] * LOG2E : -INFINITY;  // in the scores' log2 units
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const int row = q0 + 16 * j + l16;
         if (row >= T) continue;
         const float M = fmaxf(m[j], sk);
-        const float sc = m[j] == -INFINITY ? 0.0f : expf(m[j] - M);
-        const float den = l[j] * sc + (sk == -INFINITY ? 0.0f : expf(sk - M));
+        const float sc = m[j] == -INFINITY ? 0.0f : exp2_hw(m[j] - M);
+        const float den = l[j] * sc + (sk == -INFINITY ? 0.0f : exp2_hw(sk - M));
         const float inv = den > 0.0f ? sc / den * (1.0f / 16384.0f) : 0.0f;  // O carries the weights' 2^14
         float* orow = out + (uint64_t)row * nh * HD + h * HD;
         const float* gate = qg ? qg + (uint64_t)row * nh * 2 * HD + h * 2 * HD + HD : nullptr;

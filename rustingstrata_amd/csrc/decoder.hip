@@ -53,10 +53,14 @@ __global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
     __builtin_amdgcn_wave_barrier();
     float ss = 0.0f;
     if (lane == 0)
-        for (int i = 0; i < n; i += 8) {  // 8 values a read pair, added one by one in index order
-            const float4 p = *(const float4*)&s[i], q = *(const float4*)&s[i + 4];
-            ss += p.x * p.x; ss += p.y * p.y; ss += p.z * p.z; ss += p.w * p.w;
-            ss += q.x * q.x; ss += q.y * q.y; ss += q.z * q.z; ss += q.w * q.w;
+        for (int i0 = 0; i0 < n; i0 += 32) {  // 32 values read ahead (n % 32 == 0), then added one by one in order
+            float4 r[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) r[c] = *(const float4*)&s[i0 + 4 * c];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                ss += r[c].x * r[c].x; ss += r[c].y * r[c].y; ss += r[c].z * r[c].z; ss += r[c].w * r[c].w;
+            }
         }
     ss = __shfl(ss, 0, 64);
     const float sc = 1.0f / sqrtf(ss / (float)n + a.eps);
