@@ -343,16 +343,18 @@ hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t
 }
 
 // ---------------- prefill ----------------
-// grid (ceil(t / 32), nkv), G waves: wave w is query head g G + w over the block's 32 query rows (two 16-query MFMA
-// columns j), so every K/V tile in LDS serves the whole GQA group. Query row i sits at position step[0] + q0 + i and
-// sees keys base(i) .. step[0] + q0 + i (base 0, or the sliding window's start). Per tile of 64 keys:
+// grid (ceil(ceil(t / 16) / 2), nkv), G waves: wave w is query head g G + w over the block's two 16-query MFMA columns
+// j, the 16-row tiles qb and ceil(t / 16) - 1 - qb (from the two ends of the chunk, so that the blocks' causal work
+// is even), and every K/V tile in LDS serves the whole GQA group. Query row i sits at position step[0] + i and sees
+// keys base(i) .. step[0] + i (base 0, or the sliding window's start); a column takes part in a key tile only while
+// the tile holds keys its rows see. Per tile of 64 keys:
 //   S^T (16 keys x 16 queries, 4 key sub-tiles kt) = sum over dims of K (A: key row, 8 dims a lane) with Q^T hi and lo
 //   (B: query column, the same 8 dims); lane holds keys 16 kt + 4 (l / 16) + i of query 16 j + l % 16.
 //   Online softmax per query column (the lane's 16 values, then across the 4 lane groups).
 //   O^T (16 dims x 16 queries, 8 dim tiles dt) += V^T (A: dim row, 8 keys) P^T hi and lo (B: the lane's own p values:
 //   keys 4 (l / 16) + i of sub-tiles 2 c and 2 c + 1 make the 8 K-elements of k-step c, and V^T's A fragment reads
 //   the same keys).
-constexpr int PF_BQ = 32, PF_BK = 64;  // query rows, keys a tile (PfLayout's 64)
+constexpr int PF_BK = 64;  // keys a tile (PfLayout's 64)
 
 template <int HD, int G>
 __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -365,26 +367,38 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
     __shared__ __align__(16) uint16_t ks[PF_BK * L::KP];
     __shared__ __align__(16) uint16_t vs[HD * L::VP];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
-    const int q0 = ((int)gridDim.x - 1 - (int)blockIdx.x) * PF_BQ;  // heaviest tiles first
     const int g = blockIdx.y, h = g * G + wave, pos0 = step[0];
     const uint64_t kvd = (uint64_t)nkv * HD;
-    const int qlast = min(q0 + PF_BQ, T) - 1;  // last live query row of the block
-    const int last = pos0 + qlast;             // last key any of them sees
-    const int first = win > 0 ? max(pos0 + q0 + 1 - win, 0) : 0;
-    // Q^T fragments (B operand): query 16 j + l16, dims 32 ks + 8 lg .. + 7, split into f16 hi and lo after scaling
+    // the block's two query columns are 16-row tiles from opposite ends of the T rows (tiles qb and nht - 1 - qb),
+    // so every block has about the same causal work; each column's MFMAs and softmax stop at its own last key
+    const int nht = (T + 15) / 16, qb = blockIdx.x;
+    const int r0[2] = {16 * qb, 16 * (nht - 1 - qb)};
+    const bool two = nht - 1 - qb != qb;
+    int lastj[2], firstj[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        lastj[j] = pos0 + min(r0[j] + 15, T - 1);  // the last key the column's rows see
+        firstj[j] = win > 0 ? max(pos0 + r0[j] + 1 - win, 0) : 0;
+    }
+    if (!two) {
+        lastj[1] = -1;
+        firstj[1] = INT_MAX;
+    }
+    const int last = max(lastj[0], lastj[1]), first = min(firstj[0], firstj[1]);
+    // Q^T fragments (B operand): query r0[j] + l16, dims 32 ks + 8 lg .. + 7, split into f16 hi and lo after scaling
     // the query by a power of two that puts its largest value in [2^13, 2^14): the lo parts then stay normal f16
     // numbers (no subnormal precision loss) and the hi parts cannot overflow. usc[j] undoes it (times `scale`).
     h8 qh[2][KS], ql[2][KS];
     float usc[2];
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        const int row = q0 + 16 * j + l16;
+        const int row = r0[j] + l16;
         const float* qr = q + (uint64_t)row * nh * HD + h * HD;
         float v[KS][8];
         float mx = 0.0f;
 #pragma unroll
         for (int k = 0; k < KS; k++) {
-            if (row < T) {
+            if (row < T && (j == 0 || two)) {
                 const float4 a = *(const float4*)(qr + 32 * k + 8 * lg), b = *(const float4*)(qr + 32 * k + 8 * lg + 4);
                 v[k][0] = a.x; v[k][1] = a.y; v[k][2] = a.z; v[k][3] = a.w;
                 v[k][4] = b.x; v[k][5] = b.y; v[k][6] = b.z; v[k][7] = b.w;
@@ -417,7 +431,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
 #pragma unroll
         for (int d = 0; d < DT; d++) o[j][d] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-    const int qpos[2] = {pos0 + q0 + l16, pos0 + q0 + 16 + l16};  // the lane's query position per column j
+    const int qpos[2] = {pos0 + r0[0] + l16, pos0 + r0[1] + l16};  // the lane's query position per column j
     // K tile [key][dim] and V tile transposed [dim][key], chunk i = tid + NTH u of a tile: key i % 64, dims
     // 8 (i / 64) ..; the next tile's chunks are loaded into registers while this one is computed. Keys past `last`
     // are zeros (finite: p = 0 times them).
@@ -449,6 +463,9 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
         }
         __syncthreads();
         if (k0 + PF_BK <= last) fetch(k0 + PF_BK);
+        bool live[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) live[j] = k0 <= lastj[j] && k0 + PF_BK - 1 >= firstj[j];
         // S^T
         f4 s[2][4];
 #pragma unroll
@@ -459,6 +476,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 f4 c = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+                if (live[j])
 #pragma unroll
                 for (int k = 0; k < KS; k++) {
                     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[k], qh[j][k], c, 0, 0, 0);
@@ -468,9 +486,10 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
             }
         }
         // online softmax per query column; keys outside first .. qpos masked, on the tiles that have such keys
-        const bool edge = k0 + PF_BK - 1 > pos0 + q0 || (win > 0 && k0 < pos0 + qlast + 1 - win);
 #pragma unroll
         for (int j = 0; j < 2; j++) {
+            if (!live[j]) continue;
+            const bool edge = k0 + PF_BK - 1 > pos0 + r0[j] || (win > 0 && k0 < lastj[j] + 1 - win);
             const int qp = qpos[j], lo = win > 0 ? qp + 1 - win : INT_MIN;
             float mx = -INFINITY;
 #pragma unroll
@@ -513,6 +532,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
             for (int j = 0; j < 2; j++)
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
+                    if (!live[j]) break;
                     // p in [0, 1] times 2^14: the lo parts stay normal down to p ~ 2^-17
                     const float p = s[j][2 * c + (e >> 2)][e & 3] * 16384.0f;
                     const _Float16 hi = (_Float16)p;
@@ -526,18 +546,19 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
                 const h8 vf = __builtin_bit_cast(h8, make_uint4(a0.x, a0.y, a1.x, a1.y));
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
+                    if (!live[j]) continue;
                     o[j][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[j], o[j][d], 0, 0, 0);
                     o[j][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[j], o[j][d], 0, 0, 0);
                 }
             }
         }
     }
-    // out[row, h HD + 16 dt + 4 lg + i] for query row q0 + 16 j + l16
+    // out[row, h HD + 16 dt + 4 lg + i] for query row r0[j] + l16
     const float sk = sink ? sink[h] * LOG2E : -INFINITY;  // in the scores' log2 units
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        const int row = q0 + 16 * j + l16;
-        if (row >= T) continue;
+        const int row = r0[j] + l16;
+        if (row >= T || (j == 1 && !two)) continue;
         const float M = fmaxf(m[j], sk);
         const float sc = m[j] == -INFINITY ? 0.0f : exp2_hw(m[j] - M);
         const float den = l[j] * sc + (sk == -INFINITY ? 0.0f : exp2_hw(sk - M));
@@ -562,7 +583,7 @@ hipError_t launch_attn_prefill(const float* q, const uint16_t* kc, const uint16_
                                hipStream_t s) {
     if (t <= 0) return hipSuccess;
     const int G = nh / nkv;
-    const dim3 grid((unsigned)((t + PF_BQ - 1) / PF_BQ), (unsigned)nkv);
+    const dim3 grid((unsigned)(((t + 15) / 16 + 1) / 2), (unsigned)nkv);  // a pair of 16-row query tiles a block
 #define PF(HD_, G_)                                                                                               \
     if (hd == HD_ && G == G_)                                                                                     \
         attn_prefill_kernel<HD_, G_><<<grid, dim3(64 * G_), 0, s>>>(q, kc, vc, qg, out, step, t, nh, nkv, scale,  \
