@@ -185,6 +185,14 @@ def bench_floor(hip, shapes, per_shape, iters=400):
     return out
 
 
+def gemm_digit_planes(ggml, ty):
+    """Int8 MFMA planes the grouped GEMM runs per weight super-block (gemm.hip GemmFmt: a HI and a LO digit plane of
+    sc * q unless it fits int8 (Q2_K), plus a min plane for the formats with mins)."""
+    hi = ty != ggml.Q2_K
+    mins = ty in (ggml.Q2_K, ggml.Q4_K, ggml.Q5_K)
+    return (2 if hi else 1) + (1 if mins else 0)
+
+
 def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
     """E=128, top-8, H=2048, I=768; gate/up Q5_K, down Q6_K (or the given types, e.g. configs[4]'s
     Q2_K / Q3_K experts); Zipf-skewed routing; T tokens."""
@@ -211,7 +219,7 @@ def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
     tiles, ntd = hip.alloc(2 * max_tiles * 16), hip.alloc(4)
     ge, ye, x = hip.alloc(T * k * F * 4), hip.alloc(T * k * H * 4), hip.alloc(T * H * 4)
     mats = [(int(g_b), F * rb_gu), (int(d_b), H * rb_d)]  # tile lists of the gate (up: + u_b - g_b) and down
-    ev = [hip.event() for _ in range(4)]
+    ev = [hip.event() for _ in range(5)]
 
     def layer(timed=False):
         hip.router_topk(lb, E, k, 0.0, ids, wts, T)
@@ -220,6 +228,8 @@ def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
             hip.record(ev[1])
         # gate and up in one grouped GEMM: ge = silu(W_gate x) * (W_up x) (the bits of the two-call sequence)
         hip.gemm_grouped_gate_up(ty_gu, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b))
+        if timed:
+            hip.record(ev[4])
         hip.gemm_grouped(ty_d, H, F, int(tiles) + max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
                          S.ACT_STORE)
         if timed:
@@ -229,16 +239,27 @@ def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
     for _ in range(3):
         layer()
     hip.sync()
-    tot, gemm = 0.0, 0.0
+    tot, gemm, gu = 0.0, 0.0, 0.0
     for _ in range(iters):
         hip.record(ev[0])
         layer(timed=True)
         hip.record(ev[3])
         tot += hip.elapsed_ms(ev[0], ev[3])
         gemm += hip.elapsed_ms(ev[1], ev[2])
-    tot, gemm = tot / iters, gemm / iters
+        gu += hip.elapsed_ms(ev[1], ev[4])
+    tot, gemm, gu = tot / iters, gemm / iters, gu / iters
     ops = T * k * 3 * F * H * 2
-    return {"tokens": T, "ms_layer": round(tot, 4), "tok_per_s": round(T / (tot / 1e3), 1),
+    # per kernel: the gate/up launch (its x quantization included) and the down launch (h quantization included);
+    # issued int8 ops count every digit plane (the MFMA work done), useful ops the matrix product
+    roof = {"bound": "mfma", "unit": "TOP/s", "peak": INT8_PEAK_TOPS,
+            "achieved": round(ops / (gemm / 1e3) / 1e12, 1), "frac": round(ops / (gemm / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
+            "traffic": None, "kernels": {}}
+    for name, ty, ms, kops in (("gate_up", ty_gu, gu, T * k * 2 * F * H * 2), ("down", ty_d, gemm - gu, T * k * F * H * 2)):
+        planes = gemm_digit_planes(ggml, ty)
+        roof["kernels"][name] = {"type": ggml.NAMES[ty], "us": round(1000 * ms, 1), "useful_TOPS": round(kops / (ms / 1e3) / 1e12, 1),
+                                 "digit_planes": planes,
+                                 "issued_frac": round(planes * kops / (ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4)}
+    return {"roofline": roof, "tokens": T, "ms_layer": round(tot, 4), "tok_per_s": round(T / (tot / 1e3), 1),
             "grouped_gemm_ms": round(gemm, 4), "int8_TOPS": round(ops / (gemm / 1e3) / 1e12, 1),
             "mfma_frac": round(ops / (gemm / 1e3) / 1e12 / INT8_PEAK_TOPS, 4), "ops": ops,
             "types": f"gate/up {ggml.NAMES[ty_gu]}, down {ggml.NAMES[ty_d]}",

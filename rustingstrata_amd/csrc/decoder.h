@@ -16,6 +16,9 @@ struct NormRope {
     int qrows = 0; const float* qx = nullptr; uint64_t q_stride = 0; const float* qw = nullptr; float* qo = nullptr;
     int qper = 1;
     float eps = 0, base = 0; int n_rot = 0; const int* step = nullptr;
+    // base^(-2 i / n_rot) for the first nfreq pairs (filled by launch_norm_rope on the host)
+    static constexpr int NFREQ = 128;
+    int nfreq = 0; double freq[NFREQ] = {};
 };
 hipError_t launch_norm_rope(const NormRope& a, hipStream_t s);
 hipError_t launch_rope_pairs(float* x, uint64_t stride, int heads, int per, int n_rot, const int* step, float base,

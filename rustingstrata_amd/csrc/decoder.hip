@@ -3,6 +3,8 @@
 // logit rows (Backend::argmax_rows, :246), x += y and SwiGLU (:282-284), float-weight matmuls (the router's F32
 // weights through gemv / gemm_dense), embedding rows (Model::embed, src/model.rs:334-339, on the device) and seeded
 // synthetic GGUF blocks.
+#include <cmath>
+
 #include "decoder.h"
 #include "formats.h"
 
@@ -68,8 +70,10 @@ __global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
     __builtin_amdgcn_wave_barrier();
     const int half = a.n_rot / 2;
     for (int i = lane; i < half; i += 64) {
-        const double theta = (double)pos * pow((double)a.base, -2.0 * (double)i / (double)a.n_rot);
-        const float sn = (float)sin(theta), c = (float)cos(theta);
+        const double f = i < a.nfreq ? a.freq[i] : pow((double)a.base, -2.0 * (double)i / (double)a.n_rot);
+        double sd, cd;
+        sincos((double)pos * f, &sd, &cd);
+        const float sn = (float)sd, c = (float)cd;
         const float p = s[i], q = s[i + half];
         s[i] = p * c - q * sn;
         s[i + half] = p * sn + q * c;
@@ -105,9 +109,14 @@ __global__ __launch_bounds__(64 * NR_WAVES) void rope_pairs_kernel(float* x, uin
     }
 }
 
-hipError_t launch_norm_rope(const NormRope& a, hipStream_t s) {
-    const int total = a.qrows + a.rows;
+hipError_t launch_norm_rope(const NormRope& a0, hipStream_t s) {
+    const int total = a0.qrows + a0.rows;
     if (total <= 0) return hipSuccess;
+    // the rope frequencies depend only on the pair index: the host's pow (the one the CPU reference calls) fills
+    // them once per launch, so the kernel's f64 work is the sine and cosine
+    NormRope a = a0;
+    a.nfreq = a.n_rot / 2 <= NormRope::NFREQ ? a.n_rot / 2 : 0;
+    for (int i = 0; i < a.nfreq; i++) a.freq[i] = std::pow((double)a.base, -2.0 * (double)i / (double)a.n_rot);
     norm_rope_kernel<<<dim3((unsigned)((total + NR_WAVES - 1) / NR_WAVES)), dim3(64 * NR_WAVES), 0, s>>>(a);
     return hipGetLastError();
 }
@@ -289,9 +298,39 @@ __global__ __launch_bounds__(256) void gemv_f32_kernel(const float* __restrict__
     }
 }
 
+// One input (a decode step): a wave per row, a block per wave; each pass loads GF1_U 16-byte chunks of the row and of
+// x per lane before using any, so a 2048-value row takes one memory round trip. A lane sums the same chunks in the
+// same order as gemv_f32_kernel, so both kernels give the same bits.
+constexpr int GF1_U = 8;
+__global__ __launch_bounds__(64) void gemv_f32_1_kernel(const float* __restrict__ w, int rows, int cols,
+                                                        const float* __restrict__ x, float* y, int act) {
+    const int r = blockIdx.x, lane = threadIdx.x, n4 = cols / 4;
+    const float4* wr = (const float4*)(w + (uint64_t)r * cols);
+    const float4* xr = (const float4*)x;
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < n4; c0 += 64 * GF1_U) {
+        float4 wv[GF1_U], xv[GF1_U];
+#pragma unroll
+        for (int u = 0; u < GF1_U; u++) {
+            const int c = c0 + lane + 64 * u;
+            wv[u] = c < n4 ? wr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[u] = c < n4 ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < GF1_U; u++)
+            if (c0 + lane + 64 * u < n4) acc += wv[u].x * xv[u].x + wv[u].y * xv[u].y + wv[u].z * xv[u].z + wv[u].w * xv[u].w;
+    }
+    const float v = wave_sum_xor(acc);
+    if (lane == 0) y[r] = act == 2 ? y[r] + v : v;
+}
+
 hipError_t launch_gemv_f32(const float* w, int rows, int cols, const float* x, uint64_t x_stride, float* y,
                            uint64_t y_stride, int nt, int act, hipStream_t s) {
     if (!rows || !nt) return hipSuccess;
+    if (nt == 1) {
+        gemv_f32_1_kernel<<<dim3((unsigned)rows), dim3(64), 0, s>>>(w, rows, cols, x, y, act);
+        return hipGetLastError();
+    }
     for (int t0 = 0; t0 < nt; t0 += GF_NT) {
         const int n = std::min(GF_NT, nt - t0);
         gemv_f32_kernel<<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s>>>(w, rows, cols, x + t0 * x_stride, x_stride,
