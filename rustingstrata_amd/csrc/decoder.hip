@@ -46,46 +46,89 @@ __global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
         b += a.qrows;
         x = a.qx; xs = a.q_stride; w = a.qw; out = a.qo; per = a.qper; store = false;
     }
-    const int n = a.n, tok = b / per, pos = a.step[0] + tok;
+    const int n = a.n, tok = b / per, half = a.n_rot / 2;
     const float* xr = x + (uint64_t)b * xs;
     float* o = out + (uint64_t)b * n;
     float* s = sh[wave];
-    // the sum of squares in index order by one lane, as ops::rms_norm's iterator sum: the same bits as the CPU
-    for (int i = lane; i < n; i += 64) s[i] = xr[i];
-    __builtin_amdgcn_wave_barrier();
-    float ss = 0.0f;
-    if (lane == 0)
-        for (int i0 = 0; i0 < n; i0 += 32) {  // 32 values read ahead (n % 32 == 0), then added one by one in order
-            float4 r[8];
+    const float* vr = store ? a.v + (uint64_t)b * n : nullptr;
+    // every load of the wave first (the head, its norm weights, the value row), then the rope angles while they land
+    constexpr int NV = 512 / 64;
+    float xv[NV], wv[NV], vv[NV];
 #pragma unroll
-            for (int c = 0; c < 8; c++) r[c] = *(const float4*)&s[i0 + 4 * c];
+    for (int j = 0; j < NV; j++) {
+        const int i = lane + 64 * j;
+        if (i < n) {
+            xv[j] = xr[i];
+            wv[j] = w[i];
+            if (store) vv[j] = vr[i];
+        }
+    }
+    const int pos = a.step[0] + tok;
+    float sn[NV / 2], cs[NV / 2];
+#pragma unroll
+    for (int j = 0; j < NV / 2; j++) {
+        const int i = lane + 64 * j;
+        if (i < half) {
+            const double f = i < a.nfreq ? a.freq[i] : pow((double)a.base, -2.0 * (double)i / (double)a.n_rot);
+            double sd, cd;
+            sincos((double)pos * f, &sd, &cd);
+            sn[j] = (float)sd;
+            cs[j] = (float)cd;
+        }
+    }
+    // the squares by every lane (the same products the sum would form), staged for lane 0
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+        if (lane + 64 * j < n) s[lane + 64 * j] = xv[j] * xv[j];
+    __builtin_amdgcn_wave_barrier();
+    // the sum of squares in index order by one lane, as ops::rms_norm's iterator sum: the same bits as the CPU; the
+    // next 32 squares are read while the current 32 are added (n % 32 == 0)
+    float ss = 0.0f;
+    if (lane == 0) {
+        float4 r[8], nx[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) r[c] = *(const float4*)&s[4 * c];
+        for (int i0 = 0; i0 < n; i0 += 32) {
+            if (i0 + 32 < n) {
+#pragma unroll
+                for (int c = 0; c < 8; c++) nx[c] = *(const float4*)&s[i0 + 32 + 4 * c];
+            }
 #pragma unroll
             for (int c = 0; c < 8; c++) {
-                ss += r[c].x * r[c].x; ss += r[c].y * r[c].y; ss += r[c].z * r[c].z; ss += r[c].w * r[c].w;
+                ss += r[c].x; ss += r[c].y; ss += r[c].z; ss += r[c].w;
             }
+#pragma unroll
+            for (int c = 0; c < 8; c++) r[c] = nx[c];
         }
+    }
     ss = __shfl(ss, 0, 64);
     const float sc = 1.0f / sqrtf(ss / (float)n + a.eps);
-    for (int i = lane; i < n; i += 64) s[i] = s[i] * sc * w[i];
+    __builtin_amdgcn_wave_barrier();  // lane 0's reads are done before the normed values overwrite the stage
+#pragma unroll
+    for (int j = 0; j < NV; j++)
+        if (lane + 64 * j < n) s[lane + 64 * j] = xv[j] * sc * wv[j];
     __builtin_amdgcn_wave_barrier();
-    const int half = a.n_rot / 2;
-    for (int i = lane; i < half; i += 64) {
-        const double f = i < a.nfreq ? a.freq[i] : pow((double)a.base, -2.0 * (double)i / (double)a.n_rot);
-        double sd, cd;
-        sincos((double)pos * f, &sd, &cd);
-        const float sn = (float)sd, c = (float)cd;
-        const float p = s[i], q = s[i + half];
-        s[i] = p * c - q * sn;
-        s[i + half] = p * sn + q * c;
+#pragma unroll
+    for (int j = 0; j < NV / 2; j++) {
+        const int i = lane + 64 * j;
+        if (i < half) {
+            const float p = s[i], q = s[i + half];
+            s[i] = p * cs[j] - q * sn[j];
+            s[i + half] = p * sn[j] + q * cs[j];
+        }
     }
     __builtin_amdgcn_wave_barrier();
-    for (int i = lane; i < n; i += 64) o[i] = s[i];
-    if (store) {
-        const float* vr = a.v + (uint64_t)b * n;
-        const uint64_t e = ((uint64_t)pos * per + b % per) * n;
-        for (int i = lane; i < n; i += 64) {
-            a.kc[e + i] = f32_to_f16_bits(s[i]);
-            a.vc[e + i] = f32_to_f16_bits(vr[i]);
+    const uint64_t e = ((uint64_t)pos * per + b % per) * n;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int i = lane + 64 * j;
+        if (i < n) {
+            const float r = s[i];
+            o[i] = r;
+            if (store) {
+                a.kc[e + i] = f32_to_f16_bits(r);
+                a.vc[e + i] = f32_to_f16_bits(vv[j]);
+            }
         }
     }
 }

@@ -69,6 +69,7 @@ struct GemmArgs {
     int gx;               // blocks per XCD
     int pair;             // gate/up pair mode (GemmLaunch::pair)
     int64_t w2;           // pair: byte offset of the second matrix
+    int dense_p;          // dense: positions per tile (GM, or less to give every CU an item)
 };
 
 // silu(v) = v / (1 + e^-v) for the SwiGLU epilogues. e^-v = 2^t with t = -v log2(e) carried as th + tl (the
@@ -140,8 +141,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             it.cnt = min(GM, (int)(t1 >> 32));
         } else {
             it.w = (uint64_t)a.dense_w;
-            it.m0 = GM * tile;
-            it.cnt = min(GM, a.dense_n - it.m0);
+            it.m0 = a.dense_p * tile;
+            it.cnt = min(a.dense_p, a.dense_n - it.m0);
         }
         return it;
     };
@@ -477,7 +478,6 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
         if (e != hipSuccess) return e;
         attr = true;
     }
-    a.max_tiles = g.n_tiles;
     // Persistent blocks, one per CU.
     static int ncu = 0;
     if (!ncu) {
@@ -487,7 +487,16 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
         if (e != hipSuccess) return e;
     }
     const int gno = g.pair ? GN / 2 : GN;
-    const long long total = (long long)((g.rows + gno - 1) / gno) * g.n_tiles;
+    const long long nrb = (g.rows + gno - 1) / gno;
+    a.max_tiles = g.n_tiles;
+    a.dense_p = GM;
+    if (!g.tiles) {
+        // a dense matrix with few row blocks (the k and v projections) takes fewer positions per tile, down to 64,
+        // until every CU has an item: the weights are then decoded more often, but no CU idles for the whole GEMM
+        while (a.dense_p > 64 && (long long)((g.dense_n + a.dense_p - 1) / a.dense_p) * nrb < ncu) a.dense_p /= 2;
+        a.max_tiles = (g.dense_n + a.dense_p - 1) / a.dense_p;
+    }
+    const long long total = nrb * a.max_tiles;
     const long long per = (total + NXCD - 1) / NXCD;
     const long long gx = std::min<long long>(per, std::max(ncu / NXCD, 1));
     a.gx = (int)std::max<long long>(gx, 1);
