@@ -31,26 +31,55 @@ __device__ __forceinline__ float wave_sum_xor(float v) {
 // in f64 and its sine and cosine rounded to f32 as ops::rope_neox does (src/ops.rs:36-45).
 constexpr int NR_WAVES = 4;
 
-__global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
-    __shared__ __align__(16) float sh[NR_WAVES][512];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    int b = (int)blockIdx.x * NR_WAVES + wave - a.qrows;
-    if (b >= a.rows) return;
-    const float* x = a.x;
-    uint64_t xs = a.x_stride;
-    const float* w = a.w;
-    float* out = a.out;
-    int per = a.per;
-    bool store = a.kc != nullptr;
-    if (b < 0) {
-        b += a.qrows;
-        x = a.qx; xs = a.q_stride; w = a.qw; out = a.qo; per = a.qper; store = false;
+// Head gb (query heads first, then key heads) of a launch: its source row, norm weights, output row and whether it
+// stores to the KV cache.
+struct NrHead {
+    const float* xr;
+    const float* w;
+    float* o;
+    const float* vr;  // value row (key heads of a storing launch), else null
+    int b, per;
+};
+__device__ __forceinline__ NrHead nr_head(const NormRope& a, int gb) {
+    NrHead h;
+    if (gb < a.qrows) {
+        h.b = gb; h.per = a.qper;
+        h.xr = a.qx + (uint64_t)gb * a.q_stride; h.w = a.qw; h.o = a.qo + (uint64_t)gb * a.n; h.vr = nullptr;
+    } else {
+        const int b = gb - a.qrows;
+        h.b = b; h.per = a.per;
+        h.xr = a.x + (uint64_t)b * a.x_stride; h.w = a.w; h.o = a.out + (uint64_t)b * a.n;
+        h.vr = a.kc ? a.v + (uint64_t)b * a.n : nullptr;
     }
-    const int n = a.n, tok = b / per, half = a.n_rot / 2;
-    const float* xr = x + (uint64_t)b * xs;
-    float* o = out + (uint64_t)b * n;
-    float* s = sh[wave];
-    const float* vr = store ? a.v + (uint64_t)b * n : nullptr;
+    return h;
+}
+
+// The sum of squares of x[0 .. n) in index order, as ops::rms_norm's iterator sum (a multiply, then an add): the
+// CPU's bits. sq(i0, r) loads values i0 .. i0 + 31 as 8 float4; the next 32 are loaded while the current 32 are added
+// (n % 32 == 0).
+template <typename Load>
+__device__ __forceinline__ float nr_sumsq(int n, Load&& ld) {
+    float ss = 0.0f;
+    float4 r[8], nx[8];
+    ld(0, r);
+    for (int i0 = 0; i0 < n; i0 += 32) {
+        if (i0 + 32 < n) ld(i0 + 32, nx);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            ss += r[c].x * r[c].x; ss += r[c].y * r[c].y; ss += r[c].z * r[c].z; ss += r[c].w * r[c].w;
+        }
+#pragma unroll
+        for (int c = 0; c < 8; c++) r[c] = nx[c];
+    }
+    return ss;
+}
+
+// One head by one wave: out = x * (1 / sqrt(ss / n + eps)) * w, rope, and (key heads of a storing launch) the f16
+// KV store. s: the wave's 512-float LDS stage. HAVE_SS: ss is given (else lane 0 sums the head from the stage).
+template <bool HAVE_SS>
+__device__ __forceinline__ void nr_run(const NormRope& a, const NrHead& h, float* s, int lane, float ss) {
+    const int n = a.n, half = a.n_rot / 2;
+    const bool store = h.vr != nullptr;
     // every load of the wave first (the head, its norm weights, the value row), then the rope angles while they land
     constexpr int NV = 512 / 64;
     float xv[NV], wv[NV], vv[NV];
@@ -58,12 +87,12 @@ __global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
     for (int j = 0; j < NV; j++) {
         const int i = lane + 64 * j;
         if (i < n) {
-            xv[j] = xr[i];
-            wv[j] = w[i];
-            if (store) vv[j] = vr[i];
+            xv[j] = h.xr[i];
+            wv[j] = h.w[i];
+            if (store) vv[j] = h.vr[i];
         }
     }
-    const int pos = a.step[0] + tok;
+    const int pos = a.step[0] + h.b / h.per;
     float sn[NV / 2], cs[NV / 2];
 #pragma unroll
     for (int j = 0; j < NV / 2; j++) {
@@ -76,34 +105,20 @@ __global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
             cs[j] = (float)cd;
         }
     }
-    // the squares by every lane (the same products the sum would form), staged for lane 0
+    if constexpr (!HAVE_SS) {
 #pragma unroll
-    for (int j = 0; j < NV; j++)
-        if (lane + 64 * j < n) s[lane + 64 * j] = xv[j] * xv[j];
-    __builtin_amdgcn_wave_barrier();
-    // the sum of squares in index order by one lane, as ops::rms_norm's iterator sum: the same bits as the CPU; the
-    // next 32 squares are read while the current 32 are added (n % 32 == 0)
-    float ss = 0.0f;
-    if (lane == 0) {
-        float4 r[8], nx[8];
+        for (int j = 0; j < NV; j++)
+            if (lane + 64 * j < n) s[lane + 64 * j] = xv[j];
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0)
+            ss = nr_sumsq(n, [&](int i0, float4 (&r)[8]) {
 #pragma unroll
-        for (int c = 0; c < 8; c++) r[c] = *(const float4*)&s[4 * c];
-        for (int i0 = 0; i0 < n; i0 += 32) {
-            if (i0 + 32 < n) {
-#pragma unroll
-                for (int c = 0; c < 8; c++) nx[c] = *(const float4*)&s[i0 + 32 + 4 * c];
-            }
-#pragma unroll
-            for (int c = 0; c < 8; c++) {
-                ss += r[c].x; ss += r[c].y; ss += r[c].z; ss += r[c].w;
-            }
-#pragma unroll
-            for (int c = 0; c < 8; c++) r[c] = nx[c];
-        }
+                for (int c = 0; c < 8; c++) r[c] = *(const float4*)&s[i0 + 4 * c];
+            });
+        ss = __shfl(ss, 0, 64);
+        __builtin_amdgcn_wave_barrier();  // lane 0's reads are done before the normed values overwrite the stage
     }
-    ss = __shfl(ss, 0, 64);
     const float sc = 1.0f / sqrtf(ss / (float)n + a.eps);
-    __builtin_amdgcn_wave_barrier();  // lane 0's reads are done before the normed values overwrite the stage
 #pragma unroll
     for (int j = 0; j < NV; j++)
         if (lane + 64 * j < n) s[lane + 64 * j] = xv[j] * sc * wv[j];
@@ -118,17 +133,105 @@ __global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
         }
     }
     __builtin_amdgcn_wave_barrier();
-    const uint64_t e = ((uint64_t)pos * per + b % per) * n;
+    const uint64_t e = ((uint64_t)pos * h.per + h.b % h.per) * n;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int i = lane + 64 * j;
         if (i < n) {
             const float r = s[i];
-            o[i] = r;
+            h.o[i] = r;
             if (store) {
                 a.kc[e + i] = f32_to_f16_bits(r);
                 a.vc[e + i] = f32_to_f16_bits(vv[j]);
             }
+        }
+    }
+    __builtin_amdgcn_wave_barrier();  // the stage is reused by the wave's next head
+}
+
+// A wave per head (decode: few heads, each wave's latency is the launch's).
+__global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_kernel(NormRope a) {
+    __shared__ __align__(16) float sh[NR_WAVES][512];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int gb = (int)blockIdx.x * NR_WAVES + wave;
+    if (gb >= a.qrows + a.rows) return;
+    nr_run<false>(a, nr_head(a, gb), sh[wave], lane, 0.0f);
+}
+
+// Many heads of 128 values, all rotated (a prefill chunk): a block takes NR_MANY heads. Its threads stage the heads
+// (and the value rows of stored key heads) in LDS with every load issued at once; wave 0 then sums the squares a lane
+// per head (the heads' sequential chains run side by side); each wave then takes 16 consecutive heads, a lane per
+// rope pair (i, i + 64), recomputing the pair's angle only when the position changes. The arithmetic is
+// norm_rope_kernel's, so both kernels give the same bits.
+constexpr int NR_MANY = 64, NR_P = 129;  // heads a block; LDS pitch of a staged head (bank spread for the sums)
+__global__ __launch_bounds__(64 * NR_WAVES) void norm_rope_many_kernel(NormRope a) {
+    __shared__ float xs[NR_MANY][NR_P], vs[NR_MANY][NR_P];
+    __shared__ float ssq[NR_MANY];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int total = a.qrows + a.rows, g0 = (int)blockIdx.x * NR_MANY;
+    const float qw0 = a.qrows ? a.qw[lane] : 0.0f, qw1 = a.qrows ? a.qw[lane + 64] : 0.0f;
+    const float kw0 = a.rows ? a.w[lane] : 0.0f, kw1 = a.rows ? a.w[lane + 64] : 0.0f;
+    // 16-byte chunk c = tid + 256 u of the block: head c / 32, values 4 (c % 32) ..
+    float4 xv[8], vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int c = tid + 256 * u, j = c >> 5, g = g0 + j;
+        if (g < total) {
+            const NrHead h = nr_head(a, g);
+            xv[u] = *(const float4*)(h.xr + 4 * (c & 31));
+            if (h.vr) vv[u] = *(const float4*)(h.vr + 4 * (c & 31));
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int c = tid + 256 * u, j = c >> 5, g = g0 + j, i = 4 * (c & 31);
+        if (g < total) {
+            xs[j][i] = xv[u].x; xs[j][i + 1] = xv[u].y; xs[j][i + 2] = xv[u].z; xs[j][i + 3] = xv[u].w;
+            if (g >= a.qrows && a.kc) {
+                vs[j][i] = vv[u].x; vs[j][i + 1] = vv[u].y; vs[j][i + 2] = vv[u].z; vs[j][i + 3] = vv[u].w;
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float ss = 0.0f;
+        if (g0 + lane < total) {
+            const float* xr = xs[lane];
+            ss = nr_sumsq(128, [&](int i0, float4 (&r)[8]) {
+#pragma unroll
+                for (int c = 0; c < 8; c++) r[c] = make_float4(xr[i0 + 4 * c], xr[i0 + 4 * c + 1], xr[i0 + 4 * c + 2], xr[i0 + 4 * c + 3]);
+            });
+        }
+        ssq[lane] = ss;
+    }
+    __syncthreads();
+    int cur = -1;  // position of the pair angle held
+    float sn = 0.0f, cs = 1.0f;
+    for (int jj = 0; jj < NR_MANY / NR_WAVES; jj++) {
+        const int j = (NR_MANY / NR_WAVES) * wave + jj, g = g0 + j;
+        if (g >= total) break;
+        const NrHead h = nr_head(a, g);
+        const int pos = a.step[0] + h.b / h.per;
+        if (pos != cur) {
+            cur = pos;
+            const double f = lane < a.nfreq ? a.freq[lane] : pow((double)a.base, -2.0 * (double)lane / 128.0);
+            double sd, cd;
+            sincos((double)pos * f, &sd, &cd);
+            sn = (float)sd;
+            cs = (float)cd;
+        }
+        const bool q = g < a.qrows;
+        const float sc = 1.0f / sqrtf(ssq[j] / 128.0f + a.eps);
+        const float p = xs[j][lane] * sc * (q ? qw0 : kw0), r = xs[j][lane + 64] * sc * (q ? qw1 : kw1);
+        const float o0 = p * cs - r * sn, o1 = p * sn + r * cs;
+        h.o[lane] = o0;
+        h.o[lane + 64] = o1;
+        if (h.vr) {
+            const uint64_t e = ((uint64_t)pos * h.per + h.b % h.per) * 128;
+            a.kc[e + lane] = f32_to_f16_bits(o0);
+            a.kc[e + lane + 64] = f32_to_f16_bits(o1);
+            a.vc[e + lane] = f32_to_f16_bits(vs[j][lane]);
+            a.vc[e + lane + 64] = f32_to_f16_bits(vs[j][lane + 64]);
         }
     }
 }
@@ -160,7 +263,11 @@ hipError_t launch_norm_rope(const NormRope& a0, hipStream_t s) {
     NormRope a = a0;
     a.nfreq = a.n_rot / 2 <= NormRope::NFREQ ? a.n_rot / 2 : 0;
     for (int i = 0; i < a.nfreq; i++) a.freq[i] = std::pow((double)a.base, -2.0 * (double)i / (double)a.n_rot);
-    norm_rope_kernel<<<dim3((unsigned)((total + NR_WAVES - 1) / NR_WAVES)), dim3(64 * NR_WAVES), 0, s>>>(a);
+    const bool vec = ((uintptr_t)a.qx | (uintptr_t)a.x) % 16 == 0 && a.q_stride % 4 == 0 && a.x_stride % 4 == 0;
+    if (total >= 4 * NR_MANY && vec && a.n == 128 && a.n_rot == 128)  // the many-heads form: 16-byte chunks, heads of 128
+        norm_rope_many_kernel<<<dim3((unsigned)((total + NR_MANY - 1) / NR_MANY)), dim3(64 * NR_WAVES), 0, s>>>(a);
+    else
+        norm_rope_kernel<<<dim3((unsigned)((total + NR_WAVES - 1) / NR_WAVES)), dim3(64 * NR_WAVES), 0, s>>>(a);
     return hipGetLastError();
 }
 

@@ -59,10 +59,12 @@ def test_rope_neox_and_pairs(hip):
     assert max_rel_err(got[:, 10:40], want[:, 10:40]) <= 1e-6
 
 
-def test_rms_norm_rope_qk_and_kv_store(hip):
+@pytest.mark.parametrize("T", [3, 12])
+def test_rms_norm_rope_qk_and_kv_store(hip, T):
     """rms_norm_rope_qk (src/backend.rs:274-277): q heads normed and roped; k heads normed, roped and stored with
-    their v rows as f16 at cache row position * nkv + head."""
-    nh, nkv, hd, T, pos0, eps = 32, 4, 128, 3, 17, 1e-6
+    their v rows as f16 at cache row position * nkv + head. T = 3 runs the wave-per-head kernel, T = 12 (432 heads,
+    a partial last block) the lane-per-head sums of the many-heads kernel."""
+    nh, nkv, hd, pos0, eps = 32, 4, 128, 17, 1e-6
     q = normal((T, nh * hd), seed=3)
     k = normal((T, nkv * hd), seed=4)
     v = normal((T, nkv * hd), seed=5)
