@@ -202,16 +202,28 @@ template <> __device__ __forceinline__ void task<Q2_K>(const uint8_t* b, int k, 
     uint32_t dm = rd32<4>(b + 80);
     t.D = f16_to_f32(dm & 0xFFFF); t.M = f16_to_f32(dm >> 16);
 }
+// Scales 4 w .. 4 w + 3 of a Q3_K block (q3k_scales, src/quant/mod.rs:173-186) as 4 bytes, each 6-bit scale with
+// its bit 5 flipped: as a signed 6-bit field that byte is the scale minus 32.
+__device__ __forceinline__ uint32_t q3k_scale_word(const uint8_t* sc, int w) {
+    const uint32_t lo = rd32<2>(sc + 4 * (w & 1)), hi = rd32<2>(sc + 8);
+    const uint32_t nib = (w & 2 ? lo >> 4 : lo) & 0x0F0F0F0Fu;
+    // the 2 high bits of scale 4 w + i are bits 2 w, 2 w + 1 of byte i of hi
+    const int s = 4 - 2 * w;
+    return (nib | ((s >= 0 ? hi << s : hi >> -s) & 0x30303030u)) ^ 0x20202020u;
+}
 template <> __device__ __forceinline__ void task<Q3_K>(const uint8_t* b, int k, const IqTables*, Task& t) {
     int n = k >> 2, sh = 2 * (k & 3), hb = 4 * n + (k & 3);
     const uint8_t* q = b + 32 + 32 * n;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        uint32_t lo = (rd32<2>(q + 4 * j) >> sh) & 0x03030303u, h = (rd32<2>(b + 4 * j) >> hb) & 0x01010101u;
-        t.q[j] = (int)(lo | (h << 2));  // value + 4
+        // bit hb of each hmask byte to bit 2 (one shift of the word, then the mask): value + 4
+        const uint32_t h = rd32<2>(b + 4 * j), hs = hb <= 2 ? h << (2 - hb) : h >> (hb - 2);
+        t.q[j] = (int)(((rd32<2>(q + 4 * j) >> sh) & 0x03030303u) | (hs & 0x04040404u));
     }
     t.o0 = 32 * k; t.o1 = 32 * k + 16;
-    t.sc0 = q3k_scale(b + 96, 2 * k) - 32; t.sc1 = q3k_scale(b + 96, 2 * k + 1) - 32;
+    const uint32_t scw = q3k_scale_word(b + 96, k >> 1);  // scales 2 k, 2 k + 1: bytes 2 (k & 1), + 1
+    t.sc0 = __builtin_amdgcn_sbfe((int)scw, 16 * (k & 1), 6);
+    t.sc1 = __builtin_amdgcn_sbfe((int)scw, 16 * (k & 1) + 8, 6);
     t.m0 = t.m1 = 0;
     t.D = f16_to_f32(rd16(b + 108)); t.M = 0.0f;
 }

@@ -51,7 +51,8 @@ __device__ __forceinline__ int dot4w(uint32_t a, uint32_t b, uint32_t c, uint32_
 }
 // v << n for n >= 0, v >> -n otherwise: one shift once n is a constant (the callers' loops unroll fully).
 __device__ __forceinline__ uint32_t shl_by(uint32_t v, int n) { return n >= 0 ? v << n : v >> -n; }
-// n words from a 2-byte-aligned LDS address: aligned reads, shifted into place (v_alignbyte_b32).
+// n words from a 2-byte-aligned LDS address: aligned reads, shifted into place (v_alignbyte_b32). (gfx950 also
+// reads unaligned LDS addresses in hardware, but measured slower here: the Q6_K GEMV and GEMM lost 7-12%.)
 template <int N>
 __device__ __forceinline__ void words_a2(const uint8_t* p, uint32_t* out) {
     // stay a derivation of p (pointer arithmetic, not an integer round trip), so the reads keep p's address space
@@ -155,13 +156,10 @@ __device__ __forceinline__ void sb_q6(const uint8_t* b, const X& x, int& isum, f
 // The (d_b dx) s_b of block k (one term of the sum).
 template <class X>
 __device__ __forceinline__ float q8_0_term(const uint8_t* b, const X& x, int k, float dx) {
-    uint32_t w[9];
-    words_a2<9>(b + 34 * k, w);  // d (low half of w[0]) then 32 int8
     uint32_t q[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) q[i] = align_bytes(w[i + 1], w[i], 2);
+    words_a2<8>(b + 34 * k + 2, q);  // the 32 int8 after the block's f16 scale
     const int s = dot16(q, x.q16(32 * k), x.q16(32 * k + 16));
-    return (f16_to_f32(w[0] & 0xFFFF) * dx) * (float)s;
+    return (f16_to_f32(rd16(b + 34 * k)) * dx) * (float)s;
 }
 template <class X>
 __device__ __forceinline__ float sb_q8_0(const uint8_t* b, const X& x, int nb, float dx) {
