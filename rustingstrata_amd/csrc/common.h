@@ -92,6 +92,9 @@ __device__ __forceinline__ void load_lds16_so(uint64_t base, uint32_t off, const
 }
 // This wave's loads into LDS are complete (vmcnt 0; the barrier that follows publishes them to the block).
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Wait for this wave's LDS reads: before global_load_lds overwrites LDS bytes the wave has just read, since the
+// async write can land ahead of a read still queued in the LDS (a barrier carries this wait; a wave-local reuse does not).
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 // All but this wave's N most recent vector memory operations are complete (vector loads complete in order).
 template <int N>
 __device__ __forceinline__ void wait_vm() {

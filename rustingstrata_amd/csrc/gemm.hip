@@ -16,7 +16,8 @@
 // step every wave
 //   1. decodes its rows' super-block into digit-plane B operands (registers), issuing the next step's X loads
 //      between the decode units;
-//   2. after a barrier (the raw weights' one LDS buffer is free) issues the next step's raw-weight loads;
+//   2. issues the next step's raw-weight loads for its own 16 rows into their LDS rows (only this wave reads
+//      them, so no barrier: a wave that has decoded starts its tiles while the others still decode);
 //   3. runs its 16 position tiles in pairs: the two tiles' MFMA chains interleaved, then their float close.
 // The two waves of a SIMD overlap one's VALU work (decode, close) with the other's MFMAs.
 // Loads go straight from global memory into LDS (global_load_lds_dwordx4: lane l of a wave's instruction writes the
@@ -151,11 +152,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
 
     // Per-lane load addresses of an item. X instruction j of wave w fills 1 KB of LDS: positions 4 (XI w + j) + l / 16,
     // LDS chunk l % 16, which holds X chunk (l % 16) ^ (p & 15). Weight instruction i of wave w fills chunks
-    // c = 64 (w + NW i) + l (row c / NCH, chunk c % NCH, LDS offset 16 c). An X instruction whose 4 positions are all
+    // c = 64 i + l of the wave's own 16 rows (block row 16 w + c / NCH, chunk c % NCH). An X instruction whose 4 positions are all
     // past cnt is skipped; positions past cnt in a partly live one load the item's first row (their results are never
     // stored); rows past `rows` read the last row. The scale of position tid (tid < GM) goes through a register.
     constexpr int XI = GM * 16 / 64 / NW;                     // X instructions per wave per step
-    constexpr int WI = (GN * NCH + 64 * NW - 1) / (64 * NW);  // weight instructions per wave per step
+    constexpr int WI = (16 * NCH + 63) / 64;                  // weight instructions per wave per step (its 16 rows)
     static_assert(NCH <= 15 && WI <= 8, "chunk numbers of a lane's weight instructions fit one word");
     static_assert(SBB < 225, "the no-chunk number 15 lands past every super-block");
     static_assert(XI % 4 == 0, "X instructions spread evenly over the 4 decode units");
@@ -167,13 +168,11 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
         int cnt;           // the item's positions
     };
     const int rl = 16 * wave + (lane & 15);  // this lane's weight row in the block
-    // Weight instruction i of this wave: chunk wchunk(i) of the block (of the wave's matrix half in pair mode, waves
-    // 0-3 the first matrix's 64 rows, 4-7 the second's), row wchunk / NCH within it; LDS chunk wchunk + whalf.
-    const int whalf = pair ? 64 * NCH * (wave >> 2) : 0;
-    const int wlim = pair ? 64 * NCH : GN * NCH;
-    auto wchunk = [&](int i) __attribute__((always_inline)) {
-        return pair ? 64 * ((wave & 3) + 4 * i) + lane : 64 * (wave + NW * i) + lane;
-    };
+    // Weight instruction i of this wave: chunk wchunk(i) of the wave's own 16 rows (the rows it decodes: block rows
+    // 16 w .., in pair mode waves 0-3 the first matrix's 64 rows and 4-7 the second's), block row 16 w + wchunk / NCH,
+    // LDS chunk 16 w NCH + wchunk. Each wave reloads its rows for the next step as soon as its own decode is done.
+    const int wlim = 16 * NCH;
+    auto wchunk = [&](int i) __attribute__((always_inline)) { return 64 * i + lane; };
     auto addr_of = [&](const Item& it) __attribute__((always_inline)) {
         Addr ad;
         ad.cnt = it.cnt;
@@ -188,7 +187,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
                   __umul24((uint32_t)min(it.n0 + (pair ? (rl & 63) : rl), a.rows - 1), (uint32_t)a.rb);
 #pragma unroll
         for (int i = 0; i < WI; i++)
-            ad.wro[i] = __umul24((uint32_t)min(it.n0 + min(wchunk(i) / NCH, GNO - 1), a.rows - 1), (uint32_t)a.rb);
+            ad.wro[i] = __umul24((uint32_t)min(it.n0 + ((16 * wave + min(wchunk(i) / NCH, 15)) & (GNO - 1)), a.rows - 1),
+                                 (uint32_t)a.rb);
         return ad;
     };
     // X instruction j of super-block s of an item into the X buffer of step g (X and dx rotate by 2).
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < WI; i++) {
             const uint32_t t = b15 + ad.wro[i], o = (t & ~15u) + 16 * ((wcc >> (4 * i)) & 15);
-            if (o < t + SBB) load_lds16_so(base, o, raw + 16 * (whalf + wchunk(i) - lane));
+            if (o < t + SBB) load_lds16_so(base, o, raw + 16 * (16 * NCH * wave + wchunk(i) - lane));
         }
     };
     float dxv = 0.0f;
@@ -440,7 +440,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             for (int h = 0; h < XI / 4; h++)
                 if (nx) load_x1(aL, sL, g + 1, (XI / 4) * kk + h);
         });
-        __syncthreads();  // every wave has decoded: the raw buffer takes the next step's weights
+        // this wave's rows are decoded (and its reads of them done): their raw buffer takes the next step's weights
+        wait_lds();
         if (nx) load_w(iL, aL, sL);
         tiles(g, (cur.cnt + 15) >> 4);
         if (s + 1 == nsb) store(cur, g);
