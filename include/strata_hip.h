@@ -99,7 +99,9 @@ int strata_quant_xq(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t n, 
 /* ---- decode GEMV ---- */
 
 /* Backend::gemv (src/backend.rs:199): y = W x over all rows. cols must be a multiple of 256 (of 32 for Q8_0),
- * as Gpu::gemv_cols requires (src/cuda/mod.rs:567-571). */
+ * as Gpu::gemv_cols requires (src/cuda/mod.rs:567-571), and a row at most 24512 bytes (one weight tile; e.g. 43520
+ * Q4_K or 23040 Q8_0 columns). gemv, gemvn and gemvq take any such row; the MoE, paired and no-alloc GEMVs take up
+ * to 16384 columns. */
 int strata_gemv(strata_ctx* ctx, const strata_tensor* w, uint64_t x, uint64_t y);
 /* Backend::gemvn (src/backend.rs:202): y[t] = W x[t] for t < nt (1..4), each weight block read once; bit-equal
  * to strata_gemv per input. */

@@ -148,7 +148,7 @@ int check_type(int ty) {
 
 // Gpu::gemv_cols (src/cuda/mod.rs:567-571), with this backend's requirement of whole 256-value super-blocks for the
 // K and IQ types (the reference's `_p` kernels cover partial ones; no hot-path shape has them).
-int check_gemv_cols(int ty, uint64_t cols) {
+int check_gemv_cols(int ty, uint64_t cols, bool wide) {
     uint64_t b = ty == Q8_0 ? 32 : 256;
     if (cols == 0 || cols % b)
         return set_error(std::string(type_name(ty)) + " tensor with " + std::to_string(cols) +
@@ -156,8 +156,9 @@ int check_gemv_cols(int ty, uint64_t cols) {
     if (row_bytes(ty, cols) > gemv_max_row_bytes())
         return set_error(std::string(type_name(ty)) + " tensor with " + std::to_string(cols) +
                          " columns: a row exceeds the GEMV tile (" + std::to_string(gemv_max_row_bytes()) + " bytes)");
-    if (cols > 16384)
-        return set_error("GEMV with " + std::to_string(cols) + " columns: at most 16384");
+    if (!wide && cols > GEMV1_MAX_COLS)
+        return set_error("GEMV with " + std::to_string(cols) + " columns: at most " + std::to_string(GEMV1_MAX_COLS) +
+                         " on this path (gemv / gemvn / gemvq take wider rows)");
     return 0;
 }
 
@@ -422,11 +423,12 @@ int strata_gemvq(strata_ctx* c, const strata_tensor* w, uint64_t x, uint64_t x_s
     }
     if (check_ctx(c) || check_tensor(w, "gemv")) return -1;
     if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
-    if (check_gemv_cols(w->ty, w->cols) || check_align(w->ty, w->ptr, "gemv")) return -1;
+    if (check_gemv_cols(w->ty, w->cols, true) || check_align(w->ty, w->ptr, "gemv")) return -1;
     if (w->rows == 0) return 0;
     if (w->rows > (1u << 30)) return set_error("gemv: too many rows");
-    // One input: the kernel quantizes x itself; several: quantize once for all blocks.
-    if (!xq && nt > 1 && quant_into_scratch(c, x, x_stride, w->cols, nt, &xq)) return -1;
+    // One input of up to GEMV1_MAX_COLS values: the kernel quantizes x itself; several, or a wider row: quantize once
+    // for all blocks.
+    if (!xq && (nt > 1 || w->cols > GEMV1_MAX_COLS) && quant_into_scratch(c, x, x_stride, w->cols, nt, &xq)) return -1;
     GemvLaunch g;
     g.xf = (const float*)x; g.x_stride = x_stride;
     g.ty = w->ty; g.w = (const uint8_t*)w->ptr; g.rows = (int)w->rows; g.cols = (int)w->cols;
@@ -449,7 +451,7 @@ int strata_gemvn_noalloc(strata_ctx* c, const strata_tensor* w, uint64_t x, uint
                         uint64_t y_stride, uint64_t nt) {
     if (check_ctx(c) || check_tensor(w, "gemvn_noalloc")) return -1;
     if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
-    if (check_gemv_cols(w->ty, w->cols) || check_align(w->ty, w->ptr, "gemvn_noalloc")) return -1;
+    if (check_gemv_cols(w->ty, w->cols, false) || check_align(w->ty, w->ptr, "gemvn_noalloc")) return -1;
     if (nt > 1 && xq_bytes(w->cols, nt) > NOALLOC_SCRATCH_BYTES)
         return set_error("gemvn_noalloc: " + std::to_string(nt) + " inputs of " + std::to_string(w->cols) +
                          " values need " + std::to_string(xq_bytes(w->cols, nt)) + " bytes of scratch (at most " +
@@ -482,7 +484,7 @@ int strata_gemvq2(strata_ctx* c, const strata_tensor* a, const strata_tensor* b,
     }
     if (nt < 1 || nt > 4) return set_error("gemvn: " + std::to_string(nt) + " inputs (1 to 4)");
     if (a->rows > (1u << 30) || b->rows > (1u << 30)) return set_error("gemvq2: too many rows");
-    if (check_gemv_cols(a->ty, a->cols) || check_align(a->ty, a->ptr, "gemvq2") || check_align(b->ty, b->ptr, "gemvq2")) return -1;
+    if (check_gemv_cols(a->ty, a->cols, false) || check_align(a->ty, a->ptr, "gemvq2") || check_align(b->ty, b->ptr, "gemvq2")) return -1;
     if (!xq && nt > 1 && quant_into_scratch(c, x, x_stride, a->cols, nt, &xq)) return -1;
     GemvLaunch g;
     g.xf = (const float*)x; g.x_stride = x_stride;
@@ -504,7 +506,7 @@ static int moe_gemv_impl(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, ui
                          uint64_t k, uint64_t x, uint64_t x_stride, uint64_t xg, uint64_t y, int has_pair, int64_t w2,
                          int64_t y2, uint64_t xq, uint64_t xu) {
     if (check_ctx(c) || check_type(ty)) return -1;
-    if (check_gemv_cols(ty, cols) || check_align(ty, w, "moe_gemv")) return -1;
+    if (check_gemv_cols(ty, cols, false) || check_align(ty, w, "moe_gemv")) return -1;
     if (check_align(ty, stride, "moe_gemv stride") || (has_pair && check_align(ty, (uint64_t)w2, "moe_gemv pair offset"))) return -1;
     if (xg < 1 || k % xg) return set_error("moe_gemv: " + std::to_string(k) + " slots in groups of " + std::to_string(xg));
     if (k == 0 || rows == 0) return 0;
@@ -574,7 +576,7 @@ static int down_combine_fused(strata_ctx* c, int ty, uint64_t rows, uint64_t col
                               uint64_t slots, uint64_t k, uint64_t xq, uint64_t x, uint64_t wh, uint64_t sh, uint64_t sg,
                               uint64_t t) {
     if (check_ctx(c) || check_type(ty)) return -1;
-    if (check_gemv_cols(ty, cols) || check_align(ty, w, "moe_down_combine") || check_align(ty, stride, "moe_down_combine stride")) return -1;
+    if (check_gemv_cols(ty, cols, false) || check_align(ty, w, "moe_down_combine") || check_align(ty, stride, "moe_down_combine stride")) return -1;
     if (!t || !rows || !k) return 1;
     if (rows > (1u << 30) || k > 256 || t > 65535 || !slots || !wh || !x) return 0;
     DownCombineLaunch d;

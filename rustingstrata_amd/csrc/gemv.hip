@@ -70,6 +70,14 @@ __device__ __forceinline__ float ordered_sum_row(float f) {
     for (int k = 1; k < G; k++) s = f + dpp_f<0x111>(s);  // row_shr:1
     return s;
 }
+// The same fold over the 64 lanes of a wave continued from a running sum: ((run + f_0) + f_1) + ... + f_63, in every
+// lane (rows of more than 64 super-blocks: lane l holds super-block 64 p + l of pass p).
+__device__ __forceinline__ float ordered_sum_from(float run, float v) {
+    const float f = v + 0.0f;
+    float s = run;
+    for (int j = 0; j < 64; j++) s = s + __shfl(f, j);
+    return s;
+}
 __device__ __forceinline__ float ordered_sum(float v, int g) {
     const float f = v + 0.0f;
     float s = f;
@@ -190,19 +198,25 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
             float acc[NT];
 #pragma unroll
             for (int u = 0; u < NT; u++) acc[u] = 0.0f;
-            if (rr < cs.nr) {
-                const uint8_t* rowp = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb;
-                for (int sb = gl; sb < nsb; sb += G) {
+            // passes of G super-blocks, one a lane; a row of more than 64 (G = 64) takes several, the running sum
+            // carried from pass to pass so the terms still meet in super-block order
+            for (int p0 = 0; p0 < nsb; p0 += G) {
+                const int sb = p0 + gl;
+                float f[NT];
+#pragma unroll
+                for (int u = 0; u < NT; u++) f[u] = 0.0f;
+                if (rr < cs.nr && sb < nsb) {
+                    const uint8_t* rowp = tile + (cs.beg - cs.g0) + (uint64_t)rr * a.rb;
 #pragma unroll
                     for (int u = 0; u < NT; u++) {
                         const XLds xv{sx + u * cols + 256 * sb, sd + u * (cols / 32) + 8 * sb, ss + u * (cols / 16) + 16 * sb};
                         const int nv = min(256, cols - 256 * sb);
-                        acc[u] += Q32 ? sb_dot_q32<T>(rowp + sb * SBB, xv, tab, nv) : sb_dot_q8k<T>(rowp + sb * SBB, xv, tab, nv);
+                        f[u] = Q32 ? sb_dot_q32<T>(rowp + sb * SBB, xv, tab, nv) : sb_dot_q8k<T>(rowp + sb * SBB, xv, tab, nv);
                     }
                 }
-            }
 #pragma unroll
-            for (int u = 0; u < NT; u++) acc[u] = ordered_sum(acc[u], G);
+                for (int u = 0; u < NT; u++) acc[u] = p0 == 0 ? ordered_sum(f[u], G) : ordered_sum_from(acc[u], f[u]);
+            }
             if (rr < cs.nr && gl == G - 1) {
 #pragma unroll
                 for (int u = 0; u < NT; u++) cs.Y[(int64_t)u * a.y_stride + cs.r0 + rr] = acc[u];
@@ -642,6 +656,12 @@ static hipError_t gemv_nt(const GemvArgs& a, long long tiles, size_t smem, hipSt
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
             ncu = 256;
     }
+    static bool attr = false;
+    if (!attr) {  // wide rows (more than GEMV1_MAX_COLS values) stage more than 64 KB of x and tile
+        if (hipFuncSetAttribute((const void*)gemv_kernel<T, NT, Q32>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+            return hipErrorInvalidValue;
+        attr = true;
+    }
     if (cached_smem != smem) {
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_kernel<T, NT, Q32>, GEMV_THREADS, smem) != hipSuccess || n < 1) n = 1;
@@ -693,7 +713,7 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     const int maxrows = g.pair ? (g.rows > g.rows2 ? g.rows : g.rows2) : g.rows;
     const int nslots = g.ids ? g.k : 1, nz = g.pair ? 2 : 1;
     // Rows per tile: as many as fit the tile, but no fewer tiles than about 4 per CU.
-    const bool single = g.nt == 1;
+    const bool single = g.nt == 1 && g.cols <= GEMV1_MAX_COLS;
     const int rmax = (int)(((single ? GEMV1_TILE : GEMV_TILE) - 32) / a.rb);
     long long want = (long long)maxrows * nslots * nz / (4LL * ncu);
     a.R = (int)(want < 1 ? 1 : want > rmax ? rmax : want);

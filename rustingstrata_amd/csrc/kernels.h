@@ -59,5 +59,8 @@ hipError_t launch_copy(const void* src, void* dst, uint64_t bytes, hipStream_t s
 hipError_t launch_read(const void* src, uint64_t bytes, uint32_t* sink, hipStream_t s);
 // Largest row size (bytes) launch_gemv accepts.
 uint64_t gemv_max_row_bytes();
+// Columns the single-input kernel takes (a lane keeps one super-block's x in registers, at most 64 lanes a row);
+// launch_gemv runs wider single-input rows on the multi-input kernel, which needs x pre-quantized (GemvLaunch::xq).
+constexpr int GEMV1_MAX_COLS = 16384;
 
 }  // namespace strata

@@ -216,6 +216,40 @@ def test_gemv_bits_over_random_shapes(hip, ty):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (case, rows, cols, lo, int((got != want).sum()))
 
 
+@pytest.mark.parametrize("ty", ggml.TYPES)
+def test_gemv_wide_rows(hip, ty):
+    """Rows of more than 16384 values (dense FFN down projections: 18944, 24576 columns) run on the multi-input
+    kernel, several super-blocks a lane with the running sum carried in super-block order: the CPU dot's bits
+    (within rounding for Q8_0 and IQ4_XS, as for narrow rows); gemvn of two inputs gives each input's gemv bits."""
+    for cols in (18944, 24576):
+        if ggml.row_bytes(ty, cols) > 24512:
+            continue  # a row must fit one weight tile (24 KB)
+        rows = 37
+        w, x, t, got = gemv_case(hip, ty, rows, cols, seed=cols + ty)
+        want = O.matvec(ty, w, rows, cols, x)
+        assert max_rel_err(got, want) <= TOL, (cols, max_rel_err(got, want))
+        if ty not in (ggml.Q8_0, ggml.IQ4_XS):
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (cols, int((got != want).sum()))
+        xs = np.stack([x, normal(cols, seed=cols + ty + 5)])
+        y2 = hip.alloc(2 * rows * 4)
+        hip.gemvn(t, up(hip, xs), cols, y2, rows, 2)
+        got2 = down(hip, y2, np.float32, 2 * rows).reshape(2, rows)
+        assert np.array_equal(got2[0].view(np.uint32), got.view(np.uint32))
+        want2 = O.matvec(ty, w, rows, cols, xs[1])
+        assert max_rel_err(got2[1], want2) <= TOL
+
+
+def test_gemv_wide_rows_limits(hip):
+    """Rows past the 24 KB weight tile are refused; the MoE GEMV keeps the single-input kernel's 16384 columns."""
+    w = random_blocks(ggml.Q8_0, 1, 32768, seed=1)
+    t = hip.upload_tensor(ggml.Q8_0, w)
+    with pytest.raises(S.StrataError, match="exceeds the GEMV tile"):
+        hip.gemv(t, up(hip, normal(32768, seed=2)), hip.alloc(4))
+    with pytest.raises(S.StrataError, match="at most 16384"):
+        hip.moe_gemv(ggml.Q4_K, 4, 18944, t.ptr, 0, up(hip, np.zeros(1, np.int32)), 1, up(hip, normal(18944, seed=3)),
+                     18944, 1, hip.alloc(16))
+
+
 @pytest.mark.parametrize("cols", [2048, 3072, 4096])
 def test_gemv_per32_numerics(hip, cols):
     """Reference GPU numerics (per-32 x scales): against f64 dequant times as_seen(x) (tests/kernels.rs:11-19,61)."""
