@@ -65,6 +65,23 @@ __device__ __forceinline__ void att_range(const int* step, int t, int win, int& 
     n_pos = end + 1 - base;
 }
 
+// Eight softmax weights p (in [0, 1]) times 2^14 as f16 hi and lo parts for the P V MFMA: hi rounded toward zero two
+// at a time (v_cvt_pkrtz_f16_f32), lo the remainder (also toward zero), so hi + lo carries each weight to ~2^-21 of
+// its value and the lo parts stay normal f16 numbers down to p ~ 2^-17.
+__device__ __forceinline__ void split_p8(const float (&p)[8], h8& hi, h8& lo) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float a = p[2 * e] * 16384.0f, b = p[2 * e + 1] * 16384.0f;
+        const auto hh = __builtin_amdgcn_cvt_pkrtz(a, b);
+        const auto ll = __builtin_amdgcn_cvt_pkrtz(a - (float)hh[0], b - (float)hh[1]);
+        hw[e] = __builtin_bit_cast(uint32_t, hh);
+        lw[e] = __builtin_bit_cast(uint32_t, ll);
+    }
+    hi = __builtin_bit_cast(h8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+    lo = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+}
+
 // ---------------- decode ----------------
 // Positions a split of a token with n_pos positions: at least one chunk of 64, so short contexts use few waves.
 __device__ __forceinline__ int split_len(int n_pos, int ns) { return max((n_pos + ns - 1) / ns, 64); }
@@ -197,21 +214,21 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                float v = s[kt][i] * usc;
+                float v = s[kt][i];  // the raw score: usc (> 0) is applied in the exponent's fma
                 if (16 * kt + 4 * lg + i >= nc) v = -INFINITY;
                 s[kt][i] = v;
                 mx = fmaxf(mx, v);
             }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(m, mx);
+        const float mnew = fmaxf(m, mx * usc);  // max(v) usc = max(v usc): a positive factor keeps the order
         const float alpha = m == -INFINITY ? 0.0f : exp2_hw(m - mnew);
         float sum = 0.0f;
 #pragma unroll
         for (int kt = 0; kt < 4; kt++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float p = exp2_hw(s[kt][i] - mnew);  // exp2(-inf) = 0 (every chunk has a key: mnew is finite)
+                const float p = exp2_hw(__builtin_fmaf(s[kt][i], usc, -mnew));  // exp2(-inf) = 0 (mnew is finite)
                 s[kt][i] = p;
                 sum += p;
             }
@@ -225,13 +242,11 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
 #pragma unroll
         for (int c = 0; c < 2; c++) {
             h8 ph, pl;
+            {
+                float p[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                // p in [0, 1] times 2^14: the lo parts stay normal down to p ~ 2^-17
-                const float p = s[2 * c + (e >> 2)][e & 3] * 16384.0f;
-                const _Float16 hi = (_Float16)p;
-                ph[e] = hi;
-                pl[e] = (_Float16)(p - (float)hi);
+                for (int e = 0; e < 8; e++) p[e] = s[2 * c + (e >> 2)][e & 3];
+                split_p8(p, ph, pl);
             }
 #pragma unroll
             for (int d = 0; d < DT; d++) {
@@ -497,14 +512,14 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int kp = k0 + 16 * kt + 4 * lg + i;
-                    float v = s[j][kt][i] * usc[j];
+                    float v = s[j][kt][i];  // the raw score: usc (> 0) is applied in the exponent's fma
                     if (edge && (kp > qp || kp < lo)) v = -INFINITY;
                     s[j][kt][i] = v;
                     mx = fmaxf(mx, v);
                 }
             mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(m[j], mx);
+            const float mnew = fmaxf(m[j], mx * usc[j]);  // max(v) usc = max(v usc): a positive factor keeps the order
             const float alpha = m[j] == -INFINITY ? 0.0f : exp2_hw(m[j] - mnew);
             const float mref = mnew == -INFINITY ? 0.0f : mnew;  // a column with no key yet: every p is 0
             float sum = 0.0f;
@@ -512,7 +527,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
             for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float p = exp2_hw(s[j][kt][i] - mref);  // exp2(-inf) = 0
+                    const float p = exp2_hw(__builtin_fmaf(s[j][kt][i], usc[j], -mref));  // exp2(-inf) = 0
                     s[j][kt][i] = p;
                     sum += p;
                 }
@@ -529,16 +544,13 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(const float* __res
         for (int c = 0; c < 2; c++) {
             h8 ph[2], pl[2];
 #pragma unroll
-            for (int j = 0; j < 2; j++)
+            for (int j = 0; j < 2; j++) {
+                if (!live[j]) continue;
+                float p[8];
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    if (!live[j]) break;
-                    // p in [0, 1] times 2^14: the lo parts stay normal down to p ~ 2^-17
-                    const float p = s[j][2 * c + (e >> 2)][e & 3] * 16384.0f;
-                    const _Float16 hi = (_Float16)p;
-                    ph[j][e] = hi;
-                    pl[j][e] = (_Float16)(p - (float)hi);
-                }
+                for (int e = 0; e < 8; e++) p[e] = s[j][2 * c + (e >> 2)][e & 3];
+                split_p8(p, ph[j], pl[j]);
+            }
 #pragma unroll
             for (int d = 0; d < DT; d++) {
                 const uint16_t* vr = &vs[(16 * d + l16) * L::VP + 32 * c + 4 * lg];
