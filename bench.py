@@ -399,11 +399,12 @@ def bench_codebook(hip, S, ggml, iters):
     return out
 
 
-def bench_stack(hip, S, ggml, n_prompt=4096, n_decode=128, chunk=2048, n_layer=48):
+def bench_stack(hip, S, ggml, n_prompt=4096, n_decode=128, chunk=4096, n_layer=48):
     """the 48-layer Qwen3-30B-A3B-shaped stack, random-init on the device (Q2_K gate/up and Q3_K down
     experts, Q6_K attention, Q8_0 embeddings and output head), every expert resident. A uniform-random prompt of 4096
-    token ids is prefilled in chunks of `chunk`, then 128 greedy tokens are decoded (each a recorded-graph replay
-    after the first; the host writes the position before each token, the next token stays on the device)."""
+    token ids is prefilled in chunks of `chunk` (4096: the reference's prefill chunk when it is not calibrated,
+    src/main.rs:30,407), then 128 greedy tokens are decoded (each a recorded-graph replay after the first; the host
+    writes the position before each token, the next token stays on the device)."""
     from rustingstrata_amd.qwen3moe import Config, Model, Weights
     c = Config.qwen3_30b_a3b(n_layer=n_layer)
     t0 = time.time()

@@ -127,9 +127,10 @@ class Weights:
 
 
 class Model:
-    """GpuModel for the Qwen3-MoE stack: KV caches for `ctx` positions, prefill chunks of up to `chunk` tokens."""
+    """GpuModel for the Qwen3-MoE stack: KV caches for `ctx` positions, prefill chunks of up to `chunk` tokens (4096 by
+    default, the reference's prefill chunk when it is not calibrated: src/main.rs:30,407)."""
 
-    def __init__(self, hip, weights, ctx=4096 + 256, chunk=2048):
+    def __init__(self, hip, weights, ctx=4096 + 256, chunk=4096):
         self.hip, self.w, self.c = hip, weights, weights.cfg
         c = self.c
         self.ctx, self.chunk = ctx, chunk
