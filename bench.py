@@ -335,6 +335,33 @@ def codebook_blocks(ggml, ty, rows, cols, seed):
     return blk.reshape(rows, -1)
 
 
+def bench_dense_gemm(hip, S, ggml, iters=20):
+    """Dense prefill GEMMs (gemm_dense) of 4096 positions x 2048 x 2048 per type, X quantized once (SAME_X) so the
+    timed launches are the GEMM alone; int8 TOP/s of the matrix product against the 5.0 POPS peak. Q8_0 runs its own
+    kernel (per-32 float scales close each 32-block in float)."""
+    n, rows, cols = 4096, 2048, 2048
+    rng = np.random.default_rng(21)
+    x = hip.upload(rng.standard_normal((n, cols)).astype(np.float32))
+    y = hip.alloc(n * rows * 4)
+    out = {}
+    for ty in (ggml.Q8_0, ggml.Q4_K, ggml.Q6_K):
+        w = hip.upload(S.quantize_rows(ty, (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)))
+        t = S.GpuTensor(ty, rows, cols, w)
+        hip.gemm_dense(t, n, x, cols, y, rows, S.ACT_STORE)  # quantizes X
+        for _ in range(3):
+            hip.gemm_dense(t, n, x, cols, y, rows, S.ACT_STORE | S.SAME_X)
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0)
+        for _ in range(iters):
+            hip.gemm_dense(t, n, x, cols, y, rows, S.ACT_STORE | S.SAME_X)
+        hip.record(e1)
+        ms = hip.elapsed_ms(e0, e1) / iters
+        tops = 2.0 * n * rows * cols / (ms / 1e3) / 1e12
+        out[ggml.NAMES[ty]] = {"ms": round(ms, 4), "int8_TOPS": round(tops, 1), "mfma_frac": round(tops / INT8_PEAK_TOPS, 4)}
+        del t, w
+    return out
+
+
 def bench_codebook(hip, S, ggml, iters):
     """IQ2_XXS / IQ3_S / IQ4_XS experts of 2048 x 768 (out x in), 128 experts.
     T = 1: moe_gemv over 8 Zipf-routed experts, the 128 experts rotated over copies past 512 MB (GB/s of the 8 experts'
@@ -651,6 +678,8 @@ def main():
         extra["moe_decode_1"] = bench_moe_decode(hip, S, ggml, 200)
         log(f"[bench] MoE decode: {extra['moe_decode_1']}")
         extra["codebook_experts"] = bench_codebook(hip, S, ggml, 100)
+        extra["gemm_dense_4k"] = bench_dense_gemm(hip, S, ggml)
+        log(f"[bench] dense GEMMs 4096 x 2048 x 2048: {extra['gemm_dense_4k']}")
         log(f"[bench] configs[3] codebook experts: {extra['codebook_experts']}")
     if not args.no_stack:
         extra["stack_config4"] = bench_stack(hip, S, ggml)
