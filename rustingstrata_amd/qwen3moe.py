@@ -47,7 +47,7 @@ SCALE = {ggml.Q8_0: (2.2e-4, 3.2e-4), ggml.Q6_K: (1.2e-5, 1.8e-5), ggml.Q2_K: (1
 
 
 class Layer:
-    __slots__ = ("attn_norm", "q", "k", "v", "q_norm", "k_norm", "o", "ffn_norm", "router", "gate_up", "down",
+    __slots__ = ("attn_norm", "qkv", "q", "k", "v", "q_norm", "k_norm", "o", "ffn_norm", "router", "gate_up", "down",
                  "e_gu", "e_down", "up_off", "kc", "vc")
 
 
@@ -64,8 +64,8 @@ class Weights:
         c = self.cfg
         return (ggml.row_bytes(c.ty_gate_up, c.n_embd) * c.n_ff_exp, ggml.row_bytes(c.ty_down, c.n_ff_exp) * c.n_embd)
 
-    def _quant(self, ty, rows, cols, seed, buf=None):
-        t = GpuTensor(ty, rows, cols, buf if buf is not None else self.hip.alloc(rows * ggml.row_bytes(ty, cols)))
+    def _quant(self, ty, rows, cols, seed, buf=None, offset=0):
+        t = GpuTensor(ty, rows, cols, buf if buf is not None else self.hip.alloc(rows * ggml.row_bytes(ty, cols)), offset)
         lo, hi = SCALE[ty]
         self.hip.fill_blocks(t, seed, lo, hi)
         return t
@@ -88,9 +88,14 @@ class Weights:
             ly.ffn_norm = hip.upload((1.0 + 0.1 * rng.standard_normal(c.n_embd)).astype(np.float32))
             ly.q_norm = hip.upload((1.0 + 0.1 * rng.standard_normal(c.head_dim)).astype(np.float32))
             ly.k_norm = hip.upload((1.0 + 0.1 * rng.standard_normal(c.head_dim)).astype(np.float32))
-            ly.q = w._quant(c.ty_attn, c.n_head * c.head_dim, c.n_embd, b + 1)
-            ly.k = w._quant(c.ty_attn, c.n_head_kv * c.head_dim, c.n_embd, b + 2)
-            ly.v = w._quant(c.ty_attn, c.n_head_kv * c.head_dim, c.n_embd, b + 3)
+            # q, k and v rows in one buffer (one GEMV serves all three in decode), each filled from its own seed
+            nq, nkv = c.n_head * c.head_dim, c.n_head_kv * c.head_dim
+            rb = ggml.row_bytes(c.ty_attn, c.n_embd)
+            qkv = hip.alloc((nq + 2 * nkv) * rb)
+            ly.q = w._quant(c.ty_attn, nq, c.n_embd, b + 1, qkv, 0)
+            ly.k = w._quant(c.ty_attn, nkv, c.n_embd, b + 2, qkv, nq * rb)
+            ly.v = w._quant(c.ty_attn, nkv, c.n_embd, b + 3, qkv, (nq + nkv) * rb)
+            ly.qkv = GpuTensor(c.ty_attn, nq + 2 * nkv, c.n_embd, qkv)
             ly.o = w._quant(c.ty_attn, c.n_embd, c.n_head * c.head_dim, b + 4)
             ly.router = hip.upload_f32((0.02 * rng.standard_normal((c.n_expert, c.n_embd))).astype(np.float32))
             # gate and up stacks: 2 * n_expert matrices of n_ff_exp rows, one fill
@@ -116,7 +121,13 @@ class Weights:
             ly.ffn_norm = hip.upload(np.asarray(L["ffn_norm"], np.float32))
             ly.q_norm = hip.upload(np.asarray(L["q_norm"], np.float32))
             ly.k_norm = hip.upload(np.asarray(L["k_norm"], np.float32))
-            ly.q, ly.k, ly.v, ly.o = (hip.upload_tensor(c.ty_attn, L[n]) for n in ("q", "k", "v", "o"))
+            ly.o = hip.upload_tensor(c.ty_attn, L["o"])
+            qkv = [np.ascontiguousarray(L[n]) for n in ("q", "k", "v")]
+            ly.qkv = hip.upload_tensor(c.ty_attn, np.concatenate(qkv))
+            rb = qkv[0].shape[1]
+            ly.q = GpuTensor(c.ty_attn, qkv[0].shape[0], c.n_embd, ly.qkv.buf, 0)
+            ly.k = GpuTensor(c.ty_attn, qkv[1].shape[0], c.n_embd, ly.qkv.buf, qkv[0].shape[0] * rb)
+            ly.v = GpuTensor(c.ty_attn, qkv[2].shape[0], c.n_embd, ly.qkv.buf, (qkv[0].shape[0] + qkv[1].shape[0]) * rb)
             ly.router = hip.upload_f32(L["router"])
             ly.gate_up = hip.upload(np.concatenate([np.ascontiguousarray(L["gate"]).reshape(-1),
                                                     np.ascontiguousarray(L["up"]).reshape(-1)]))
@@ -161,7 +172,9 @@ class Model:
         # decode buffers
         self.hq = A(H + H // 8)
         self.mix = A(H * 4)
-        self.dq, self.dk, self.dv = A(nh * hd * 4), A(kv * 4), A(kv * 4)
+        # the decode's q, k and v outputs of the one q/k/v GEMV, back to back
+        self.dqkv = A((nh * hd + 2 * kv) * 4)
+        self.dq, self.dk, self.dv = int(self.dqkv), int(self.dqkv) + 4 * nh * hd, int(self.dqkv) + 4 * (nh * hd + kv)
         self.dqo, self.dko = A(nh * hd * 4), A(kv * 4)
         self.datt = A(nh * hd * 4)
         self.part = A(hip.attn_part_floats(nh, hd) * 4)
@@ -245,8 +258,7 @@ class Model:
         hip.get_rows(w.embd, self.tok, 1, x)
         for ly in w.layers:
             hip.rms_norm_q(x, H, ly.attn_norm, self.h, H, H, 1, c.eps, xq=self.hq)
-            hip.gemvq(ly.q, self.h, H, self.hq, self.dq, nh * hd, 1)
-            hip.gemvq2(ly.k, ly.v, self.h, H, self.hq, self.dk, self.dv, 1)
+            hip.gemvq(ly.qkv, self.h, H, self.hq, self.dqkv, nh * hd + 2 * kv, 1)  # q, k and v in one launch
             hip.rms_norm_rope_qk(self.dq, hd, ly.q_norm, self.dqo, nh, nh, self.dk, ly.k_norm, self.dko, nkv, nkv, hd,
                                  c.eps, hd, self.step, c.rope_base, self.dv, ly.kc, ly.vc)
             hip.attn_decode(self.dqo, ly.kc, ly.vc, 0, self.datt, self.part, self.step, nh, nkv, hd,
