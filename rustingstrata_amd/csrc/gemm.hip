@@ -512,8 +512,9 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
 // K=64 MFMA step yields the two blocks' int32 sums separately (lanes 0-31 of the weight operand carry the first
 // block's values and zeros for the second, lanes 32-63 the reverse: two MFMAs per step, no extra MFMA work), and each
 // block closes in float at once: acc += dx (d0 s0 + d1 s1). A block of 4 waves takes a 64-row block of one tile and
-// walks the tile's positions 64 at a time; wave w owns rows 16 w .. 16 w + 15.
-constexpr int Q8_ROWS = 64, Q8_POS = 64, Q8_SB = 272, Q8_RP = 280;  // rows, positions per pass, bytes per 256 values, LDS row pitch
+// walks the tile's positions Q8_POS (128) at a time, the next step's X, scales and weights loaded into registers while the current one is computed; wave w owns rows 16 w .. 16 w + 15.
+constexpr int Q8_ROWS = 64, Q8_POS = 128, Q8_SB = 272, Q8_RP = 280;  // rows, positions per pass, bytes per 256 values, LDS row pitch
+constexpr int Q8_NT = Q8_POS / 16;  // MFMA position tiles per pass
 
 __global__ __launch_bounds__(256) void gemm_q8_0_kernel(GemmArgs a) {
     __shared__ __align__(16) int8_t xs8[Q8_POS * 256];
@@ -537,29 +538,56 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(GemmArgs a) {
     }
     const int cols = a.cols, nsb = cols / 256, rl = 16 * wave + (lane & 15);
     auto xrow_of = [&](int p) { p = p < cnt ? p : 0; return a.xrow ? a.xrow[m0 + p] : m0 + p; };
+    // Per step (256 values): the X rows of the pass's positions (thread: 4 16-byte chunks), their scales and the
+    // rows' 272 bytes of weights (thread: QW words of the rows' 4-byte-aligned covers) go through registers, the next
+    // step's loads in flight while this one is computed from LDS.
+    constexpr int QW = (Q8_ROWS * (Q8_RP / 4) + 255) / 256;
+    v4i xv[Q8_POS * 16 / 256];
+    uint32_t wv[QW];
+    float dxv = 0.0f;
     for (int p0 = 0; p0 < cnt; p0 += Q8_POS) {
-        float acc[4][4];
+        uint32_t xoff[Q8_POS * 16 / 256];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int u = 0; u < Q8_POS * 16 / 256; u++) {
+            const int c = tid + 256 * u, p = c >> 4, ch = c & 15;
+            xoff[u] = (uint32_t)xrow_of(p0 + p) * (uint32_t)cols + 16 * ch;
+        }
+        const uint32_t dxo = (uint32_t)xrow_of(p0 + (tid & (Q8_POS - 1))) * (uint32_t)(cols / 32);
+        auto fetch = [&](int sb) {
+#pragma unroll
+            for (int u = 0; u < Q8_POS * 16 / 256; u++) xv[u] = *gptr<v4i>((uint64_t)(a.xq + xoff[u] + 256 * sb));
+            if (tid < Q8_POS) dxv = *gptr<float>((uint64_t)(a.xd + dxo + 8 * sb));
+#pragma unroll
+            for (int u = 0; u < QW; u++) {
+                const int c = tid + 256 * u, r = c / (Q8_RP / 4), j = c % (Q8_RP / 4);
+                const uint64_t beg = w + (uint64_t)min(n0 + min(r, Q8_ROWS - 1), a.rows - 1) * a.rb + (uint64_t)sb * Q8_SB;
+                const uint64_t a4 = beg & ~(uint64_t)3;
+                wv[u] = 0;
+                if (c < Q8_ROWS * (Q8_RP / 4) && a4 + 4 * (uint64_t)j < beg + Q8_SB) wv[u] = *gptr<uint32_t>(a4 + 4 * (uint64_t)j);
+            }
+        };
+        float acc[Q8_NT][4];
+#pragma unroll
+        for (int i = 0; i < Q8_NT; i++)
 #pragma unroll
             for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
+        fetch(0);
         for (int sb = 0; sb < nsb; sb++) {
             __syncthreads();  // the previous step's readers are done
-            // X: 64 positions x 256 bytes, 16-byte chunk c of position p at chunk c ^ (p & 15)
-            for (int c = tid; c < Q8_POS * 16; c += 256) {
-                const int p = c >> 4, ch = c & 15;
-                const uint32_t xr = (uint32_t)xrow_of(p0 + p);
-                *(v4i*)(xs8 + p * 256 + 16 * (ch ^ (p & 15))) = *gptr<v4i>((uint64_t)(a.xq + (uint64_t)xr * cols + 256 * sb + 16 * ch));
+            // X: Q8_POS positions x 256 bytes, 16-byte chunk c of position p at chunk c ^ (p & 15)
+#pragma unroll
+            for (int u = 0; u < Q8_POS * 16 / 256; u++) {
+                const int c = tid + 256 * u, p = c >> 4, ch = c & 15;
+                *(v4i*)(xs8 + p * 256 + 16 * (ch ^ (p & 15))) = xv[u];
             }
-            if (tid < Q8_POS) dx8[tid] = *gptr<float>((uint64_t)(a.xd + (uint64_t)xrow_of(p0 + tid) * (cols / 32) + 8 * sb));
-            // weights: each row's 272 bytes of the step from their 4-byte-aligned cover (rows past `rows` read the last)
-            for (int c = tid; c < Q8_ROWS * (Q8_RP / 4); c += 256) {
-                const int r = c / (Q8_RP / 4), j = c % (Q8_RP / 4);
-                const uint64_t beg = w + (uint64_t)min(n0 + r, a.rows - 1) * a.rb + (uint64_t)sb * Q8_SB;
-                const uint64_t a4 = beg & ~(uint64_t)3;
-                if (a4 + 4 * (uint64_t)j < beg + Q8_SB) *(uint32_t*)(ws8 + r * Q8_RP + 4 * j) = *gptr<uint32_t>(a4 + 4 * (uint64_t)j);
+            if (tid < Q8_POS) dx8[tid] = dxv;
+#pragma unroll
+            for (int u = 0; u < QW; u++) {
+                const int c = tid + 256 * u;
+                if (c < Q8_ROWS * (Q8_RP / 4)) *(uint32_t*)(ws8 + 4 * c) = wv[u];
             }
             __syncthreads();
+            if (sb + 1 < nsb) fetch(sb + 1);
             const uint64_t rbeg = w + (uint64_t)min(n0 + rl, a.rows - 1) * a.rb + (uint64_t)sb * Q8_SB;
             const uint8_t* wr = ws8 + rl * Q8_RP + (uint32_t)(rbeg & 3);
 #pragma unroll
@@ -570,24 +598,28 @@ __global__ __launch_bounds__(256) void gemm_q8_0_kernel(GemmArgs a) {
                 const v4i qw = {(int)qv[0], (int)qv[1], (int)qv[2], (int)qv[3]}, z = {0, 0, 0, 0};
                 const v4i b0 = kl < 2 ? qw : z, b1 = kl < 2 ? z : qw;
                 const float d0 = h16(wr + 34 * (2 * kk)), d1 = h16(wr + 34 * (2 * kk + 1));
+                // the 2 Q8_NT MFMAs first, then their closes (each result is used 2 Q8_NT issues after its MFMA)
+                v4i c0[Q8_NT], c1[Q8_NT];
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < Q8_NT; i++) {
                     const v4i av = *(const v4i*)(xs8 + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
-                    const v4i c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b0, z, 0, 0, 0);
-                    const v4i c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b1, z, 0, 0, 0);
+                    c0[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b0, z, 0, 0, 0);
+                    c1[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b1, z, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < Q8_NT; i++)
 #pragma unroll
                     for (int q = 0; q < 4; q++) {  // sum += (d dx) s per 32-block, in order (src/cpu_moe.rs:319-325)
                         const float dxq = dx8[16 * i + 4 * kl + q];
-                        acc[i][q] = acc[i][q] + (d0 * dxq) * (float)c0[q];
-                        acc[i][q] = acc[i][q] + (d1 * dxq) * (float)c1[q];
+                        acc[i][q] = acc[i][q] + (d0 * dxq) * (float)c0[i][q];
+                        acc[i][q] = acc[i][q] + (d1 * dxq) * (float)c1[i][q];
                     }
-                }
             }
         }
         // outputs: weight row n0 + rl, positions p0 + 16 i + 4 kl + q
         if (n0 + rl < a.rows) {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < Q8_NT; i++)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const int m = p0 + 16 * i + 4 * kl + q;
