@@ -58,6 +58,29 @@ __device__ __forceinline__ void load_iq_tables(IqTables* t) {
         if (i < 128) t->ksigns[i] = STRATA_KSIGNS_IQ2XS[i];
     }
 }
+// The same in two halves for a block of 256 threads: the thread's entries into registers (the loads may then fly with
+// the kernel's first weight loads), and later into LDS (the caller synchronises after the store).
+struct IqRegs {
+    uint32_t g3[2];
+    uint64_t g2;
+    uint8_t ks;
+};
+__device__ __forceinline__ IqRegs load_iq_regs() {
+    const int i = threadIdx.x;
+    IqRegs r;
+    r.g3[0] = STRATA_IQ3S_GRID[i];
+    r.g3[1] = STRATA_IQ3S_GRID[i + 256];
+    r.g2 = STRATA_IQ2XXS_GRID[i];
+    r.ks = STRATA_KSIGNS_IQ2XS[i & 127];
+    return r;
+}
+__device__ __forceinline__ void store_iq_regs(IqTables* t, const IqRegs& r) {
+    const int i = threadIdx.x;
+    t->iq3s[i] = r.g3[0];
+    t->iq3s[i + 256] = r.g3[1];
+    t->iq2xxs[i] = r.g2;
+    if (i < 128) t->ksigns[i] = r.ks;
+}
 
 // ---------------------------------------------------------------------------------------------------------
 // Exact dequantization of values 32 k .. 32 k + 32 of the super-block at b (global memory).

@@ -462,7 +462,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
                    o_tile = o_ss + ncp / 4, o_part = o_tile + GEMV1_TILE + 16;
     int* xss = (int*)(smem + o_ss);
     IqTables* tab = (IqTables*)smem;
-    if constexpr (IQ) load_iq_tables(tab);
+    static_assert(GEMV1_THREADS == 256, "load_iq_regs covers the tables with 256 threads");
     int8_t* xl = (int8_t*)(smem + o_x);
     float* xld = (float*)(smem + o_xd);
     uint8_t* tile = smem + o_tile;
@@ -529,6 +529,10 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     XEarly xe;
     if (early) x_fetch<SW>(a, sp.xrow, xe);
     issue(sp);
+    // the IQ codebooks into registers behind the first tile's loads (both round trips at once), into LDS before the
+    // first tile is computed
+    IqRegs iqr;
+    if constexpr (IQ) iqr = load_iq_regs();
     // the tile after next is located while the next one is in flight
     int tn = next_valid(t + gridDim.x);
     Span spn = sp;
@@ -538,6 +542,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     const bool has_sb = gl < nsb;
     XReg x;
     int cur_xrow = -1;
+    if constexpr (IQ) store_iq_regs(tab, iqr);  // visible after the barrier that ends the first tile's staging
     while (true) {
         __syncthreads();  // the previous tile's readers are done with the LDS tile
         if (sp.xrow != cur_xrow) {
