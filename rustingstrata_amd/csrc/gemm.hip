@@ -408,8 +408,8 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     };
 
     // The super-block steps of this block's items run as one stream g = k * nsb + s (G steps): step g loads the X rows
-    // and scales of step g + 1 and, once every wave has decoded, the raw weights of step g + 1 into the buffer just
-    // decoded. The load state (iL, aL, sL) describes step g + 1; cur and rbeg describe step g.
+    // and scales of step g + 1 and, once this wave has decoded its rows, their raw weights of step g + 1 into the
+    // buffer just decoded. The load state (iL, aL, sL) describes step g + 1; cur and rbeg describe step g.
     const int G = nitems * nsb;
     int kL = 0, sL = 0;
     Item iL = item_at(0);
