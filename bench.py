@@ -268,7 +268,7 @@ def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
 
 
 def bench_moe_decode(hip, S, ggml, iters):
-    """configs[2] at 1 token: route -> paired gate/up moe_gemv (h quantized inside it) -> swiglu_q +
+    """configs[2] at 1 token: route + paired gate/up moe_gemv as one launch (h quantized inside it) -> swiglu_q +
     moe_down_combine as one down GEMV (the SwiGLU quantized inside it) + combine (src/gpu_model.rs:3383-3412), over 2 copies of the 128 experts
     (884 MB, past the Infinity Cache)."""
     E, H, F, k = 128, 2048, 768, 8
@@ -290,9 +290,10 @@ def bench_moe_decode(hip, S, ggml, iters):
 
     def token(i):
         gu, d = copies[i % 2]
-        hip.moe_route(logits[i % 4], E, k, 0.0, table, ids, wts, slots, wh, 1)
-        # h is quantized inside the gate/up GEMV (quant_xq's arithmetic, the same bits)
-        hip.moe_gemv(ggml.Q5_K, F, H, gu, F * rb_gu, slots, k, h, H, k, g, pair=(E * F * rb_gu, k * F * 4))
+        # the route inside the paired gate/up GEMV (every block ranks the logits itself; moe_route then moe_gemv,
+        # the same bits), h quantized inside it (quant_xq's arithmetic)
+        hip.moe_route_gemv(logits[i % 4], E, k, 0.0, table, ids, wts, slots, wh, ggml.Q5_K, F, H, gu, F * rb_gu, h, g,
+                           pair=(E * F * rb_gu, k * F * 4))
         # swiglu_q + moe_down_combine with the SwiGLU and its quantization inside the down GEMV (same bits)
         hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d, H * rb_d, slots, k, g, int(g) + k * F * 4, ye, x, wh, 0, 0, 1)
 
@@ -622,8 +623,7 @@ def main():
     if args.profile_gemv:
         profile_gemv(hip, S, ggml)
         return
-    if args.profile_decode:
-        USE_GRAPHS = False
+    if args.profile_decode:  # eager tokens, then (unless --eager) the same tokens as graph replays
         print(json.dumps({"moe_decode_1": bench_moe_decode(hip, S, ggml, 200)}), flush=True)
         return
     if args.profile_moe:

@@ -143,6 +143,16 @@ int strata_router_topk(strata_ctx* ctx, uint64_t p, uint64_t n, uint64_t k, floa
  * wts[j] on a hit, else 0. */
 int strata_moe_route(strata_ctx* ctx, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t table,
                      uint64_t ids, uint64_t wts, uint64_t slots, uint64_t wh, uint64_t t, int sigmoid);
+/* Backend::moe_route with mb = 0 for one token followed by Backend::moe_gemv of its k slots on the token's x (the
+ * decode sequence src/gpu_model.rs:3383-3390; src/backend.rs:413-417, 223-226) as one launch: every block of the
+ * GEMV ranks the n logits itself (n <= 128; more: two launches) and takes slot j's expert from that ranking, and the
+ * launch stores ids, wts, slots and wh as strata_moe_route does. The GEMV is strata_moe_gemv with ids = slots,
+ * xg = k (one x row of cols floats, or xq pre-quantized) and the optional pair; rows = 0 routes only. Outputs
+ * equal strata_moe_route then strata_moe_gemv bit for bit. */
+int strata_moe_route_gemv(strata_ctx* ctx, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t table,
+                          uint64_t ids, uint64_t wts, uint64_t slots, uint64_t wh, int sigmoid, int ty, uint64_t rows,
+                          uint64_t cols, uint64_t w, uint64_t stride, uint64_t x, uint64_t y, int has_pair, int64_t w2,
+                          int64_t y2, uint64_t xq);
 /* Backend::rms_norm (src/backend.rs:232; ops::rms_norm src/ops.rs:3-7; kernel src/cuda/kernels.cu:1504-1550): `rows`
  * rows (x_stride, out_stride in floats), out[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * w; out may be x. */
 int strata_rms_norm(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t out_stride,

@@ -68,6 +68,8 @@ SIGNATURES = {
     "strata_moe_gemv": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, I32, I64, I64, U64],
     "strata_router_topk": [CTX, U64, U64, U64, F32, U64, U64, U64, I32],
     "strata_moe_route": [CTX, U64, U64, U64, F32, U64, U64, U64, U64, U64, U64, I32],
+    "strata_moe_route_gemv": [CTX, U64, U64, U64, F32, U64, U64, U64, U64, U64, I32, I32, U64, U64, U64, U64, U64,
+                              U64, I32, I64, I64, U64],
     "strata_swiglu_q": [CTX, U64, U64, U64, U64, U64, ctypes.POINTER(U64)],
     "strata_moe_combine": [CTX, U64, U64, U64, U64, U64, U64, U64, U64],
     "strata_moe_down_combine": [CTX, I32, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64],
@@ -324,6 +326,14 @@ class HipBackend:
     def moe_route(self, p, n, k, extra_scale, table, ids, wts, slots, wh, t, sigmoid=False):
         _check(lib().strata_moe_route(self._ctx, int(p), n, k, extra_scale, int(table), int(ids), int(wts),
                                       int(slots), int(wh), t, int(sigmoid)))
+
+    def moe_route_gemv(self, p, n, k, extra_scale, table, ids, wts, slots, wh, ty, rows, cols, w, stride, x, y,
+                       pair=None, xq=0, sigmoid=False):
+        """moe_route of one token, then moe_gemv of its k slots (ids = slots, xg = k) as one launch."""
+        has, w2, y2 = (1, pair[0], pair[1]) if pair is not None else (0, 0, 0)
+        _check(lib().strata_moe_route_gemv(self._ctx, int(p), n, k, extra_scale, int(table), int(ids), int(wts),
+                                           int(slots), int(wh), int(sigmoid), ty, rows, cols, int(w), stride, int(x),
+                                           int(y), has, w2, y2, int(xq)))
 
     def swiglu_q(self, g, u, n, rows, xq):
         r = U64()

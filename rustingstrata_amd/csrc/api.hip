@@ -528,6 +528,36 @@ int strata_moe_gemv(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint64_
     return moe_gemv_impl(c, ty, rows, cols, w, stride, ids, k, x, x_stride, xg, y, has_pair, w2, y2, xq, 0);
 }
 
+int strata_moe_route_gemv(strata_ctx* c, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t table,
+                          uint64_t ids, uint64_t wts, uint64_t slots, uint64_t wh, int sigmoid, int ty, uint64_t rows,
+                          uint64_t cols, uint64_t w, uint64_t stride, uint64_t x, uint64_t y, int has_pair, int64_t w2,
+                          int64_t y2, uint64_t xq) {
+    if (check_ctx(c) || check_type(ty)) return -1;
+    if (n > 512 || k > 32 || k > n || k == 0) return set_error("moe_route_gemv: " + std::to_string(n) + " experts, top " + std::to_string(k));
+    if (!table || !slots || !wh || !ids || !wts) return set_error("moe_route_gemv: null table, ids, wts, slots or wh");
+    if (!rows) return strata_moe_route(c, p, n, k, extra_scale, table, ids, wts, slots, wh, 1, sigmoid);
+    if (check_gemv_cols(ty, cols, false) || check_align(ty, w, "moe_route_gemv")) return -1;
+    if (check_align(ty, stride, "moe_route_gemv stride") || (has_pair && check_align(ty, (uint64_t)w2, "moe_route_gemv pair offset"))) return -1;
+    if (n <= 128) {
+        GemvLaunch g;
+        g.xf = (const float*)x; g.x_stride = cols;
+        g.ty = ty; g.w = (const uint8_t*)w; g.rows = (int)rows; g.cols = (int)cols; g.nt = 1;
+        g.xq = (const int8_t*)xq; g.n_xrows = 1; g.y = (float*)y; g.y_stride = 0;
+        g.numerics = c->numerics;
+        g.ids = (const int*)slots; g.k = (int)k; g.xg = (int)k; g.stride = (int64_t)stride;
+        g.pair = has_pair != 0; g.w2 = w2; g.y2 = y2; g.rows2 = (int)rows;
+        g.rp = (const float*)p; g.rn = (int)n; g.rscale = extra_scale; g.rtable = (const int*)table;
+        g.rids = (int*)ids; g.rwts = (float*)wts; g.rwh = (float*)wh; g.rsig = sigmoid;
+        const hipError_t e = launch_gemv(g, c->stream);
+        if (e != hipErrorNotSupported) {
+            STRATA_HIP(e);
+            return 0;
+        }
+    }
+    if (strata_moe_route(c, p, n, k, extra_scale, table, ids, wts, slots, wh, 1, sigmoid)) return -1;
+    return strata_moe_gemv(c, ty, rows, cols, w, stride, slots, k, x, cols, k, y, has_pair, w2, y2, xq);
+}
+
 int strata_router_topk(strata_ctx* c, uint64_t p, uint64_t n, uint64_t k, float extra_scale, uint64_t ids,
                        uint64_t wts, uint64_t t, int sigmoid) {
     if (check_ctx(c)) return -1;

@@ -12,6 +12,7 @@
 #include "sbdot.h"
 #include "kernels.h"
 #include "xlane.h"
+#include "route.h"
 #include "../../include/strata_hip.h"
 
 namespace strata {
@@ -43,6 +44,16 @@ struct GemvArgs {
     int ntr_s, ns_s;
     int quarter;         // single-input kernel: every tile fits one pass of a wave (at most 64 / G rows), and the four
                          // waves each take one quarter of every super-block (sb_quarter / sb_close)
+    // single-input moe kernel that routes its one token first (MODE bit 3): every block ranks the rn logits at rp
+    // (route_block4) and takes slot j's expert from its own result; block 0 also stores ids, wts, slots (= ids
+    // above) and wh, as route_block_kernel does
+    const float* rp;
+    const int* rtable;
+    int* rids;
+    float* rwts;
+    float* rwh;
+    float rscale;
+    int rn, rsig;
 };
 
 // LDS layout: [IqTables (IQ types)][x int8: nt * cols][x scales: nt * cols / 32 f32][x sums: nt * cols / 16
@@ -447,10 +458,10 @@ static void magic(uint32_t d, uint32_t& m, int& s) {
 
 // MODE: bit 0 SW (x rows are silu(xf) * xu), bit 1 the quarter split (GemvArgs::quarter), bit 2 one plain matrix
 // (no expert ids, no pair: tile t is row tile t and every tile is valid, with none of the general indexing's
-// divisions, tens of instructions each).
+// divisions, tens of instructions each), bit 3 the routing prologue (GemvArgs::rp).
 template <int T, bool Q32, int MODE>
 __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
-    constexpr bool SW = MODE & 1, QU = MODE & 2, plain = MODE & 4;
+    constexpr bool SW = MODE & 1, QU = MODE & 2, plain = MODE & 4, ROUTE = MODE & 8;
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -469,6 +480,11 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     uint32_t* qpart = (uint32_t*)(smem + o_part);  // quarter split: waves 1-3's outputs, 2 words a lane
 
     const int total = a.ntr * a.nslots * a.nz;
+    __shared__ RouteLds rl;  // (ROUTE) the routing's LDS; rl.tops[j]: slot j's expert
+    auto expert = [&](int slot) {
+        if constexpr (ROUTE) return rl.tops[slot];
+        else return sload(a.ids + slot);
+    };
     // one plain matrix (no slots, no pair, no expert ids): tile t is row tile t, and every tile is valid; the
     // divisions below (tens of instructions each) stay off that path
     auto valid = [&](int t) {
@@ -476,7 +492,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
         const int rest = fdiv(t, a.ntr_m, a.ntr_s), rt = t - rest * a.ntr, z = fdiv(rest, a.ns_m, a.ns_s),
                   slot = rest - z * a.nslots;
         if (rt * a.R >= (z ? a.rows2 : a.rows)) return false;
-        return !a.ids || sload(a.ids + slot) >= 0;  // a slot not routed here leaves its output untouched
+        return !a.ids || expert(slot) >= 0;  // a slot not routed here leaves its output untouched
     };
     auto next_valid = [&](int t) {
         while (t < total && !valid(t)) t += gridDim.x;
@@ -501,7 +517,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
             sp.Y = (float*)((uint8_t*)a.y + (z ? a.y2 : 0));
             sp.xrow = 0;
             if (a.ids) {
-                W += (int64_t)sload(a.ids + slot) * a.stride;
+                W += (int64_t)expert(slot) * a.stride;
                 sp.xrow = slot / a.xg;
                 sp.Y += (int64_t)slot * rows;
             }
@@ -522,12 +538,26 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
         }
     };
 
+    const bool early = a.cols <= (SW ? 1 : 2) * XH;
+    XEarly xe;
+    if constexpr (ROUTE) {
+        // the token's x (row 0) is requested before the routing, whose ranks then name the experts
+        if (early) x_fetch<SW>(a, 0, xe);
+        int id = 0, sl = -1;
+        float w = 0.0f;
+        route_block4(a.rp, a.rn, a.nslots, a.rscale, a.rtable, a.rsig, &rl, id, w, sl);
+        // route_block4 leaves rank j's slot in rl.tops[j] (read after its closing barrier) and in thread j's sl
+        if (blockIdx.x == 0 && tid < a.nslots) {
+            a.rids[tid] = id;
+            a.rwts[tid] = w;
+            ((int*)a.ids)[tid] = sl;
+            a.rwh[tid] = sl >= 0 ? w : 0.0f;
+        }
+    }
     int t = next_valid(blockIdx.x);
     if (t >= total) return;
     Span sp = span(t);
-    const bool early = a.cols <= (SW ? 1 : 2) * XH;
-    XEarly xe;
-    if (early) x_fetch<SW>(a, sp.xrow, xe);
+    if (!ROUTE && early) x_fetch<SW>(a, sp.xrow, xe);
     issue(sp);
     // the IQ codebooks into registers behind the first tile's loads (both round trips at once), into LDS before the
     // first tile is computed
@@ -640,8 +670,10 @@ static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, 
 
 template <int T>
 static hipError_t gemv1_t(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
-    const int mode = (a.xu ? 1 : 0) | (a.quarter ? 2 : 0) | (!a.xu && !a.ids && a.nz == 1 ? 4 : 0);
+    const int mode = (a.xu ? 1 : 0) | (a.quarter ? 2 : 0) | (!a.xu && !a.ids && a.nz == 1 ? 4 : 0) | (a.rp ? 8 : 0);
     switch (mode) {
+    case 8: return a.per32 ? gemv1_launch<T, true, 8>(a, tiles, smem, s) : gemv1_launch<T, false, 8>(a, tiles, smem, s);
+    case 10: return a.per32 ? gemv1_launch<T, true, 10>(a, tiles, smem, s) : gemv1_launch<T, false, 10>(a, tiles, smem, s);
     case 0: return a.per32 ? gemv1_launch<T, true, 0>(a, tiles, smem, s) : gemv1_launch<T, false, 0>(a, tiles, smem, s);
     case 1: return a.per32 ? gemv1_launch<T, true, 1>(a, tiles, smem, s) : gemv1_launch<T, false, 1>(a, tiles, smem, s);
     case 2: return a.per32 ? gemv1_launch<T, true, 2>(a, tiles, smem, s) : gemv1_launch<T, false, 2>(a, tiles, smem, s);
@@ -704,6 +736,8 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     a.rows = g.rows; a.rows2 = g.pair ? g.rows2 : 0; a.cols = g.cols; a.nt = g.nt; a.y_stride = g.y_stride;
     a.rb = row_bytes(g.ty, g.cols);
     a.per32 = g.numerics == STRATA_NUM_Q8_32;
+    a.rp = g.rp; a.rtable = g.rtable; a.rids = g.rids; a.rwts = g.rwts; a.rwh = g.rwh; a.rscale = g.rscale;
+    a.rn = g.rn; a.rsig = g.rsig;
     {
         int nsb = (g.cols + 255) / 256;
         a.G = 1;
@@ -738,6 +772,8 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     magic((uint32_t)a.ntr, a.ntr_m, a.ntr_s);
     magic((uint32_t)a.nslots, a.ns_m, a.ns_s);
     const long long grid = (long long)a.ntr * nslots * nz;  // tiles
+    if (g.rp && (!single || !g.ids || g.xu || g.k > 32 || g.k != g.xg || g.rn < g.k || g.rn > 128))
+        return hipErrorNotSupported;
     bool iq = g.ty == IQ2_XXS || g.ty == IQ3_S;
     if (single) {
         const uint32_t ncp = (g.cols + 255) & ~255;

@@ -35,6 +35,16 @@ struct GemvLaunch {
     bool pair = false;
     int64_t w2 = 0, y2 = 0;
     int rows2 = 0;
+    // moe_gemv of one token that routes it first (single input, no SwiGLU input): the launch ranks the rn <= 128
+    // logits at rp as moe_route does (top k, k <= 32) and writes ids, wts, wh and the slots (to `ids` above, which the
+    // GEMV's slots then are). hipErrorNotSupported: a shape this does not take.
+    const float* rp = nullptr;
+    const int* rtable = nullptr;
+    int* rids = nullptr;
+    float* rwts = nullptr;
+    float* rwh = nullptr;
+    float rscale = 0.0f;
+    int rn = 0, rsig = 0;
 };
 hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s);
 // moe_down_combine as one launch: x[tk] += sum_j wh[tk k + j] W_{slots[j]} x_j (slots in order) + the shared expert,

@@ -16,8 +16,8 @@ Per prefill chunk of t tokens at position pos (step[0] = pos):
     SwiGLU epilogue ; down grouped GEMM ; x += moe_combine_seq.
 Per decode token (recorded once as a graph and replayed; the step buffer carries the position):
     x = embed(token) ; per layer: h, hq = rms_norm_q(x (+= mix)) ; q = gemvq ; k, v = gemvq2 ; rms_norm_rope_qk ;
-    attn_decode ; mix = gemvq(o) ; h, hq = rms_norm_q(x += mix) ; logits = gemv(router) ; moe_route ; paired
-    gate/up moe_gemv ; moe_down_swiglu_combine (x += sum w y) ; then rms_norm, output gemv, argmax_rows.
+    attn_decode ; mix = gemvq(o) ; h, hq = rms_norm_q(x += mix) ; logits = gemv(router) ; moe_route and the paired
+    gate/up moe_gemv as one launch (moe_route_gemv) ; moe_down_swiglu_combine (x += sum w y) ; then rms_norm, output gemv, argmax_rows.
 """
 import numpy as np
 
@@ -266,9 +266,10 @@ class Model:
             hip.gemv(ly.o, self.datt, self.mix)
             hip.rms_norm_q(x, H, ly.ffn_norm, self.h, H, H, 1, c.eps, xq=self.hq, res=self.mix)
             hip.gemv(ly.router, self.h, self.dl)
-            hip.moe_route(self.dl, E, k, 0.0, self.table, self.dids, self.dwts, self.dslots, self.dwh, 1)
-            hip.moe_gemv(c.ty_gate_up, F, H, ly.gate_up, ly.e_gu, self.dslots, k, self.h, H, k, self.g2,
-                         pair=(ly.up_off, k * F * 4), xq=self.hq)
+            # the route inside the gate/up GEMV launch (moe_route then moe_gemv, the same bits)
+            hip.moe_route_gemv(self.dl, E, k, 0.0, self.table, self.dids, self.dwts, self.dslots, self.dwh,
+                               c.ty_gate_up, F, H, ly.gate_up, ly.e_gu, self.h, self.g2, pair=(ly.up_off, k * F * 4),
+                               xq=self.hq)
             hip.moe_down_swiglu_combine(c.ty_down, H, F, ly.down, ly.e_down, self.dslots, k, self.g2,
                                         int(self.g2) + k * F * 4, self.ye1, x, self.dwh, 0, 0, 1)
         hip.rms_norm(x, H, w.output_norm, self.h, H, H, 1, c.eps)

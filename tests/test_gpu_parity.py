@@ -850,6 +850,43 @@ def test_down_combine_one_launch_all_types(hip, ty, k, F, t):
     assert max_rel_err(gb.reshape(t, H), want) <= TOL
 
 
+@pytest.mark.parametrize("ty", ggml.TYPES)
+@pytest.mark.parametrize("n,k,F,H,pair,sig", [(128, 8, 768, 2048, True, False), (64, 4, 512, 1024, False, True),
+                                              (96, 6, 300, 512, True, False), (256, 8, 256, 512, False, False)])
+def test_moe_route_gemv_equals_two_launches(hip, ty, n, k, F, H, pair, sig):
+    """moe_route_gemv (the route of one token computed by every block of its gate/up GEMV) gives ids, wts, slots, wh
+    and the experts' outputs bit for bit equal to moe_route then moe_gemv (src/gpu_model.rs:3383-3390): softmax and
+    sigmoid routing, an extra scale, experts not resident (table -1), the paired launch, x as f32 or pre-quantized,
+    n = 256 (routed by its own launch), three tokens in a row (no state kept between launches)."""
+    cols = F if F % 256 == 0 else 256
+    rb = ggml.row_bytes(ty, cols)
+    wm = random_blocks(ty, (2 if pair else 1) * n * F, cols, seed=500 + ty)
+    wb = up(hip, wm)
+    tab = np.arange(n, dtype=np.int32)
+    tab[::5] = -1
+    table = up(hip, tab)
+    x = normal(cols, seed=501)
+    xb = up(hip, x)
+    xq = hip.alloc(cols + cols // 8)
+    hip.quant_xq(xb, cols, cols, 1, xq)
+    pr = (n * F * rb, k * F * 4) if pair else None
+    outs = [[hip.alloc(k * 4) for _ in range(4)] + [hip.alloc(2 * k * F * 4)] for _ in range(2)]
+    for tok in range(3):
+        lb = up(hip, zipf_logits(1, n, seed=510 + tok)[0])
+        for q in (0, xq):
+            ids, wts, slots, wh, y = outs[0]
+            hip.moe_route(lb, n, k, 0.5, table, ids, wts, slots, wh, 1, sigmoid=sig)
+            hip.moe_gemv(ty, F, cols, wb, F * rb, slots, k, xb, cols, k, y, pair=pr, xq=q)
+            ids2, wts2, slots2, wh2, y2 = outs[1]
+            hip.moe_route_gemv(lb, n, k, 0.5, table, ids2, wts2, slots2, wh2, ty, F, cols, wb, F * rb, xb, y2,
+                               pair=pr, xq=q, sigmoid=sig)
+            for a, b, dt in ((ids, ids2, np.int32), (wts, wts2, np.float32), (slots, slots2, np.int32),
+                             (wh, wh2, np.float32)):
+                assert np.array_equal(down(hip, a, dt, k).view(np.uint32), down(hip, b, dt, k).view(np.uint32)), tok
+            ya, yb = down(hip, y, np.float32, 2 * k * F), down(hip, y2, np.float32, 2 * k * F)
+            assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (tok, int((ya != yb).sum()))
+
+
 def test_errors_do_not_launch(hip):
     t = S.GpuTensor(ggml.Q4_K, 4, 300, hip.alloc(4 * 2048))
     with pytest.raises(S.StrataError, match="GEMV needs a multiple of 256"):
