@@ -42,6 +42,7 @@ struct GemvArgs {
     uint64_t x_stride;   // floats between the f32 x rows
     uint32_t ntr_m, ns_m; // magic multipliers and shifts dividing by ntr and nslots (fdiv)
     int ntr_s, ns_s;
+    int small;           // single-input kernel, one plain matrix: every tile spans at most GEMV1_CH_SMALL chunks a thread
     int quarter;         // single-input kernel: every tile fits one pass of a wave (at most 64 / G rows), and the four
                          // waves each take one quarter of every super-block (sb_quarter / sb_close)
     // single-input moe kernel that routes its one token first (MODE bit 3): every block ranks the rn logits at rp
@@ -249,6 +250,7 @@ constexpr int GEMV1_CH = 12;
 constexpr int GEMV1_WAVES = 4;          // waves of a single-input GEMV block
 constexpr int GEMV1_THREADS = 64 * GEMV1_WAVES;
 constexpr int GEMV1_TILE = GEMV1_THREADS * 16 * GEMV1_CH;
+constexpr int GEMV1_CH_SMALL = 5;  // (one plain matrix whose tiles span at most 20 KB: only the loads it needs)
 
 // Quantize x row xr (n values) into LDS (n int8, then n / 32 scales) with quant_xq's arithmetic (quant.hip): the
 // block's 256 threads take 8 values each, a group of 32 lanes one 256-value block.
@@ -458,10 +460,12 @@ static void magic(uint32_t d, uint32_t& m, int& s) {
 
 // MODE: bit 0 SW (x rows are silu(xf) * xu), bit 1 the quarter split (GemvArgs::quarter), bit 2 one plain matrix
 // (no expert ids, no pair: tile t is row tile t and every tile is valid, with none of the general indexing's
-// divisions, tens of instructions each), bit 3 the routing prologue (GemvArgs::rp).
+// divisions, tens of instructions each), bit 3 the routing prologue (GemvArgs::rp), bit 4 small tiles
+// (GemvArgs::small: GEMV1_CH_SMALL loads a thread, a smaller LDS tile).
 template <int T, bool Q32, int MODE>
 __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     constexpr bool SW = MODE & 1, QU = MODE & 2, plain = MODE & 4, ROUTE = MODE & 8;
+    constexpr int CH = (MODE & 16) ? GEMV1_CH_SMALL : GEMV1_CH, TILE = GEMV1_THREADS * 16 * CH;
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -470,7 +474,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     // LDS: [IqTables][x int8 (whole super-blocks, padded: xpad)][x scales][x per-16 sums][tile]
     const uint32_t ncp = (cols + 255) & ~255;
     const uint32_t o_x = IQ ? up16(sizeof(IqTables)) : 0u, o_xd = o_x + xpad_bytes(ncp), o_ss = o_xd + ncp / 8,
-                   o_tile = o_ss + ncp / 4, o_part = o_tile + GEMV1_TILE + 16;
+                   o_tile = o_ss + ncp / 4, o_part = o_tile + TILE + 16;
     int* xss = (int*)(smem + o_ss);
     IqTables* tab = (IqTables*)smem;
     static_assert(GEMV1_THREADS == 256, "load_iq_regs covers the tables with 256 threads");
@@ -527,12 +531,12 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
         sp.nch = (int)((((sp.beg + (uint64_t)sp.nr * a.rb) + 15) & ~(uint64_t)15) - sp.g0) >> 4;
         return sp;
     };
-    v4u wv[GEMV1_CH];
+    v4u wv[CH];
     // every lane loads every instruction (chunks past the span repeat its last chunk and land past the tile's bytes
     // in LDS), so no load or store sits under a branch and the LDS stores wait for their own loads only
     auto issue = [&](const Span& sp) {
 #pragma unroll
-        for (int i = 0; i < GEMV1_CH; i++) {
+        for (int i = 0; i < CH; i++) {
             const int c = min(tid + GEMV1_THREADS * i, sp.nch - 1);
             wv[i] = __builtin_nontemporal_load(gptr<v4u>(sp.g0 + 16 * (uint64_t)c));
         }
@@ -584,7 +588,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
             cur_xrow = sp.xrow;
         }
 #pragma unroll
-        for (int i = 0; i < GEMV1_CH; i++)
+        for (int i = 0; i < CH; i++)
             *(v4u*)(tile + 16 * (tid + GEMV1_THREADS * i)) = wv[i];
         __syncthreads();
         const Span cs = sp;
@@ -670,8 +674,11 @@ static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, 
 
 template <int T>
 static hipError_t gemv1_t(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
-    const int mode = (a.xu ? 1 : 0) | (a.quarter ? 2 : 0) | (!a.xu && !a.ids && a.nz == 1 ? 4 : 0) | (a.rp ? 8 : 0);
+    const int mode = (a.xu ? 1 : 0) | (a.quarter ? 2 : 0) | (!a.xu && !a.ids && a.nz == 1 ? 4 : 0) | (a.rp ? 8 : 0) |
+                     (a.small ? 16 : 0);
     switch (mode) {
+    case 20: return a.per32 ? gemv1_launch<T, true, 20>(a, tiles, smem, s) : gemv1_launch<T, false, 20>(a, tiles, smem, s);
+    case 22: return a.per32 ? gemv1_launch<T, true, 22>(a, tiles, smem, s) : gemv1_launch<T, false, 22>(a, tiles, smem, s);
     case 8: return a.per32 ? gemv1_launch<T, true, 8>(a, tiles, smem, s) : gemv1_launch<T, false, 8>(a, tiles, smem, s);
     case 10: return a.per32 ? gemv1_launch<T, true, 10>(a, tiles, smem, s) : gemv1_launch<T, false, 10>(a, tiles, smem, s);
     case 0: return a.per32 ? gemv1_launch<T, true, 0>(a, tiles, smem, s) : gemv1_launch<T, false, 0>(a, tiles, smem, s);
@@ -778,7 +785,10 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     if (single) {
         const uint32_t ncp = (g.cols + 255) & ~255;
         a.quarter = a.R <= 64 / a.G;
-        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + xpad_bytes(ncp) + ncp / 8 + ncp / 4 + GEMV1_TILE + 16 +
+        const uint64_t span_ch = ((uint64_t)a.R * a.rb + 15) / 16 + 1;  // 16-byte chunks a tile spans, at most
+        a.small = !g.xu && !g.ids && !g.pair && span_ch <= (uint64_t)GEMV1_THREADS * GEMV1_CH_SMALL;
+        const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + xpad_bytes(ncp) + ncp / 8 + ncp / 4 +
+                             GEMV1_THREADS * 16 * (a.small ? GEMV1_CH_SMALL : GEMV1_CH) + 16 +
                              (a.quarter ? 3 * 64 * 8 : 0);
         switch (g.ty) {
         case Q8_0: return gemv1_t<Q8_0>(a, grid, smem1, s);
