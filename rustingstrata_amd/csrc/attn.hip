@@ -92,26 +92,40 @@ template <int HD> struct PfLayout {
     static constexpr int VP = 64 + 4;          // halves per V^T row (8-byte pad)
 };
 
-// grid (ATT_SPLITS, nkv, nt), one wave a block. Wave (s, g, t) serves the G = nh / nkv query heads of KV head g over
-// the s-th share of token t's positions, 64 keys a chunk, on f16 MFMA (v_mfma_f32_16x16x32_f16) with f32 accuracy:
-// the G heads are the MFMA's 16 columns (padded), so
-//   S^T (16 keys x 16 heads, 4 key sub-tiles kt) = K (A: key row, 8 dims a lane) Q^T (B: head column; q split into
-//   f16 hi and lo after scaling it by a power of two that puts its largest value in [2^13, 2^14));
-//   the online softmax of a head runs over the lane's 16 values and its 4 lane groups;
-//   O^T (16 dims x 16 heads, DT dim tiles) += V^T (A: dim row, 8 keys) P^T (B: the lane's own weights, times 2^14,
-//   split hi and lo), the keys of each K-step the same in both operands.
-// K and V rows arrive by 16-byte loads, all in flight together (one memory round trip a chunk; lane l loads keys
-// 4 (l % 16) .. + 3, dims HD / 4 (l / 16) .. of each), K stored as is, V transposed 4 keys a write.
-// The wave leaves [acc (hd) | max | sum] per head in part (max in log2 units); attn_merge_kernel combines the splits.
+// grid (ATT_SPLITS, nkv, nt), 4 waves a block. Block (s, g, t) serves the G = nh / nkv query heads of KV head g over
+// the s-th share of token t's positions, 64 keys a chunk, and wave w takes keys 16 w .. 16 w + 15 of each chunk with
+// its own online softmax (running max m, sum l, accumulator o per head), on f16 MFMA with f32 accuracy:
+//   S^T (16 keys x 16 heads) = K (A: key row, 8 dims a lane; v_mfma_f32_16x16x32_f16) Q^T (B: head column; q split
+//   into f16 hi and lo after scaling it by a power of two that puts its largest value in [2^13, 2^14));
+//   the softmax of a head runs over the lane's 4 values and its 4 lane groups;
+//   O^T (16 dims x 16 heads, DT dim tiles) += V^T (A: dim row, 4 keys; v_mfma_f32_16x16x16f16) P^T (B: the lane's
+//   own 4 weights, times 2^14, split hi and lo: the score tile's layout is the K = 16 operand's).
+// Each wave loads its 16 keys' K and V rows (lane l: keys 4 (l % 4) .. + 3, dims 8 (l / 4) .. + 7), K into its own
+// LDS rows as is and V transposed. After the last chunk the four waves' (m, l, o) meet in LDS and the block leaves
+// [acc (hd) | max | sum] per head in part (max in log2 units); attn_merge_kernel combines the splits.
+constexpr int DEC_WAVES = 4;
+template <int HD>
+struct DecLayout {
+    static constexpr int KP = HD + 8;    // halves per K row (16-byte pad: rows start in spread banks)
+    static constexpr int VP = 16 + 4;    // halves per V^T row of a wave's 16 keys (8-byte pad)
+    static constexpr int WAVE = 16 * KP * 2 + HD * VP * 2;  // bytes of one wave's K and V^T tiles
+    static constexpr int MERGE = DEC_WAVES * (HD * 16 + 32) * 4;  // the waves' o, m and l for the block merge
+    static constexpr int BYTES = DEC_WAVES * WAVE > MERGE ? DEC_WAVES * WAVE : MERGE;
+};
 template <int HD, int G>
-__global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                         const uint16_t* __restrict__ vc, float* __restrict__ part,
-                                                         const int* step, int nh, int nkv, float scale, int win) {
-    using L = PfLayout<HD>;
-    constexpr int KS = HD / 32, DT = HD / 16, DW = HD / 4, NL = DW / 8;  // dims a lane loads; 16-byte loads a key
-    __shared__ __align__(16) uint16_t ks[64 * L::KP];
-    __shared__ __align__(16) uint16_t vs[HD * L::VP];
-    const int split = blockIdx.x, g = blockIdx.y, t = blockIdx.z, lane = threadIdx.x, l16 = lane & 15, lg = lane >> 4;
+__global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float* __restrict__ q,
+                                                                     const uint16_t* __restrict__ kc,
+                                                                     const uint16_t* __restrict__ vc,
+                                                                     float* __restrict__ part, const int* step, int nh,
+                                                                     int nkv, float scale, int win) {
+    using L = DecLayout<HD>;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    constexpr int KS = HD / 32, DT = HD / 16, NDG = HD / 8;  // K-steps of the scores; dim tiles; 8-dim groups
+    __shared__ __align__(16) uint8_t lds[L::BYTES];
+    const int split = blockIdx.x, g = blockIdx.y, t = blockIdx.z, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    uint16_t* ks = (uint16_t*)(lds + wave * L::WAVE);
+    uint16_t* vs = ks + 16 * L::KP;
     const int h0 = g * G, ns = gridDim.x;
     const uint64_t kvd = (uint64_t)nkv * HD;
     // the query first (it does not depend on the position), then the first chunk's K and V rows as soon as the
@@ -133,7 +147,9 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
     att_range(step, t, win, base, n_pos);
     const int per_s = split_len(n_pos, ns);
     const int p0 = split * per_s, p1 = min(n_pos, p0 + per_s);
-    if (p0 >= n_pos) return;  // past the token's positions: the merge reads only the splits that have some
+    if (p0 >= n_pos) return;  // (the whole block) past the token's positions: the merge reads only the splits that have some
+    const int kq = lane & 3, dg = lane >> 2;  // this lane's load keys 4 kq .., dims 8 dg ..
+    const bool loader = dg < NDG;
     // Q^T fragments: head h0 + l16 (zero past G), dims 32 k + 8 lg .. + 7; usc undoes the scaling (times `scale`)
     h8 qh[KS], ql[KS];
     float usc = 0.0f;
@@ -144,17 +160,14 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
     for (int c0 = p0; c0 < p1; c0 += 64) {
         const int nc = min(64, p1 - c0);
         {
-            // the chunk's K and V rows into registers (keys past nc repeat key nc - 1: finite, and their weights
-            // are 0)
-            uint4 kb[4][NL], vb[4][NL];
+            // this wave's 16 keys of the chunk (keys past nc repeat key nc - 1: finite, and their weights are 0)
+            uint4 kb[4], vb[4];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                const uint64_t off = (uint64_t)(base + c0 + min(4 * l16 + kk, nc - 1)) * kvd + g * HD + DW * lg;
-#pragma unroll
-                for (int j = 0; j < NL; j++) {
-                    kb[kk][j] = *(const uint4*)(kc + off + 8 * j);
-                    vb[kk][j] = *(const uint4*)(vc + off + 8 * j);
-                }
+                const uint64_t off = (uint64_t)(base + c0 + min(16 * wave + 4 * kq + kk, nc - 1)) * kvd + g * HD +
+                                     8 * min(dg, NDG - 1);
+                kb[kk] = *(const uint4*)(kc + off);
+                vb[kk] = *(const uint4*)(vc + off);
             }
             if (c0 == p0) {
                 // the query's fragments while the first chunk's rows are in flight: scaled by the power of two
@@ -180,97 +193,113 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float* __restrict
                         ql[k][e] = (_Float16)(x - (float)hi);
                     }
             }
+            if (loader) {
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++)
-#pragma unroll
-                for (int j = 0; j < NL; j++) *(uint4*)&ks[(4 * l16 + kk) * L::KP + DW * lg + 8 * j] = kb[kk][j];
-#pragma unroll
-            for (int j = 0; j < NL; j++)
+                for (int kk = 0; kk < 4; kk++) *(uint4*)&ks[(4 * kq + kk) * L::KP + 8 * dg] = kb[kk];
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
                     const int sh = 16 * (e & 1);
-                    const uint32_t a0 = (u4c(vb[0][j], e >> 1) >> sh) & 0xFFFFu, a1 = (u4c(vb[1][j], e >> 1) >> sh) & 0xFFFFu;
-                    const uint32_t a2 = (u4c(vb[2][j], e >> 1) >> sh) & 0xFFFFu, a3 = (u4c(vb[3][j], e >> 1) >> sh) & 0xFFFFu;
-                    *(uint2*)&vs[(DW * lg + 8 * j + e) * L::VP + 4 * l16] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
+                    const uint32_t a0 = (u4c(vb[0], e >> 1) >> sh) & 0xFFFFu, a1 = (u4c(vb[1], e >> 1) >> sh) & 0xFFFFu;
+                    const uint32_t a2 = (u4c(vb[2], e >> 1) >> sh) & 0xFFFFu, a3 = (u4c(vb[3], e >> 1) >> sh) & 0xFFFFu;
+                    *(uint2*)&vs[(8 * dg + e) * L::VP + 4 * kq] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
                 }
+            }
         }
         __builtin_amdgcn_wave_barrier();
-        // S^T: lane holds keys 16 kt + 4 lg + i of head l16
-        f4 s[4];
+        // S^T: lane holds keys 16 wave + 4 lg + i of head l16
+        f4 sv = (f4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-            f4 c = (f4){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int k = 0; k < KS; k++) {
-                const h8 kf = *(const h8*)&ks[(16 * kt + l16) * L::KP + 32 * k + 8 * lg];
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[k], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[k], c, 0, 0, 0);
-            }
-            s[kt] = c;
+        for (int k = 0; k < KS; k++) {
+            const h8 kf = *(const h8*)&ks[l16 * L::KP + 32 * k + 8 * lg];
+            sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[k], sv, 0, 0, 0);
+            sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[k], sv, 0, 0, 0);
         }
-        // online softmax of head l16 over the chunk
+        // online softmax of head l16 over the wave's keys of the chunk
         float mx = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float v = s[kt][i];  // the raw score: usc (> 0) is applied in the exponent's fma
-                if (16 * kt + 4 * lg + i >= nc) v = -INFINITY;
-                s[kt][i] = v;
-                mx = fmaxf(mx, v);
-            }
+        for (int i = 0; i < 4; i++) {
+            float v = sv[i];  // the raw score: usc (> 0) is applied in the exponent's fma
+            if (16 * wave + 4 * lg + i >= nc) v = -INFINITY;
+            sv[i] = v;
+            mx = fmaxf(mx, v);
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mnew = fmaxf(m, mx * usc);  // max(v) usc = max(v usc): a positive factor keeps the order
         const float alpha = m == -INFINITY ? 0.0f : exp2_hw(m - mnew);
-        float sum = 0.0f;
+        const float mref = mnew == -INFINITY ? 0.0f : mnew;  // a wave with no key yet: every p is 0
+        float sum = 0.0f, p[4];
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float p = exp2_hw(__builtin_fmaf(s[kt][i], usc, -mnew));  // exp2(-inf) = 0 (mnew is finite)
-                s[kt][i] = p;
-                sum += p;
-            }
+        for (int i = 0; i < 4; i++) {
+            p[i] = exp2_hw(__builtin_fmaf(sv[i], usc, -mref));  // exp2(-inf) = 0
+            sum += p[i];
+        }
         sum += __shfl_xor(sum, 16, 64);
         sum += __shfl_xor(sum, 32, 64);
         l = l * alpha + sum;
         m = mnew;
 #pragma unroll
         for (int d = 0; d < DT; d++) o[d] *= alpha;
-        // O^T += V^T P^T: K-step c takes keys 32 c + 16 (e / 4) + 4 lg + e % 4 as its K-element e
+        // O^T += V^T P^T over the wave's 16 keys: the weights times 2^14 as f16 hi and lo parts (rounded toward
+        // zero, the lo parts normal down to p ~ 2^-17)
+        h4 ph, pl;
+        {
+            const float a0 = p[0] * 16384.0f, a1 = p[1] * 16384.0f, a2 = p[2] * 16384.0f, a3 = p[3] * 16384.0f;
+            const auto h01 = __builtin_amdgcn_cvt_pkrtz(a0, a1), h23 = __builtin_amdgcn_cvt_pkrtz(a2, a3);
+            const auto l01 = __builtin_amdgcn_cvt_pkrtz(a0 - (float)h01[0], a1 - (float)h01[1]);
+            const auto l23 = __builtin_amdgcn_cvt_pkrtz(a2 - (float)h23[0], a3 - (float)h23[1]);
+            ph = __builtin_bit_cast(h4, make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23)));
+            pl = __builtin_bit_cast(h4, make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23)));
+        }
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            h8 ph, pl;
-            {
-                float p[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) p[e] = s[2 * c + (e >> 2)][e & 3];
-                split_p8(p, ph, pl);
-            }
-#pragma unroll
-            for (int d = 0; d < DT; d++) {
-                const uint16_t* vr = &vs[(16 * d + l16) * L::VP + 32 * c + 4 * lg];
-                const uint2 a0 = *(const uint2*)vr, a1 = *(const uint2*)(vr + 16);
-                const h8 vf = __builtin_bit_cast(h8, make_uint4(a0.x, a0.y, a1.x, a1.y));
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[d], 0, 0, 0);
-                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[d], 0, 0, 0);
-            }
+        for (int d = 0; d < DT; d++) {
+            const h4 vf = __builtin_bit_cast(h4, *(const uint2*)&vs[(16 * d + l16) * L::VP + 4 * lg]);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, ph, o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pl, o[d], 0, 0, 0);
         }
         __builtin_amdgcn_wave_barrier();  // ks and vs are rewritten by the next chunk
     }
-    // partials of head h0 + l16: dims 16 d + 4 lg + i (the weights' 2^14 taken out), max and sum
-    if (l16 < G) {
-        float* pp = part + ((uint64_t)(t * nh + h0 + l16) * ns + split) * (HD + 2);
+    // the four waves' partials meet in LDS: ow[w][dim][head], mw[w][head], lw[w][head]
+    __syncthreads();  // every wave is done with its K and V tiles
+    float* ow = (float*)lds;
+    float* mw = ow + DEC_WAVES * HD * 16;
+    float* lw = mw + DEC_WAVES * 16;
 #pragma unroll
-        for (int d = 0; d < DT; d++) {
-            const float r = 1.0f / 16384.0f;
+    for (int d = 0; d < DT; d++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) pp[16 * d + 4 * lg + i] = o[d][i] * r;
+        for (int i = 0; i < 4; i++) ow[(wave * HD + 16 * d + 4 * lg + i) * 16 + l16] = o[d][i];
+    if (lg == 0) {
+        mw[wave * 16 + l16] = m;
+        lw[wave * 16 + l16] = l;
+    }
+    __syncthreads();
+    // thread: head tid / 16, dims (tid % 16) HD / 16 ..; the waves added in wave order
+    constexpr int DPT = HD / 16;
+    const int hh = tid >> 4, dd0 = (tid & 15) * DPT;
+    if (hh < G) {
+        float mws[DEC_WAVES], M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < DEC_WAVES; w++) {
+            mws[w] = mw[w * 16 + hh];
+            M = fmaxf(M, mws[w]);
         }
-        if (lg == 0) {
-            pp[HD] = m;
-            pp[HD + 1] = l;
+        float ew[DEC_WAVES], Lsum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < DEC_WAVES; w++) {
+            ew[w] = mws[w] == -INFINITY ? 0.0f : exp2_hw(mws[w] - M);
+            Lsum += lw[w * 16 + hh] * ew[w];
+        }
+        float* pp = part + ((uint64_t)(t * nh + h0 + hh) * ns + split) * (HD + 2);
+#pragma unroll
+        for (int e = 0; e < DPT; e++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int w = 0; w < DEC_WAVES; w++) acc += ow[(w * HD + dd0 + e) * 16 + hh] * ew[w];
+            pp[dd0 + e] = acc * (1.0f / 16384.0f);  // the weights' 2^14 taken out
+        }
+        if ((tid & 15) == 0) {
+            pp[HD] = M;
+            pp[HD + 1] = Lsum;
         }
     }
 }
@@ -339,7 +368,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
 template <int HD, int G>
 static void decode_t(const float* q, const uint16_t* kc, const uint16_t* vc, float* part, const int* step, int nh,
                      int nkv, float scale, int nt, int win, hipStream_t s) {
-    attn_decode_kernel<HD, G><<<dim3(ATT_SPLITS, (unsigned)nkv, (unsigned)nt), dim3(64), 0, s>>>(q, kc, vc, part, step,
+    attn_decode_kernel<HD, G><<<dim3(ATT_SPLITS, (unsigned)nkv, (unsigned)nt), dim3(64 * DEC_WAVES), 0, s>>>(q, kc, vc, part, step,
                                                                                             nh, nkv, scale, win);
 }
 
