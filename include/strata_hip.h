@@ -162,6 +162,15 @@ int strata_rms_norm(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w, 
  * [rows x n int8][rows x n / 32 f32 scales]. */
 int strata_rms_norm_q(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t out_stride,
                       uint64_t n, uint64_t rows, float eps, uint64_t xq, uint64_t res);
+/* Backend::moe_combine with mb = 0 and no shared expert (src/backend.rs:418-419) followed by Backend::rms_norm_q
+ * (src/backend.rs:233-235) of the same rows, as a layer's end meets the next layer's attention norm in the decode
+ * (src/gpu_model.rs:3383-3412, then 1950-2016): per token row r, x[r] += sum_{j<k, wh[r k + j] != 0} wh[r k + j]
+ * ye[r k + j] (in slot order), then out = rms_norm(x) * w and xq as strata_rms_norm_q writes them. x rows are n floats
+ * apart (moe_combine's layout); rows of up to 2048 values (a multiple of 8, 16-byte aligned) run as one launch,
+ * others as the two calls. The same bits as strata_moe_combine then strata_rms_norm_q. */
+int strata_combine_rms_norm_q(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t ye, uint64_t wh, uint64_t k,
+                              uint64_t w, uint64_t out, uint64_t out_stride, uint64_t n, uint64_t rows, float eps,
+                              uint64_t xq);
 /* Backend::swiglu_q (src/backend.rs:313-318; kernel src/cuda/kernels.cu:1826-1839): silu(g) * u over `rows` rows
  * of n floats, quantized into xq as strata_quant_xq does; g is left as is. *ret = xq (the address the following
  * GEMV reads). */
@@ -180,7 +189,8 @@ int strata_moe_down_combine(strata_ctx* ctx, int ty, uint64_t rows, uint64_t col
 /* Backend::swiglu_q followed by Backend::moe_down_combine with mb = 0 (src/backend.rs:313-318, 436-442; the decode
  * sequence src/gpu_model.rs:3383-3412) in one GEMV launch: the x row of slot j is silu(g[j]) * u[j] (t * k rows of
  * cols floats each, g and u with the same layout), quantized inside the down GEMV with swiglu_q's arithmetic (the same
- * int8 values and scales), then moe_combine of ye into x with weights wh. */
+ * int8 values and scales), then moe_combine of ye into x with weights wh. x = 0: the down GEMV into ye only (its
+ * combine left to strata_combine_rms_norm_q). */
 int strata_moe_down_swiglu_combine(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t w, uint64_t stride,
                                    uint64_t slots, uint64_t k, uint64_t g, uint64_t u, uint64_t ye, uint64_t x,
                                    uint64_t wh, uint64_t sh, uint64_t sg, uint64_t t);

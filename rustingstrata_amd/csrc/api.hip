@@ -386,6 +386,26 @@ int strata_quant_xq(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t n, ui
     return 0;
 }
 
+int strata_combine_rms_norm_q(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t ye, uint64_t wh, uint64_t k,
+                              uint64_t w, uint64_t out, uint64_t out_stride, uint64_t n, uint64_t rows, float eps,
+                              uint64_t xq) {
+    if (check_ctx(c)) return -1;
+    if (!x || !w || !out || !ye || !wh) return set_error("combine_rms_norm_q: null x, w, out, ye or wh");
+    if (xq && n % 32) return set_error("rms_norm_q: " + std::to_string(n) + " values (a multiple of 32 to quantize)");
+    if (k == 0 || k > 4096 || n > (1u << 30) || rows > 65535) return set_error("combine_rms_norm_q: " + std::to_string(rows) + " rows of " + std::to_string(k) + " slots");
+    if (x_stride != n) return set_error("combine_rms_norm_q: x rows must be n floats apart (moe_combine's layout)");
+    const hipError_t e = launch_rms_norm_q((float*)x, x_stride, (const float*)w, (float*)out, out_stride, (int)n, (int)rows,
+                                           eps, (int8_t*)xq, nullptr, c->numerics, c->stream, (const float*)ye,
+                                           (const float*)wh, (int)k);
+    if (e != hipErrorNotSupported) {
+        STRATA_HIP(e);
+        return 0;
+    }
+    // rows the one-round-trip form does not take: the combine, then the norm
+    if (strata_moe_combine(c, x, ye, wh, k, 0, 0, n, rows)) return -1;
+    return strata_rms_norm_q(c, x, x_stride, w, out, out_stride, n, rows, eps, xq, 0);
+}
+
 int strata_rms_norm_q(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t out_stride,
                       uint64_t n, uint64_t rows, float eps, uint64_t xq, uint64_t res) {
     if (check_ctx(c)) return -1;
@@ -637,6 +657,7 @@ int strata_moe_down_swiglu_combine(strata_ctx* c, int ty, uint64_t rows, uint64_
                                    uint64_t wh, uint64_t sh, uint64_t sg, uint64_t t) {
     if (check_ctx(c)) return -1;
     if (!g || !u) return set_error("moe_down_swiglu_combine: null g or u");
+    if (!x) return moe_gemv_impl(c, ty, rows, cols, w, stride, slots, t * k, g, cols, 1, ye, 0, 0, 0, 0, u);
     // (the one-launch layout would quantize every slot's SwiGLU in every block: slower than two launches)
     if (moe_gemv_impl(c, ty, rows, cols, w, stride, slots, t * k, g, cols, 1, ye, 0, 0, 0, 0, u)) return -1;
     return strata_moe_combine(c, x, ye, wh, k, sh, sg, rows, t);

@@ -11,8 +11,11 @@ inline uint64_t xq_bytes(uint64_t n, uint64_t nt) { return nt * (n + n / 8); }
 hipError_t launch_dequant(int ty, const uint8_t* w, uint64_t rows, uint64_t cols, float* out, hipStream_t s);
 // quant_xq under numerics `mode` (STRATA_NUM_*): rows t < nt of x (t * x_stride floats apart) into out.
 hipError_t launch_quant_xq(const float* x, uint64_t x_stride, int n, int nt, int8_t* out, int mode, hipStream_t s);
+// With ye: x += sum_j wh[j] ye[j] over each row's ck slots (moe_combine's arithmetic) in place of res; rows of at most
+// 2048 values (a multiple of 8, 16-byte aligned) only, else hipErrorNotSupported.
 hipError_t launch_rms_norm_q(float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride, int n, int rows,
-                             float eps, int8_t* xq, const float* res, int mode, hipStream_t s);
+                             float eps, int8_t* xq, const float* res, int mode, hipStream_t s, const float* ye = nullptr,
+                             const float* wh = nullptr, int ck = 0);
 
 struct GemvLaunch {
     int ty = 0;

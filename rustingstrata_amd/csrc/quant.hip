@@ -138,10 +138,13 @@ __global__ __launch_bounds__(256) void quant_xq_kernel(const float* __restrict__
 // of squares is a fixed tree (per-thread sums, DPP within 32 lanes, then the 8 half-waves in order). Rows of up to 2048
 // values (a multiple of 8, 16-byte aligned rows) take one memory round trip: each thread keeps its 8 consecutive
 // values in registers from the loads to the quantization.
+// With ye (one-round-trip rows only): res is the MoE combine of the row's token instead, sum_j wh[j] ye[j] over its
+// ck slots in order (a slot of weight 0 adds nothing), combine_kernel's arithmetic, so x gets moe_combine's bits.
 __global__ __launch_bounds__(256) void rms_norm_q_kernel(float* x, uint64_t x_stride, const float* __restrict__ w,
                                                          float* out, uint64_t out_stride, int n, float eps,
                                                          int8_t* xq, const float* __restrict__ res, int rows, int mode,
-                                                         int vec) {
+                                                         int vec, const float* __restrict__ ye,
+                                                         const float* __restrict__ wh, int ck) {
     __shared__ float part[8];
     const int r = blockIdx.x, tid = threadIdx.x;
     float* xr = x + (uint64_t)r * x_stride;
@@ -164,6 +167,33 @@ __global__ __launch_bounds__(256) void rms_norm_q_kernel(float* x, uint64_t x_st
 #pragma unroll
                 for (int j = 0; j < 8; j++) v[j] = v[j] + ev[j];
             }
+            if (ye) {
+                // 8 slots' rows in flight at a time, then their products added in slot order
+                const float* yr = ye + (uint64_t)r * ck * n + i;
+                const float* wr = wh + (uint64_t)r * ck;
+                float y[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+                for (int j0 = 0; j0 < ck; j0 += 8) {
+                    float ws[8];
+                    float4 ya[8], yb[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        const int j = min(j0 + u, ck - 1);
+                        ws[u] = j0 + u < ck ? wr[j] : 0.0f;
+                        ya[u] = *(const float4*)(yr + (uint64_t)j * n);
+                        yb[u] = *(const float4*)(yr + (uint64_t)j * n + 4);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; u++) {
+                        if (ws[u] != 0.0f) {
+                            const float yv[8] = {ya[u].x, ya[u].y, ya[u].z, ya[u].w, yb[u].x, yb[u].y, yb[u].z, yb[u].w};
+#pragma unroll
+                            for (int e = 0; e < 8; e++) y[e] += ws[u] * yv[e];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = v[j] + y[j];
+            }
         } else {
 #pragma unroll
             for (int j = 0; j < 8; j++) v[j] = wv[j] = 0.0f;
@@ -177,7 +207,7 @@ __global__ __launch_bounds__(256) void rms_norm_q_kernel(float* x, uint64_t x_st
         s += xl32f<3>(s);
         s += xl32f<4>(s);
         if ((tid & 31) == 0) part[tid >> 5] = s;
-        if (res && live) {
+        if ((res || ye) && live) {
             *(float4*)(xr + i) = make_float4(v[0], v[1], v[2], v[3]);
             *(float4*)(xr + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
         }
@@ -232,12 +262,14 @@ __global__ __launch_bounds__(256) void rms_norm_q_kernel(float* x, uint64_t x_st
 }
 
 hipError_t launch_rms_norm_q(float* x, uint64_t x_stride, const float* w, float* out, uint64_t out_stride, int n, int rows,
-                             float eps, int8_t* xq, const float* res, int mode, hipStream_t s) {
+                             float eps, int8_t* xq, const float* res, int mode, hipStream_t s, const float* ye,
+                             const float* wh, int ck) {
     if (!n || !rows) return hipSuccess;
-    const int vec = ((uintptr_t)x | (uintptr_t)w | (uintptr_t)out | (uintptr_t)res) % 16 == 0 && x_stride % 4 == 0 &&
-                    out_stride % 4 == 0;
+    const int vec = ((uintptr_t)x | (uintptr_t)w | (uintptr_t)out | (uintptr_t)res | (uintptr_t)ye) % 16 == 0 &&
+                    x_stride % 4 == 0 && out_stride % 4 == 0;
+    if (ye && (res || !vec || n > 2048 || n % 8 || ck < 1)) return hipErrorNotSupported;
     rms_norm_q_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, x_stride, w, out, out_stride, n, eps, xq, res, rows, mode,
-                                                                 vec);
+                                                                 vec, ye, wh, ck);
     return hipGetLastError();
 }
 

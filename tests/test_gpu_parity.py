@@ -141,6 +141,44 @@ def test_rms_norm_q(hip, n, rows, res, inplace):
     assert np.abs(down(hip, o2, np.float32, rows * n).reshape(rows, n) - O.rms_norm(got, w, 1e-6)).max() < 1e-5
 
 
+@pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])
+@pytest.mark.parametrize("n,rows,k,quant", [(2048, 1, 8, True), (768, 3, 6, True), (2048, 2, 12, False),
+                                           (512, 4, 1, True), (4096, 2, 8, True)])
+def test_combine_rms_norm_q_equals_two_calls(hip, numerics, n, rows, k, quant):
+    """combine_rms_norm_q (a layer's moe_combine and the next attention norm in one launch) leaves x, out and xq
+    bit-equal to moe_combine then rms_norm_q (src/backend.rs:418-419, 233-235), with slots of weight 0, more slots
+    than one round of 8 (k = 12), and n = 4096 (two launches); out against ops::rms_norm of the combined x."""
+    rng = np.random.default_rng(n + rows + k)
+    x0 = normal((rows, n), seed=n + k)
+    ye = normal((rows * k, n), seed=n + k + 1)
+    wh = rng.uniform(0.1, 0.5, rows * k).astype(np.float32)
+    wh[::5] = 0.0
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    yb, whb, wb = up(hip, ye), up(hip, wh), up(hip, w)
+    old = hip.numerics()
+    hip.set_numerics(numerics)
+    try:
+        xa, xb = up(hip, x0), up(hip, x0)
+        oa, ob = hip.alloc(rows * n * 4), hip.alloc(rows * n * 4)
+        qa, qb = (hip.alloc(rows * (n + n // 8)), hip.alloc(rows * (n + n // 8))) if quant else (0, 0)
+        hip.moe_combine(xa, yb, whb, k, 0, 0, n, rows)
+        hip.rms_norm_q(xa, n, wb, oa, n, n, rows, 1e-6, xq=qa)
+        hip.combine_rms_norm_q(xb, yb, whb, k, wb, ob, n, rows, 1e-6, xq=qb)
+    finally:
+        hip.set_numerics(old)
+    for a, b, m in ((xa, xb, rows * n), (oa, ob, rows * n)):
+        assert np.array_equal(down(hip, a, np.uint32, m), down(hip, b, np.uint32, m))
+    if quant:
+        assert np.array_equal(down(hip, qa, np.uint8, rows * (n + n // 8)), down(hip, qb, np.uint8, rows * (n + n // 8)))
+    xc = down(hip, xb, np.float32, rows * n).reshape(rows, n)
+    want = O.rms_norm(xc, w, 1e-6)
+    got = down(hip, ob, np.float32, rows * n).reshape(rows, n)
+    assert np.abs(got - want).max() / np.abs(want).max() < 1e-6
+    # x itself against the combine in f64 (slot order aside)
+    wx = x0.astype(np.float64) + np.einsum("rk,rkn->rn", wh.reshape(rows, k).astype(np.float64), ye.reshape(rows, k, n))
+    assert np.abs(xc - wx).max() < 1e-5
+
+
 def test_quant_xq_per32_bit_exact(hip):
     n, nt = 1024, 2
     x = normal((nt, n), seed=5)
