@@ -165,12 +165,20 @@ int strata_rms_norm_q(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w
 /* Backend::moe_combine with mb = 0 and no shared expert (src/backend.rs:418-419) followed by Backend::rms_norm_q
  * (src/backend.rs:233-235) of the same rows, as a layer's end meets the next layer's attention norm in the decode
  * (src/gpu_model.rs:3383-3412, then 1950-2016): per token row r, x[r] += sum_{j<k, wh[r k + j] != 0} wh[r k + j]
- * ye[r k + j] (in slot order), then out = rms_norm(x) * w and xq as strata_rms_norm_q writes them. x rows are n floats
- * apart (moe_combine's layout); rows of up to 2048 values (a multiple of 8, 16-byte aligned) run as one launch,
- * others as the two calls. The same bits as strata_moe_combine then strata_rms_norm_q. */
+ * ye[r k + j] (in slot order), then out = rms_norm(x) * w and xq as strata_rms_norm_q writes them. With res (not 0,
+ * rows n floats apart) x += res comes first, as strata_rms_norm_q's res. x rows are n floats apart (moe_combine's
+ * layout); rows of up to 2048 values (a multiple of 8, 16-byte aligned) run as one launch, others as separate calls.
+ * The same bits as strata_add(x, res), strata_moe_combine, then strata_rms_norm_q. */
 int strata_combine_rms_norm_q(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t ye, uint64_t wh, uint64_t k,
                               uint64_t w, uint64_t out, uint64_t out_stride, uint64_t n, uint64_t rows, float eps,
-                              uint64_t xq);
+                              uint64_t xq, uint64_t res);
+/* Backend::rms_norm_q of one row (src/backend.rs:233-235) followed by Backend::gemv of an F32 matrix on its output
+ * (the decode's FFN norm and router logits, src/gpu_model.rs:3370-3383) in one launch: h = rms_norm(x + res) * nw
+ * (strata_rms_norm_q's bits), xq its quantization (when not 0), y = w h (strata_gemv's bits for an F32 matrix of n
+ * columns). x is NOT written: the caller adds res into x later (strata_combine_rms_norm_q takes it as its res).
+ * n <= 2048, a multiple of 8, 16-byte aligned rows; otherwise an error. */
+int strata_rms_norm_q_gemv_f32(strata_ctx* ctx, uint64_t x, uint64_t res, uint64_t nw, uint64_t h, uint64_t xq,
+                               uint64_t n, float eps, const strata_tensor* w, uint64_t y);
 /* Backend::swiglu_q (src/backend.rs:313-318; kernel src/cuda/kernels.cu:1826-1839): silu(g) * u over `rows` rows
  * of n floats, quantized into xq as strata_quant_xq does; g is left as is. *ret = xq (the address the following
  * GEMV reads). */

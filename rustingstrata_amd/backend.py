@@ -60,7 +60,8 @@ SIGNATURES = {
     "strata_quant_xq": [CTX, U64, U64, U64, U64, U64],
     "strata_rms_norm": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float],
     "strata_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
-    "strata_combine_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64],
+    "strata_combine_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
+    "strata_rms_norm_q_gemv_f32": [CTX, U64, U64, U64, U64, U64, U64, ctypes.c_float, TP, U64],
     "strata_gemv": [CTX, TP, U64, U64],
     "strata_gemvn": [CTX, TP, U64, U64, U64, U64, U64],
     "strata_gemvn_noalloc": [CTX, TP, U64, U64, U64, U64, U64],
@@ -297,10 +298,16 @@ class HipBackend:
     def rms_norm(self, x, x_stride, w, out, out_stride, n, rows, eps):
         _check(lib().strata_rms_norm(self._ctx, int(x), x_stride, int(w), int(out), out_stride, n, rows, eps))
 
-    def combine_rms_norm_q(self, x, ye, wh, k, w, out, n, rows, eps, xq=0):
-        """moe_combine (no shared expert) of ye into x, then rms_norm_q of x, in one launch where the rows allow."""
+    def combine_rms_norm_q(self, x, ye, wh, k, w, out, n, rows, eps, xq=0, res=0):
+        """x += res (when given), moe_combine (no shared expert) of ye into x, then rms_norm_q of x, in one launch
+        where the rows allow."""
         _check(lib().strata_combine_rms_norm_q(self._ctx, int(x), n, int(ye), int(wh), k, int(w), int(out), n, n, rows,
-                                               eps, int(xq)))
+                                               eps, int(xq), int(res)))
+
+    def rms_norm_q_gemv_f32(self, x, res, nw, h, xq, n, eps, w, y):
+        """h = rms_norm(x + res) * nw (and xq), y = w h for an F32 matrix, one launch; x is not written."""
+        _check(lib().strata_rms_norm_q_gemv_f32(self._ctx, int(x), int(res), int(nw), int(h), int(xq), n, eps,
+                                                w._c(), int(y)))
 
     def rms_norm_q(self, x, x_stride, w, out, out_stride, n, rows, eps, xq=0, res=0):
         _check(lib().strata_rms_norm_q(self._ctx, int(x), x_stride, int(w), int(out), out_stride, n, rows, eps, int(xq),

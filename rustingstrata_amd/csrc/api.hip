@@ -388,22 +388,40 @@ int strata_quant_xq(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t n, ui
 
 int strata_combine_rms_norm_q(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t ye, uint64_t wh, uint64_t k,
                               uint64_t w, uint64_t out, uint64_t out_stride, uint64_t n, uint64_t rows, float eps,
-                              uint64_t xq) {
+                              uint64_t xq, uint64_t res) {
     if (check_ctx(c)) return -1;
     if (!x || !w || !out || !ye || !wh) return set_error("combine_rms_norm_q: null x, w, out, ye or wh");
     if (xq && n % 32) return set_error("rms_norm_q: " + std::to_string(n) + " values (a multiple of 32 to quantize)");
     if (k == 0 || k > 4096 || n > (1u << 30) || rows > 65535) return set_error("combine_rms_norm_q: " + std::to_string(rows) + " rows of " + std::to_string(k) + " slots");
     if (x_stride != n) return set_error("combine_rms_norm_q: x rows must be n floats apart (moe_combine's layout)");
     const hipError_t e = launch_rms_norm_q((float*)x, x_stride, (const float*)w, (float*)out, out_stride, (int)n, (int)rows,
-                                           eps, (int8_t*)xq, nullptr, c->numerics, c->stream, (const float*)ye,
+                                           eps, (int8_t*)xq, (const float*)res, c->numerics, c->stream, (const float*)ye,
                                            (const float*)wh, (int)k);
     if (e != hipErrorNotSupported) {
         STRATA_HIP(e);
         return 0;
     }
-    // rows the one-round-trip form does not take: the combine, then the norm
+    // rows the one-round-trip form does not take: x += res, the combine, then the norm
+    if (res && strata_add(c, x, res, n * rows)) return -1;
     if (strata_moe_combine(c, x, ye, wh, k, 0, 0, n, rows)) return -1;
     return strata_rms_norm_q(c, x, x_stride, w, out, out_stride, n, rows, eps, xq, 0);
+}
+
+int strata_rms_norm_q_gemv_f32(strata_ctx* c, uint64_t x, uint64_t res, uint64_t nw, uint64_t h, uint64_t xq,
+                               uint64_t n, float eps, const strata_tensor* w, uint64_t y) {
+    if (check_ctx(c)) return -1;
+    if (!w || !w->ptr) return set_error("rms_norm_q_gemv_f32: null matrix");
+    if (!x || !res || !nw || !h || !y) return set_error("rms_norm_q_gemv_f32: null x, res, nw, h or y");
+    if (w->ty != 0 || w->cols != n) return set_error("rms_norm_q_gemv_f32: an F32 matrix of " + std::to_string(n) + " columns");
+    if (w->rows == 0 || w->rows >= (1ull << 31)) return set_error("rms_norm_q_gemv_f32: " + std::to_string(w->rows) + " rows");
+    if (xq && n % 32) return set_error("rms_norm_q: " + std::to_string(n) + " values (a multiple of 32 to quantize)");
+    const hipError_t e = launch_rms_norm_gemv_f32((const float*)x, (const float*)res, (const float*)nw, (float*)h,
+                                                  (int8_t*)xq, (int)n, eps, c->numerics, (const float*)w->ptr,
+                                                  (int)w->rows, (float*)y, c->stream);
+    if (e == hipErrorNotSupported)
+        return set_error("rms_norm_q_gemv_f32: rows of at most 2048 values, a multiple of 8, 16-byte aligned");
+    STRATA_HIP(e);
+    return 0;
 }
 
 int strata_rms_norm_q(strata_ctx* c, uint64_t x, uint64_t x_stride, uint64_t w, uint64_t out, uint64_t out_stride,

@@ -7,6 +7,7 @@
 
 #include "decoder.h"
 #include "formats.h"
+#include "xlane.h"
 
 namespace strata {
 
@@ -17,11 +18,6 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float v) {
     return b;
 }
 
-__device__ __forceinline__ float wave_sum_xor(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 // ---- rms_norm + rope (+ KV store) ----
 // One wave per head, n <= 512, the head staged in LDS. The sum of squares runs in index order on one lane (n adds per

@@ -10,6 +10,10 @@ inline uint64_t xq_bytes(uint64_t n, uint64_t nt) { return nt * (n + n / 8); }
 
 hipError_t launch_dequant(int ty, const uint8_t* w, uint64_t rows, uint64_t cols, float* out, hipStream_t s);
 // quant_xq under numerics `mode` (STRATA_NUM_*): rows t < nt of x (t * x_stride floats apart) into out.
+// h = rms_norm(x + res) * nw (+ its quantization into xq when not null), y = W h for an F32 rows x n matrix, one
+// launch; x is not written. hipErrorNotSupported: n > 2048, n % 8, or rows not 16-byte aligned.
+hipError_t launch_rms_norm_gemv_f32(const float* x, const float* res, const float* nw, float* h, int8_t* xq, int n,
+                                   float eps, int mode, const float* W, int rows, float* y, hipStream_t s);
 hipError_t launch_quant_xq(const float* x, uint64_t x_stride, int n, int nt, int8_t* out, int mode, hipStream_t s);
 // With ye: x += sum_j wh[j] ye[j] over each row's ck slots (moe_combine's arithmetic) in place of res; rows of at most
 // 2048 values (a multiple of 8, 16-byte aligned) only, else hipErrorNotSupported.

@@ -138,8 +138,9 @@ __global__ __launch_bounds__(256) void quant_xq_kernel(const float* __restrict__
 // of squares is a fixed tree (per-thread sums, DPP within 32 lanes, then the 8 half-waves in order). Rows of up to 2048
 // values (a multiple of 8, 16-byte aligned rows) take one memory round trip: each thread keeps its 8 consecutive
 // values in registers from the loads to the quantization.
-// With ye (one-round-trip rows only): res is the MoE combine of the row's token instead, sum_j wh[j] ye[j] over its
-// ck slots in order (a slot of weight 0 adds nothing), combine_kernel's arithmetic, so x gets moe_combine's bits.
+// With ye (one-round-trip rows only): after res (when not null) the MoE combine of the row's token is added too, sum_j
+// wh[j] ye[j] over its ck slots in order (a slot of weight 0 adds nothing), combine_kernel's arithmetic, so x gets the
+// bits of x += res then moe_combine.
 __global__ __launch_bounds__(256) void rms_norm_q_kernel(float* x, uint64_t x_stride, const float* __restrict__ w,
                                                          float* out, uint64_t out_stride, int n, float eps,
                                                          int8_t* xq, const float* __restrict__ res, int rows, int mode,
@@ -267,9 +268,98 @@ hipError_t launch_rms_norm_q(float* x, uint64_t x_stride, const float* w, float*
     if (!n || !rows) return hipSuccess;
     const int vec = ((uintptr_t)x | (uintptr_t)w | (uintptr_t)out | (uintptr_t)res | (uintptr_t)ye) % 16 == 0 &&
                     x_stride % 4 == 0 && out_stride % 4 == 0;
-    if (ye && (res || !vec || n > 2048 || n % 8 || ck < 1)) return hipErrorNotSupported;
+    if (ye && (!vec || n > 2048 || n % 8 || ck < 1)) return hipErrorNotSupported;
     rms_norm_q_kernel<<<dim3((unsigned)rows), dim3(256), 0, s>>>(x, x_stride, w, out, out_stride, n, eps, xq, res, rows, mode,
                                                                  vec, ye, wh, ck);
+    return hipGetLastError();
+}
+
+// rms_norm_q of one row followed by an F32 GEMV of its output (a decode step's FFN norm and router logits): every
+// block normalizes h = (x + res) * (1 / sqrt(mean((x + res)^2) + eps)) * nw itself with rms_norm_q_kernel's
+// one-round-trip arithmetic (the same bits), block 0 stores h and its quantization (xq), and wave w of block b takes
+// matrix row 4 b + w with gemv_f32_1_kernel's arithmetic (8 16-byte chunks a lane, then the xor butterfly). The row's
+// weights are requested before the norm. x is not written: the caller adds res into x later (the combine after the
+// MoE takes it as its res). n <= 2048, a multiple of 8, 16-byte aligned rows.
+__global__ __launch_bounds__(256) void rms_norm_gemv_f32_kernel(const float* __restrict__ x, const float* __restrict__ res,
+                                                                const float* __restrict__ nw, float* h, int8_t* xq,
+                                                                int n, float eps, int mode,
+                                                                const float* __restrict__ W, int rows, float* y) {
+    __shared__ float part[8];
+    __shared__ __align__(16) float hs[2048];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, n4 = n / 4;
+    const int r = 4 * (int)blockIdx.x + wave;
+    float4 wv[8];
+    {
+        const float4* wr = (const float4*)(W + (uint64_t)min(r, rows - 1) * n);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int c = lane + 64 * u;
+            wv[u] = c < n4 ? wr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    const int i = 8 * tid;
+    const bool live = i < n;
+    float v[8], wn[8];
+    if (live) {
+        const float4 a = *(const float4*)(x + i), b = *(const float4*)(x + i + 4);
+        const float4 c = *(const float4*)(nw + i), d = *(const float4*)(nw + i + 4);
+        const float4 e = *(const float4*)(res + i), f = *(const float4*)(res + i + 4);
+        const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}, ev[8] = {e.x, e.y, e.z, e.w, f.x, f.y, f.z, f.w};
+        wn[0] = c.x; wn[1] = c.y; wn[2] = c.z; wn[3] = c.w; wn[4] = d.x; wn[5] = d.y; wn[6] = d.z; wn[7] = d.w;
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = xv[j] + ev[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = wn[j] = 0.0f;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) s += v[j] * v[j];
+    s += xl32f<0>(s);
+    s += xl32f<1>(s);
+    s += xl32f<2>(s);
+    s += xl32f<3>(s);
+    s += xl32f<4>(s);
+    if ((tid & 31) == 0) part[tid >> 5] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < 8; hh++) tot += part[hh];
+    const float sc = 1.0f / sqrtf(tot / (float)n + eps);
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = live ? v[j] * sc * wn[j] : 0.0f;
+    if (live) {
+        *(float4*)(hs + i) = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4*)(hs + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if (blockIdx.x == 0) {
+        if (live) {
+            *(float4*)(h + i) = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4*)(h + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        if (xq) quant8_group(v, i, live, mode, xq, (float*)(xq + n));
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int c = lane + 64 * u;
+        if (c < n4) {
+            const float4 xv = *(const float4*)(hs + 4 * c);
+            acc += wv[u].x * xv.x + wv[u].y * xv.y + wv[u].z * xv.z + wv[u].w * xv.w;
+        }
+    }
+    const float t = wave_sum_xor(acc);
+    if (lane == 0 && r < rows) y[r] = t;
+}
+
+hipError_t launch_rms_norm_gemv_f32(const float* x, const float* res, const float* nw, float* h, int8_t* xq, int n,
+                                   float eps, int mode, const float* W, int rows, float* y, hipStream_t s) {
+    if (n > 2048 || n % 8 || n <= 0 || rows <= 0 ||
+        ((uintptr_t)x | (uintptr_t)res | (uintptr_t)nw | (uintptr_t)h | (uintptr_t)W) % 16)
+        return hipErrorNotSupported;
+    rms_norm_gemv_f32_kernel<<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s>>>(x, res, nw, h, xq, n, eps, mode, W,
+                                                                                  rows, y);
     return hipGetLastError();
 }
 

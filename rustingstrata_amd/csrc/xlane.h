@@ -21,6 +21,13 @@ __device__ __forceinline__ int xl32(int v) {
 template <int STEP>
 __device__ __forceinline__ float xl32f(float v) { return __int_as_float(xl32<STEP>(__float_as_int(v))); }
 
+// Sum over the 64 lanes of a wave by an xor butterfly (distances 32, 16, .., 1), the same in every lane.
+__device__ __forceinline__ float wave_sum_xor(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
 // Inclusive prefix sum over the 64 lanes of a wave in lane order, by DPP: Hillis-Steele shifts within each row of 16
 // (lanes shifted in from outside the row read 0), then row 0's and row 2's totals added into rows 1 and 3, then
 // lane 31's into rows 2 and 3.

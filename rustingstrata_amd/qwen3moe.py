@@ -16,10 +16,10 @@ Per prefill chunk of t tokens at position pos (step[0] = pos):
     SwiGLU epilogue ; down grouped GEMM ; x += moe_combine_seq.
 Per decode token (recorded once as a graph and replayed; the step buffer carries the position):
     x = embed(token) ; per layer: h, hq = rms_norm_q(x) ; q, k, v = gemvq (one launch) ; rms_norm_rope_qk ;
-    attn_decode ; mix = gemvq(o) ; h, hq = rms_norm_q(x += mix) ; logits = gemv(router) ; moe_route and the paired
-    gate/up moe_gemv as one launch (moe_route_gemv) ; the down GEMV (moe_down_swiglu_combine, SwiGLU inside) ; its
-    combine x += sum w y runs with the next layer's attention norm (combine_rms_norm_q) ; then the output norm (with the
-    last combine), output gemv, argmax_rows.
+    attn_decode ; mix = gemvq(o) ; h, hq = rms_norm_q(x + mix) and logits = gemv(router, h) as one launch ;
+    moe_route and the paired gate/up moe_gemv as one launch (moe_route_gemv) ; the down GEMV (moe_down_swiglu_combine, SwiGLU inside) ; its
+    x += mix and the combine x += sum w y run with the next layer's attention norm (combine_rms_norm_q) ; then the
+    output norm (with the last of them), output gemv, argmax_rows.
 """
 import numpy as np
 
@@ -261,16 +261,18 @@ class Model:
         for li, ly in enumerate(w.layers):
             if li == 0:
                 hip.rms_norm_q(x, H, ly.attn_norm, self.h, H, H, 1, c.eps, xq=self.hq)
-            else:  # the previous layer's combine (x += sum w y) and this layer's attention norm, one launch
-                hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, ly.attn_norm, self.h, H, 1, c.eps, xq=self.hq)
+            else:  # the previous layer's x += mix, its combine (x += sum w y) and this layer's attention norm
+                hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, ly.attn_norm, self.h, H, 1, c.eps, xq=self.hq,
+                                       res=self.mix)
             hip.gemvq(ly.qkv, self.h, H, self.hq, self.dqkv, nh * hd + 2 * kv, 1)  # q, k and v in one launch
             hip.rms_norm_rope_qk(self.dq, hd, ly.q_norm, self.dqo, nh, nh, self.dk, ly.k_norm, self.dko, nkv, nkv, hd,
                                  c.eps, hd, self.step, c.rope_base, self.dv, ly.kc, ly.vc)
             hip.attn_decode(self.dqo, ly.kc, ly.vc, 0, self.datt, self.part, self.step, nh, nkv, hd,
                             float(1.0 / np.sqrt(hd)), 1)
             hip.gemv(ly.o, self.datt, self.mix)
-            hip.rms_norm_q(x, H, ly.ffn_norm, self.h, H, H, 1, c.eps, xq=self.hq, res=self.mix)
-            hip.gemv(ly.router, self.h, self.dl)
+            # h, hq = rms_norm_q(x + mix) and the router logits in one launch (x += mix is left to the next
+            # combine_rms_norm_q, which adds mix before the combine: the same bits)
+            hip.rms_norm_q_gemv_f32(x, self.mix, ly.ffn_norm, self.h, self.hq, H, c.eps, ly.router, self.dl)
             # the route inside the gate/up GEMV launch (moe_route then moe_gemv, the same bits)
             hip.moe_route_gemv(self.dl, E, k, 0.0, self.table, self.dids, self.dwts, self.dslots, self.dwh,
                                c.ty_gate_up, F, H, ly.gate_up, ly.e_gu, self.h, self.g2, pair=(ly.up_off, k * F * 4),
@@ -278,7 +280,7 @@ class Model:
             # the down GEMV (SwiGLU quantized inside) into ye1; its combine runs with the next norm
             hip.moe_down_swiglu_combine(c.ty_down, H, F, ly.down, ly.e_down, self.dslots, k, self.g2,
                                         int(self.g2) + k * F * 4, self.ye1, 0, self.dwh, 0, 0, 1)
-        hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, w.output_norm, self.h, H, 1, c.eps)
+        hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, w.output_norm, self.h, H, 1, c.eps, res=self.mix)
         hip.gemv(w.output, self.h, self.logits)
         hip.argmax_rows(self.logits, c.n_vocab, 1, self.tok)
 

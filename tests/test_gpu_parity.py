@@ -142,12 +142,13 @@ def test_rms_norm_q(hip, n, rows, res, inplace):
 
 
 @pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])
-@pytest.mark.parametrize("n,rows,k,quant", [(2048, 1, 8, True), (768, 3, 6, True), (2048, 2, 12, False),
-                                           (512, 4, 1, True), (4096, 2, 8, True)])
-def test_combine_rms_norm_q_equals_two_calls(hip, numerics, n, rows, k, quant):
-    """combine_rms_norm_q (a layer's moe_combine and the next attention norm in one launch) leaves x, out and xq
-    bit-equal to moe_combine then rms_norm_q (src/backend.rs:418-419, 233-235), with slots of weight 0, more slots
-    than one round of 8 (k = 12), and n = 4096 (two launches); out against ops::rms_norm of the combined x."""
+@pytest.mark.parametrize("n,rows,k,quant,res", [(2048, 1, 8, True, True), (768, 3, 6, True, False),
+                                               (2048, 2, 12, False, True), (512, 4, 1, True, False),
+                                               (4096, 2, 8, True, True)])
+def test_combine_rms_norm_q_equals_two_calls(hip, numerics, n, rows, k, quant, res):
+    """combine_rms_norm_q (x += res, a layer's moe_combine and the next attention norm in one launch) leaves x, out and
+    xq bit-equal to add, moe_combine then rms_norm_q (src/backend.rs:418-419, 233-235), with slots of weight 0, more
+    slots than one round of 8 (k = 12), and n = 4096 (separate launches); out against ops::rms_norm of the new x."""
     rng = np.random.default_rng(n + rows + k)
     x0 = normal((rows, n), seed=n + k)
     ye = normal((rows * k, n), seed=n + k + 1)
@@ -161,9 +162,12 @@ def test_combine_rms_norm_q_equals_two_calls(hip, numerics, n, rows, k, quant):
         xa, xb = up(hip, x0), up(hip, x0)
         oa, ob = hip.alloc(rows * n * 4), hip.alloc(rows * n * 4)
         qa, qb = (hip.alloc(rows * (n + n // 8)), hip.alloc(rows * (n + n // 8))) if quant else (0, 0)
+        rb = up(hip, normal((rows, n), seed=n + k + 2)) if res else 0
+        if res:
+            hip.add(xa, rb, rows * n)
         hip.moe_combine(xa, yb, whb, k, 0, 0, n, rows)
         hip.rms_norm_q(xa, n, wb, oa, n, n, rows, 1e-6, xq=qa)
-        hip.combine_rms_norm_q(xb, yb, whb, k, wb, ob, n, rows, 1e-6, xq=qb)
+        hip.combine_rms_norm_q(xb, yb, whb, k, wb, ob, n, rows, 1e-6, xq=qb, res=rb)
     finally:
         hip.set_numerics(old)
     for a, b, m in ((xa, xb, rows * n), (oa, ob, rows * n)):
@@ -175,8 +179,44 @@ def test_combine_rms_norm_q_equals_two_calls(hip, numerics, n, rows, k, quant):
     got = down(hip, ob, np.float32, rows * n).reshape(rows, n)
     assert np.abs(got - want).max() / np.abs(want).max() < 1e-6
     # x itself against the combine in f64 (slot order aside)
+    if res:
+        x0 = x0 + normal((rows, n), seed=n + k + 2)
     wx = x0.astype(np.float64) + np.einsum("rk,rkn->rn", wh.reshape(rows, k).astype(np.float64), ye.reshape(rows, k, n))
     assert np.abs(xc - wx).max() < 1e-5
+
+
+@pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])
+@pytest.mark.parametrize("n,rows", [(2048, 128), (512, 61), (1024, 3)])
+def test_rms_norm_q_gemv_f32_equals_two_calls(hip, numerics, n, rows):
+    """rms_norm_q_gemv_f32 (the decode's FFN norm and router logits in one launch): h and hq bit-equal to
+    rms_norm_q(x + res), y bit-equal to gemv of the F32 matrix on that h (src/backend.rs:233-235, src/gpu_model.rs
+    router), x left as it was; a row count that is not a multiple of 4 (61)."""
+    x0, r0 = normal(n, seed=n + 1), normal(n, seed=n + 2)
+    w = np.random.default_rng(n).uniform(0.5, 1.5, n).astype(np.float32)
+    W = (0.05 * normal((rows, n), seed=n + 3)).astype(np.float32)
+    wb, Wt = up(hip, w), hip.upload_f32(W)
+    old = hip.numerics()
+    hip.set_numerics(numerics)
+    try:
+        xa, xb, rb = up(hip, x0), up(hip, x0), up(hip, r0)
+        ha, hb = hip.alloc(n * 4), hip.alloc(n * 4)
+        qa, qb = hip.alloc(n + n // 8), hip.alloc(n + n // 8)
+        ya, yb = hip.alloc(rows * 4), hip.alloc(rows * 4)
+        hip.rms_norm_q(xa, n, wb, ha, n, n, 1, 1e-6, xq=qa, res=rb)
+        hip.gemv(Wt, ha, ya)
+        hip.rms_norm_q_gemv_f32(xb, rb, wb, hb, qb, n, 1e-6, Wt, yb)
+    finally:
+        hip.set_numerics(old)
+    assert np.array_equal(down(hip, xb, np.float32, n), x0)
+    assert np.array_equal(down(hip, ha, np.uint32, n), down(hip, hb, np.uint32, n))
+    assert np.array_equal(down(hip, qa, np.uint8, n + n // 8), down(hip, qb, np.uint8, n + n // 8))
+    assert np.array_equal(down(hip, ya, np.uint32, rows), down(hip, yb, np.uint32, rows))
+    h = down(hip, hb, np.float32, n)
+    assert np.abs(h - O.rms_norm((x0 + r0)[None, :], w, 1e-6)[0]).max() / np.abs(h).max() < 1e-6
+    yw = W.astype(np.float64) @ h.astype(np.float64)
+    assert np.abs(down(hip, yb, np.float32, rows) - yw).max() / np.abs(yw).max() < 1e-5
+    with pytest.raises(S.StrataError, match="rms_norm_q_gemv_f32"):
+        hip.rms_norm_q_gemv_f32(xb, rb, wb, hb, qb, n + 8, 1e-6, Wt, yb)
 
 
 def test_quant_xq_per32_bit_exact(hip):
