@@ -103,6 +103,10 @@ template <int HD> struct PfLayout {
 // Each wave loads its 16 keys' K and V rows (lane l: keys 4 (l % 4) .. + 3, dims 8 (l / 4) .. + 7), K into its own
 // LDS rows as is and V transposed. After the last chunk the four waves' (m, l, o) meet in LDS and the block leaves
 // [acc (hd) | max | sum] per head in part (max in log2 units); attn_merge_kernel combines the splits.
+// NR (one decode token): the query heads arrive raw and the block applies rms_norm_rope_qk itself (norm_rope_kernel's
+// arithmetic: the same bits), and the block whose split holds the token's own position also norms and ropes its key
+// head, stores the new key and value into the f16 caches and uses them for that position (no block reads it from the
+// cache): one launch in place of rms_norm_rope_qk + kv store + attention.
 constexpr int DEC_WAVES = 4;
 template <int HD>
 struct DecLayout {
@@ -112,12 +116,12 @@ struct DecLayout {
     static constexpr int MERGE = DEC_WAVES * (HD * 16 + 32) * 4;  // the waves' o, m and l for the block merge
     static constexpr int BYTES = DEC_WAVES * WAVE > MERGE ? DEC_WAVES * WAVE : MERGE;
 };
-template <int HD, int G>
+template <int HD, int G, bool NR>
 __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float* __restrict__ q,
                                                                      const uint16_t* __restrict__ kc,
                                                                      const uint16_t* __restrict__ vc,
                                                                      float* __restrict__ part, const int* step, int nh,
-                                                                     int nkv, float scale, int win) {
+                                                                     int nkv, float scale, int win, NormRope nr) {
     using L = DecLayout<HD>;
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
     constexpr int KS = HD / 32, DT = HD / 16, NDG = HD / 8;  // K-steps of the scores; dim tiles; 8-dim groups
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
     // the query first (it does not depend on the position), then the first chunk's K and V rows as soon as the
     // position is known, so the round trips overlap
     f4 qv[2 * KS];  // dims 32 k + 8 lg .. + 3 and + 4 .. + 7
-    {
+    if constexpr (!NR) {
         const float* qr = q + (uint64_t)t * nh * HD + (uint64_t)(h0 + l16) * HD;
 #pragma unroll
         for (int k = 0; k < KS; k++) {
@@ -148,6 +152,92 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
     const int per_s = split_len(n_pos, ns);
     const int p0 = split * per_s, p1 = min(n_pos, p0 + per_s);
     if (p0 >= n_pos) return;  // (the whole block) past the token's positions: the merge reads only the splits that have some
+    // NR: the new position's key and value (f16), in LDS for the split that holds the position
+    __shared__ __align__(16) uint16_t knew[NR ? HD : 8], vnew[NR ? HD : 8];
+    const int pos_new = step[0];
+    const bool last = NR && p1 == n_pos;
+    if constexpr (NR) {
+        // raw heads into LDS: the G query heads, then (last split) the key and value heads of KV head g
+        __shared__ __align__(16) float raw[(G + 2) * HD];
+        __shared__ float ssq[G + 1];
+        const int nhd = G + (last ? 2 : 0);
+        for (int c = tid; c < nhd * HD / 4; c += 64 * DEC_WAVES) {
+            const int j = c / (HD / 4), i = 4 * (c % (HD / 4));
+            const float* src = j < G ? nr.qx + (uint64_t)(h0 + j) * nr.q_stride
+                                     : j == G ? nr.x + (uint64_t)g * nr.x_stride : nr.v + (uint64_t)g * HD;
+            *(float4*)&raw[j * HD + i] = *(const float4*)(src + i);
+        }
+        __syncthreads();
+        // the heads' sums of squares in index order, a lane per head (the reference's iterator sum)
+        if (wave == 0 && lane < G + (last ? 1 : 0)) {
+            const float* xr = raw + lane * HD;
+            ssq[lane] = nr_sumsq(HD, [&](int i0, float4 (&r)[8]) {
+#pragma unroll
+                for (int c = 0; c < 8; c++) r[c] = *(const float4*)&xr[i0 + 4 * c];
+            });
+        }
+        // the rope angles of this lane's pairs (lane + 64 j), f64 as ops::rope_neox
+        const int half = nr.n_rot / 2;
+        constexpr int NPJ = (HD / 2 + 63) / 64;
+        float sn[NPJ], cs[NPJ];
+#pragma unroll
+        for (int j = 0; j < NPJ; j++) {
+            const int i = lane + 64 * j;
+            sn[j] = cs[j] = 0.0f;
+            if (i < half) {
+                const double f = i < nr.nfreq ? nr.freq[i] : pow((double)nr.base, -2.0 * (double)i / (double)nr.n_rot);
+                double sd, cd;
+                sincos((double)pos_new * f, &sd, &cd);
+                sn[j] = (float)sd;
+                cs[j] = (float)cd;
+            }
+        }
+        __syncthreads();
+        // head j by wave j % 4: x * (1 / sqrt(ss / n + eps)) * w, then the rope, in place
+        for (int j = wave; j < G + (last ? 1 : 0); j += DEC_WAVES) {
+            float* hr = raw + j * HD;
+            const float* wr = j < G ? nr.qw : nr.w;
+            const float sc = 1.0f / sqrtf(ssq[j] / (float)HD + nr.eps);
+#pragma unroll
+            for (int u = 0; u < HD / 64; u++) hr[lane + 64 * u] = hr[lane + 64 * u] * sc * wr[lane + 64 * u];
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int u = 0; u < NPJ; u++) {
+                const int i = lane + 64 * u;
+                if (i < half) {
+                    const float pa = hr[i], pb = hr[i + half];
+                    hr[i] = pa * cs[u] - pb * sn[u];
+                    hr[i + half] = pa * sn[u] + pb * cs[u];
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (j == G) {
+                // the new key and value: into the caches (row pos_new nkv + g) and into LDS for this split
+                const uint64_t e = ((uint64_t)pos_new * nkv + g) * HD;
+#pragma unroll
+                for (int u = 0; u < HD / 64; u++) {
+                    const int i = lane + 64 * u;
+                    const _Float16 kh = (_Float16)hr[i], vh = (_Float16)raw[(G + 1) * HD + i];
+                    const uint16_t kb16 = __builtin_bit_cast(uint16_t, kh), vb16 = __builtin_bit_cast(uint16_t, vh);
+                    knew[i] = kb16;
+                    vnew[i] = vb16;
+                    ((uint16_t*)nr.kc)[e + i] = kb16;
+                    ((uint16_t*)nr.vc)[e + i] = vb16;
+                }
+            }
+        }
+        __syncthreads();
+        // the query fragments from the normed, roped heads
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            qv[2 * k] = (f4){0.0f, 0.0f, 0.0f, 0.0f};
+            qv[2 * k + 1] = qv[2 * k];
+            if (l16 < G) {
+                qv[2 * k] = *(const f4*)&raw[l16 * HD + 32 * k + 8 * lg];
+                qv[2 * k + 1] = *(const f4*)&raw[l16 * HD + 32 * k + 8 * lg + 4];
+            }
+        }
+    }
     const int kq = lane & 3, dg = lane >> 2;  // this lane's load keys 4 kq .., dims 8 dg ..
     const bool loader = dg < NDG;
     // Q^T fragments: head h0 + l16 (zero past G), dims 32 k + 8 lg .. + 7; usc undoes the scaling (times `scale`)
@@ -164,10 +254,15 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
             uint4 kb[4], vb[4];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                const uint64_t off = (uint64_t)(base + c0 + min(16 * wave + 4 * kq + kk, nc - 1)) * kvd + g * HD +
-                                     8 * min(dg, NDG - 1);
-                kb[kk] = *(const uint4*)(kc + off);
-                vb[kk] = *(const uint4*)(vc + off);
+                const int kp = base + c0 + min(16 * wave + 4 * kq + kk, nc - 1);
+                const uint64_t off = (uint64_t)kp * kvd + g * HD + 8 * min(dg, NDG - 1);
+                if (NR && last && kp == pos_new) {  // the new position: this block's own key and value
+                    kb[kk] = *(const uint4*)&knew[8 * min(dg, NDG - 1)];
+                    vb[kk] = *(const uint4*)&vnew[8 * min(dg, NDG - 1)];
+                } else {
+                    kb[kk] = *(const uint4*)(kc + off);
+                    vb[kk] = *(const uint4*)(vc + off);
+                }
             }
             if (c0 == p0) {
                 // the query's fragments while the first chunk's rows are in flight: scaled by the power of two
@@ -367,17 +462,33 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
 
 template <int HD, int G>
 static void decode_t(const float* q, const uint16_t* kc, const uint16_t* vc, float* part, const int* step, int nh,
-                     int nkv, float scale, int nt, int win, hipStream_t s) {
-    attn_decode_kernel<HD, G><<<dim3(ATT_SPLITS, (unsigned)nkv, (unsigned)nt), dim3(64 * DEC_WAVES), 0, s>>>(q, kc, vc, part, step,
-                                                                                            nh, nkv, scale, win);
+                     int nkv, float scale, int nt, int win, const NormRope* nr, hipStream_t s) {
+    const dim3 grid(ATT_SPLITS, (unsigned)nkv, (unsigned)nt), block(64 * DEC_WAVES);
+    if (nr)
+        attn_decode_kernel<HD, G, true><<<grid, block, 0, s>>>(q, kc, vc, part, step, nh, nkv, scale, win, *nr);
+    else
+        attn_decode_kernel<HD, G, false><<<grid, block, 0, s>>>(q, kc, vc, part, step, nh, nkv, scale, win, NormRope{});
 }
 
 hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
                               float* part, const int* step, int nh, int nkv, int hd, float scale, int nt,
-                              const float* sink, int win, hipStream_t s) {
+                              const float* sink, int win, hipStream_t s, const NormRope* nr0) {
     if (nt <= 0) return hipSuccess;
     const int G = nh / nkv;
-#define DEC(HD_, G_) if (hd == HD_ && G == G_) decode_t<HD_, G_>(q, kc, vc, part, step, nh, nkv, scale, nt, win, s); else
+    NormRope nrf;
+    const NormRope* nr = nullptr;
+    if (nr0) {
+        // one token, heads of hd (rows of the f16 caches), the rope frequencies from the host's pow as in
+        // launch_norm_rope
+        if (nt != 1 || nr0->n != hd || nr0->n_rot > hd || nr0->n_rot % 2 || !nr0->kc || !nr0->vc ||
+            ((uintptr_t)nr0->qx | (uintptr_t)nr0->x | (uintptr_t)nr0->v) % 16 || nr0->q_stride % 4 || nr0->x_stride % 4)
+            return hipErrorNotSupported;
+        nrf = *nr0;
+        nrf.nfreq = nrf.n_rot / 2 <= NormRope::NFREQ ? nrf.n_rot / 2 : 0;
+        for (int i = 0; i < nrf.nfreq; i++) nrf.freq[i] = std::pow((double)nrf.base, -2.0 * (double)i / (double)nrf.n_rot);
+        nr = &nrf;
+    }
+#define DEC(HD_, G_) if (hd == HD_ && G == G_) decode_t<HD_, G_>(q, kc, vc, part, step, nh, nkv, scale, nt, win, nr, s); else
     DEC(128, 1) DEC(128, 2) DEC(128, 4) DEC(128, 8) DEC(64, 1) DEC(64, 2) DEC(64, 4) DEC(64, 8)
     return hipErrorInvalidValue;
 #undef DEC

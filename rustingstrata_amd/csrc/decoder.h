@@ -21,6 +21,27 @@ struct NormRope {
     int nfreq = 0; double freq[NFREQ] = {};
 };
 hipError_t launch_norm_rope(const NormRope& a, hipStream_t s);
+
+// The sum of squares of x[0 .. n) in index order, as ops::rms_norm's iterator sum (a multiply, then an add): the
+// CPU's bits. sq(i0, r) loads values i0 .. i0 + 31 as 8 float4; the next 32 are loaded while the current 32 are added
+// (n % 32 == 0).
+template <typename Load>
+__device__ __forceinline__ float nr_sumsq(int n, Load&& ld) {
+    float ss = 0.0f;
+    float4 r[8], nx[8];
+    ld(0, r);
+    for (int i0 = 0; i0 < n; i0 += 32) {
+        if (i0 + 32 < n) ld(i0 + 32, nx);
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            ss += r[c].x * r[c].x; ss += r[c].y * r[c].y; ss += r[c].z * r[c].z; ss += r[c].w * r[c].w;
+        }
+#pragma unroll
+        for (int c = 0; c < 8; c++) r[c] = nx[c];
+    }
+    return ss;
+}
+
 hipError_t launch_rope_pairs(float* x, uint64_t stride, int heads, int per, int n_rot, const int* step, float base,
                              int lo, int hi, hipStream_t s);
 hipError_t launch_kv_store(const float* k, const float* v, uint16_t* kc, uint16_t* vc, int n, int t, const int* step,
@@ -42,9 +63,11 @@ hipError_t launch_fill_blocks(int ty, uint8_t* w, uint64_t n_blocks, uint64_t se
 
 // Attention (attn.hip). Caches: f16 rows of nkv * hd values per position.
 constexpr int ATT_SPLITS = 128;  // position splits of a decode token (part rows per head)
+// With nr (one token): the query heads are nr's raw q rows (q unused) and rms_norm_rope_qk with the KV store of nr
+// runs inside the launch (the same bits as launch_norm_rope first); hipErrorNotSupported for shapes it does not take.
 hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
                               float* part, const int* step, int nh, int nkv, int hd, float scale, int nt,
-                              const float* sink, int win, hipStream_t s);
+                              const float* sink, int win, hipStream_t s, const NormRope* nr = nullptr);
 hipError_t launch_attn_prefill(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
                                const int* step, int t, int nh, int nkv, int hd, float scale, const float* sink, int win,
                                hipStream_t s);

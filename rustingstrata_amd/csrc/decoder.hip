@@ -50,26 +50,6 @@ __device__ __forceinline__ NrHead nr_head(const NormRope& a, int gb) {
     return h;
 }
 
-// The sum of squares of x[0 .. n) in index order, as ops::rms_norm's iterator sum (a multiply, then an add): the
-// CPU's bits. sq(i0, r) loads values i0 .. i0 + 31 as 8 float4; the next 32 are loaded while the current 32 are added
-// (n % 32 == 0).
-template <typename Load>
-__device__ __forceinline__ float nr_sumsq(int n, Load&& ld) {
-    float ss = 0.0f;
-    float4 r[8], nx[8];
-    ld(0, r);
-    for (int i0 = 0; i0 < n; i0 += 32) {
-        if (i0 + 32 < n) ld(i0 + 32, nx);
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-            ss += r[c].x * r[c].x; ss += r[c].y * r[c].y; ss += r[c].z * r[c].z; ss += r[c].w * r[c].w;
-        }
-#pragma unroll
-        for (int c = 0; c < 8; c++) r[c] = nx[c];
-    }
-    return ss;
-}
-
 // One head by one wave: out = x * (1 / sqrt(ss / n + eps)) * w, rope, and (key heads of a storing launch) the f16
 // KV store. s: the wave's 512-float LDS stage. HAVE_SS: ss is given (else lane 0 sums the head from the stage).
 template <bool HAVE_SS>

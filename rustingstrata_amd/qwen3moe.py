@@ -15,8 +15,8 @@ Per prefill chunk of t tokens at position pos (step[0] = pos):
     logits = gemm_dense(router F32, h) ; router_topk ; moe_sort (on the device) ; gate/up grouped GEMM with the
     SwiGLU epilogue ; down grouped GEMM ; x += moe_combine_seq.
 Per decode token (recorded once as a graph and replayed; the step buffer carries the position):
-    x = embed(token) ; per layer: h, hq = rms_norm_q(x) ; q, k, v = gemvq (one launch) ; rms_norm_rope_qk ;
-    attn_decode ; mix = gemvq(o) ; h, hq = rms_norm_q(x + mix) and logits = gemv(router, h) as one launch ;
+    x = embed(token) ; per layer: h, hq = rms_norm_q(x) ; q, k, v = gemvq (one launch) ; rms_norm_rope_qk with the
+    KV store and attn_decode as one launch ; mix = gemvq(o) ; h, hq = rms_norm_q(x + mix) and logits = gemv(router, h) as one launch ;
     moe_route and the paired gate/up moe_gemv as one launch (moe_route_gemv) ; the down GEMV (moe_down_swiglu_combine, SwiGLU inside) ; its
     x += mix and the combine x += sum w y run with the next layer's attention norm (combine_rms_norm_q) ; then the
     output norm (with the last of them), output gemv, argmax_rows.
@@ -265,10 +265,11 @@ class Model:
                 hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, ly.attn_norm, self.h, H, 1, c.eps, xq=self.hq,
                                        res=self.mix)
             hip.gemvq(ly.qkv, self.h, H, self.hq, self.dqkv, nh * hd + 2 * kv, 1)  # q, k and v in one launch
-            hip.rms_norm_rope_qk(self.dq, hd, ly.q_norm, self.dqo, nh, nh, self.dk, ly.k_norm, self.dko, nkv, nkv, hd,
-                                 c.eps, hd, self.step, c.rope_base, self.dv, ly.kc, ly.vc)
-            hip.attn_decode(self.dqo, ly.kc, ly.vc, 0, self.datt, self.part, self.step, nh, nkv, hd,
-                            float(1.0 / np.sqrt(hd)), 1)
+            # q/k norms, rope and the KV store inside the attention launch (the same bits as rms_norm_rope_qk with
+            # the KV store, then attn_decode)
+            hip.rms_norm_rope_attn_decode(self.dq, hd, ly.q_norm, self.dk, ly.k_norm, self.dv, c.eps, hd, c.rope_base,
+                                          ly.kc, ly.vc, 0, self.datt, self.part, self.step, nh, nkv, hd,
+                                          float(1.0 / np.sqrt(hd)))
             hip.gemv(ly.o, self.datt, self.mix)
             # h, hq = rms_norm_q(x + mix) and the router logits in one launch (x += mix is left to the next
             # combine_rms_norm_q, which adds mix before the combine: the same bits)

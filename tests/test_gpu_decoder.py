@@ -153,6 +153,46 @@ def test_attn_decode_sink_gate_window(hip):
     assert max_rel_err(got, want) <= TOL and rel_l2(got, want) <= 1e-6
 
 
+@pytest.mark.parametrize("nh,nkv,hd,pos,n_rot,win,extras", [(32, 4, 128, 4099, 128, 0, False), (32, 4, 128, 63, 128, 0, True),
+                                                         (8, 8, 64, 0, 64, 0, False), (16, 4, 64, 300, 32, 0, False),
+                                                         (32, 4, 128, 450, 128, 128, True), (16, 8, 128, 64, 128, 0, False)])
+def test_rms_norm_rope_attn_decode_equals_unfused(hip, nh, nkv, hd, pos, n_rot, win, extras):
+    """rms_norm_rope_attn_decode (the q/k norms, rope and KV store inside the attention launch) gives the attention
+    output and the caches bit-equal to rms_norm_rope_qk with the KV store followed by attn_decode
+    (src/backend.rs:250-277, 383-410): positions at a split edge (63, 64), the first (0), a partial rope (n_rot 32),
+    a window with sink and gate, GQA groups 1, 2, 4 and 8; and the output against the CPU attention over the caches."""
+    rng = np.random.default_rng(pos + nh + hd)
+    P = pos + 5
+    kc16, vc16 = f16_cache(rng, P, nkv * hd, 1.5), f16_cache(rng, P, nkv * hd)
+    qkv = normal(nh * hd + 2 * nkv * hd, seed=pos + 1)
+    qw = np.random.default_rng(pos + 2).uniform(0.5, 1.5, hd).astype(np.float32)
+    kw = np.random.default_rng(pos + 3).uniform(0.5, 1.5, hd).astype(np.float32)
+    xb, qwb, kwb = up(hip, qkv), up(hip, qw), up(hip, kw)
+    q, k, v = int(xb), int(xb) + 4 * nh * hd, int(xb) + 4 * (nh + nkv) * hd
+    step = i32(hip, [pos, 0])
+    qg = up(hip, normal(nh * 2 * hd, seed=pos + 4)) if extras else 0
+    sink = up(hip, normal(nh, seed=pos + 5) + 2) if extras else 0
+    kc1, vc1, kc2, vc2 = up(hip, kc16), up(hip, vc16), up(hip, kc16), up(hip, vc16)
+    qo, ko = hip.alloc(nh * hd * 4), hip.alloc(nkv * hd * 4)
+    o1, o2 = hip.alloc(nh * hd * 4), hip.alloc(nh * hd * 4)
+    part = hip.alloc(hip.attn_part_floats(nh, hd) * 4)
+    scale, eps, base = 1.0 / np.sqrt(hd), 1e-6, 1e6
+    hip.rms_norm_rope_qk(q, hd, qwb, qo, nh, nh, k, kwb, ko, nkv, nkv, hd, eps, n_rot, step, base, v, kc1, vc1)
+    hip.attn_decode(qo, kc1, vc1, qg, o1, part, step, nh, nkv, hd, scale, 1, sink=sink, win=win)
+    hip.rms_norm_rope_attn_decode(q, hd, qwb, k, kwb, v, eps, n_rot, base, kc2, vc2, qg, o2, part, step, nh, nkv, hd,
+                                  scale, sink=sink, win=win)
+    m = P * nkv * hd
+    assert np.array_equal(hip.get(kc1, np.uint16, m), hip.get(kc2, np.uint16, m))
+    assert np.array_equal(hip.get(vc1, np.uint16, m), hip.get(vc2, np.uint16, m))
+    g1, g2 = hip.get(o1, np.float32, nh * hd), hip.get(o2, np.float32, nh * hd)
+    assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32)), int((g1 != g2).sum())
+    if not extras:
+        kf = hip.get(kc2, np.uint16, m).view(np.float16).astype(np.float32).reshape(P, nkv * hd)
+        vf = hip.get(vc2, np.uint16, m).view(np.float16).astype(np.float32).reshape(P, nkv * hd)
+        want = O.attention(hip.get(qo, np.float32, nh * hd), kf, vf, 0, pos + 1, nh, nkv, hd, scale)
+        assert max_rel_err(g2, want) <= TOL
+
+
 def prefill_case(hip, nh, nkv, hd, T, pos0, seed, rows=None, sink=None, gate=False, win=0):
     """Runs the prefill and checks the given rows: within 1e-3 max relative error of the CPU attention (or of the
     CPU's own distance from the f64 attention, whichever is larger: long, diffuse rows average V down to small
