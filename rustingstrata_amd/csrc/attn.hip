@@ -168,31 +168,34 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
             *(float4*)&raw[j * HD + i] = *(const float4*)(src + i);
         }
         __syncthreads();
-        // the heads' sums of squares in index order, a lane per head (the reference's iterator sum)
-        if (wave == 0 && lane < G + (last ? 1 : 0)) {
+        // the heads' sums of squares in index order, a lane per head (the reference's iterator sum), by wave 1 while
+        // wave 0 computes the rope angles
+        __shared__ float rsn[HD / 2], rcs[HD / 2];
+        if (wave == 1 && lane < G + (last ? 1 : 0)) {
             const float* xr = raw + lane * HD;
             ssq[lane] = nr_sumsq(HD, [&](int i0, float4 (&r)[8]) {
 #pragma unroll
                 for (int c = 0; c < 8; c++) r[c] = *(const float4*)&xr[i0 + 4 * c];
             });
         }
-        // the rope angles of this lane's pairs (lane + 64 j), f64 as ops::rope_neox
+        // the rope angles of pair i (lane i of wave 0; n_rot / 2 <= 64), f64 as ops::rope_neox
         const int half = nr.n_rot / 2;
         constexpr int NPJ = (HD / 2 + 63) / 64;
+        if (wave == 0 && lane < half) {
+            const double f = lane < nr.nfreq ? nr.freq[lane] : pow((double)nr.base, -2.0 * (double)lane / (double)nr.n_rot);
+            double sd, cd;
+            sincos((double)pos_new * f, &sd, &cd);
+            rsn[lane] = (float)sd;
+            rcs[lane] = (float)cd;
+        }
+        __syncthreads();
         float sn[NPJ], cs[NPJ];
 #pragma unroll
         for (int j = 0; j < NPJ; j++) {
             const int i = lane + 64 * j;
-            sn[j] = cs[j] = 0.0f;
-            if (i < half) {
-                const double f = i < nr.nfreq ? nr.freq[i] : pow((double)nr.base, -2.0 * (double)i / (double)nr.n_rot);
-                double sd, cd;
-                sincos((double)pos_new * f, &sd, &cd);
-                sn[j] = (float)sd;
-                cs[j] = (float)cd;
-            }
+            sn[j] = i < half ? rsn[i] : 0.0f;
+            cs[j] = i < half ? rcs[i] : 0.0f;
         }
-        __syncthreads();
         // head j by wave j % 4: x * (1 / sqrt(ss / n + eps)) * w, then the rope, in place
         for (int j = wave; j < G + (last ? 1 : 0); j += DEC_WAVES) {
             float* hr = raw + j * HD;
