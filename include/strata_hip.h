@@ -312,11 +312,13 @@ uint64_t strata_attn_part_floats(uint64_t nh, uint64_t hd);
  * ropes the query heads it serves itself, and the block whose position split holds step[0] also builds that
  * position's key and value, stores them and uses them directly. q: nh raw heads q_stride floats apart; k, v: nkv raw
  * heads of hd floats; out and part as strata_attn_decode_gq (one token). The same bits as strata_rms_norm_rope_qk
- * with the KV store followed by strata_attn_decode_gq; q, k, v 16-byte aligned with strides of a multiple of 4. */
+ * with the KV store followed by strata_attn_decode_gq; q, k, v 16-byte aligned with strides of a multiple of 4.
+ * xq (not 0; nh hd a multiple of 256): out also quantized as strata_quant_xq does, for the o projection's
+ * strata_gemvq. */
 int strata_rms_norm_rope_attn_decode(strata_ctx* ctx, uint64_t q, uint64_t q_stride, uint64_t qw, uint64_t k,
                                      uint64_t kw, uint64_t v, float eps, uint64_t n_rot, float base, uint64_t kc,
                                      uint64_t vc, uint64_t qg, uint64_t out, uint64_t part, uint64_t step, uint64_t nh,
-                                     uint64_t nkv, uint64_t hd, float scale, uint64_t sink, uint64_t win);
+                                     uint64_t nkv, uint64_t hd, float scale, uint64_t sink, uint64_t win, uint64_t xq);
 /* Backend::attn_decode / attn_decode_gq (src/backend.rs:383-410; kernels src/cuda/kernels.cu:2123-2626): nt query
  * tokens (rows of q, qg and out per token), token t over positions 0 ..= step[2 t] (the last `win` when win > 0),
  * otherwise as strata_attn_prefill. part: nt * strata_attn_part_floats(nh, hd) floats of scratch. K / V loads are

@@ -61,7 +61,7 @@ SIGNATURES = {
     "strata_rms_norm": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float],
     "strata_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
     "strata_rms_norm_rope_attn_decode": [CTX, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, ctypes.c_float, U64,
-                                         U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
+                                         U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64, U64],
     "strata_combine_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
     "strata_rms_norm_q_gemv_f32": [CTX, U64, U64, U64, U64, U64, U64, ctypes.c_float, TP, U64],
     "strata_gemv": [CTX, TP, U64, U64],
@@ -439,11 +439,12 @@ class HipBackend:
                                              int(vc)))
 
     def rms_norm_rope_attn_decode(self, q, q_stride, qw, k, kw, v, eps, n_rot, base, kc, vc, qg, out, part, step, nh,
-                                  nkv, hd, scale, sink=0, win=0):
-        """rms_norm_rope_qk of one token's raw q / k heads with the KV store, then attn_decode, as one launch."""
+                                  nkv, hd, scale, sink=0, win=0, xq=0):
+        """rms_norm_rope_qk of one token's raw q / k heads with the KV store, then attn_decode, as one launch (out
+        also quantized into xq when given)."""
         _check(lib().strata_rms_norm_rope_attn_decode(self._ctx, int(q), q_stride, int(qw), int(k), int(kw), int(v), eps,
                                                       n_rot, base, int(kc), int(vc), int(qg), int(out), int(part),
-                                                      int(step), nh, nkv, hd, scale, int(sink), win))
+                                                      int(step), nh, nkv, hd, scale, int(sink), win, int(xq)))
 
     def kv_store(self, k, v, kc, vc, n, t, step, hd):
         _check(lib().strata_kv_store(self._ctx, int(k), int(v), int(kc), int(vc), n, t, int(step), hd))

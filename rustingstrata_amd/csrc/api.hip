@@ -905,7 +905,8 @@ static int check_attn(uint64_t nh, uint64_t nkv, uint64_t hd, const char* what) 
 int strata_rms_norm_rope_attn_decode(strata_ctx* c, uint64_t q, uint64_t q_stride, uint64_t qw, uint64_t k,
                                      uint64_t kw, uint64_t v, float eps, uint64_t n_rot, float base, uint64_t kc,
                                      uint64_t vc, uint64_t qg, uint64_t out, uint64_t part, uint64_t step, uint64_t nh,
-                                     uint64_t nkv, uint64_t hd, float scale, uint64_t sink, uint64_t win) {
+                                     uint64_t nkv, uint64_t hd, float scale, uint64_t sink, uint64_t win,
+                                     uint64_t xq) {
     if (check_ctx(c) || check_attn(nh, nkv, hd, "attention decode") || check_rope(hd, n_rot)) return -1;
     if (!q || !qw || !k || !kw || !v || !kc || !vc || !out || !step) return set_error("rms_norm_rope_attn_decode: null argument");
     if (!part) return set_error("attention decode: null part buffer");
@@ -917,9 +918,11 @@ int strata_rms_norm_rope_attn_decode(strata_ctx* c, uint64_t q, uint64_t q_strid
     a.eps = eps; a.base = base; a.n_rot = (int)n_rot; a.step = (const int*)step;
     const hipError_t e = launch_attn_decode(nullptr, (const uint16_t*)kc, (const uint16_t*)vc, (const float*)qg,
                                             (float*)out, (float*)part, (const int*)step, (int)nh, (int)nkv, (int)hd,
-                                            scale, 1, (const float*)sink, (int)win, c->stream, &a);
+                                            scale, 1, (const float*)sink, (int)win, c->stream, &a, (int8_t*)xq,
+                                            c->numerics);
     if (e == hipErrorNotSupported)
-        return set_error("rms_norm_rope_attn_decode: q, k and v 16-byte aligned with row strides of a multiple of 4");
+        return set_error("rms_norm_rope_attn_decode: q, k and v 16-byte aligned with row strides of a multiple of 4, "
+                         "and nh hd a multiple of 256 with xq");
     STRATA_HIP(e);
     return 0;
 }

@@ -14,6 +14,7 @@
 #include <climits>
 
 #include "decoder.h"
+#include "quant8.h"
 #include "xlane.h"
 
 namespace strata {
@@ -402,17 +403,23 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
     }
 }
 
-// grid (nh, nt), 4 waves: out = sum_s acc_s 2^(m_s - M) / (sum_s l_s 2^(m_s - M) + 2^(sink log2(e) - M)) (sigmoid
-// gate), the maxima in log2 units.
-// Wave w takes splits w, w + 4, ..: their weights (a lane each), then the weighted sum of their partial rows (lane =
-// dims), all of its loads in flight together; the 4 wave sums are added in wave order through LDS.
-template <int HD>
-__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qg,
-                                                         float* __restrict__ out, int nh, int ns,
-                                                         const float* __restrict__ sink, const int* step, int win) {
+// grid (nh / HPB, nt), HPB groups of 4 waves, group j serving head HPB blockIdx.x + j: out = sum_s acc_s 2^(m_s - M) /
+// (sum_s l_s 2^(m_s - M) + 2^(sink log2(e) - M)) (sigmoid gate), the maxima in log2 units.
+// Wave w of a group takes splits w, w + 4, ..: their weights (a lane each), then the weighted sum of their partial rows
+// (lane = dims), all of its loads in flight together; the 4 wave sums are added in wave order through LDS.
+// With xq (HPB = 256 / HD: a block's heads are one 256-value group of the row) the block also quantizes its outputs
+// as quant_xq does into xq ([nt rows of nh HD int8][nt rows of nh HD / 32 scales]), for a GEMV that takes x
+// pre-quantized.
+template <int HD, int HPB>
+__global__ __launch_bounds__(256 * HPB) void attn_merge_kernel(const float* __restrict__ part, const float* __restrict__ qg,
+                                                               float* __restrict__ out, int nh, int ns,
+                                                               const float* __restrict__ sink, const int* step, int win,
+                                                               int8_t* xq, int mode) {
     constexpr int DL = HD / 64, SW = ATT_SPLITS / 4;  // dims a lane; splits a wave
-    __shared__ float sm[4], sd[4], so[4][HD];
-    const int h = blockIdx.x, t = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ float sm[HPB][4], sd[HPB][4], so[HPB][4][HD];
+    __shared__ __align__(16) float ob[HPB * HD];
+    const int grp = threadIdx.x >> 8, h = blockIdx.x * HPB + grp, t = blockIdx.y;
+    const int wave = (threadIdx.x >> 6) & 3, lane = threadIdx.x & 63;
     const float* pp = part + (uint64_t)(t * nh + h) * ns * (HD + 2);
     {
         // the splits that hold positions (the decode leaves the others unwritten)
@@ -432,9 +439,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
 #pragma unroll
         for (int d = 0; d < DL; d++) a[i][d] = pp[min(wave + 4 * i, ns - 1) * (HD + 2) + DL * lane + d];
     float M = wave_max64(ms);
-    if (lane == 0) sm[wave] = M;
+    if (lane == 0) sm[grp][wave] = M;
     __syncthreads();
-    M = fmaxf(fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3])), sk);
+    M = fmaxf(fmaxf(fmaxf(sm[grp][0], sm[grp][1]), fmaxf(sm[grp][2], sm[grp][3])), sk);
     const float e = ms == -INFINITY ? 0.0f : exp2_hw(ms - M);
     const float den = wave_sum64(ls * e);
     float o[DL];
@@ -446,20 +453,35 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
 #pragma unroll
         for (int d = 0; d < DL; d++) o[d] += a[i][d] * es;
     }
-    if (lane == 0) sd[wave] = den;
+    if (lane == 0) sd[grp][wave] = den;
 #pragma unroll
-    for (int d = 0; d < DL; d++) so[wave][DL * lane + d] = o[d];
+    for (int d = 0; d < DL; d++) so[grp][wave][DL * lane + d] = o[d];
     __syncthreads();
-    if (wave) return;
-    float dt = sd[0] + sd[1] + sd[2] + sd[3];
-    if (sk != -INFINITY) dt += exp2_hw(sk - M);
+    if (wave == 0) {
+        float dt = sd[grp][0] + sd[grp][1] + sd[grp][2] + sd[grp][3];
+        if (sk != -INFINITY) dt += exp2_hw(sk - M);
 #pragma unroll
-    for (int d = 0; d < DL; d++) {
-        const int dd = DL * lane + d;
-        const float ov = so[0][dd] + so[1][dd] + so[2][dd] + so[3][dd];
-        float r = dt > 0.0f ? ov / dt : 0.0f;
-        if (qg) r *= sigmoid_f(qg[(uint64_t)t * nh * 2 * HD + h * 2 * HD + HD + dd]);
-        out[(uint64_t)t * nh * HD + h * HD + dd] = r;
+        for (int d = 0; d < DL; d++) {
+            const int dd = DL * lane + d;
+            const float ov = so[grp][0][dd] + so[grp][1][dd] + so[grp][2][dd] + so[grp][3][dd];
+            float r = dt > 0.0f ? ov / dt : 0.0f;
+            if (qg) r *= sigmoid_f(qg[(uint64_t)t * nh * 2 * HD + h * 2 * HD + HD + dd]);
+            out[(uint64_t)t * nh * HD + h * HD + dd] = r;
+            ob[grp * HD + dd] = r;
+        }
+    }
+    if constexpr (HPB * HD == 256) {
+        if (xq) {
+            __syncthreads();
+            if (threadIdx.x < 32) {
+                const int i = 8 * threadIdx.x, n = nh * HD, nt = gridDim.y;
+                const float4 v0 = *(const float4*)&ob[i], v1 = *(const float4*)&ob[i + 4];
+                const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                const uint64_t c0 = (uint64_t)blockIdx.x * 256;
+                quant8_group(v, i, true, mode, xq + (uint64_t)t * n + c0,
+                             (float*)(xq + (uint64_t)nt * n) + ((uint64_t)t * n + c0) / 32);
+            }
+        }
     }
 }
 
@@ -475,8 +497,9 @@ static void decode_t(const float* q, const uint16_t* kc, const uint16_t* vc, flo
 
 hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
                               float* part, const int* step, int nh, int nkv, int hd, float scale, int nt,
-                              const float* sink, int win, hipStream_t s, const NormRope* nr0) {
+                              const float* sink, int win, hipStream_t s, const NormRope* nr0, int8_t* xq, int mode) {
     if (nt <= 0) return hipSuccess;
+    if (xq && (nh * hd) % 256) return hipErrorNotSupported;
     const int G = nh / nkv;
     NormRope nrf;
     const NormRope* nr = nullptr;
@@ -495,8 +518,14 @@ hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t
     DEC(128, 1) DEC(128, 2) DEC(128, 4) DEC(128, 8) DEC(64, 1) DEC(64, 2) DEC(64, 4) DEC(64, 8)
     return hipErrorInvalidValue;
 #undef DEC
-    if (hd == 128) attn_merge_kernel<128><<<dim3((unsigned)nh, (unsigned)nt), dim3(256), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink, step, win);
-    else attn_merge_kernel<64><<<dim3((unsigned)nh, (unsigned)nt), dim3(256), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink, step, win);
+    if (xq && hd == 128)
+        attn_merge_kernel<128, 2><<<dim3((unsigned)(nh / 2), (unsigned)nt), dim3(512), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink, step, win, xq, mode);
+    else if (xq)
+        attn_merge_kernel<64, 4><<<dim3((unsigned)(nh / 4), (unsigned)nt), dim3(1024), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink, step, win, xq, mode);
+    else if (hd == 128)
+        attn_merge_kernel<128, 1><<<dim3((unsigned)nh, (unsigned)nt), dim3(256), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink, step, win, nullptr, mode);
+    else
+        attn_merge_kernel<64, 1><<<dim3((unsigned)nh, (unsigned)nt), dim3(256), 0, s>>>(part, qg, out, nh, ATT_SPLITS, sink, step, win, nullptr, mode);
     return hipGetLastError();
 }
 

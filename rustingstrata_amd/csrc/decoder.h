@@ -64,10 +64,12 @@ hipError_t launch_fill_blocks(int ty, uint8_t* w, uint64_t n_blocks, uint64_t se
 // Attention (attn.hip). Caches: f16 rows of nkv * hd values per position.
 constexpr int ATT_SPLITS = 128;  // position splits of a decode token (part rows per head)
 // With nr (one token): the query heads are nr's raw q rows (q unused) and rms_norm_rope_qk with the KV store of nr
-// runs inside the launch (the same bits as launch_norm_rope first); hipErrorNotSupported for shapes it does not take.
+// runs inside the launch (the same bits as launch_norm_rope first). With xq: out also quantized as quant_xq does
+// under numerics `mode` (nh hd a multiple of 256). hipErrorNotSupported for shapes it does not take.
 hipError_t launch_attn_decode(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
                               float* part, const int* step, int nh, int nkv, int hd, float scale, int nt,
-                              const float* sink, int win, hipStream_t s, const NormRope* nr = nullptr);
+                              const float* sink, int win, hipStream_t s, const NormRope* nr = nullptr,
+                              int8_t* xq = nullptr, int mode = 0);
 hipError_t launch_attn_prefill(const float* q, const uint16_t* kc, const uint16_t* vc, const float* qg, float* out,
                                const int* step, int t, int nh, int nkv, int hd, float scale, const float* sink, int win,
                                hipStream_t s);

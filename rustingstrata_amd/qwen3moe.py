@@ -178,6 +178,7 @@ class Model:
         self.dqkv = A((nh * hd + 2 * kv) * 4)
         self.dq, self.dk, self.dv = int(self.dqkv), int(self.dqkv) + 4 * nh * hd, int(self.dqkv) + 4 * (nh * hd + kv)
         self.dqo, self.dko = A(nh * hd * 4), A(kv * 4)
+        self.aq = A(nh * hd + nh * hd // 8)  # the attention output quantized (quant_xq layout) for the o GEMV
         self.datt = A(nh * hd * 4)
         self.part = A(hip.attn_part_floats(nh, hd) * 4)
         self.dl = A(E * 4)
@@ -269,8 +270,8 @@ class Model:
             # the KV store, then attn_decode)
             hip.rms_norm_rope_attn_decode(self.dq, hd, ly.q_norm, self.dk, ly.k_norm, self.dv, c.eps, hd, c.rope_base,
                                           ly.kc, ly.vc, 0, self.datt, self.part, self.step, nh, nkv, hd,
-                                          float(1.0 / np.sqrt(hd)))
-            hip.gemv(ly.o, self.datt, self.mix)
+                                          float(1.0 / np.sqrt(hd)), xq=self.aq)
+            hip.gemvq(ly.o, self.datt, nh * hd, self.aq, self.mix, H, 1)  # x quantized by the attention's merge
             # h, hq = rms_norm_q(x + mix) and the router logits in one launch (x += mix is left to the next
             # combine_rms_norm_q, which adds mix before the combine: the same bits)
             hip.rms_norm_q_gemv_f32(x, self.mix, ly.ffn_norm, self.h, self.hq, H, c.eps, ly.router, self.dl)

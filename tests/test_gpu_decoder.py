@@ -179,8 +179,13 @@ def test_rms_norm_rope_attn_decode_equals_unfused(hip, nh, nkv, hd, pos, n_rot, 
     scale, eps, base = 1.0 / np.sqrt(hd), 1e-6, 1e6
     hip.rms_norm_rope_qk(q, hd, qwb, qo, nh, nh, k, kwb, ko, nkv, nkv, hd, eps, n_rot, step, base, v, kc1, vc1)
     hip.attn_decode(qo, kc1, vc1, qg, o1, part, step, nh, nkv, hd, scale, 1, sink=sink, win=win)
+    aq = hip.alloc(nh * hd + nh * hd // 8)
     hip.rms_norm_rope_attn_decode(q, hd, qwb, k, kwb, v, eps, n_rot, base, kc2, vc2, qg, o2, part, step, nh, nkv, hd,
-                                  scale, sink=sink, win=win)
+                                  scale, sink=sink, win=win, xq=aq)
+    # the output quantized by the merge: quant_xq's bits
+    aq2 = hip.alloc(nh * hd + nh * hd // 8)
+    hip.quant_xq(o2, nh * hd, nh * hd, 1, aq2)
+    assert np.array_equal(hip.get(aq, np.uint8, nh * hd + nh * hd // 8), hip.get(aq2, np.uint8, nh * hd + nh * hd // 8))
     m = P * nkv * hd
     assert np.array_equal(hip.get(kc1, np.uint16, m), hip.get(kc2, np.uint16, m))
     assert np.array_equal(hip.get(vc1, np.uint16, m), hip.get(vc2, np.uint16, m))
