@@ -290,6 +290,13 @@ int strata_rms_norm_rope_kv(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint
 int strata_rms_norm_rope_qk(strata_ctx* ctx, uint64_t q, uint64_t q_stride, uint64_t qw, uint64_t qo, uint64_t qrows,
                             uint64_t qper, uint64_t k, uint64_t kw, uint64_t ko, uint64_t krows, uint64_t kper, uint64_t n,
                             float eps, uint64_t n_rot, uint64_t step, float base, uint64_t v, uint64_t kc, uint64_t vc);
+/* strata_rms_norm_rope_qk reading the heads from a fused q/k/v output (the prefill's one GEMM over a layer's q, k and
+ * v rows): token t's query head h at q + t q_tstride + h q_stride, key head g at k + t k_tstride + g n, value row at
+ * v + t v_tstride + g n (floats). Outputs (qo, ko) and the KV store as strata_rms_norm_rope_qk, the same bits. */
+int strata_rms_norm_rope_qk_t(strata_ctx* ctx, uint64_t q, uint64_t q_tstride, uint64_t q_stride, uint64_t qw,
+                              uint64_t qo, uint64_t qrows, uint64_t qper, uint64_t k, uint64_t k_tstride, uint64_t kw,
+                              uint64_t ko, uint64_t krows, uint64_t kper, uint64_t n, float eps, uint64_t n_rot,
+                              uint64_t step, float base, uint64_t v, uint64_t v_tstride, uint64_t kc, uint64_t vc);
 /* Backend::kv_store (src/backend.rs:380; kernel src/cuda/kernels.cu:2181-2186): t tokens of n values (k and v
  * rows) into the f16 caches at positions step[0] ... */
 int strata_kv_store(strata_ctx* ctx, uint64_t k, uint64_t v, uint64_t kc, uint64_t vc, uint64_t n, uint64_t t,

@@ -62,6 +62,8 @@ SIGNATURES = {
     "strata_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
     "strata_rms_norm_rope_attn_decode": [CTX, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, ctypes.c_float, U64,
                                          U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64, U64],
+    "strata_rms_norm_rope_qk_t": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64,
+                                  ctypes.c_float, U64, U64, ctypes.c_float, U64, U64, U64, U64],
     "strata_combine_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
     "strata_rms_norm_q_gemv_f32": [CTX, U64, U64, U64, U64, U64, U64, ctypes.c_float, TP, U64],
     "strata_gemv": [CTX, TP, U64, U64],
@@ -445,6 +447,13 @@ class HipBackend:
         _check(lib().strata_rms_norm_rope_attn_decode(self._ctx, int(q), q_stride, int(qw), int(k), int(kw), int(v), eps,
                                                       n_rot, base, int(kc), int(vc), int(qg), int(out), int(part),
                                                       int(step), nh, nkv, hd, scale, int(sink), win, int(xq)))
+
+    def rms_norm_rope_qk_t(self, q, q_tstride, q_stride, qw, qo, qrows, qper, k, k_tstride, kw, ko, krows, kper, n,
+                           eps, n_rot, step, base, v, v_tstride, kc, vc):
+        """rms_norm_rope_qk over heads read at token strides (a fused q/k/v output)."""
+        _check(lib().strata_rms_norm_rope_qk_t(self._ctx, int(q), q_tstride, q_stride, int(qw), int(qo), qrows, qper,
+                                               int(k), k_tstride, int(kw), int(ko), krows, kper, n, eps, n_rot,
+                                               int(step), base, int(v), v_tstride, int(kc), int(vc)))
 
     def kv_store(self, k, v, kc, vc, n, t, step, hd):
         _check(lib().strata_kv_store(self._ctx, int(k), int(v), int(kc), int(vc), n, t, int(step), hd))

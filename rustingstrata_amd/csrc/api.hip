@@ -844,6 +844,28 @@ int strata_rope_neox(strata_ctx* c, uint64_t x, uint64_t stride, uint64_t heads,
     return strata_rope_pairs(c, x, stride, heads, per, n_rot, step, base, 0, n_rot / 2);
 }
 
+int strata_rms_norm_rope_qk_t(strata_ctx* c, uint64_t q, uint64_t q_tstride, uint64_t q_stride, uint64_t qw, uint64_t qo,
+                              uint64_t qrows, uint64_t qper, uint64_t k, uint64_t k_tstride, uint64_t kw, uint64_t ko,
+                              uint64_t krows, uint64_t kper, uint64_t n, float eps, uint64_t n_rot, uint64_t step,
+                              float base, uint64_t v, uint64_t v_tstride, uint64_t kc, uint64_t vc) {
+    if (check_ctx(c) || check_rope(n, n_rot)) return -1;
+    if ((qrows && (!qper || qrows % qper)) || (krows && (!kper || krows % kper)))
+        return set_error("rms_norm_rope: rows must be whole tokens of heads");
+    if (kc && (!v || !vc)) return set_error("rms_norm_rope_kv: null v or value cache");
+    if (qrows + krows >= (1u << 31)) return set_error("rms_norm_rope: too many rows");
+    if ((qrows && q_tstride < qper * q_stride) || (krows && k_tstride < kper * n) || (kc && v_tstride < kper * n))
+        return set_error("rms_norm_rope: a token stride shorter than its heads");
+    NormRope a;
+    a.x = (const float*)k; a.x_stride = n; a.x_tstride = k_tstride; a.w = (const float*)kw; a.out = (float*)ko;
+    a.n = (int)n; a.rows = (int)krows; a.per = (int)(kper ? kper : 1);
+    a.v = (const float*)v; a.v_tstride = v_tstride; a.kc = (uint16_t*)kc; a.vc = (uint16_t*)vc;
+    a.qrows = (int)qrows; a.qx = (const float*)q; a.q_stride = q_stride; a.q_tstride = q_tstride; a.qw = (const float*)qw;
+    a.qo = (float*)qo; a.qper = (int)(qper ? qper : 1);
+    a.eps = eps; a.base = base; a.n_rot = (int)n_rot; a.step = (const int*)step;
+    STRATA_HIP(launch_norm_rope(a, c->stream));
+    return 0;
+}
+
 int strata_rms_norm_rope_qk(strata_ctx* c, uint64_t q, uint64_t q_stride, uint64_t qw, uint64_t qo, uint64_t qrows,
                             uint64_t qper, uint64_t k, uint64_t kw, uint64_t ko, uint64_t krows, uint64_t kper, uint64_t n,
                             float eps, uint64_t n_rot, uint64_t step, float base, uint64_t v, uint64_t kc, uint64_t vc) {

@@ -8,7 +8,8 @@ namespace strata {
 // rms_norm_rope over `rows` heads of n: head b (token b / per, position step[0] + b / per) from x + b x_stride into
 // out + b n, normed with w then NEOX-roped on its first n_rot values; with
 // kc, also stored with its v row (v + b n) into the f16 caches at row (position per + b % per). q rows first: the
-// first qrows heads come from qx (q_stride, qw, qo, qper) and are never stored.
+// first qrows heads come from qx (q_stride, qw, qo, qper) and are never stored. With token strides (below) head b
+// is read at token b / per times the token stride plus head b % per times the head stride (a fused q/k/v output).
 struct NormRope {
     const float* x = nullptr; uint64_t x_stride = 0; const float* w = nullptr; float* out = nullptr;
     int n = 0, rows = 0, per = 1;
@@ -16,6 +17,9 @@ struct NormRope {
     int qrows = 0; const float* qx = nullptr; uint64_t q_stride = 0; const float* qw = nullptr; float* qo = nullptr;
     int qper = 1;
     float eps = 0, base = 0; int n_rot = 0; const int* step = nullptr;
+    // floats between consecutive tokens' first heads of q, x (keys) and v; 0: the heads of all tokens back to back
+    // (qper q_stride, per x_stride, per n)
+    uint64_t q_tstride = 0, x_tstride = 0, v_tstride = 0;
     // base^(-2 i / n_rot) for the first nfreq pairs (filled by launch_norm_rope on the host)
     static constexpr int NFREQ = 128;
     int nfreq = 0; double freq[NFREQ] = {};

@@ -40,12 +40,13 @@ __device__ __forceinline__ NrHead nr_head(const NormRope& a, int gb) {
     NrHead h;
     if (gb < a.qrows) {
         h.b = gb; h.per = a.qper;
-        h.xr = a.qx + (uint64_t)gb * a.q_stride; h.w = a.qw; h.o = a.qo + (uint64_t)gb * a.n; h.vr = nullptr;
+        h.xr = a.qx + (uint64_t)(gb / a.qper) * a.q_tstride + (uint64_t)(gb % a.qper) * a.q_stride;
+        h.w = a.qw; h.o = a.qo + (uint64_t)gb * a.n; h.vr = nullptr;
     } else {
-        const int b = gb - a.qrows;
+        const int b = gb - a.qrows, tk = b / a.per, hh = b - tk * a.per;
         h.b = b; h.per = a.per;
-        h.xr = a.x + (uint64_t)b * a.x_stride; h.w = a.w; h.o = a.out + (uint64_t)b * a.n;
-        h.vr = a.kc ? a.v + (uint64_t)b * a.n : nullptr;
+        h.xr = a.x + (uint64_t)tk * a.x_tstride + (uint64_t)hh * a.x_stride; h.w = a.w; h.o = a.out + (uint64_t)b * a.n;
+        h.vr = a.kc ? a.v + (uint64_t)tk * a.v_tstride + (uint64_t)hh * a.n : nullptr;
     }
     return h;
 }
@@ -237,9 +238,13 @@ hipError_t launch_norm_rope(const NormRope& a0, hipStream_t s) {
     // the rope frequencies depend only on the pair index: the host's pow (the one the CPU reference calls) fills
     // them once per launch, so the kernel's f64 work is the sine and cosine
     NormRope a = a0;
+    if (!a.q_tstride) a.q_tstride = (uint64_t)a.qper * a.q_stride;
+    if (!a.x_tstride) a.x_tstride = (uint64_t)a.per * a.x_stride;
+    if (!a.v_tstride) a.v_tstride = (uint64_t)a.per * a.n;
     a.nfreq = a.n_rot / 2 <= NormRope::NFREQ ? a.n_rot / 2 : 0;
     for (int i = 0; i < a.nfreq; i++) a.freq[i] = std::pow((double)a.base, -2.0 * (double)i / (double)a.n_rot);
-    const bool vec = ((uintptr_t)a.qx | (uintptr_t)a.x) % 16 == 0 && a.q_stride % 4 == 0 && a.x_stride % 4 == 0;
+    const bool vec = ((uintptr_t)a.qx | (uintptr_t)a.x | (uintptr_t)a.v) % 16 == 0 && a.q_stride % 4 == 0 &&
+                     a.x_stride % 4 == 0 && a.q_tstride % 4 == 0 && a.x_tstride % 4 == 0 && a.v_tstride % 4 == 0;
     if (total >= 4 * NR_MANY && vec && a.n == 128 && a.n_rot == 128)  // the many-heads form: 16-byte chunks, heads of 128
         norm_rope_many_kernel<<<dim3((unsigned)((total + NR_MANY - 1) / NR_MANY)), dim3(64 * NR_WAVES), 0, s>>>(a);
     else

@@ -10,8 +10,9 @@ takes host arrays (tests build small models with them and check the device stack
 
 Per prefill chunk of t tokens at position pos (step[0] = pos):
     x = embed(tokens)
-    per layer: h = rms_norm(x) ; q, k, v = gemm_dense(h) (k and v reuse q's int8 X) ; rms_norm_rope_qk (q/k norms,
-    NEOX rope, f16 KV store) ; attn_prefill (causal) ; x += gemm_dense(o, attn) ; h = rms_norm(x) ;
+    per layer: h = rms_norm(x) ; q, k, v = gemm_dense(qkv, h) (one GEMM over the layer's q/k/v rows) ;
+    rms_norm_rope_qk (q/k norms, NEOX rope, f16 KV store, reading the heads in place) ; attn_prefill (causal) ;
+    x += gemm_dense(o, attn) ; h = rms_norm(x) ;
     logits = gemm_dense(router F32, h) ; router_topk ; moe_sort (on the device) ; gate/up grouped GEMM with the
     SwiGLU epilogue ; down grouped GEMM ; x += moe_combine_seq.
 Per decode token (recorded once as a graph and replayed; the step buffer carries the position):
@@ -24,7 +25,7 @@ Per decode token (recorded once as a graph and replayed; the step buffer carries
 import numpy as np
 
 from . import ggml
-from .backend import ACT_ADD, ACT_STORE, SAME_X, GpuTensor, StrataError
+from .backend import ACT_ADD, ACT_STORE, GpuTensor, StrataError
 
 
 class Config:
@@ -159,9 +160,9 @@ class Model:
         # prefill buffers (rows of the chunk)
         self.x = A(n * H * 4)
         self.h = A(n * H * 4)
-        self.qa = A(n * nh * hd * 4)
+        self.qkvp = A(n * (nh * hd + 2 * kv) * 4)  # the chunk's q, k and v rows from one GEMM
         self.qb = A(n * nh * hd * 4)
-        self.kraw, self.kk, self.vv = A(n * kv * 4), A(n * kv * 4), A(n * kv * 4)
+        self.kk = A(n * kv * 4)
         self.att = A(n * nh * hd * 4)
         self.rl = A(n * E * 4)
         self.ids, self.wts = A(n * k * 4), A(n * k * 4)
@@ -215,11 +216,12 @@ class Model:
             layer_hook(-1, self.x)
         for il, ly in enumerate(w.layers):
             hip.rms_norm(self.x, H, ly.attn_norm, self.h, H, H, t, c.eps)
-            hip.gemm_dense(ly.q, t, self.h, H, self.qa, nh * hd, ACT_STORE)
-            hip.gemm_dense(ly.k, t, self.h, H, self.kraw, kv, ACT_STORE | SAME_X)
-            hip.gemm_dense(ly.v, t, self.h, H, self.vv, kv, ACT_STORE | SAME_X)
-            hip.rms_norm_rope_qk(self.qa, hd, ly.q_norm, self.qb, t * nh, nh, self.kraw, ly.k_norm, self.kk, t * nkv,
-                                 nkv, hd, c.eps, hd, self.step, c.rope_base, self.vv, ly.kc, ly.vc)
+            # q, k and v as one GEMM over the layer's q/k/v rows; the norms, rope and KV store read its heads in place
+            qkv_n = nh * hd + 2 * kv
+            hip.gemm_dense(ly.qkv, t, self.h, H, self.qkvp, qkv_n, ACT_STORE)
+            hip.rms_norm_rope_qk_t(self.qkvp, qkv_n, hd, ly.q_norm, self.qb, t * nh, nh, int(self.qkvp) + 4 * nh * hd,
+                                   qkv_n, ly.k_norm, self.kk, t * nkv, nkv, hd, c.eps, hd, self.step, c.rope_base,
+                                   int(self.qkvp) + 4 * (nh * hd + kv), qkv_n, ly.kc, ly.vc)
             hip.attn_prefill(self.qb, ly.kc, ly.vc, 0, self.att, self.step, t, nh, nkv, hd, scale)
             hip.gemm_dense(ly.o, t, self.att, nh * hd, self.x, H, ACT_ADD)
             hip.rms_norm(self.x, H, ly.ffn_norm, self.h, H, H, t, c.eps)

@@ -63,7 +63,8 @@ def test_rope_neox_and_pairs(hip):
 def test_rms_norm_rope_qk_and_kv_store(hip, T):
     """rms_norm_rope_qk (src/backend.rs:274-277): q heads normed and roped; k heads normed, roped and stored with
     their v rows as f16 at cache row position * nkv + head. T = 3 runs the wave-per-head kernel, T = 12 (432 heads,
-    a partial last block) the lane-per-head sums of the many-heads kernel."""
+    a partial last block) the lane-per-head sums of the many-heads kernel; both also reading the heads in place from
+    fused q/k/v rows (rms_norm_rope_qk_t)."""
     nh, nkv, hd, pos0, eps = 32, 4, 128, 17, 1e-6
     q = normal((T, nh * hd), seed=3)
     k = normal((T, nkv * hd), seed=4)
@@ -89,6 +90,21 @@ def test_rms_norm_rope_qk_and_kv_store(hip, T):
     assert np.array_equal(kcache[pos0:pos0 + T].reshape(-1), got_k.astype(np.float16).view(np.uint16).reshape(-1))
     assert np.array_equal(vcache[pos0:pos0 + T], v.astype(np.float16).view(np.uint16))
     assert not kcache[:pos0].any() and not kcache[pos0 + T:].any()
+    # the same heads read in place from one fused q/k/v row per token (rms_norm_rope_qk_t): the same bits
+    W = nh * hd + 2 * nkv * hd
+    qkv = up(hip, np.concatenate([q, k, v], axis=1))
+    kc3, vc3 = hip.alloc(P * nkv * hd * 2), hip.alloc(P * nkv * hd * 2)
+    qo3, ko3 = hip.alloc(T * nh * hd * 4), hip.alloc(T * nkv * hd * 4)
+    hip.rms_norm_rope_qk_t(qkv, W, hd, up(hip, qw), qo3, T * nh, nh, int(qkv) + 4 * nh * hd, W, up(hip, kw), ko3,
+                           T * nkv, nkv, hd, eps, hd, i32(hip, [pos0, 0]), 1e6, int(qkv) + 4 * (nh + nkv) * hd, W,
+                           kc3, vc3)
+    assert np.array_equal(hip.get(qo3, np.uint32, T * nh * hd), got_q.reshape(-1).view(np.uint32))
+    assert np.array_equal(hip.get(ko3, np.uint32, T * nkv * hd), got_k.reshape(-1).view(np.uint32))
+    assert np.array_equal(hip.get(kc3, np.uint16, P * nkv * hd), kcache.reshape(-1))
+    assert np.array_equal(hip.get(vc3, np.uint16, P * nkv * hd), vcache.reshape(-1))
+    with pytest.raises(S.StrataError, match="token stride"):
+        hip.rms_norm_rope_qk_t(qkv, 8, hd, up(hip, qw), qo3, T * nh, nh, int(qkv), W, up(hip, kw), ko3, T * nkv, nkv,
+                               hd, eps, hd, i32(hip, [pos0, 0]), 1e6, int(qkv), W, kc3, vc3)
     # kv_store of the same rows at another position: the same f16 bits
     kc2, vc2 = hip.alloc(P * nkv * hd * 2), hip.alloc(P * nkv * hd * 2)
     hip.kv_store(ko, up(hip, v), kc2, vc2, nkv * hd, T, i32(hip, [5, 0]), hd)
