@@ -476,7 +476,7 @@ hipError_t launch_gemv_f32(const float* w, int rows, int cols, const float* x, u
 // block of 4 waves takes 64 positions (a lane each) x 8 weight rows (2 a wave, 2 chains a lane); per step of 64 k the
 // block stages x transposed ([k][position]: a lane's reads hit distinct banks) and the 8 rows' weights in LDS, and a
 // lane reads its x value once per k and the weights as wave-wide broadcasts (one 16-byte read for 4 k of a row). ----
-constexpr int GF_M = 64, GF_RW = 2, GF_R = 4 * GF_RW, GF_K = 64;  // GF_RW rows (chains) a wave
+constexpr int GF_M = 64, GF_RW = 4, GF_R = 4 * GF_RW, GF_K = 64;  // GF_RW rows (chains) a wave (4: 102 -> 87 us at 4096 x 128 x 2048)
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ w, int rows, int cols,
                                                        const float* __restrict__ x, uint64_t x_stride, float* y,
                                                        uint64_t y_stride, int n, int act) {
