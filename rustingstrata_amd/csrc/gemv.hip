@@ -773,9 +773,10 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
         a.R = 2 * fill <= rpb ? std::min(fill, rmax) : std::min(rpb, rmax);
     }
     if (single && a.R > rpb) a.R -= a.R % rpb;
-    // x already quantized (no per-block quantization to amortize) and one matrix: tiles of one wave pass (the quarter
-    // split) when they all fit one round of blocks (Q6_K 5120 x 2048: 5.1 -> 4.7 us; 2048 x 4096: 4.9 -> 4.2 us)
-    if (single && g.xq && !g.ids && !g.pair && a.R > 64 / a.G &&
+    // x already quantized (no per-block quantization to amortize), or Q8_0 (whose per-32 float closes make a lane's
+    // dot chain the longest), and one matrix: tiles of one wave pass (the quarter split) when they all fit one round of
+    // blocks (Q6_K 5120 x 2048 from xq: 5.1 -> 4.7 us; 2048 x 4096: 4.9 -> 4.2 us; Q8_0 6144 x 2048: 6.9 -> 5.7 us)
+    if (single && (g.xq || g.ty == Q8_0) && !g.ids && !g.pair && a.R > 64 / a.G &&
         (long long)(maxrows + 64 / a.G - 1) / (64 / a.G) <= 3LL * ncu)
         a.R = std::min(64 / a.G, rmax);
     a.ntr = (maxrows + a.R - 1) / a.R;
