@@ -157,6 +157,23 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
     __shared__ __align__(16) uint16_t knew[NR ? HD : 8], vnew[NR ? HD : 8];
     const int pos_new = step[0];
     const bool last = NR && p1 == n_pos;
+    const int kq = lane & 3, dg = lane >> 2;  // this lane's load keys 4 kq .., dims 8 dg ..
+    const bool loader = dg < NDG;
+    // NR: the chunk's K and V rows (this wave's 16 keys; keys past nc repeat key nc - 1: finite, and their weights are
+    // 0) go into these function-scope registers, the first chunk's requested before the norms and rope, which run
+    // while they are in flight (without NR they are requested in the loop, behind the query's loads)
+    uint4 kbn[NR ? 4 : 1], vbn[NR ? 4 : 1];
+    auto load_n = [&](int c0) __attribute__((always_inline)) {
+        const int nc = min(64, p1 - c0);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const int kp = base + c0 + min(16 * wave + 4 * kq + kk, nc - 1);
+            const uint64_t off = (uint64_t)kp * kvd + g * HD + 8 * min(dg, NDG - 1);
+            kbn[kk & (NR ? 3 : 0)] = *(const uint4*)(kc + off);
+            vbn[kk & (NR ? 3 : 0)] = *(const uint4*)(vc + off);
+        }
+    };
+    if constexpr (NR) load_n(p0);
     if constexpr (NR) {
         // raw heads into LDS: the G query heads, then (last split) the key and value heads of KV head g
         __shared__ __align__(16) float raw[(G + 2) * HD];
@@ -242,8 +259,6 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
             }
         }
     }
-    const int kq = lane & 3, dg = lane >> 2;  // this lane's load keys 4 kq .., dims 8 dg ..
-    const bool loader = dg < NDG;
     // Q^T fragments: head h0 + l16 (zero past G), dims 32 k + 8 lg .. + 7; usc undoes the scaling (times `scale`)
     h8 qh[KS], ql[KS];
     float usc = 0.0f;
@@ -253,21 +268,8 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
     float m = -INFINITY, l = 0.0f;
     for (int c0 = p0; c0 < p1; c0 += 64) {
         const int nc = min(64, p1 - c0);
-        {
-            // this wave's 16 keys of the chunk (keys past nc repeat key nc - 1: finite, and their weights are 0)
-            uint4 kb[4], vb[4];
-#pragma unroll
-            for (int kk = 0; kk < 4; kk++) {
-                const int kp = base + c0 + min(16 * wave + 4 * kq + kk, nc - 1);
-                const uint64_t off = (uint64_t)kp * kvd + g * HD + 8 * min(dg, NDG - 1);
-                if (NR && last && kp == pos_new) {  // the new position: this block's own key and value
-                    kb[kk] = *(const uint4*)&knew[8 * min(dg, NDG - 1)];
-                    vb[kk] = *(const uint4*)&vnew[8 * min(dg, NDG - 1)];
-                } else {
-                    kb[kk] = *(const uint4*)(kc + off);
-                    vb[kk] = *(const uint4*)(vc + off);
-                }
-            }
+        // stage(kb, vb): the query's fragments (first chunk), then the chunk's K rows and V^T into the wave's LDS tiles
+        auto stage = [&](uint4 (&kb)[4], uint4 (&vb)[4]) __attribute__((always_inline)) {
             if (c0 == p0) {
                 // the query's fragments while the first chunk's rows are in flight: scaled by the power of two
                 // that puts its largest value in [2^13, 2^14), so the lo parts stay normal f16 numbers
@@ -303,6 +305,29 @@ __global__ __launch_bounds__(64 * DEC_WAVES) void attn_decode_kernel(const float
                     *(uint2*)&vs[(8 * dg + e) * L::VP + 4 * kq] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
                 }
             }
+        };
+        if constexpr (NR) {
+            if (c0 != p0) load_n(c0);
+            if (last) {
+                // the new position (its cache row may not have landed yet): this block's own key and value
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++)
+                    if (base + c0 + min(16 * wave + 4 * kq + kk, nc - 1) == pos_new) {
+                        kbn[kk & (NR ? 3 : 0)] = *(const uint4*)&knew[8 * min(dg, NDG - 1)];
+                        vbn[kk & (NR ? 3 : 0)] = *(const uint4*)&vnew[8 * min(dg, NDG - 1)];
+                    }
+            }
+            stage(*(uint4(*)[4])kbn, *(uint4(*)[4])vbn);
+        } else {
+            uint4 kb[4], vb[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const int kp = base + c0 + min(16 * wave + 4 * kq + kk, nc - 1);
+                const uint64_t off = (uint64_t)kp * kvd + g * HD + 8 * min(dg, NDG - 1);
+                kb[kk] = *(const uint4*)(kc + off);
+                vb[kk] = *(const uint4*)(vc + off);
+            }
+            stage(kb, vb);
         }
         __builtin_amdgcn_wave_barrier();
         // S^T: lane holds keys 16 wave + 4 lg + i of head l16
