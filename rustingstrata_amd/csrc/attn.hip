@@ -458,11 +458,25 @@ __global__ __launch_bounds__(256 * HPB) void attn_merge_kernel(const float* __re
     const int sl = wave + 4 * lane;
     const float ms = lane < SW && sl < ns ? pp[sl * (HD + 2) + HD] : -INFINITY;
     const float ls = lane < SW && sl < ns ? pp[sl * (HD + 2) + HD + 1] : 0.0f;
+    // (8-byte loads where a lane's dims pair up; splits past ns are not loaded: a wave-uniform bound)
     float a[SW][DL];
 #pragma unroll
-    for (int i = 0; i < SW; i++)
+    for (int i = 0; i < SW; i++) {
+        if (wave + 4 * i < ns) {
+            const float* src = pp + (wave + 4 * i) * (HD + 2) + DL * lane;
+            if constexpr (DL == 2) {
+                const float2 v = *(const float2*)src;
+                a[i][0] = v.x;
+                a[i][1] = v.y;
+            } else {
 #pragma unroll
-        for (int d = 0; d < DL; d++) a[i][d] = pp[min(wave + 4 * i, ns - 1) * (HD + 2) + DL * lane + d];
+                for (int d = 0; d < DL; d++) a[i][d] = src[d];
+            }
+        } else {
+#pragma unroll
+            for (int d = 0; d < DL; d++) a[i][d] = 0.0f;
+        }
+    }
     float M = wave_max64(ms);
     if (lane == 0) sm[grp][wave] = M;
     __syncthreads();
