@@ -965,6 +965,32 @@ def test_moe_route_gemv_equals_two_launches(hip, ty, n, k, F, H, pair, sig):
             assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (tok, int((ya != yb).sum()))
 
 
+def test_moe_route_gemv_division_ties(hip):
+    """moe_route_gemv on tokens whose softmax division ties two experts (the ranking of the unnormalised values names
+    them in the other order, so blocks that requested their first tile from the ranking request it again): ids equal
+    ops::top_k's, and every output equals moe_route then moe_gemv bit for bit."""
+    logits, flips = _division_tie_logits(12, seed=7)
+    assert flips >= 3
+    n, k, F, cols = 128, 8, 256, 512
+    ty = ggml.Q4_K
+    rb = ggml.row_bytes(ty, cols)
+    wb = up(hip, random_blocks(ty, 2 * n * F, cols, seed=77))
+    table = up(hip, np.arange(n, dtype=np.int32))
+    xb = up(hip, normal(cols, seed=78))
+    pr = (n * F * rb, k * F * 4)
+    for row in logits:
+        lb = up(hip, row)
+        a = [hip.alloc(k * 4) for _ in range(4)] + [hip.alloc(2 * k * F * 4)]
+        b = [hip.alloc(k * 4) for _ in range(4)] + [hip.alloc(2 * k * F * 4)]
+        hip.moe_route(lb, n, k, 0.0, table, a[0], a[1], a[2], a[3], 1)
+        hip.moe_gemv(ty, F, cols, wb, F * rb, a[2], k, xb, cols, k, a[4], pair=pr)
+        hip.moe_route_gemv(lb, n, k, 0.0, table, b[0], b[1], b[2], b[3], ty, F, cols, wb, F * rb, xb, b[4], pair=pr)
+        wi, _ = O.route(row[None, :], k)
+        assert np.array_equal(down(hip, b[0], np.int32, k), wi.reshape(-1))
+        for x, y, m in zip(a, b, (k, k, k, k, 2 * k * F)):
+            assert np.array_equal(down(hip, x, np.uint32, m), down(hip, y, np.uint32, m))
+
+
 def test_errors_do_not_launch(hip):
     t = S.GpuTensor(ggml.Q4_K, 4, 300, hip.alloc(4 * 2048))
     with pytest.raises(S.StrataError, match="GEMV needs a multiple of 256"):
