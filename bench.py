@@ -325,6 +325,50 @@ def bench_moe_decode(hip, S, ggml, iters):
             "GB/s": round(bts / us / 1e3, 1), "pct_peak": round(100 * bts / us / 1e3 / HBM_PEAK_GBS, 1)}
 
 
+def bench_attn_decode(hip, S, positions=(255, 1023, 4099), layers=48):
+    """configs[4]'s decode attention alone (32 query heads over 4 KV heads of 128, f16 caches): attn_decode + its
+    split merge over `layers` caches in turn (past the Infinity Cache at 4K), replayed from a recorded graph; the
+    K/V bytes a call reads and the time per call at each position."""
+    nh, nkv, hd = 32, 4, 128
+    out = {}
+    for pos in positions:
+        rng = np.random.default_rng(pos)
+        kv = (rng.standard_normal((pos + 1) * nkv * hd) * 0.5).astype(np.float16)
+        caches = [(hip.upload(kv), hip.upload(kv)) for _ in range(layers)]
+        q = hip.upload(rng.standard_normal(nh * hd).astype(np.float32))
+        o = hip.alloc(nh * hd * 4)
+        part = hip.alloc(hip.attn_part_floats(nh, hd) * 4)
+        step = hip.upload(np.array([pos, 0], dtype=np.int32))
+        sc = float(1 / np.sqrt(hd))
+
+        def run():
+            for kc, vc in caches:
+                hip.attn_decode(q, kc, vc, 0, o, part, step, nh, nkv, hd, sc, 1)
+
+        run()
+        hip.sync()
+        e0, e1 = hip.event(), hip.event()
+        if USE_GRAPHS:
+            hip.graph(("attn", pos), run)
+            hip.graph(("attn", pos), None)
+            hip.sync()
+            hip.record(e0)
+            for _ in range(20):
+                hip.graph(("attn", pos), None)
+            hip.record(e1)
+            hip.drop_graphs()
+        else:
+            hip.record(e0)
+            for _ in range(20):
+                run()
+            hip.record(e1)
+        us = 1000 * hip.elapsed_ms(e0, e1) / (20 * layers)
+        nbytes = 2 * (pos + 1) * nkv * hd * 2
+        out[f"positions {pos + 1}"] = {"us": round(us, 2), "kv_bytes": nbytes, "GB/s": round(nbytes / us / 1e3, 1)}
+        del caches
+    return out
+
+
 def codebook_blocks(ggml, ty, rows, cols, seed):
     """configs[3] weights: grid indices, sign bits and sub-block scales uniform from a seed (random block bytes), with
     each block's f16 d set to 2^-6 so every value is finite."""
@@ -602,6 +646,8 @@ def main():
                     help="only run the Q4_K lm-head GEMV and a 256 MB copy kernel 50 times each (for rocprofv3)")
     ap.add_argument("--profile-moe", action="store_true",
                     help="only run the configs[2] 4K-token MoE prefill layer (--moe-iters times, for rocprofv3)")
+    ap.add_argument("--profile-attn", action="store_true",
+                    help="only configs[4]'s decode attention (+ merge) at 256, 1024 and 4100 positions")
     ap.add_argument("--profile-decode", action="store_true",
                     help="only run the configs[2] 1-token MoE decode layer 200 times, eagerly (for rocprofv3)")
     ap.add_argument("--eager", action="store_true", help="launch every op from the host (no recorded graphs)")
@@ -622,6 +668,9 @@ def main():
     log(f"[bench] {hip.device()}")
     if args.profile_gemv:
         profile_gemv(hip, S, ggml)
+        return
+    if args.profile_attn:
+        print(json.dumps({"attn_decode": bench_attn_decode(hip, S)}), flush=True)
         return
     if args.profile_decode:  # eager tokens, then (unless --eager) the same tokens as graph replays
         print(json.dumps({"moe_decode_1": bench_moe_decode(hip, S, ggml, 200)}), flush=True)
