@@ -17,7 +17,7 @@ from . import ggml
 
 LIB_PATH = os.environ.get("STRATA_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libstrata_hip.so")
 NUM_Q8K, NUM_Q8_32 = 0, 1
-ACT_STORE, ACT_SWIGLU, ACT_ADD, SAME_X = 0, 1, 2, 4
+ACT_STORE, ACT_SWIGLU, ACT_ADD, SAME_X, X_Q = 0, 1, 2, 4, 8
 GEMM_BM = 128  # positions per tile (src/backend.rs:16)
 F32_TYPE = 0   # GGUF type id of float32 matrices (gemv / gemm_dense accept them)
 

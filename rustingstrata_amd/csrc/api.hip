@@ -736,16 +736,17 @@ static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint
     if (check_ctx(c) || check_type(ty)) return -1;
     if (cols == 0 || cols % 256)
         return set_error(std::string(type_name(ty)) + " matrix with " + std::to_string(cols) + " columns: GEMM needs a multiple of 256");
-    int op = act & ~STRATA_SAME_X;
+    int op = act & ~(STRATA_SAME_X | STRATA_X_Q);
     if (op < 0 || op > 2) return set_error("gemm: act " + std::to_string(act));
+    if ((act & STRATA_X_Q) && x_stride != cols) return set_error("gemm: a quantized X (STRATA_X_Q) has rows of cols values");
     if (dense_w && check_align(ty, (uint64_t)dense_w, "gemm_dense")) return -1;
     if (n_tiles == 0 || rows == 0) return 0;
     if (rows > (1u << 24) || row_bytes(ty, cols) >= (1u << 24) || n_tiles > 65535 * 64) return set_error("gemm: too large");
     if (ty == Q8_0 && n_tiles > 65535) return set_error("gemm: Q8_0 with more than 65535 tiles");
     // the kernel addresses X and a weight matrix with 32-bit byte offsets
     if (n_x * cols >= (1ull << 32) || rows * row_bytes(ty, cols) >= (1ull << 32)) return set_error("gemm: X or W of 4 GiB or more");
-    uint64_t xq = 0;
-    if (gemm_x(c, cols, n_x, x, x_stride, act & STRATA_SAME_X, &xq)) return -1;
+    uint64_t xq = x;  // STRATA_X_Q: X quantized by the caller
+    if (!(act & STRATA_X_Q) && gemm_x(c, cols, n_x, x, x_stride, act & STRATA_SAME_X, &xq)) return -1;
     GemmLaunch g;
     g.ty = ty; g.rows = (int)rows; g.cols = (int)cols;
     g.tiles = (const uint64_t*)tiles; g.n_tiles = (int)n_tiles; g.n_tiles_dev = n_tiles_dev;
@@ -780,7 +781,7 @@ int strata_gemm_grouped_gate_up(strata_ctx* c, int ty, uint64_t rows, uint64_t c
     if (rows % 64) return set_error("gemm_grouped_gate_up: " + std::to_string(rows) + " rows (a multiple of 64)");
     if (y % 16 || y_stride % 4) return set_error("gemm_grouped_gate_up: y rows must be 16-byte aligned");
     if (check_align(ty, (uint64_t)up_offset, "gemm_grouped_gate_up up offset")) return -1;
-    if (flags & ~STRATA_SAME_X) return set_error("gemm_grouped_gate_up: flags " + std::to_string(flags));
+    if (flags & ~(STRATA_SAME_X | STRATA_X_Q)) return set_error("gemm_grouped_gate_up: flags " + std::to_string(flags));
     return gemm_common(c, ty, rows, cols, tiles, max_tiles, (const int*)n_tiles_dev, x, x_stride, n_x, xrow, y, y_stride,
                        flags, nullptr, 0, true, up_offset);
 }

@@ -25,7 +25,7 @@ Per decode token (recorded once as a graph and replayed; the step buffer carries
 import numpy as np
 
 from . import ggml
-from .backend import ACT_ADD, ACT_STORE, GpuTensor, StrataError
+from .backend import ACT_ADD, ACT_STORE, NUM_Q8K, X_Q, GpuTensor, StrataError
 
 
 class Config:
@@ -161,6 +161,7 @@ class Model:
         self.x = A(n * H * 4)
         self.h = A(n * H * 4)
         self.qkvp = A(n * (nh * hd + 2 * kv) * 4)  # the chunk's q, k and v rows from one GEMM
+        self.hqp = A(n * (H + H // 8))  # h quantized by the norms (quant_xq layout), the GEMMs' X
         self.qb = A(n * nh * hd * 4)
         self.kk = A(n * kv * 4)
         self.att = A(n * nh * hd * 4)
@@ -215,23 +216,29 @@ class Model:
         if layer_hook:
             layer_hook(-1, self.x)
         for il, ly in enumerate(w.layers):
-            hip.rms_norm(self.x, H, ly.attn_norm, self.h, H, H, t, c.eps)
+            # h quantized by the norm itself (X_Q: the GEMM takes it as is; the GEMM's X is always Q8_K numerics)
+            xq_ok = hip.numerics() == NUM_Q8K
+            hip.rms_norm_q(self.x, H, ly.attn_norm, self.h, H, H, t, c.eps, xq=self.hqp if xq_ok else 0)
             # q, k and v as one GEMM over the layer's q/k/v rows; the norms, rope and KV store read its heads in place
             qkv_n = nh * hd + 2 * kv
-            hip.gemm_dense(ly.qkv, t, self.h, H, self.qkvp, qkv_n, ACT_STORE)
+            if xq_ok:
+                hip.gemm_dense(ly.qkv, t, self.hqp, H, self.qkvp, qkv_n, ACT_STORE | X_Q)
+            else:
+                hip.gemm_dense(ly.qkv, t, self.h, H, self.qkvp, qkv_n, ACT_STORE)
             hip.rms_norm_rope_qk_t(self.qkvp, qkv_n, hd, ly.q_norm, self.qb, t * nh, nh, int(self.qkvp) + 4 * nh * hd,
                                    qkv_n, ly.k_norm, self.kk, t * nkv, nkv, hd, c.eps, hd, self.step, c.rope_base,
                                    int(self.qkvp) + 4 * (nh * hd + kv), qkv_n, ly.kc, ly.vc)
             hip.attn_prefill(self.qb, ly.kc, ly.vc, 0, self.att, self.step, t, nh, nkv, hd, scale)
             hip.gemm_dense(ly.o, t, self.att, nh * hd, self.x, H, ACT_ADD)
-            hip.rms_norm(self.x, H, ly.ffn_norm, self.h, H, H, t, c.eps)
+            hip.rms_norm_q(self.x, H, ly.ffn_norm, self.h, H, H, t, c.eps, xq=self.hqp if xq_ok else 0)
             hip.gemm_dense(ly.router, t, self.h, H, self.rl, E, ACT_STORE)
             hip.router_topk(self.rl, E, k, 0.0, self.ids, self.wts, t)
             hip.moe_sort(self.ids, t, k, E, self.off, self.xrow, self.inv,
                          [(int(ly.gate_up), ly.e_gu), (int(ly.down), ly.e_down)], self.tiles, self.max_tiles,
                          self.ntd, err_dev=self.err, chunk=self.tchunk)
-            hip.gemm_grouped_gate_up(c.ty_gate_up, F, H, self.tiles, self.max_tiles, self.ntd, self.h, H, t, self.xrow,
-                                     self.ge, F, ly.up_off)
+            hip.gemm_grouped_gate_up(c.ty_gate_up, F, H, self.tiles, self.max_tiles, self.ntd,
+                                     self.hqp if xq_ok else self.h, H, t, self.xrow, self.ge, F, ly.up_off,
+                                     flags=X_Q if xq_ok else 0)
             hip.gemm_grouped(c.ty_down, H, F, int(self.tiles) + self.max_tiles * 16, self.max_tiles, self.ntd, self.ge,
                              F, t * k, 0, self.ye, H, ACT_STORE)
             hip.moe_combine_seq(self.x, self.ye, self.wts, self.inv, k, 0, 0, H, t)

@@ -991,6 +991,42 @@ def test_moe_route_gemv_division_ties(hip):
             assert np.array_equal(down(hip, x, np.uint32, m), down(hip, y, np.uint32, m))
 
 
+@pytest.mark.parametrize("ty", [ggml.Q6_K, ggml.Q4_K, ggml.Q8_0])
+def test_gemm_from_rms_norm_q_xq(hip, ty):
+    """STRATA_X_Q: a GEMM over the X that rms_norm_q quantized beside its output (the prefill's norms feeding the
+    q/k/v and gate/up GEMMs) equals the GEMM quantizing the f32 output itself, bit for bit (gemm_dense and the fused
+    gate/up grouped GEMM); a quantized X with another row stride is an error."""
+    T, H, R = 300, 512, 192
+    x = normal((T, H), seed=90)
+    w = np.random.default_rng(91).uniform(0.5, 1.5, H).astype(np.float32)
+    xb, wb = up(hip, x), up(hip, w)
+    h = hip.alloc(T * H * 4)
+    xq = hip.alloc(T * (H + H // 8))
+    hip.rms_norm_q(xb, H, wb, h, H, H, T, 1e-6, xq=xq)
+    W = hip.upload_tensor(ty, random_blocks(ty, R, H, seed=92 + ty))
+    ya, yb = hip.alloc(T * R * 4), hip.alloc(T * R * 4)
+    hip.gemm_dense(W, T, h, H, ya, R, S.ACT_STORE)
+    hip.gemm_dense(W, T, xq, H, yb, R, S.ACT_STORE | S.X_Q)
+    assert np.array_equal(down(hip, ya, np.uint32, T * R), down(hip, yb, np.uint32, T * R))
+    with pytest.raises(S.StrataError, match="quantized X"):
+        hip.gemm_dense(W, T, xq, 2 * H, yb, R, S.ACT_STORE | S.X_Q)
+    if ty == ggml.Q8_0:
+        return
+    # the fused gate/up grouped GEMM over 2 experts' tiles (rows 0..149 on expert 0, 150..299 on expert 1)
+    E, F = 2, 128
+    rb = ggml.row_bytes(ty, H)
+    gu = up(hip, random_blocks(ty, 2 * E * F, H, seed=93 + ty))
+    tiles = np.zeros(2 * 2, dtype=np.uint64)
+    for e, (m0, cnt) in enumerate(((0, 150), (150, 150))):
+        tiles[2 * e] = int(gu) + e * F * rb
+        tiles[2 * e + 1] = m0 | (cnt << 32)
+    tb, ntd, xrow = up(hip, tiles), up(hip, np.array([2], dtype=np.int32)), up(hip, np.arange(T, dtype=np.int32))
+    ga, gb = hip.alloc(T * F * 4), hip.alloc(T * F * 4)
+    hip.gemm_grouped_gate_up(ty, F, H, tb, 2, ntd, h, H, T, xrow, ga, F, E * F * rb)
+    hip.gemm_grouped_gate_up(ty, F, H, tb, 2, ntd, xq, H, T, xrow, gb, F, E * F * rb, flags=S.X_Q)
+    assert np.array_equal(down(hip, ga, np.uint32, T * F), down(hip, gb, np.uint32, T * F))
+
+
 def test_errors_do_not_launch(hip):
     t = S.GpuTensor(ggml.Q4_K, 4, 300, hip.alloc(4 * 2048))
     with pytest.raises(S.StrataError, match="GEMV needs a multiple of 256"):
