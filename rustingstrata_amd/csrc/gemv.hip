@@ -250,6 +250,10 @@ constexpr int GEMV1_CH = 12;
 constexpr int GEMV1_WAVES = 4;          // waves of a single-input GEMV block
 constexpr int GEMV1_THREADS = 64 * GEMV1_WAVES;
 constexpr int GEMV1_TILE = GEMV1_THREADS * 16 * GEMV1_CH;
+// 16-byte loads a thread of a full tile of one plain matrix, per type (the MoE and pair forms keep GEMV1_CH; lm-head
+// rows 151936 x 2048 in the sweep, % of HBM peak with 10 /
+// 12 / 14: Q4_K 72.8 / 70.1 / 67.3, Q5_K 74.3 / 69.4 / 68.9, Q6_K 67.2 / 68.5 / 71.4, Q8_0 75.9 / 77.7 / 78.6)
+__host__ __device__ constexpr int gemv1_ch(int T) { return T == Q4_K || T == Q5_K ? 10 : T == Q6_K ? 14 : GEMV1_CH; }
 constexpr int GEMV1_CH_SMALL = 5;  // (one plain matrix whose tiles span at most 20 KB: only the loads it needs)
 
 // Quantize x row xr (n values) into LDS (n int8, then n / 32 scales) with quant_xq's arithmetic (quant.hip): the
@@ -465,7 +469,7 @@ static void magic(uint32_t d, uint32_t& m, int& s) {
 template <int T, bool Q32, int MODE>
 __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     constexpr bool SW = MODE & 1, QU = MODE & 2, plain = MODE & 4, ROUTE = MODE & 8;
-    constexpr int CH = (MODE & 16) ? GEMV1_CH_SMALL : GEMV1_CH, TILE = GEMV1_THREADS * 16 * CH;
+    constexpr int CH = (MODE & 16) ? GEMV1_CH_SMALL : plain ? gemv1_ch(T) : GEMV1_CH, TILE = GEMV1_THREADS * 16 * CH;
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
@@ -760,7 +764,8 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     const int nslots = g.ids ? g.k : 1, nz = g.pair ? 2 : 1;
     // Rows per tile: as many as fit the tile, but no fewer tiles than about 4 per CU.
     const bool single = g.nt == 1 && g.cols <= GEMV1_MAX_COLS;
-    const int rmax = (int)(((single ? GEMV1_TILE : GEMV_TILE) - 32) / a.rb);
+    const bool plain1 = single && !g.xu && !g.ids && !g.pair;  // the kernel's one-plain-matrix instantiation
+    const int rmax = (int)(((single ? GEMV1_THREADS * 16 * (plain1 ? gemv1_ch(g.ty) : GEMV1_CH) : GEMV_TILE) - 32) / a.rb);
     long long want = (long long)maxrows * nslots * nz / (4LL * ncu);
     a.R = (int)(want < 1 ? 1 : want > rmax ? rmax : want);
     if (a.R < 1) a.R = 1;
@@ -794,7 +799,7 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
         const uint64_t span_ch = ((uint64_t)a.R * a.rb + 15) / 16 + 1;  // 16-byte chunks a tile spans, at most
         a.small = !g.xu && !g.ids && !g.pair && span_ch <= (uint64_t)GEMV1_THREADS * GEMV1_CH_SMALL;
         const size_t smem1 = (iq ? up16(sizeof(IqTables)) : 0) + xpad_bytes(ncp) + ncp / 8 + ncp / 4 +
-                             GEMV1_THREADS * 16 * (a.small ? GEMV1_CH_SMALL : GEMV1_CH) + 16 +
+                             GEMV1_THREADS * 16 * (a.small ? GEMV1_CH_SMALL : plain1 ? gemv1_ch(g.ty) : GEMV1_CH) + 16 +
                              (a.quarter ? 3 * 64 * 8 : 0);
         switch (g.ty) {
         case Q8_0: return gemv1_t<Q8_0>(a, grid, smem1, s);
