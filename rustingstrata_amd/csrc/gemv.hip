@@ -252,8 +252,9 @@ constexpr int GEMV1_THREADS = 64 * GEMV1_WAVES;
 constexpr int GEMV1_TILE = GEMV1_THREADS * 16 * GEMV1_CH;
 // 16-byte loads a thread of a full tile of one plain matrix, per type (the MoE and pair forms keep GEMV1_CH; lm-head
 // rows 151936 x 2048 in the sweep, % of HBM peak with 10 /
-// 12 / 14: Q4_K 72.8 / 70.1 / 67.3, Q5_K 74.3 / 69.4 / 68.9, Q6_K 67.2 / 68.5 / 71.4, Q8_0 75.9 / 77.7 / 78.6)
-__host__ __device__ constexpr int gemv1_ch(int T) { return T == Q4_K || T == Q5_K ? 10 : T == Q6_K ? 14 : GEMV1_CH; }
+// 12 / 14: Q4_K 72.8 / 70.1 / 67.3, Q5_K 74.3 / 69.4 / 68.9, Q6_K 67.2 / 68.5 / 71.4, Q8_0 75.9 / 77.7 / 78.6,
+// Q3_K 43.8 / 42.6 / 40.8, Q2_K 48.4 / 49.6 / 47.5)
+__host__ __device__ constexpr int gemv1_ch(int T) { return T == Q4_K || T == Q5_K || T == Q3_K ? 10 : T == Q6_K ? 14 : GEMV1_CH; }
 constexpr int GEMV1_CH_SMALL = 5;  // (one plain matrix whose tiles span at most 20 KB: only the loads it needs)
 
 // Quantize x row xr (n values) into LDS (n int8, then n / 32 scales) with quant_xq's arithmetic (quant.hip): the
