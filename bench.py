@@ -503,7 +503,7 @@ def bench_stack(hip, S, ggml, n_prompt=4096, n_decode=128, chunk=4096, n_layer=4
     dec_ms = hip.elapsed_ms(e1, e2)
     wall_dec = time.time() - t1
     toks = hip.get(m.tok, np.int32, 1)
-    hip.drop_graphs()
+    m.close()
     wbytes = sum(t.bytes() for t in [w.embd, w.output]) + sum(
         ly.q.bytes() + ly.k.bytes() + ly.v.bytes() + ly.o.bytes() for ly in w.layers) + n_layer * (
         2 * c.n_expert * w.strides()[0] + c.n_expert * w.strides()[1])

@@ -178,6 +178,37 @@ class GpuTensor:
         return ctypes.byref(_Tensor(self.ty, 0, self.rows, self.cols, self.ptr))
 
 
+class Graph:
+    """An executable graph recorded from the ops a function queues; destroyed by close() or when collected, before
+    the buffers it keeps alive can be freed."""
+
+    def __init__(self, backend, f, keep=()):
+        self.backend = backend
+        _check(lib().strata_graph_begin(backend._ctx))
+        try:
+            f()
+        finally:
+            out = P()
+            rc = lib().strata_graph_end(backend._ctx, ctypes.byref(out))
+        _check(rc)
+        self.handle = out
+        self._fin = weakref.finalize(self, Graph._destroy, backend._ctx_ref, out, tuple(keep))
+
+    @staticmethod
+    def _destroy(ref, handle, keep):
+        # keep (the buffers the graph addresses) is released only after this returns
+        if ref.ctx is not None:
+            lib().strata_graph_destroy(ref.ctx, handle)
+
+    def launch(self):
+        if not self._fin.alive:
+            raise StrataError("launch of a destroyed graph")
+        _check(lib().strata_graph_launch(self.backend._ctx, self.handle))
+
+    def close(self):
+        self._fin()
+
+
 class _CtxRef:
     def __init__(self, ctx):
         self.ctx = ctx
@@ -270,26 +301,26 @@ class HipBackend:
         return GpuTensor(ty, rows, cols, self.upload(blocks))
 
     # ---- recorded graphs (Backend::graph, src/backend.rs:118-120) ----
+    def record_graph(self, f, keep=()):
+        """Record the ops `f` queues as a Graph (replayed by Graph.launch). The graph holds the raw addresses of the
+        buffers those ops use: pass them (or the objects owning them) as `keep`, and the graph keeps them alive until
+        it is destroyed, so no replay can touch freed memory."""
+        return Graph(self, f, keep)
+
     def graph(self, key, f):
         """Run the ops `f` queues as the graph recorded under `key`, recording it on first use; `f` runs only when
-        recording, so its ops must read per-call values from device memory."""
-        g = self._graphs.get(key) if hasattr(self, "_graphs") else None
+        recording, so its ops must read per-call values from device memory. The caller keeps the buffers the ops use
+        alive until drop_graphs()."""
+        if not hasattr(self, "_graphs"):
+            self._graphs = {}
+        g = self._graphs.get(key)
         if g is None:
-            if not hasattr(self, "_graphs"):
-                self._graphs = {}
-            _check(lib().strata_graph_begin(self._ctx))
-            try:
-                f()
-            finally:
-                out = P()
-                rc = lib().strata_graph_end(self._ctx, ctypes.byref(out))
-            _check(rc)
-            g = self._graphs[key] = out
-        _check(lib().strata_graph_launch(self._ctx, g))
+            g = self._graphs[key] = Graph(self, f)
+        g.launch()
 
     def drop_graphs(self):
         for g in getattr(self, "_graphs", {}).values():
-            lib().strata_graph_destroy(self._ctx, g)
+            g.close()
         self._graphs = {}
 
     # ---- ops ----
@@ -307,6 +338,8 @@ class HipBackend:
         where the rows allow."""
         _check(lib().strata_combine_rms_norm_q(self._ctx, int(x), n, int(ye), int(wh), k, int(w), int(out), n, n, rows,
                                                eps, int(xq), int(res)))
+
+    RMS_NORM_GEMV_MAX = 2048  # values of a row the fused norm + F32 GEMV launch takes
 
     def rms_norm_q_gemv_f32(self, x, res, nw, h, xq, n, eps, w, y):
         """h = rms_norm(x + res) * nw (and xq), y = w h for an F32 matrix, one launch; x is not written."""

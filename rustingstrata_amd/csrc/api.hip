@@ -357,6 +357,8 @@ int strata_graph_launch(strata_ctx* c, void* graph) {
 
 int strata_graph_destroy(strata_ctx* c, void* graph) {
     if (check_ctx(c)) return -1;
+    // a replay still queued must finish before its executable graph goes (and before the caller frees its buffers)
+    STRATA_HIP(hipStreamSynchronize(c->stream));
     STRATA_HIP(hipGraphExecDestroy((hipGraphExec_t)graph));
     if (c->graphs > 0 && --c->graphs == 0) {
         // No graph holds a retired scratch address any more.

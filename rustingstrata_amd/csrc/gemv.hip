@@ -660,10 +660,18 @@ template <int T, bool Q32, int MODE>
 static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
     static int ncu = 0, per_cu = 0;
     static size_t cached_smem = 0;
+    static size_t attr = 64 * 1024;  // dynamic LDS the kernel is set up for
     if (!ncu) {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
             ncu = 256;
+    }
+    // a wide row's x staging plus a full per-type tile can pass the default 64 KB of dynamic LDS (Q6_K at 16384
+    // columns: ~82 KB); a CU has 160 KB
+    if (smem > attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)gemv1_kernel<T, Q32, MODE>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+        attr = smem;
     }
     if (cached_smem != smem) {
         int n = 0;
@@ -705,7 +713,7 @@ static hipError_t gemv_nt(const GemvArgs& a, long long tiles, size_t smem, hipSt
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
             ncu = 256;
     }
-    static bool attr = false;
+    static size_t attr = 64 * 1024;  // dynamic LDS the kernel is set up for
     if (!attr) {  // wide rows (more than GEMV1_MAX_COLS values) stage more than 64 KB of x and tile
         if (hipFuncSetAttribute((const void*)gemv_kernel<T, NT, Q32>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
             return hipErrorInvalidValue;
@@ -999,7 +1007,7 @@ __global__ __launch_bounds__(DC_THREADS) void moe_down_combine_kernel(DcArgs a) 
 
 template <int T, bool Q32>
 static hipError_t dc_launch(const DcArgs& a, int t, size_t smem, hipStream_t s) {
-    static bool attr = false;
+    static size_t attr = 64 * 1024;  // dynamic LDS the kernel is set up for
     if (!attr) {
         if (hipFuncSetAttribute((const void*)moe_down_combine_kernel<T, Q32>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
             return hipErrorInvalidValue;

@@ -25,7 +25,7 @@ Per decode token (recorded once as a graph and replayed; the step buffer carries
 import numpy as np
 
 from . import ggml
-from .backend import ACT_ADD, ACT_STORE, NUM_Q8K, X_Q, GpuTensor, StrataError
+from .backend import ACT_ADD, ACT_STORE, NUM_Q8K, X_Q, Buf, GpuTensor, StrataError
 
 
 class Config:
@@ -51,7 +51,7 @@ SCALE = {ggml.Q8_0: (2.2e-4, 3.2e-4), ggml.Q6_K: (1.2e-5, 1.8e-5), ggml.Q2_K: (1
 
 class Layer:
     __slots__ = ("attn_norm", "qkv", "q", "k", "v", "q_norm", "k_norm", "o", "ffn_norm", "router", "gate_up", "down",
-                 "e_gu", "e_down", "up_off", "kc", "vc")
+                 "e_gu", "e_down", "up_off")
 
 
 class Weights:
@@ -150,9 +150,9 @@ class Model:
         self.ctx, self.chunk = ctx, chunk
         self.pos = 0
         kv = c.n_head_kv * c.head_dim
-        for ly in weights.layers:
-            ly.kc = hip.alloc(ctx * hip.kv_words(kv) * 2)
-            ly.vc = hip.alloc(ctx * hip.kv_words(kv) * 2)
+        # this model's f16 KV caches, one pair per layer (several models may share one Weights)
+        self.kc = [hip.alloc(ctx * hip.kv_words(kv) * 2) for _ in weights.layers]
+        self.vc = [hip.alloc(ctx * hip.kv_words(kv) * 2) for _ in weights.layers]
         self.step = hip.alloc(8)
         H, nh, hd, E, k, F = c.n_embd, c.n_head, c.head_dim, c.n_expert, c.n_expert_used, c.n_ff_exp
         n = chunk
@@ -190,6 +190,7 @@ class Model:
         self.ye1 = A(k * H * 4)
         self.logits = A(c.n_vocab * 4)
         self.tok = A(4)
+        self._graph = None  # the recorded decode token (this model's own: it holds this model's addresses)
 
     def reset(self):
         self.pos = 0
@@ -227,8 +228,8 @@ class Model:
                 hip.gemm_dense(ly.qkv, t, self.h, H, self.qkvp, qkv_n, ACT_STORE)
             hip.rms_norm_rope_qk_t(self.qkvp, qkv_n, hd, ly.q_norm, self.qb, t * nh, nh, int(self.qkvp) + 4 * nh * hd,
                                    qkv_n, ly.k_norm, self.kk, t * nkv, nkv, hd, c.eps, hd, self.step, c.rope_base,
-                                   int(self.qkvp) + 4 * (nh * hd + kv), qkv_n, ly.kc, ly.vc)
-            hip.attn_prefill(self.qb, ly.kc, ly.vc, 0, self.att, self.step, t, nh, nkv, hd, scale)
+                                   int(self.qkvp) + 4 * (nh * hd + kv), qkv_n, self.kc[il], self.vc[il])
+            hip.attn_prefill(self.qb, self.kc[il], self.vc[il], 0, self.att, self.step, t, nh, nkv, hd, scale)
             hip.gemm_dense(ly.o, t, self.att, nh * hd, self.x, H, ACT_ADD)
             hip.rms_norm_q(self.x, H, ly.ffn_norm, self.h, H, H, t, c.eps, xq=self.hqp if xq_ok else 0)
             hip.gemm_dense(ly.router, t, self.h, H, self.rl, E, ACT_STORE)
@@ -267,23 +268,29 @@ class Model:
         H, nh, nkv, hd, E, k, F = c.n_embd, c.n_head, c.n_head_kv, c.head_dim, c.n_expert, c.n_expert_used, c.n_ff_exp
         kv = nkv * hd
         x = self.x  # row 0
+        # the FFN norm and the router logits as one launch take rows of up to 2048 values
+        fused_router = H <= self.hip.RMS_NORM_GEMV_MAX
         hip.get_rows(w.embd, self.tok, 1, x)
         for li, ly in enumerate(w.layers):
             if li == 0:
                 hip.rms_norm_q(x, H, ly.attn_norm, self.h, H, H, 1, c.eps, xq=self.hq)
             else:  # the previous layer's x += mix, its combine (x += sum w y) and this layer's attention norm
                 hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, ly.attn_norm, self.h, H, 1, c.eps, xq=self.hq,
-                                       res=self.mix)
+                                       res=self.mix if fused_router else 0)
             hip.gemvq(ly.qkv, self.h, H, self.hq, self.dqkv, nh * hd + 2 * kv, 1)  # q, k and v in one launch
             # q/k norms, rope and the KV store inside the attention launch (the same bits as rms_norm_rope_qk with
             # the KV store, then attn_decode)
             hip.rms_norm_rope_attn_decode(self.dq, hd, ly.q_norm, self.dk, ly.k_norm, self.dv, c.eps, hd, c.rope_base,
-                                          ly.kc, ly.vc, 0, self.datt, self.part, self.step, nh, nkv, hd,
+                                          self.kc[li], self.vc[li], 0, self.datt, self.part, self.step, nh, nkv, hd,
                                           float(1.0 / np.sqrt(hd)), xq=self.aq)
             hip.gemvq(ly.o, self.datt, nh * hd, self.aq, self.mix, H, 1)  # x quantized by the attention's merge
             # h, hq = rms_norm_q(x + mix) and the router logits in one launch (x += mix is left to the next
             # combine_rms_norm_q, which adds mix before the combine: the same bits)
-            hip.rms_norm_q_gemv_f32(x, self.mix, ly.ffn_norm, self.h, self.hq, H, c.eps, ly.router, self.dl)
+            if fused_router:
+                hip.rms_norm_q_gemv_f32(x, self.mix, ly.ffn_norm, self.h, self.hq, H, c.eps, ly.router, self.dl)
+            else:  # rows too wide for the fused launch: x += mix here, the norm, then the router GEMV (the same bits)
+                hip.rms_norm_q(x, H, ly.ffn_norm, self.h, H, H, 1, c.eps, xq=self.hq, res=self.mix)
+                hip.gemv(ly.router, self.h, self.dl)
             # the route inside the gate/up GEMV launch (moe_route then moe_gemv, the same bits)
             hip.moe_route_gemv(self.dl, E, k, 0.0, self.table, self.dids, self.dwts, self.dslots, self.dwh,
                                c.ty_gate_up, F, H, ly.gate_up, ly.e_gu, self.h, self.g2, pair=(ly.up_off, k * F * 4),
@@ -291,7 +298,8 @@ class Model:
             # the down GEMV (SwiGLU quantized inside) into ye1; its combine runs with the next norm
             hip.moe_down_swiglu_combine(c.ty_down, H, F, ly.down, ly.e_down, self.dslots, k, self.g2,
                                         int(self.g2) + k * F * 4, self.ye1, 0, self.dwh, 0, 0, 1)
-        hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, w.output_norm, self.h, H, 1, c.eps, res=self.mix)
+        hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, w.output_norm, self.h, H, 1, c.eps,
+                               res=self.mix if fused_router else 0)
         hip.gemv(w.output, self.h, self.logits)
         hip.argmax_rows(self.logits, c.n_vocab, 1, self.tok)
 
@@ -302,7 +310,18 @@ class Model:
             raise StrataError(f"context full ({self.ctx} tokens)")
         self._set_step(self.pos)
         if graph:
-            self.hip.graph(("decode", id(self)), self._decode_ops)
+            if self._graph is None:
+                # the graph keeps every buffer it addresses alive (the weights with their KV caches, this model's
+                # scratch) until it is destroyed
+                keep = [self.w] + self.kc + self.vc + [v for v in vars(self).values() if isinstance(v, Buf)]
+                self._graph = self.hip.record_graph(self._decode_ops, keep)
+            self._graph.launch()
         else:
             self._decode_ops()
         self.pos += 1
+
+    def close(self):
+        """Destroy the recorded decode graph (it is also destroyed when the model is collected)."""
+        if self._graph is not None:
+            self._graph.close()
+            self._graph = None

@@ -276,6 +276,23 @@ def test_gemv_sweep_shapes(hip, ty, rows):
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
 
 
+@pytest.mark.parametrize("ty", [ggml.Q3_K, ggml.Q4_K, ggml.Q6_K])
+@pytest.mark.parametrize("cols", [14336, 16384])
+def test_gemv_wide_rows_full_tiles(hip, ty, cols):
+    """One plain matrix of wide rows (up to the single-input kernel's 16384 columns) and thousands of rows, so every
+    block takes the type's full tile with x's staging beside it (past 64 KB of LDS for Q6_K): the CPU dot's bits on
+    every row."""
+    rows = 3000
+    w = random_blocks(ty, rows, cols, seed=cols + ty)
+    x = normal(cols, seed=cols + ty + 1)
+    t = hip.upload_tensor(ty, w)
+    y = hip.alloc(rows * 4)
+    hip.gemv(t, up(hip, x), y)
+    got = down(hip, y, np.float32, rows)
+    want = O.matvec(ty, w, rows, cols, x, threads=min(16, os.cpu_count() or 1))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), int((got != want).sum())
+
+
 @pytest.mark.parametrize("ty", [ggml.Q2_K, ggml.Q3_K, ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S])
 def test_gemv_bits_over_random_shapes(hip, ty):
     """The CPU dot's bits over seeded random shapes (1-300 rows, 256-8192 columns) and weight scales spanning
@@ -755,6 +772,22 @@ def test_moe_prefill_layer_full_size(hip):
     gate, upw, dn = moe_weights(E, H, F, seed=140)
     hs = normal((T, H), seed=141)
     logits = zipf_logits(T, E, seed=142)
+    ids_w, wts_w = O.route(logits, k)
+    want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, hs, ids_w, wts_w,
+                           threads=min(16, os.cpu_count() or 1))
+    got = run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True)
+    assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
+    assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits), got)
+
+
+def test_moe_prefill_layer_512_tokens(hip):
+    """configs[2] at its 512-token size (128 experts, Zipf-skewed: most experts get a few dozen routed rows, so the
+    grouped GEMMs run their small-tile form): the device layer against cpu_moe::experts_multi on every token, fused
+    and unfused gate/up bit for bit."""
+    E, H, F, T, k = 128, 2048, 768, 512, 8
+    gate, upw, dn = moe_weights(E, H, F, seed=240)
+    hs = normal((T, H), seed=241)
+    logits = zipf_logits(T, E, seed=242)
     ids_w, wts_w = O.route(logits, k)
     want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, hs, ids_w, wts_w,
                            threads=min(16, os.cpu_count() or 1))
