@@ -193,9 +193,10 @@ def gemm_digit_planes(ggml, ty):
     return (2 if hi else 1) + (1 if mins else 0)
 
 
-def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
+def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None, small=None):
     """E=128, top-8, H=2048, I=768; gate/up Q5_K, down Q6_K (or the given types, e.g. configs[4]'s
-    Q2_K / Q3_K experts); Zipf-skewed routing; T tokens."""
+    Q2_K / Q3_K experts); Zipf-skewed routing; T tokens. small: the 64-position GEMM kernel over 64-position tiles
+    (None: the backend's choice for T k / E routed rows per expert)."""
     E, H, F, k = 128, 2048, 768, 8
     ty_gu = ggml.Q5_K if ty_gu is None else ty_gu
     ty_d = ggml.Q6_K if ty_d is None else ty_d
@@ -213,7 +214,7 @@ def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
     hs = rng.standard_normal((T, H)).astype(np.float32)
     lb, hb = hip.upload(logits), hip.upload(hs)
     ids, wts = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
-    chunk = hip.gemm_block_positions()  # tile lists sized to the GEMM's blocks
+    chunk, fl = hip.moe_tile_plan(T, k, E, small)  # tile lists sized to the GEMM's blocks
     max_tiles = T * k // chunk + E
     off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
     tiles, ntd = hip.alloc(2 * max_tiles * 16), hip.alloc(4)
@@ -227,11 +228,12 @@ def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
         if timed:
             hip.record(ev[1])
         # gate and up in one grouped GEMM: ge = silu(W_gate x) * (W_up x) (the bits of the two-call sequence)
-        hip.gemm_grouped_gate_up(ty_gu, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b))
+        hip.gemm_grouped_gate_up(ty_gu, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b),
+                                 flags=fl)
         if timed:
             hip.record(ev[4])
         hip.gemm_grouped(ty_d, H, F, int(tiles) + max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
-                         S.ACT_STORE)
+                         S.ACT_STORE | fl)
         if timed:
             hip.record(ev[2])
         hip.moe_combine_seq(x, ye, wts, inv, k, 0, 0, H, T)
@@ -263,6 +265,7 @@ def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None):
             "grouped_gemm_ms": round(gemm, 4), "int8_TOPS": round(ops / (gemm / 1e3) / 1e12, 1),
             "mfma_frac": round(ops / (gemm / 1e3) / 1e12 / INT8_PEAK_TOPS, 4), "ops": ops,
             "types": f"gate/up {ggml.NAMES[ty_gu]}, down {ggml.NAMES[ty_d]}",
+            "gemm_kernel": "64-position tiles (SMALL_TILES)" if fl else f"{chunk}-position tiles",
             "routing": "N(0,1) logits + 8 * rank^-1.1 over a seeded expert permutation (Zipf s=1.1, scale 8), "
                        "softmax top-8, seed 11"}
 
@@ -446,7 +449,7 @@ def bench_codebook(hip, S, ggml, iters):
         logits = (rng.standard_normal((T, E)) + 8.0 * perm.astype(np.float64) ** -1.1).astype(np.float32)
         lb, hb = hip.upload(logits), hip.upload(rng.standard_normal((T, cols)).astype(np.float32))
         ids, wts = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
-        chunk = hip.gemm_block_positions()
+        chunk, fl = hip.moe_tile_plan(T, k, E)
         max_tiles = T * k // chunk + E
         off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
         tiles, ntd = hip.alloc(max_tiles * 16), hip.alloc(4)
@@ -458,7 +461,7 @@ def bench_codebook(hip, S, ggml, iters):
             hip.moe_sort(ids, T, k, E, off, xrow, inv, [(int(pool) + c * one, rows * rb)], tiles, max_tiles, ntd, chunk=chunk)
             e0, e1 = hip.event(), hip.event()
             hip.record(e0)
-            hip.gemm_grouped(ty, rows, cols, tiles, max_tiles, ntd, hb, cols, T, xrow, ye, rows, S.ACT_STORE)
+            hip.gemm_grouped(ty, rows, cols, tiles, max_tiles, ntd, hb, cols, T, xrow, ye, rows, S.ACT_STORE | fl)
             hip.record(e1)
             if i >= 3:
                 gemm_ms += hip.elapsed_ms(e0, e1)

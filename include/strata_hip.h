@@ -40,7 +40,8 @@ enum { STRATA_NUM_Q8K = 0, STRATA_NUM_Q8_32 = 1 };
 /* GGUF type id of float32 tensors. */
 enum { STRATA_F32 = 0 };
 
-enum { STRATA_ACT_STORE = 0, STRATA_ACT_SWIGLU = 1, STRATA_ACT_ADD = 2, STRATA_SAME_X = 4, STRATA_X_Q = 8 };
+enum { STRATA_ACT_STORE = 0, STRATA_ACT_SWIGLU = 1, STRATA_ACT_ADD = 2, STRATA_SAME_X = 4, STRATA_X_Q = 8,
+       STRATA_SMALL_TILES = 16 };
 /* STRATA_X_Q (quantized-matrix GEMMs, no counterpart in the reference): x is X already quantized in strata_quant_xq's
  * layout under STRATA_NUM_Q8K (n_x rows of cols int8, then their scales; x_stride = cols), e.g. the xq that
  * strata_rms_norm_q wrote beside its output, so the GEMM skips its own quantization of X (the same bits). */

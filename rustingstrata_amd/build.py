@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libstrata_hip.so")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["api.hip", "quant.hip", "gemv.hip", "moe.hip", "gemm.hip", "decoder.hip", "attn.hip", "quantize.cpp"]
+SOURCES = ["api.hip", "quant.hip", "gemv.hip", "moe.hip", "gemm.hip", "gemm_small.hip", "decoder.hip", "attn.hip", "quantize.cpp"]
 ARCH = os.environ.get("STRATA_OFFLOAD_ARCH", "gfx950")
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",

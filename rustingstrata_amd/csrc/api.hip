@@ -738,7 +738,7 @@ static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint
     if (check_ctx(c) || check_type(ty)) return -1;
     if (cols == 0 || cols % 256)
         return set_error(std::string(type_name(ty)) + " matrix with " + std::to_string(cols) + " columns: GEMM needs a multiple of 256");
-    int op = act & ~(STRATA_SAME_X | STRATA_X_Q);
+    int op = act & ~(STRATA_SAME_X | STRATA_X_Q | STRATA_SMALL_TILES);
     if (op < 0 || op > 2) return set_error("gemm: act " + std::to_string(act));
     if ((act & STRATA_X_Q) && x_stride != cols) return set_error("gemm: a quantized X (STRATA_X_Q) has rows of cols values");
     if (dense_w && check_align(ty, (uint64_t)dense_w, "gemm_dense")) return -1;
@@ -756,6 +756,7 @@ static int gemm_common(strata_ctx* c, int ty, uint64_t rows, uint64_t cols, uint
     g.xq = (const uint8_t*)xq; g.n_x = (int)n_x; g.xrow = (const int*)xrow;
     g.y = (float*)y; g.y_stride = (int64_t)y_stride; g.act = op;
     g.pair = pair; g.w2 = w2;
+    g.small = (act & STRATA_SMALL_TILES) != 0;
     STRATA_HIP(launch_gemm(g, c->stream));
     return 0;
 }
@@ -783,7 +784,8 @@ int strata_gemm_grouped_gate_up(strata_ctx* c, int ty, uint64_t rows, uint64_t c
     if (rows % 64) return set_error("gemm_grouped_gate_up: " + std::to_string(rows) + " rows (a multiple of 64)");
     if (y % 16 || y_stride % 4) return set_error("gemm_grouped_gate_up: y rows must be 16-byte aligned");
     if (check_align(ty, (uint64_t)up_offset, "gemm_grouped_gate_up up offset")) return -1;
-    if (flags & ~(STRATA_SAME_X | STRATA_X_Q)) return set_error("gemm_grouped_gate_up: flags " + std::to_string(flags));
+    if (flags & ~(STRATA_SAME_X | STRATA_X_Q | STRATA_SMALL_TILES))
+        return set_error("gemm_grouped_gate_up: flags " + std::to_string(flags));
     return gemm_common(c, ty, rows, cols, tiles, max_tiles, (const int*)n_tiles_dev, x, x_stride, n_x, xrow, y, y_stride,
                        flags, nullptr, 0, true, up_offset);
 }

@@ -28,8 +28,11 @@ struct GemmLaunch {
     // 16-byte aligned)
     bool pair = false;
     int64_t w2 = 0;
+    // tiles of a few dozen positions: the 64-position kernel with two steps of loads in flight (gemm_small.hip)
+    bool small = false;
 };
 hipError_t launch_gemm(const GemmLaunch& g, hipStream_t s);
+hipError_t launch_gemm_small(const GemmLaunch& g, hipStream_t s);
 // Positions of one GEMM block (a tile list's chunks of this size give every block a full tile).
 uint64_t gemm_block_positions();
 

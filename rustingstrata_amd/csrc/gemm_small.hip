@@ -1,0 +1,421 @@
+// Grouped GEMM on int8 MFMA for tile lists whose tiles hold a few dozen positions (a 512-token MoE layer over 128
+// experts routes ~32 rows to an expert): the same products and the same bits as gemm_kernel (gemm.hip; reference
+// kernels gemmi_q / gemms_*, src/cuda/kernels.cu:1355-1497, chosen by tile size in src/cuda/mod.rs:587-620).
+//
+// With few positions a block's super-block step is short (the 16 rows a wave decodes, then one or two MFMA tile
+// pairs), so a weight load issued one step ahead does not land in time. This kernel keeps two steps in flight:
+//   * a block takes 64 positions x 128 weight rows (8 waves, 16 rows each, as gemm_kernel; pair mode 64 gate + 64 up);
+//   * X rows and their scales sit in a ring of three LDS buffers, raw weights in two per wave, and step g issues the
+//     loads of step g + 2 (X and scales between its decode units, its own weight rows right after its decode);
+//   * every wave issues the same number of loads each step (positions past a tile's count load its first row, weight
+//     chunks a row does not need reload its first chunk into the wave's padded region), so the end of step g waits
+//     with vmcnt for step g + 1's loads alone, and the block barrier does not drain step g + 2's;
+//   * a tile of more than 64 positions runs as consecutive 64-position chunks (any tile list is computed whole; the
+//     fast case is a tile list built with chunks of 64, strata_moe_sort's chunk = 64).
+// Each wave keeps its own copy of a step's 64 X scales (one 4-byte load-to-LDS per lane), so scales need no barrier.
+#include <algorithm>
+
+#include "gemm_dev.h"
+#include "../../include/strata_hip.h"
+
+namespace strata {
+
+namespace {
+constexpr int SM = 64;                  // positions per block
+constexpr int SN = 128;                 // weight rows per block (pair: 64 + 64)
+constexpr int SW = 8;                   // waves per block
+constexpr int STT = SM / 16;            // MFMA position tiles per block
+constexpr int SXB = SM * 256;           // bytes of one X buffer
+constexpr int SXI = SM * 16 / 64 / SW;  // X load instructions per wave and step
+constexpr int NXB = 3;                  // X (and scale) buffers: steps g, g + 1, g + 2
+constexpr int SDX = SW * SM;            // floats of one scale buffer (a copy per wave)
+}  // namespace
+
+template <int T> struct SmallFmt : GemmPlanes<T> {
+    static constexpr int WI = (16 * GemmPlanes<T>::NCH + 63) / 64;  // weight load instructions per wave and step
+    static constexpr int WREG = 64 * WI * 16;                        // LDS bytes of a wave's raw rows (whole instructions)
+    static constexpr int WBUF = SW * WREG;                           // bytes of one raw weight buffer
+    static constexpr int NLOAD = SXI + WI + 1;                       // loads per wave and step
+};
+
+// 4 bytes per lane from a wave-uniform base plus a per-lane offset into LDS at lds + 4 * lane (global_load_lds_dword).
+__device__ __forceinline__ void load_lds4_so(uint64_t base, uint32_t off, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32)) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(sb), "s"(m0) : "memory", "m0");
+}
+// Block barrier after this wave's LDS operations complete, without waiting for its loads in flight (a
+// __syncthreads() fence would also wait for every outstanding vector memory operation).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
+
+template <int T>
+__global__ __launch_bounds__(64 * SW, 1) void gemm_small_kernel(GemmArgs a) {
+    using F = SmallFmt<T>;
+    constexpr int NP = F::NP, SBB = sb_bytes(T), NCH = F::NCH, RAWP = F::RAWP, WI = F::WI, WREG = F::WREG,
+                  WBUF = F::WBUF, NLOAD = F::NLOAD;
+    constexpr int P_HI = 0, P_LO = F::HI ? 1 : 0, P_M = F::HI ? 2 : 1;
+    constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
+    static_assert(NCH <= 15 && WI <= 8, "chunk numbers of a lane's weight instructions fit one word");
+    static_assert(SBB < 225, "the no-chunk number 15 lands past every super-block");
+    static_assert(SXI == 2, "the decode hook issues two X instructions and the scales");
+    extern __shared__ __align__(16) uint8_t smem[];
+    // LDS: [X: NXB x SXB][scales: NXB x SDX floats][raw W: 2 x WBUF][IqTables]
+    int8_t* xs = (int8_t*)smem;
+    float* dxs = (float*)(smem + NXB * SXB);
+    uint8_t* raw = (uint8_t*)(dxs + NXB * SDX);
+    IqTables* tab = (IqTables*)(raw + 2 * WBUF);
+
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int cols = a.cols, nsb = cols / 256;
+
+    // Items (tile, row block), item = tile * nrb + row block, dealt to the blocks in turn (block b takes items b,
+    // b + grid, ...: with tiles this small the items' costs vary with their expert's load, and dealing them round the
+    // whole grid balances the blocks better than giving each XCD a contiguous range; measured 0.285 -> 0.268 ms for
+    // a 512-token layer's grouped GEMMs). A tile of more than 64 positions runs as consecutive 64-position chunks of
+    // its item.
+    const int ntiles = a.n_tiles_dev ? min(sload(a.n_tiles_dev), a.max_tiles) : a.max_tiles;
+    const bool pair = a.pair != 0;
+    const int GNO = pair ? SN / 2 : SN;
+    const int nrb = (a.rows + GNO - 1) / GNO, total = nrb * ntiles;
+    const int ibeg = blockIdx.x, gstep = gridDim.x;
+    const int nitems = ibeg < total ? (total - ibeg + gstep - 1) / gstep : 0;
+
+    struct Item {
+        uint64_t w;
+        int m0, cnt, n0;  // cnt 0: no item
+        int rest;         // positions of the tile after this chunk
+    };
+    // chunk pc of item k (k < nitems)
+    auto item_at = [&](int k, int pc) __attribute__((always_inline)) {
+        Item it;
+        const int id = ibeg + k * gstep, tile = id / nrb;
+        it.n0 = (id - tile * nrb) * GNO;
+        const uint64_t t0 = sload(a.tiles + 2 * tile), t1 = sload(a.tiles + 2 * tile + 1);
+        const int cnt = min(256, (int)(t1 >> 32)) - SM * pc;
+        it.w = t0;
+        it.m0 = (int)(uint32_t)t1 + SM * pc;
+        it.cnt = max(0, min(SM, cnt));
+        it.rest = cnt - it.cnt;
+        return it;
+    };
+    // the next chunk with positions: chunk pc + 1 of item k while the tile has positions left, else the first chunk
+    // of the next item with positions (cnt 0 past the last item)
+    auto next_item = [&](int& k, int& pc, const Item& prev) __attribute__((always_inline)) {
+        if (prev.rest > 0) {
+            ++pc;
+            return item_at(k, pc);
+        }
+        Item it{0, 0, 0, 0, 0};
+        pc = 0;
+        for (++k; k < nitems; k++) {
+            it = item_at(k, 0);
+            if (it.cnt > 0) break;
+        }
+        return it;
+    };
+
+    if constexpr (IQ) load_iq_tables(tab);
+
+    struct Addr {
+        uint32_t xo[SXI];  // X byte offsets of this lane's two position rows (+ chunk)
+        uint32_t dxo;      // byte offset of the scales of position `lane`
+        uint32_t rbeg;     // this lane's decode row: byte offset from W, plus W mod 16
+        uint32_t wro[WI];  // byte offsets from W of the rows of this lane's weight chunks
+    };
+    const int rl = 16 * wave + (lane & 15);
+    const int wlim = 16 * NCH;
+    auto wchunk = [&](int i) __attribute__((always_inline)) { return 64 * i + lane; };
+    auto addr_of = [&](const Item& it) __attribute__((always_inline)) {
+        Addr ad;
+        auto xrow_of = [&](int p) { p = p < it.cnt ? p : 0; return a.xrow ? a.xrow[it.m0 + p] : it.m0 + p; };
+#pragma unroll
+        for (int j = 0; j < SXI; j++) {
+            const int p = 4 * (SXI * wave + j) + (lane >> 4);
+            ad.xo[j] = (uint32_t)xrow_of(p) * (uint32_t)cols + 16 * ((lane & 15) ^ (p & 15));
+        }
+        ad.dxo = 4u * (uint32_t)xrow_of(lane) * (uint32_t)(cols / 32);
+        ad.rbeg = (uint32_t)(it.w & 15) + (pair && wave >= 4 ? (uint32_t)(a.w2 & 15) : 0u) +
+                  __umul24((uint32_t)min(it.n0 + (pair ? (rl & 63) : rl), a.rows - 1), (uint32_t)a.rb);
+#pragma unroll
+        for (int i = 0; i < WI; i++)
+            ad.wro[i] = __umul24((uint32_t)min(it.n0 + ((16 * wave + min(wchunk(i) / NCH, 15)) & (GNO - 1)), a.rows - 1),
+                                 (uint32_t)a.rb);
+        return ad;
+    };
+    uint32_t wcc = 0;  // chunk number within its row of each weight instruction's chunk (15: none)
+#pragma unroll
+    for (int i = 0; i < WI; i++) wcc |= (uint32_t)(wchunk(i) < wlim ? wchunk(i) % NCH : 15) << (4 * i);
+
+    // The loads of one step; every call issues exactly SXI, 1 and WI instructions.
+    auto load_x = [&](const Addr& ad, int s, int xb, const int j) __attribute__((always_inline)) {
+        load_lds16_so((uint64_t)(a.xq + 256 * s), ad.xo[j], xs + xb * SXB + 1024 * (SXI * wave + j));
+    };
+    auto load_dx = [&](const Addr& ad, int s, int xb) __attribute__((always_inline)) {
+        load_lds4_so((uint64_t)(a.xd + 8 * s), ad.dxo, dxs + xb * SDX + SM * wave);
+    };
+    auto load_w = [&](const Item& it, const Addr& ad, int s, int wb) __attribute__((always_inline)) {
+        const uint64_t beg = it.w + (pair && wave >= 4 ? (uint64_t)a.w2 : 0) + (uint64_t)s * SBB, base = beg & ~(uint64_t)15;
+        const uint32_t b15 = (uint32_t)(beg & 15);
+        uint8_t* dst = raw + wb * WBUF + wave * WREG;
+#pragma unroll
+        for (int i = 0; i < WI; i++) {
+            const uint32_t t = b15 + ad.wro[i];
+            uint32_t o = (t & ~15u) + 16 * ((wcc >> (4 * i)) & 15);
+            if (o >= t + SBB) o = t & ~15u;  // a chunk the row does not need: its first chunk again
+            load_lds16_so(base, o, dst + 16 * 64 * i);
+        }
+    };
+
+    float acc[STT][4];
+#pragma unroll
+    for (int i = 0; i < STT; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
+    const int kl = lane >> 4, aswz = lane & 15;
+    v4i B[4][NP];
+    float D = 0.0f, M = 0.0f;
+    auto decode = [&](uint32_t rbeg, int s, int wb, auto&& hook) __attribute__((always_inline)) {
+        const uint8_t* b = raw + wb * WBUF + wave * WREG + (lane & 15) * RAWP + ((rbeg + (uint32_t)s * SBB) & 15);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            uint32_t hi[4], lo[4];
+            int m;
+            Dec<T>::run(b, 4 * kk + kl, tab, hi, lo, m);
+            if constexpr (F::HI) B[kk][P_HI] = (v4i){(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+            B[kk][P_LO] = (v4i){(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+            if constexpr (F::MIN) {
+                const int mw = (int)((uint32_t)m * 0x01010101u);
+                B[kk][P_M] = (v4i){mw, mw, mw, mw};
+            }
+            hook(kk);
+        }
+        Dec<T>::scales(b, D, M);
+    };
+    auto mfma_pair = [&](const int i, int xb, v4i (&c0)[NP], v4i (&c1)[NP]) __attribute__((always_inline)) {
+        const int8_t* xp = xs + xb * SXB;
+        v4i a0[4], a1[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            a0[kk] = *(const v4i*)(xp + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
+            a1[kk] = *(const v4i*)(xp + (16 * (i + 1) + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++) {
+                c0[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[kk], B[kk][pl], kk ? c0[pl] : (v4i){0, 0, 0, 0}, 0, 0, 0);
+                c1[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[kk], B[kk][pl], kk ? c1[pl] : (v4i){0, 0, 0, 0}, 0, 0, 0);
+            }
+    };
+    // the reference's float steps, rounded one by one (src/cpu_moe.rs:327-377): sum += (D dx) s - (M dx) m
+    auto close_pair = [&](const int i, int xb, const v4i (&c0)[NP], const v4i (&c1)[NP]) __attribute__((always_inline)) {
+        const float* dw = dxs + xb * SDX + SM * wave;
+        const float4 d0 = *(const float4*)(dw + 16 * i + 4 * kl);
+        const float4 d1 = *(const float4*)(dw + 16 * (i + 1) + 4 * kl);
+        const float dq0[4] = {d0.x, d0.y, d0.z, d0.w}, dq1[4] = {d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int iv0 = F::HI ? (c0[P_HI][q] << 8) + c0[P_LO][q] : c0[P_LO][q];
+            const int iv1 = F::HI ? (c1[P_HI][q] << 8) + c1[P_LO][q] : c1[P_LO][q];
+            float f0 = (D * dq0[q]) * (float)iv0, f1 = (D * dq1[q]) * (float)iv1;
+            if constexpr (F::MIN) {
+                f0 = f0 - (M * dq0[q]) * (float)c0[P_M][q];
+                f1 = f1 - (M * dq1[q]) * (float)c1[P_M][q];
+            }
+            acc[i][q] = acc[i][q] + f0;
+            acc[i + 1][q] = acc[i + 1][q] + f1;
+        }
+    };
+    auto tiles = [&](int xb, int ntt) __attribute__((always_inline)) {
+        static_for<0, STT / 2>([&](auto I) {
+            constexpr int i = 2 * decltype(I)::value;
+            if (i < ntt) {
+                v4i c0[NP], c1[NP];
+                mfma_pair(i, xb, c0, c1);
+                close_pair(i, xb, c0, c1);
+            }
+        });
+    };
+    // Results of an item. Pair mode: the up waves (4-7) stage their outputs in the X buffer of this step, the gate
+    // waves (0-3) store silu(gate) x up for their (row, position) outputs. Otherwise each lane stores its own values.
+    auto store = [&](const Item& it, int xb) __attribute__((always_inline)) {
+        const int ntt = (it.cnt + 15) >> 4;
+        const int col = pair ? (rl & 63) : rl;
+        float* yb = a.y + (int64_t)(it.m0 + 4 * kl) * a.y_stride + it.n0 + col;
+        const int left = it.cnt - 4 * kl;
+        if (pair) {
+            float* S = (float*)(xs + xb * SXB);  // [64 positions][64 columns], column XOR-swizzled by 16 kl
+            lds_barrier();                        // every wave's tiles are done with this X buffer
+            if (wave >= 4) {
+                static_for<0, STT>([&](auto I) {
+                    constexpr int i = decltype(I)::value;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) S[(16 * i + 4 * kl + q) * 64 + (col ^ (kl << 4))] = acc[i][q];
+                });
+            }
+            lds_barrier();
+            if (wave < 4) {
+                static_for<0, STT>([&](auto I) {
+                    constexpr int i = decltype(I)::value;
+                    if (i < ntt) {
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            if (16 * i + q < left)
+                                yb[(int64_t)(16 * i + q) * a.y_stride] =
+                                    silu_dev(acc[i][q]) * S[(16 * i + 4 * kl + q) * 64 + (col ^ (kl << 4))];
+                    }
+                });
+            }
+        } else if (it.n0 + rl < a.rows) {
+            auto put = [&](auto OP) __attribute__((always_inline)) {
+                constexpr int op = decltype(OP)::value;
+                static_for<0, STT>([&](auto I) {
+                    constexpr int i = decltype(I)::value;
+                    if (i < ntt) {
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            if (16 * i + q < left) {
+                                float* yp = yb + (int64_t)(16 * i + q) * a.y_stride;
+                                const float v = acc[i][q];
+                                if constexpr (op == STRATA_ACT_STORE) *yp = v;
+                                else if constexpr (op == STRATA_ACT_SWIGLU) *yp = silu_dev(*yp) * v;
+                                else *yp += v;
+                            }
+                        }
+                    }
+                });
+            };
+            if (a.act == STRATA_ACT_STORE) put(std::integral_constant<int, STRATA_ACT_STORE>{});
+            else if (a.act == STRATA_ACT_SWIGLU) put(std::integral_constant<int, STRATA_ACT_SWIGLU>{});
+            else put(std::integral_constant<int, STRATA_ACT_ADD>{});
+        }
+#pragma unroll
+        for (int i = 0; i < STT; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
+    };
+
+    // The step stream: cur (step g), q1 (step g + 1) and the load state L (step g + 2: item index kL, super-block sL).
+    struct Step {
+        Item it;
+        uint32_t rbeg;
+        int s;
+    };
+    int kL = -1, pcL = 0, sL = 0;
+    Item iL = next_item(kL, pcL, Item{0, 0, 0, 0, 0});
+    if (iL.cnt == 0) return;  // no work: no load was issued
+    Addr aL = addr_of(iL);
+    auto advance = [&]() __attribute__((always_inline)) {
+        if (++sL == nsb) {
+            sL = 0;
+            iL = next_item(kL, pcL, iL);
+            if (iL.cnt) aL = addr_of(iL);
+        }
+    };
+    auto issue_all = [&](int xb, int wb) __attribute__((always_inline)) {
+        load_x(aL, sL, xb, 0);
+        load_x(aL, sL, xb, 1);
+        load_dx(aL, sL, xb);
+        load_w(iL, aL, sL, wb);
+    };
+    // prologue: steps 0 and 1
+    Step cur{iL, aL.rbeg, sL};
+    issue_all(0, 0);
+    advance();
+    Step q1{iL, aL.rbeg, sL};
+    if (iL.cnt) {
+        issue_all(1, 1);
+        advance();
+        wait_vm<NLOAD>();
+    } else {
+        wait_vm<0>();
+    }
+    __syncthreads();  // the IQ tables and step 0's X
+
+    int xb = 0, wb = 0;  // buffers of step g
+    while (true) {
+        const bool l2 = iL.cnt != 0;  // step g + 2 exists
+        const int xb2 = xb == 0 ? 2 : xb - 1;
+        decode(cur.rbeg, cur.s, wb, [&](int kk) __attribute__((always_inline)) {
+            if (l2) {
+                if (kk < SXI) load_x(aL, sL, xb2, kk);
+                else if (kk == SXI) load_dx(aL, sL, xb2);
+            }
+        });
+        wait_lds();  // this wave's reads of its raw rows are done: step g + 2's rows take the buffer
+        if (l2) load_w(iL, aL, sL, wb);
+        tiles(xb, (cur.it.cnt + 15) >> 4);
+        const bool last = cur.s + 1 == nsb;
+        if (last) store(cur.it, xb);
+        if (q1.it.cnt == 0) break;  // step g was the block's last
+        cur = q1;
+        if (l2) {
+            q1 = Step{iL, aL.rbeg, sL};
+            advance();
+        } else {
+            q1.it.cnt = 0;
+        }
+        // step g + 1's loads have landed (step g + 2's may still fly, unless an item's stores were issued after them)
+        if (last || !l2) wait_vm<0>();
+        else wait_vm<NLOAD>();
+        lds_barrier();
+        xb = xb == 2 ? 0 : xb + 1;
+        wb ^= 1;
+    }
+}
+
+template <int T>
+static size_t gemm_small_smem() {
+    size_t b = (size_t)NXB * SXB + (size_t)NXB * SDX * 4 + 2 * (size_t)SmallFmt<T>::WBUF;
+    if (T == IQ2_XXS || T == IQ3_S) b += sizeof(IqTables);
+    return b;
+}
+
+template <int T>
+static hipError_t gemm_small_t(const GemmLaunch& g, hipStream_t s) {
+    GemmArgs a{};
+    a.tiles = g.tiles; a.n_tiles_dev = g.n_tiles_dev;
+    a.xq = (const int8_t*)g.xq; a.xd = (const float*)(g.xq + (uint64_t)g.n_x * g.cols);
+    a.xrow = g.xrow; a.y = g.y; a.y_stride = g.y_stride; a.rows = g.rows; a.cols = g.cols; a.act = g.act;
+    a.pair = g.pair ? 1 : 0;
+    a.w2 = g.w2;
+    a.rb = row_bytes(T, g.cols);
+    a.max_tiles = g.n_tiles;
+    const size_t smem = gemm_small_smem<T>();
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)gemm_small_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    static int ncu = 0;
+    if (!ncu) {
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+    }
+    const int gno = g.pair ? SN / 2 : SN;
+    const long long total = (long long)((g.rows + gno - 1) / gno) * g.n_tiles;
+    if (total >= (1ll << 31)) return hipErrorInvalidValue;
+    const long long grid = std::max<long long>(std::min<long long>(total, ncu), 1);  // persistent: one block per CU
+    gemm_small_kernel<T><<<dim3((unsigned)grid), 64 * SW, smem, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_small(const GemmLaunch& g, hipStream_t s) {
+    switch (g.ty) {
+    case Q2_K: return gemm_small_t<Q2_K>(g, s);
+    case Q3_K: return gemm_small_t<Q3_K>(g, s);
+    case Q4_K: return gemm_small_t<Q4_K>(g, s);
+    case Q5_K: return gemm_small_t<Q5_K>(g, s);
+    case Q6_K: return gemm_small_t<Q6_K>(g, s);
+    case IQ2_XXS: return gemm_small_t<IQ2_XXS>(g, s);
+    case IQ3_S: return gemm_small_t<IQ3_S>(g, s);
+    case IQ4_XS: return gemm_small_t<IQ4_XS>(g, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace strata

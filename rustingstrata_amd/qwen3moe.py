@@ -13,8 +13,9 @@ Per prefill chunk of t tokens at position pos (step[0] = pos):
     per layer: h = rms_norm(x) ; q, k, v = gemm_dense(qkv, h) (one GEMM over the layer's q/k/v rows) ;
     rms_norm_rope_qk (q/k norms, NEOX rope, f16 KV store, reading the heads in place) ; attn_prefill (causal) ;
     x += gemm_dense(o, attn) ; h = rms_norm(x) ;
-    logits = gemm_dense(router F32, h) ; router_topk ; moe_sort (on the device) ; gate/up grouped GEMM with the
-    SwiGLU epilogue ; down grouped GEMM ; x += moe_combine_seq.
+    logits = gemm_dense(router F32, h) ; router_topk ; moe_sort (on the device; 64-position tiles and the small-tile
+    GEMM form when the chunk routes few rows to an expert) ; gate/up grouped GEMM with the SwiGLU epilogue ; down
+    grouped GEMM ; x += moe_combine_seq.
 Per decode token (recorded once as a graph and replayed; the step buffer carries the position):
     x = embed(token) ; per layer: h, hq = rms_norm_q(x) ; q, k, v = gemvq (one launch) ; rms_norm_rope_qk with the
     KV store and attn_decode as one launch ; mix = gemvq(o) ; h, hq = rms_norm_q(x + mix) and logits = gemv(router, h) as one launch ;
@@ -168,8 +169,7 @@ class Model:
         self.rl = A(n * E * 4)
         self.ids, self.wts = A(n * k * 4), A(n * k * 4)
         self.off, self.xrow, self.inv = A((E + 1) * 4), A(n * k * 4), A(n * k * 4)
-        self.tchunk = hip.gemm_block_positions()
-        self.max_tiles = n * k // self.tchunk + E
+        self.max_tiles = n * k // 64 + E  # room for the tile lists of either GEMM form (64 or 256 positions a tile)
         self.tiles, self.ntd, self.err = A(2 * self.max_tiles * 16), A(4), A(4)
         self.ge, self.ye = A(n * k * F * 4), A(n * k * H * 4)
         self.tok_in = A(n * 4)
@@ -234,14 +234,16 @@ class Model:
             hip.rms_norm_q(self.x, H, ly.ffn_norm, self.h, H, H, t, c.eps, xq=self.hqp if xq_ok else 0)
             hip.gemm_dense(ly.router, t, self.h, H, self.rl, E, ACT_STORE)
             hip.router_topk(self.rl, E, k, 0.0, self.ids, self.wts, t)
+            # few routed rows an expert (short chunks): 64-position tiles and the GEMM form for them
+            tchunk, small = hip.moe_tile_plan(t, k, E)
             hip.moe_sort(self.ids, t, k, E, self.off, self.xrow, self.inv,
                          [(int(ly.gate_up), ly.e_gu), (int(ly.down), ly.e_down)], self.tiles, self.max_tiles,
-                         self.ntd, err_dev=self.err, chunk=self.tchunk)
+                         self.ntd, err_dev=self.err, chunk=tchunk)
             hip.gemm_grouped_gate_up(c.ty_gate_up, F, H, self.tiles, self.max_tiles, self.ntd,
                                      self.hqp if xq_ok else self.h, H, t, self.xrow, self.ge, F, ly.up_off,
-                                     flags=X_Q if xq_ok else 0)
+                                     flags=(X_Q if xq_ok else 0) | small)
             hip.gemm_grouped(c.ty_down, H, F, int(self.tiles) + self.max_tiles * 16, self.max_tiles, self.ntd, self.ge,
-                             F, t * k, 0, self.ye, H, ACT_STORE)
+                             F, t * k, 0, self.ye, H, ACT_STORE | small)
             hip.moe_combine_seq(self.x, self.ye, self.wts, self.inv, k, 0, 0, H, t)
             if layer_hook:
                 layer_hook(il, self.x)

@@ -636,10 +636,12 @@ def tile_list(hip, base, stride, spans):
 
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K,
                                 ggml.Q8_0])
-def test_gemm_tiles_match_cpu(hip, ty):
+@pytest.mark.parametrize("fl", [0, S.SMALL_TILES], ids=["blocks256", "small64"])
+def test_gemm_tiles_match_cpu(hip, ty, fl):
     """tests/kernels.rs:355-447: tiles (0, 128), (128, 16), (144, 26) with X gathered through xrow; act store, then
     SwiGLU into the stored gate, then add. Tiles (170, 256) and (426, 200) fill this backend's 256-position blocks;
-    200 rows give one whole 128-row block (outputs staged through LDS) and a partial one (stored lane by lane)."""
+    200 rows give one whole 128-row block (outputs staged through LDS) and a partial one (stored lane by lane).
+    SMALL_TILES: the 64-position kernel (tiles past 64 positions taken as several items), the same bits."""
     rows, cols, E, n_x = 200, 512, 3, 100
     rb = ggml.row_bytes(ty, cols)
     w = random_blocks(ty, E * rows, cols, seed=ty)
@@ -651,7 +653,7 @@ def test_gemm_tiles_match_cpu(hip, ty):
     tiles, nt = tile_list(hip, int(wb), rows * rb, spans)
     y = hip.alloc(npos * rows * 4)
     xb, xr = up(hip, x), up(hip, xrow)
-    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_STORE)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_STORE | fl)
     got = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
     want = np.zeros((npos, rows), dtype=np.float32)
     for e, m0, c in spans:
@@ -664,17 +666,18 @@ def test_gemm_tiles_match_cpu(hip, ty):
         # each 32-value sub-block in float on the CPU (src/cpu_moe.rs:195-212), here once per super-block.
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), int((got != want).sum())
     # act 1: y = silu(y) * (W x) with the same x (SAME_X), then act 2: y += W x
-    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_SWIGLU | S.SAME_X)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_SWIGLU | S.SAME_X | fl)
     got2 = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
     want2 = want / (1 + np.exp(-want.astype(np.float64))) * want
     assert max_rel_err(got2, want2) <= TOL
-    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_ADD | S.SAME_X)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_ADD | S.SAME_X | fl)
     got3 = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
     assert max_rel_err(got3, want2 + want) <= TOL
 
 
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
-def test_gemm_gate_up_fused_matches_two_calls(hip, ty):
+@pytest.mark.parametrize("fl", [0, S.SMALL_TILES], ids=["blocks256", "small64"])
+def test_gemm_gate_up_fused_matches_two_calls(hip, ty, fl):
     """gemm_grouped_gate_up gives the bits of gemm (gate, act store) followed by gemm (up, act SwiGLU, same X) over the
     same tiles (src/gpu_model/prefill.rs), with partial and full 256-position tiles and 3 column blocks of 64."""
     rows, cols, E, n_x = 192, 512, 3, 100
@@ -693,7 +696,7 @@ def test_gemm_gate_up_fused_matches_two_calls(hip, ty):
     y1, y2 = hip.alloc(npos * rows * 4), hip.alloc(npos * rows * 4)
     hip.gemm(ty, rows, cols, tg, nt, xb, cols, n_x, xr, y1, rows, S.ACT_STORE)
     hip.gemm(ty, rows, cols, tu, nt, xb, cols, n_x, xr, y1, rows, S.ACT_SWIGLU | S.SAME_X)
-    hip.gemm_grouped_gate_up(ty, rows, cols, tg, nt, ntd, xb, cols, n_x, xr, y2, rows, up_off)
+    hip.gemm_grouped_gate_up(ty, rows, cols, tg, nt, ntd, xb, cols, n_x, xr, y2, rows, up_off, flags=fl)
     a, b = down(hip, y1, np.float32, npos * rows), down(hip, y2, np.float32, npos * rows)
     assert np.array_equal(a, b), np.abs(a - b).max()
     # against the oracle through the gate and up results
@@ -760,8 +763,9 @@ def test_moe_prefill_layer_matches_experts_multi(hip):
     want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, hs, ids_w, wts_w)
     got = run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits)
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
-    # gate and up as one grouped GEMM: the same bits
+    # gate and up as one grouped GEMM, and the 64-position kernel over 64-position tiles: the same bits
     assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True), got)
+    assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True, small=True), got)
 
 
 def test_moe_prefill_layer_full_size(hip):
@@ -791,18 +795,21 @@ def test_moe_prefill_layer_512_tokens(hip):
     ids_w, wts_w = O.route(logits, k)
     want = O.experts_multi(ggml.Q5_K, ggml.Q6_K, gate, upw, dn, H, F, hs, ids_w, wts_w,
                            threads=min(16, os.cpu_count() or 1))
-    got = run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True)
+    got = run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True, small=True)
     assert max_rel_err(got, want) <= TOL, max_rel_err(got, want)
-    assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits), got)
+    assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, small=True), got)
+    assert np.array_equal(run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=True), got)
 
 
-def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=False):
+def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=False, small=False):
+    """The prefill MoE block; small: tiles of at most 64 positions and the 64-position GEMM kernel."""
     rb_gu, rb_d = ggml.row_bytes(ggml.Q5_K, H), ggml.row_bytes(ggml.Q6_K, F)
     g_b, u_b, d_b = up(hip, gate), up(hip, upw), up(hip, dn)
     hb, lb = up(hip, hs), up(hip, logits)
     ids, wts = hip.alloc(T * k * 4), hip.alloc(T * k * 4)
     hip.router_topk(lb, E, k, 0.0, ids, wts, T)
-    chunk = hip.gemm_block_positions()
+    chunk = 64 if small else hip.gemm_block_positions()
+    fl = S.SMALL_TILES if small else 0
     max_tiles = T * k // chunk + E
     off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
     tiles, ntd = hip.alloc(3 * max_tiles * 16), hip.alloc(4)
@@ -810,13 +817,14 @@ def run_prefill(hip, E, H, F, T, k, gate, upw, dn, hs, logits, fused=False):
                  tiles, max_tiles, ntd, chunk=chunk)
     ge, ye = hip.alloc(T * k * F * 4), hip.alloc(T * k * H * 4)
     if fused:
-        hip.gemm_grouped_gate_up(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b))
+        hip.gemm_grouped_gate_up(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, int(u_b) - int(g_b),
+                                 flags=fl)
     else:
-        hip.gemm_grouped(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, S.ACT_STORE)
+        hip.gemm_grouped(ggml.Q5_K, F, H, tiles, max_tiles, ntd, hb, H, T, xrow, ge, F, S.ACT_STORE | fl)
         hip.gemm_grouped(ggml.Q5_K, F, H, int(tiles) + max_tiles * 16, max_tiles, ntd, hb, H, T, xrow, ge, F,
-                         S.ACT_SWIGLU | S.SAME_X)
+                         S.ACT_SWIGLU | S.SAME_X | fl)
     hip.gemm_grouped(ggml.Q6_K, H, F, int(tiles) + 2 * max_tiles * 16, max_tiles, ntd, ge, F, T * k, 0, ye, H,
-                     S.ACT_STORE)
+                     S.ACT_STORE | fl)
     x = hip.alloc(T * H * 4)
     hip.moe_combine_seq(x, ye, wts, inv, k, 0, 0, H, T)
     return down(hip, x, np.float32, T * H).reshape(T, H)
