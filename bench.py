@@ -253,14 +253,27 @@ def bench_moe(hip, S, ggml, T, iters, ty_gu=None, ty_d=None, small=None):
     ops = T * k * 3 * F * H * 2
     # per kernel: the gate/up launch (its x quantization included) and the down launch (h quantization included);
     # issued int8 ops count every digit plane (the MFMA work done), useful ops the matrix product
+    # HBM bytes per launch of each GEMM from rocprofv3 FETCH_SIZE / WRITE_SIZE scaled by a copy kernel
+    # (profiles/moe_prefill_4k.md, the 4096-token configs[2] layer); None for other shapes or when absent
+    traffic = {}
+    prof = os.path.join(ROOT, "profiles", "moe_prefill_4k.md")
+    if T == 4096 and ty_gu == ggml.Q5_K and ty_d == ggml.Q6_K and os.path.exists(prof):
+        for line in open(prof):
+            if line.startswith("traffic_bytes_per_launch "):
+                name, v = line[len("traffic_bytes_per_launch "):].split(":")
+                traffic[name.strip()] = int(v)
     roof = {"bound": "mfma", "unit": "TOP/s", "peak": INT8_PEAK_TOPS,
             "achieved": round(ops / (gemm / 1e3) / 1e12, 1), "frac": round(ops / (gemm / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
-            "traffic": None, "kernels": {}}
+            "traffic": sum(traffic.values()) if len(traffic) == 2 else None, "kernels": {}}
+    wbytes = {"gate_up": E * 2 * F * rb_gu, "down": E * H * rb_d}  # every expert's weights, read once
     for name, ty, ms, kops in (("gate_up", ty_gu, gu, T * k * 2 * F * H * 2), ("down", ty_d, gemm - gu, T * k * F * H * 2)):
         planes = gemm_digit_planes(ggml, ty)
         roof["kernels"][name] = {"type": ggml.NAMES[ty], "us": round(1000 * ms, 1), "useful_TOPS": round(kops / (ms / 1e3) / 1e12, 1),
                                  "digit_planes": planes,
-                                 "issued_frac": round(planes * kops / (ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4)}
+                                 "issued_frac": round(planes * kops / (ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
+                                 "weight_bytes": wbytes[name],
+                                 "hbm_floor_us": round(wbytes[name] / HBM_PEAK_GBS / 1e3, 1),
+                                 "traffic": traffic.get(name)}
     return {"roofline": roof, "tokens": T, "ms_layer": round(tot, 4), "tok_per_s": round(T / (tot / 1e3), 1),
             "grouped_gemm_ms": round(gemm, 4), "int8_TOPS": round(ops / (gemm / 1e3) / 1e12, 1),
             "mfma_frac": round(ops / (gemm / 1e3) / 1e12 / INT8_PEAK_TOPS, 4), "ops": ops,
@@ -469,7 +482,9 @@ def bench_codebook(hip, S, ggml, iters):
         ops = T * k * rows * cols * 2
         out[name] = {"decode_us": round(us, 2), "decode_GB/s": round(bts / us / 1e3, 1),
                      "decode_pct_peak": round(100 * bts / us / 1e3 / HBM_PEAK_GBS, 1),
-                     "prefill512_gemm_ms": round(gemm_ms, 4), "prefill512_int8_TOPS": round(ops / (gemm_ms / 1e3) / 1e12, 1)}
+                     "prefill512_gemm_ms": round(gemm_ms, 4), "prefill512_int8_TOPS": round(ops / (gemm_ms / 1e3) / 1e12, 1),
+            "prefill512_hbm_floor_us": round(E * rows * rb / HBM_PEAK_GBS / 1e3, 1),
+            "prefill512_gemm_kernel": "64-position tiles (SMALL_TILES)" if fl else f"{chunk}-position tiles"}
         hip.drop_graphs()
     return out
 
@@ -648,7 +663,8 @@ def main():
     ap.add_argument("--profile-gemv", action="store_true",
                     help="only run the Q4_K lm-head GEMV and a 256 MB copy kernel 50 times each (for rocprofv3)")
     ap.add_argument("--profile-moe", action="store_true",
-                    help="only run the configs[2] 4K-token MoE prefill layer (--moe-iters times, for rocprofv3)")
+                    help="only run the configs[2] MoE prefill layer at 4096 and 512 tokens (--moe-iters times each) "
+                         "and a 256 MiB copy kernel as often (for rocprofv3)")
     ap.add_argument("--profile-attn", action="store_true",
                     help="only configs[4]'s decode attention (+ merge) at 256, 1024 and 4100 positions")
     ap.add_argument("--profile-decode", action="store_true",
@@ -679,7 +695,14 @@ def main():
         print(json.dumps({"moe_decode_1": bench_moe_decode(hip, S, ggml, 200)}), flush=True)
         return
     if args.profile_moe:
-        print(json.dumps({"moe_prefill_4k": bench_moe(hip, S, ggml, 4096, args.moe_iters)}), flush=True)
+        out = {"moe_prefill_4k": bench_moe(hip, S, ggml, 4096, args.moe_iters),
+               "moe_prefill_512": bench_moe(hip, S, ggml, 512, args.moe_iters)}
+        # a plain copy of known size, to scale the GEMMs' FETCH_SIZE / WRITE_SIZE counters
+        src, dst = hip.alloc(256 << 20), hip.alloc(256 << 20)
+        for _ in range(args.moe_iters):
+            hip.copy_kernel(src, dst, 256 << 20)
+        hip.sync()
+        print(json.dumps(out), flush=True)
         return
     if args.stack_only:
         print(json.dumps({"stack_config4": bench_stack(hip, S, ggml)}), flush=True)
