@@ -176,6 +176,15 @@ int strata_rms_norm_q(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t w
 int strata_combine_rms_norm_q(strata_ctx* ctx, uint64_t x, uint64_t x_stride, uint64_t ye, uint64_t wh, uint64_t k,
                               uint64_t w, uint64_t out, uint64_t out_stride, uint64_t n, uint64_t rows, float eps,
                               uint64_t xq, uint64_t res);
+/* No single counterpart in the reference (a decode fusion of src/gpu_model.rs:3383-3412 and 1950-2016): the MoE
+ * combine of one token with the next norm and the GEMV that reads it, in one launch. x_out = x + res + sum_j wh[j]
+ * ye[j] (slots j < k in order, rows of n = w->cols floats; res may be 0, k may be 0), then y = W h with h =
+ * rms_norm(x_out) * nw quantized as Q8_K: the bits of strata_combine_rms_norm_q (strata_rms_norm_q with res when
+ * k = 0) followed by strata_gemvq on its quantized output. x is only read (every block of the GEMV normalizes the row
+ * itself), x_out (when not 0) is written, and must not be x. One row of at most 2048 values (a multiple of 8),
+ * k <= 8, 16-byte aligned rows, STRATA_NUM_Q8K; otherwise an error, and the caller makes the two calls. */
+int strata_combine_rms_norm_gemv(strata_ctx* ctx, uint64_t x, uint64_t res, uint64_t ye, uint64_t wh, uint64_t k,
+                                 uint64_t nw, float eps, const strata_tensor* w, uint64_t x_out, uint64_t y);
 /* Backend::rms_norm_q of one row (src/backend.rs:233-235) followed by Backend::gemv of an F32 matrix on its output
  * (the decode's FFN norm and router logits, src/gpu_model.rs:3370-3383) in one launch: h = rms_norm(x + res) * nw
  * (strata_rms_norm_q's bits), xq its quantization (when not 0), y = w h (strata_gemv's bits for an F32 matrix of n

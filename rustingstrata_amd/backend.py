@@ -66,6 +66,7 @@ SIGNATURES = {
                                   ctypes.c_float, U64, U64, ctypes.c_float, U64, U64, U64, U64],
     "strata_combine_rms_norm_q": [CTX, U64, U64, U64, U64, U64, U64, U64, U64, U64, U64, ctypes.c_float, U64, U64],
     "strata_rms_norm_q_gemv_f32": [CTX, U64, U64, U64, U64, U64, U64, ctypes.c_float, TP, U64],
+    "strata_combine_rms_norm_gemv": [CTX, U64, U64, U64, U64, U64, U64, ctypes.c_float, TP, U64, U64],
     "strata_gemv": [CTX, TP, U64, U64],
     "strata_gemvn": [CTX, TP, U64, U64, U64, U64, U64],
     "strata_gemvn_noalloc": [CTX, TP, U64, U64, U64, U64, U64],
@@ -339,7 +340,14 @@ class HipBackend:
         _check(lib().strata_combine_rms_norm_q(self._ctx, int(x), n, int(ye), int(wh), k, int(w), int(out), n, n, rows,
                                                eps, int(xq), int(res)))
 
-    RMS_NORM_GEMV_MAX = 2048  # values of a row the fused norm + F32 GEMV launch takes
+    RMS_NORM_GEMV_MAX = 2048  # values of a row the fused norm + GEMV launches take
+
+    def combine_rms_norm_gemv(self, x, res, ye, wh, k, nw, eps, w, x_out, y):
+        """x_out = x + res + sum_j wh[j] ye[j] (j < k), y = W rms_norm(x_out) nw, one launch (the bits of
+        combine_rms_norm_q then gemvq); res, ye / wh (k = 0) and x_out may be 0."""
+        _check(lib().strata_combine_rms_norm_gemv(self._ctx, int(x), int(res), int(ye), int(wh), k, int(nw), eps,
+                                                   w._c(), int(x_out), int(y)))
+
 
     def rms_norm_q_gemv_f32(self, x, res, nw, h, xq, n, eps, w, y):
         """h = rms_norm(x + res) * nw (and xq), y = w h for an F32 matrix, one launch; x is not written."""

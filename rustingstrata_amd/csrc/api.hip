@@ -409,6 +409,30 @@ int strata_combine_rms_norm_q(strata_ctx* c, uint64_t x, uint64_t x_stride, uint
     return strata_rms_norm_q(c, x, x_stride, w, out, out_stride, n, rows, eps, xq, 0);
 }
 
+int strata_combine_rms_norm_gemv(strata_ctx* c, uint64_t x, uint64_t res, uint64_t ye, uint64_t wh, uint64_t k,
+                                 uint64_t nw, float eps, const strata_tensor* w, uint64_t x_out, uint64_t y) {
+    if (check_ctx(c) || check_tensor(w, "combine_rms_norm_gemv")) return -1;
+    if (!x || !nw || !y || (k && (!ye || !wh))) return set_error("combine_rms_norm_gemv: null x, nw, y, ye or wh");
+    const uint64_t n = w->cols;
+    if (k > 8 || n > 2048 || n % 8 || x_out == x || c->numerics != STRATA_NUM_Q8K ||
+        ((x | res | ye | nw | x_out) % 16))
+        return set_error("combine_rms_norm_gemv: one row of at most 2048 values (a multiple of 8, 16-byte aligned), "
+                         "at most 8 slots, x_out not x, Q8_K numerics (" + std::to_string(n) + " values, " +
+                         std::to_string(k) + " slots)");
+    if (check_gemv_cols(w->ty, w->cols, false) || check_align(w->ty, w->ptr, "combine_rms_norm_gemv")) return -1;
+    if (w->rows == 0 || w->rows > (1u << 30)) return set_error("combine_rms_norm_gemv: " + std::to_string(w->rows) + " rows");
+    GemvLaunch g;
+    g.xf = (const float*)x; g.x_stride = n;
+    g.ty = w->ty; g.w = (const uint8_t*)w->ptr; g.rows = (int)w->rows; g.cols = (int)n;
+    g.nt = 1; g.n_xrows = 1; g.y = (float*)y; g.numerics = c->numerics;
+    g.nw = (const float*)nw; g.nres = (const float*)res; g.nye = (const float*)ye; g.nwh = (const float*)wh;
+    g.nxw = (float*)x_out; g.neps = eps; g.nck = (int)k;
+    const hipError_t e = launch_gemv(g, c->stream);
+    if (e == hipErrorNotSupported) return set_error(std::string("combine_rms_norm_gemv: ") + type_name(w->ty) + " not supported");
+    STRATA_HIP(e);
+    return 0;
+}
+
 int strata_rms_norm_q_gemv_f32(strata_ctx* c, uint64_t x, uint64_t res, uint64_t nw, uint64_t h, uint64_t xq,
                                uint64_t n, float eps, const strata_tensor* w, uint64_t y) {
     if (check_ctx(c)) return -1;

@@ -55,6 +55,16 @@ struct GemvArgs {
     float* rwh;
     float rscale;
     int rn, rsig;
+    // single-input plain kernel with the norm prologue (MODE bit 5): x (xf) is first h = rms_norm(x + nres + sum_j
+    // nwh[j] nye[j]) * nw (rms_norm_q_kernel's one-round-trip arithmetic, combine slots in order), the GEMV then
+    // runs on h; block 0 writes x + nres + the combine to nxw (when not null; never xf itself: other blocks read it)
+    const float* nw;
+    const float* nres;
+    const float* nye;
+    const float* nwh;
+    float* nxw;
+    float neps;
+    int nck;
 };
 
 // LDS layout: [IqTables (IQ types)][x int8: nt * cols][x scales: nt * cols / 32 f32][x sums: nt * cols / 16
@@ -364,16 +374,44 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int xrow, int8_t* xl,
 // and quantization overlap the weights' flight: (f32 x) this thread's 8 values of each half (XH values); (xq) its
 // 16-byte chunk and scale.
 constexpr int XH = 8 * GEMV1_THREADS;  // values of one half of an early x row
+constexpr int NORM_SLOTS = 8;  // combine slots the norm prologue takes
 struct XEarly {
     v4f f0, f1, u0, u1, f2, f3;
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     v4u q;
     float d;
+    // norm prologue: this thread's 8 values of res and nw, and of each combine slot, with the slots' weights
+    v4f r0, r1, w0, w1, y0[NORM_SLOTS], y1[NORM_SLOTS];
+    float ws[NORM_SLOTS];
 };
-template <bool SW>
+template <bool SW, bool NORM = false>
 __device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) {
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x;
+    if constexpr (NORM) {
+        // one row of at most 2048 values: thread tid's values 8 tid .. 8 tid + 7, as rms_norm_q_kernel holds them
+        if (8 * tid < a.cols) {
+            const uint64_t o = 32 * (uint64_t)tid;
+            e.f0 = *gptr<v4f>((uint64_t)a.xf + o);
+            e.f1 = *gptr<v4f>((uint64_t)a.xf + o + 16);
+            e.w0 = *gptr<v4f>((uint64_t)a.nw + o);
+            e.w1 = *gptr<v4f>((uint64_t)a.nw + o + 16);
+            if (a.nres) {
+                e.r0 = *gptr<v4f>((uint64_t)a.nres + o);
+                e.r1 = *gptr<v4f>((uint64_t)a.nres + o + 16);
+            }
+#pragma unroll
+            for (int u = 0; u < NORM_SLOTS; u++) {
+                e.ws[u] = u < a.nck ? a.nwh[u] : 0.0f;
+                if (u < a.nck) {
+                    const uint64_t yr = (uint64_t)(a.nye + (uint64_t)u * a.cols) + o;
+                    e.y0[u] = *gptr<v4f>(yr);
+                    e.y1[u] = *gptr<v4f>(yr + 16);
+                }
+            }
+        }
+        return;
+    }
     if (a.xq) {
         if (tid < a.cols / 16) e.q = *gptr<v4u>((uint64_t)(a.xq + (uint64_t)xrow * a.cols) + 16 * tid);
         if (tid < a.cols / 32) e.d = *gptr<float>((uint64_t)(a.xd + (uint64_t)xrow * (a.cols / 32)) + 4 * tid);
@@ -395,10 +433,69 @@ __device__ __forceinline__ void x_fetch(const GemvArgs& a, int xrow, XEarly& e) 
             }
     }
 }
-template <bool Q32, bool SW>
-__device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t* xl, float* xld, int* xss) {
+template <bool Q32, bool SW, bool NORM = false>
+__device__ __forceinline__ void x_put(const GemvArgs& a, const XEarly& e, int8_t* xl, float* xld, int* xss,
+                                      float* npart = nullptr) {
     typedef unsigned v4u __attribute__((ext_vector_type(4)));
     const int tid = threadIdx.x, n = a.cols;
+    if constexpr (NORM) {
+        // rms_norm_q_kernel's one-round-trip path, operation for operation: x + res, then the combine's products
+        // added in slot order (a slot of weight 0 adds nothing), the per-thread sum of squares, the DPP sum within
+        // 32 lanes, the 8 half-waves in order; then h = v * scale * nw, quantized as quant_xq does
+        const int i = 8 * tid;
+        const bool live = i < n;
+        float v[8], wn[8];
+        if (live) {
+            const float xv[8] = {e.f0.x, e.f0.y, e.f0.z, e.f0.w, e.f1.x, e.f1.y, e.f1.z, e.f1.w};
+            const float wv[8] = {e.w0.x, e.w0.y, e.w0.z, e.w0.w, e.w1.x, e.w1.y, e.w1.z, e.w1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) { v[j] = xv[j]; wn[j] = wv[j]; }
+            if (a.nres) {
+                const float rv[8] = {e.r0.x, e.r0.y, e.r0.z, e.r0.w, e.r1.x, e.r1.y, e.r1.z, e.r1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = v[j] + rv[j];
+            }
+            if (a.nck) {
+                float y[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int u = 0; u < NORM_SLOTS; u++) {
+                    if (e.ws[u] != 0.0f) {
+                        const float yv[8] = {e.y0[u].x, e.y0[u].y, e.y0[u].z, e.y0[u].w,
+                                             e.y1[u].x, e.y1[u].y, e.y1[u].z, e.y1[u].w};
+#pragma unroll
+                        for (int q = 0; q < 8; q++) y[q] += e.ws[u] * yv[q];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = v[j] + y[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = wn[j] = 0.0f;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) s += v[j] * v[j];
+        s += xl32f<0>(s);
+        s += xl32f<1>(s);
+        s += xl32f<2>(s);
+        s += xl32f<3>(s);
+        s += xl32f<4>(s);
+        if ((tid & 31) == 0) npart[tid >> 5] = s;
+        if (blockIdx.x == 0 && a.nxw && live) {
+            *(float4*)(a.nxw + i) = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4*)(a.nxw + i + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 8; h++) tot += npart[h];
+        const float sc = 1.0f / sqrtf(tot / (float)n + a.neps);
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = live ? v[j] * sc * wn[j] : 0.0f;
+        quant8_lds<Q32>(v, i, live, xl, xld, xss);
+        return;
+    }
     if (a.xq) {
         if (tid < n / 16) {
             *(v4u*)(xl + xpad(16 * tid)) = e.q;
@@ -469,7 +566,8 @@ static void magic(uint32_t d, uint32_t& m, int& s) {
 // (GemvArgs::small: GEMV1_CH_SMALL loads a thread, a smaller LDS tile).
 template <int T, bool Q32, int MODE>
 __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
-    constexpr bool SW = MODE & 1, QU = MODE & 2, plain = MODE & 4, ROUTE = MODE & 8;
+    constexpr bool SW = MODE & 1, QU = MODE & 2, plain = MODE & 4, ROUTE = MODE & 8, NORM = MODE & 32;
+    static_assert(!NORM || (plain && !SW && !ROUTE), "the norm prologue is for one plain matrix");
     constexpr int CH = (MODE & 16) ? GEMV1_CH_SMALL : plain ? gemv1_ch(T) : GEMV1_CH, TILE = GEMV1_THREADS * 16 * CH;
     constexpr bool IQ = T == IQ2_XXS || T == IQ3_S;
     constexpr int SBB = sb_bytes(T);
@@ -566,7 +664,8 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     int t = next_valid(blockIdx.x);
     if (t >= total) return;
     Span sp = span(t);
-    if (!ROUTE && early) x_fetch<SW>(a, sp.xrow, xe);
+    if (!ROUTE && early) x_fetch<SW, NORM>(a, sp.xrow, xe);
+    __shared__ float npart[NORM ? 8 : 1];  // the norm prologue's half-wave sums
     issue(sp);
     // the IQ codebooks into registers behind the first tile's loads (both round trips at once), into LDS before the
     // first tile is computed
@@ -585,7 +684,7 @@ __global__ __launch_bounds__(GEMV1_THREADS) void gemv1_kernel(GemvArgs a) {
     while (true) {
         __syncthreads();  // the previous tile's readers are done with the LDS tile
         if (sp.xrow != cur_xrow) {
-            if (early && cur_xrow < 0) x_put<Q32, SW>(a, xe, xl, xld, xss);
+            if (early && cur_xrow < 0) x_put<Q32, SW, NORM>(a, xe, xl, xld, xss, npart);
             else stage_x<Q32, SW>(a, sp.xrow, xl, xld, xss);
             __syncthreads();
             // every lane has its slice before the copy can change again: the next staging follows the loop's barrier
@@ -688,7 +787,17 @@ static hipError_t gemv1_launch(const GemvArgs& a, long long tiles, size_t smem, 
 template <int T>
 static hipError_t gemv1_t(const GemvArgs& a, long long tiles, size_t smem, hipStream_t s) {
     const int mode = (a.xu ? 1 : 0) | (a.quarter ? 2 : 0) | (!a.xu && !a.ids && a.nz == 1 ? 4 : 0) | (a.rp ? 8 : 0) |
-                     (a.small ? 16 : 0);
+                     (a.small ? 16 : 0) | (a.nw ? 32 : 0);
+    if (a.nw) {  // the norm prologue: one plain matrix, Q8_K numerics
+        if (a.per32) return hipErrorNotSupported;
+        switch (mode) {
+        case 36: return gemv1_launch<T, false, 36>(a, tiles, smem, s);
+        case 38: return gemv1_launch<T, false, 38>(a, tiles, smem, s);
+        case 52: return gemv1_launch<T, false, 52>(a, tiles, smem, s);
+        case 54: return gemv1_launch<T, false, 54>(a, tiles, smem, s);
+        default: return hipErrorNotSupported;
+        }
+    }
     switch (mode) {
     case 20: return a.per32 ? gemv1_launch<T, true, 20>(a, tiles, smem, s) : gemv1_launch<T, false, 20>(a, tiles, smem, s);
     case 22: return a.per32 ? gemv1_launch<T, true, 22>(a, tiles, smem, s) : gemv1_launch<T, false, 22>(a, tiles, smem, s);
@@ -758,6 +867,7 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     a.per32 = g.numerics == STRATA_NUM_Q8_32;
     a.rp = g.rp; a.rtable = g.rtable; a.rids = g.rids; a.rwts = g.rwts; a.rwh = g.rwh; a.rscale = g.rscale;
     a.rn = g.rn; a.rsig = g.rsig;
+    a.nw = g.nw; a.nres = g.nres; a.nye = g.nye; a.nwh = g.nwh; a.nxw = g.nxw; a.neps = g.neps; a.nck = g.nck;
     {
         int nsb = (g.cols + 255) / 256;
         a.G = 1;
@@ -790,7 +900,11 @@ hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s) {
     // x already quantized (no per-block quantization to amortize), or Q8_0 (whose per-32 float closes make a lane's
     // dot chain the longest), and one matrix: tiles of one wave pass (the quarter split) when they all fit one round of
     // blocks (Q6_K 5120 x 2048 from xq: 5.1 -> 4.7 us; 2048 x 4096: 4.9 -> 4.2 us; Q8_0 6144 x 2048: 6.9 -> 5.7 us)
-    if (single && (g.xq || g.ty == Q8_0) && !g.ids && !g.pair && a.R > 64 / a.G &&
+    if (g.nw && !(single && plain1 && !g.xq && g.cols <= 2048 && g.cols % 8 == 0 && g.nck >= 0 &&
+                  g.nck <= NORM_SLOTS && (g.nck == 0 || (g.nye && g.nwh)) && g.nxw != g.xf &&
+                  (((uintptr_t)g.xf | (uintptr_t)g.nw | (uintptr_t)g.nres | (uintptr_t)g.nye | (uintptr_t)g.nxw) % 16) == 0))
+        return hipErrorNotSupported;
+    if (single && (g.xq || g.ty == Q8_0 || g.nw) && !g.ids && !g.pair && a.R > 64 / a.G &&
         (long long)(maxrows + 64 / a.G - 1) / (64 / a.G) <= 3LL * ncu)
         a.R = std::min(64 / a.G, rmax);
     a.ntr = (maxrows + a.R - 1) / a.R;

@@ -52,6 +52,16 @@ struct GemvLaunch {
     float* rwh = nullptr;
     float rscale = 0.0f;
     int rn = 0, rsig = 0;
+    // one plain matrix, single f32 input xf of at most 2048 values: the GEMV runs on h = rms_norm(xf + nres + sum_j
+    // nwh[j] nye[j] (j < nck <= 8, rows of cols floats)) * nw with rms_norm_q's arithmetic; block 0 writes xf + nres +
+    // the combine to nxw (may be null; not xf). hipErrorNotSupported: any other shape.
+    const float* nw = nullptr;
+    const float* nres = nullptr;
+    const float* nye = nullptr;
+    const float* nwh = nullptr;
+    float* nxw = nullptr;
+    float neps = 0.0f;
+    int nck = 0;
 };
 hipError_t launch_gemv(const GemvLaunch& g, hipStream_t s);
 // moe_down_combine as one launch: x[tk] += sum_j wh[tk k + j] W_{slots[j]} x_j (slots in order) + the shared expert,

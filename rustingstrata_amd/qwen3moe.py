@@ -17,11 +17,13 @@ Per prefill chunk of t tokens at position pos (step[0] = pos):
     GEMM form when the chunk routes few rows to an expert) ; gate/up grouped GEMM with the SwiGLU epilogue ; down
     grouped GEMM ; x += moe_combine_seq.
 Per decode token (recorded once as a graph and replayed; the step buffer carries the position):
-    x = embed(token) ; per layer: h, hq = rms_norm_q(x) ; q, k, v = gemvq (one launch) ; rms_norm_rope_qk with the
+    x = embed(token) ; per layer: x += mix + the previous layer's combine, h = rms_norm(x), q, k, v = W h as one
+    launch (combine_rms_norm_gemv; x alternates between two rows) ; rms_norm_rope_qk with the
     KV store and attn_decode as one launch ; mix = gemvq(o) ; h, hq = rms_norm_q(x + mix) and logits = gemv(router, h) as one launch ;
     moe_route and the paired gate/up moe_gemv as one launch (moe_route_gemv) ; the down GEMV (moe_down_swiglu_combine, SwiGLU inside) ; its
-    x += mix and the combine x += sum w y run with the next layer's attention norm (combine_rms_norm_q) ; then the
-    output norm (with the last of them), output gemv, argmax_rows.
+    x += mix and the combine x += sum w y run with the next layer's attention norm and q/k/v GEMV ; then the
+    output norm and output gemv (with the last of them, one launch), argmax_rows. Rows wider than 2048 values take
+    the separate launches (combine_rms_norm_q, gemvq; rms_norm_q, gemv).
 """
 import numpy as np
 
@@ -160,6 +162,7 @@ class Model:
         A = hip.alloc
         # prefill buffers (rows of the chunk)
         self.x = A(n * H * 4)
+        self.x2 = A(H * 4)  # the decode's second hidden-state row
         self.h = A(n * H * 4)
         self.qkvp = A(n * (nh * hd + 2 * kv) * 4)  # the chunk's q, k and v rows from one GEMM
         self.hqp = A(n * (H + H // 8))  # h quantized by the norms (quant_xq layout), the GEMMs' X
@@ -269,17 +272,34 @@ class Model:
         hip, c, w = self.hip, self.c, self.w
         H, nh, nkv, hd, E, k, F = c.n_embd, c.n_head, c.n_head_kv, c.head_dim, c.n_expert, c.n_expert_used, c.n_ff_exp
         kv = nkv * hd
-        x = self.x  # row 0
-        # the FFN norm and the router logits as one launch take rows of up to 2048 values
+        # the FFN norm and the router logits as one launch, and a layer's combine with the next norm and the GEMV
+        # reading it as one launch, take rows of up to 2048 values (and at most 8 slots, Q8_K numerics)
         fused_router = H <= self.hip.RMS_NORM_GEMV_MAX
+        fused_qkv = fused_router and k <= 8 and hip.numerics() == NUM_Q8K
+        # the hidden state: in the fused form every q/k/v GEMV block reads x while block 0 writes x + mix + the
+        # combine, so the layers alternate between two rows
+        xs = [self.x, self.x2]
+        cur = 0
+        x = xs[cur]
         hip.get_rows(w.embd, self.tok, 1, x)
         for li, ly in enumerate(w.layers):
-            if li == 0:
-                hip.rms_norm_q(x, H, ly.attn_norm, self.h, H, H, 1, c.eps, xq=self.hq)
-            else:  # the previous layer's x += mix, its combine (x += sum w y) and this layer's attention norm
-                hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, ly.attn_norm, self.h, H, 1, c.eps, xq=self.hq,
-                                       res=self.mix if fused_router else 0)
-            hip.gemvq(ly.qkv, self.h, H, self.hq, self.dqkv, nh * hd + 2 * kv, 1)  # q, k and v in one launch
+            if fused_qkv:
+                # x (+ the previous layer's mix and combine, into the other row), this layer's attention norm and the
+                # q/k/v GEMV in one launch (the bits of combine_rms_norm_q, or rms_norm_q, then gemvq)
+                if li == 0:
+                    hip.combine_rms_norm_gemv(x, 0, 0, 0, 0, ly.attn_norm, c.eps, ly.qkv, 0, self.dqkv)
+                else:
+                    hip.combine_rms_norm_gemv(x, self.mix, self.ye1, self.dwh, k, ly.attn_norm, c.eps, ly.qkv,
+                                              xs[1 - cur], self.dqkv)
+                    cur = 1 - cur
+                    x = xs[cur]
+            else:
+                if li == 0:
+                    hip.rms_norm_q(x, H, ly.attn_norm, self.h, H, H, 1, c.eps, xq=self.hq)
+                else:  # the previous layer's x += mix, its combine (x += sum w y) and this layer's attention norm
+                    hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, ly.attn_norm, self.h, H, 1, c.eps, xq=self.hq,
+                                           res=self.mix if fused_router else 0)
+                hip.gemvq(ly.qkv, self.h, H, self.hq, self.dqkv, nh * hd + 2 * kv, 1)  # q, k and v in one launch
             # q/k norms, rope and the KV store inside the attention launch (the same bits as rms_norm_rope_qk with
             # the KV store, then attn_decode)
             hip.rms_norm_rope_attn_decode(self.dq, hd, ly.q_norm, self.dk, ly.k_norm, self.dv, c.eps, hd, c.rope_base,
@@ -300,9 +320,13 @@ class Model:
             # the down GEMV (SwiGLU quantized inside) into ye1; its combine runs with the next norm
             hip.moe_down_swiglu_combine(c.ty_down, H, F, ly.down, ly.e_down, self.dslots, k, self.g2,
                                         int(self.g2) + k * F * 4, self.ye1, 0, self.dwh, 0, 0, 1)
-        hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, w.output_norm, self.h, H, 1, c.eps,
-                               res=self.mix if fused_router else 0)
-        hip.gemv(w.output, self.h, self.logits)
+        if fused_qkv:
+            hip.combine_rms_norm_gemv(x, self.mix, self.ye1, self.dwh, k, w.output_norm, c.eps, w.output, 0,
+                                      self.logits)
+        else:
+            hip.combine_rms_norm_q(x, self.ye1, self.dwh, k, w.output_norm, self.h, H, 1, c.eps,
+                                   res=self.mix if fused_router else 0)
+            hip.gemv(w.output, self.h, self.logits)
         hip.argmax_rows(self.logits, c.n_vocab, 1, self.tok)
 
     def decode_step(self, graph=True):

@@ -185,6 +185,39 @@ def test_combine_rms_norm_q_equals_two_calls(hip, numerics, n, rows, k, quant, r
     assert np.abs(xc - wx).max() < 1e-5
 
 
+@pytest.mark.parametrize("ty,rows,n", [(ggml.Q6_K, 5120, 2048), (ggml.Q8_0, 3001, 2048), (ggml.Q4_K, 700, 1024),
+                                        (ggml.Q2_K, 4096, 2048), (ggml.Q5_K, 64, 512)])
+@pytest.mark.parametrize("k,res", [(8, True), (5, True), (0, True), (0, False)])
+def test_combine_rms_norm_gemv_equals_two_calls(hip, ty, rows, n, k, res):
+    """combine_rms_norm_gemv (the previous layer's x += res and MoE combine, this layer's norm and the GEMV reading it,
+    in one launch) against combine_rms_norm_q (rms_norm_q when k = 0) then gemvq on its quantized output: x_out and y
+    bit-equal, x untouched; slots of weight 0; the matrix types and shapes of the decode (q/k/v, the output head)."""
+    rng = np.random.default_rng(rows + n + k)
+    x0 = normal(n, seed=n + k + rows)
+    ye = normal((max(k, 1), n), seed=n + k + 1)
+    wh = rng.uniform(0.1, 0.5, max(k, 1)).astype(np.float32)
+    wh[::3] = 0.0
+    nw = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    r0 = normal(n, seed=n + 7)
+    w = random_blocks(ty, rows, n, seed=rows + ty)
+    t = hip.upload_tensor(ty, w)
+    yb, whb, nwb, rb = up(hip, ye), up(hip, wh), up(hip, nw), (up(hip, r0) if res else 0)
+    xa, xb, xo = up(hip, x0), up(hip, x0), hip.alloc(n * 4)
+    h, hq = hip.alloc(n * 4), hip.alloc(n + n // 8)
+    ya, yf = hip.alloc(rows * 4), hip.alloc(rows * 4)
+    if k:
+        hip.combine_rms_norm_q(xa, yb, whb, k, nwb, h, n, 1, 1e-6, xq=hq, res=rb)
+    else:
+        hip.rms_norm_q(xa, n, nwb, h, n, n, 1, 1e-6, xq=hq, res=rb)
+    hip.gemvq(t, h, n, hq, ya, rows, 1)
+    hip.combine_rms_norm_gemv(xb, rb, yb if k else 0, whb if k else 0, k, nwb, 1e-6, t, xo, yf)
+    assert np.array_equal(down(hip, xb, np.float32, n), x0)  # x is only read
+    assert np.array_equal(down(hip, xo, np.uint32, n), down(hip, xa, np.uint32, n))
+    assert np.array_equal(down(hip, yf, np.uint32, rows), down(hip, ya, np.uint32, rows))
+    with pytest.raises(S.StrataError, match="x_out not x"):
+        hip.combine_rms_norm_gemv(xb, rb, 0, 0, 0, nwb, 1e-6, t, xb, yf)
+
+
 @pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])
 @pytest.mark.parametrize("n,rows", [(2048, 128), (512, 61), (1024, 3)])
 def test_rms_norm_q_gemv_f32_equals_two_calls(hip, numerics, n, rows):
