@@ -233,13 +233,40 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
             acc[i + 1][q] = acc[i + 1][q] + f1;
         }
     };
+    // one tile (the last of an odd count: a tile pair would spend a whole tile's MFMAs and closes on no positions)
+    auto mfma_one = [&](const int i, int g, v4i (&c0)[NP]) __attribute__((always_inline)) {
+        const int8_t* xb = xs + (g & 1) * XBUF;
+        v4i a0[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) a0[kk] = *(const v4i*)(xb + (16 * i + aswz) * 256 + 16 * ((4 * kk + kl) ^ aswz));
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int pl = 0; pl < NP; pl++)
+                c0[pl] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[kk], B[kk][pl], kk ? c0[pl] : (v4i){0, 0, 0, 0}, 0, 0, 0);
+    };
+    auto close_one = [&](const int i, int g, const v4i (&c0)[NP]) __attribute__((always_inline)) {
+        const float4 d0 = *(const float4*)(dxs + (g & 1) * GM + 16 * i + 4 * kl);
+        const float dq0[4] = {d0.x, d0.y, d0.z, d0.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int iv0 = F::HI ? (c0[P_HI][q] << 8) + c0[P_LO][q] : c0[P_LO][q];
+            float f0 = (D * dq0[q]) * (float)iv0;
+            if constexpr (F::MIN) f0 = f0 - (M * dq0[q]) * (float)c0[P_M][q];
+            acc[i][q] = acc[i][q] + f0;
+        }
+    };
     auto tiles = [&](int g, int ntt) __attribute__((always_inline)) {
         static_for<0, NTT / 2>([&](auto I) {
             constexpr int i = 2 * decltype(I)::value;
-            if (i < ntt) {
+            if (i + 1 < ntt) {
                 v4i c0[NP], c1[NP];
                 mfma_pair(i, g, c0, c1);
                 close_pair(i, g, c0, c1);
+            } else if (i < ntt) {
+                v4i c0[NP];
+                mfma_one(i, g, c0);
+                close_one(i, g, c0);
             }
         });
     };
