@@ -83,9 +83,11 @@ def test_config3_moe_gemv_t1(hip, ty, rows, cols):
 
 
 @pytest.mark.parametrize("ty", [ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS])
-def test_config3_grouped_gemm_t512(hip, ty):
-    """T = 512: route -> device sort (256-position chunks) -> gemm_grouped over 128 experts of 2048 x 768; every
-    routed (token, expert) pair checked against the dequantized f64 dot, 256 of them against cpu_moe::matvec."""
+@pytest.mark.parametrize("small", [False, True], ids=["tiles256", "tiles64"])
+def test_config3_grouped_gemm_t512(hip, ty, small):
+    """T = 512: route -> device sort -> gemm_grouped over 128 experts of 2048 x 768, with 256-position tiles and with
+    the 64-position tiles and GEMM form the backend picks at this size (SMALL_TILES); every routed (token, expert)
+    pair checked against the dequantized f64 dot, 256 of them against cpu_moe::matvec."""
     E, k, T, rows, cols = 128, 8, 512, 2048, 768
     w = expert_bank(ty, E, rows, cols, seed=400 + ty)
     wb = hip.upload(w)
@@ -96,13 +98,14 @@ def test_config3_grouped_gemm_t512(hip, ty):
     ids = hip.alloc(T * k * 4)
     hip.router_topk(hip.upload(logits), E, k, 0.0, ids, hip.alloc(T * k * 4), T)
     assert np.array_equal(hip.get(ids, np.int32, T * k).reshape(T, k), ids_w)
-    chunk = hip.gemm_block_positions()
+    chunk, fl = hip.moe_tile_plan(T, k, E, small)
+    assert (fl != 0) == small and hip.moe_tile_plan(T, k, E) == (64, S.SMALL_TILES)
     max_tiles = T * k // chunk + E
     off, xrow, inv = hip.alloc((E + 1) * 4), hip.alloc(T * k * 4), hip.alloc(T * k * 4)
     tiles, ntd = hip.alloc(max_tiles * 16), hip.alloc(4)
     hip.moe_sort(ids, T, k, E, off, xrow, inv, [(int(wb), rows * rb)], tiles, max_tiles, ntd, chunk=chunk)
     y = hip.alloc(T * k * rows * 4)
-    hip.gemm_grouped(ty, rows, cols, tiles, max_tiles, ntd, hip.upload(xs), cols, T, xrow, y, rows, S.ACT_STORE)
+    hip.gemm_grouped(ty, rows, cols, tiles, max_tiles, ntd, hip.upload(xs), cols, T, xrow, y, rows, S.ACT_STORE | fl)
     got = hip.get(y, np.float32, T * k * rows).reshape(T * k, rows)
     off_w, xrow_w, _ = O.sort_by_expert(ids_w, E)
     assert np.array_equal(hip.get(xrow, np.int32, T * k), xrow_w)
