@@ -313,32 +313,51 @@ def bench_moe_decode(hip, S, ggml, iters):
         # swiglu_q + moe_down_combine with the SwiGLU and its quantization inside the down GEMV (same bits)
         hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d, H * rb_d, slots, k, g, int(g) + k * F * 4, ye, x, wh, 0, 0, 1)
 
-    for i in range(20):
-        token(i)
-    hip.sync()
-    e0, e1 = hip.event(), hip.event()
-    hip.record(e0)
-    for i in range(iters):
-        token(i)
-    hip.record(e1)
-    us_eager = 1000 * hip.elapsed_ms(e0, e1) / iters
-    us = us_eager
-    if USE_GRAPHS:
-        # 8 tokens a recorded graph (both weight copies, all four logit vectors), replayed the way the reference's
-        # decode replays CUDA graphs (src/cuda/mod.rs:868-888): host launch gaps do not count as GPU time
-        ng = 8
-        hip.graph("decode", lambda: [token(i) for i in range(ng)])
+    # as the decoder stack runs the layer: h arrives quantized (the FFN norm writes hq beside h) and the combine
+    # rides with the next layer's norm and q/k/v GEMV (combine_rms_norm_gemv), so the layer is two launches
+    hq = hip.alloc(H + H // 8)
+    hip.quant_xq(h, H, H, 1, hq)
+
+    def token_stack(i):
+        gu, d = copies[i % 2]
+        hip.moe_route_gemv(logits[i % 4], E, k, 0.0, table, ids, wts, slots, wh, ggml.Q5_K, F, H, gu, F * rb_gu, h, g,
+                           pair=(E * F * rb_gu, k * F * 4), xq=hq)
+        hip.moe_down_swiglu_combine(ggml.Q6_K, H, F, d, H * rb_d, slots, k, g, int(g) + k * F * 4, ye, 0, wh, 0, 0, 1)
+
+    def timed(fn, key):
+        for i in range(20):
+            fn(i)
         hip.sync()
-        reps = max(1, -(-iters // ng))
+        e0, e1 = hip.event(), hip.event()
         hip.record(e0)
-        for _ in range(reps):
-            hip.graph("decode", None)
+        for i in range(iters):
+            fn(i)
         hip.record(e1)
-        us = 1000 * hip.elapsed_ms(e0, e1) / (reps * ng)
-        hip.drop_graphs()
+        us_eager = 1000 * hip.elapsed_ms(e0, e1) / iters
+        us = us_eager
+        if USE_GRAPHS:
+            # 8 tokens a recorded graph (both weight copies, all four logit vectors), replayed the way the reference's
+            # decode replays CUDA graphs (src/cuda/mod.rs:868-888): host launch gaps do not count as GPU time
+            ng = 8
+            hip.graph(key, lambda: [fn(i) for i in range(ng)])
+            hip.sync()
+            reps = max(1, -(-iters // ng))
+            hip.record(e0)
+            for _ in range(reps):
+                hip.graph(key, None)
+            hip.record(e1)
+            us = 1000 * hip.elapsed_ms(e0, e1) / (reps * ng)
+            hip.drop_graphs()
+        return us, us_eager
+
+    us, us_eager = timed(token, "decode")
+    us_s, _ = timed(token_stack, "decode_stack")
     bts = k * (2 * F * rb_gu + H * rb_d)
     return {"us_per_token": round(us, 2), "us_per_token_eager": round(us_eager, 2), "expert_bytes": bts,
-            "GB/s": round(bts / us / 1e3, 1), "pct_peak": round(100 * bts / us / 1e3 / HBM_PEAK_GBS, 1)}
+            "GB/s": round(bts / us / 1e3, 1), "pct_peak": round(100 * bts / us / 1e3 / HBM_PEAK_GBS, 1),
+            "us_per_token_as_in_stack": round(us_s, 2), "pct_peak_as_in_stack": round(100 * bts / us_s / 1e3 / HBM_PEAK_GBS, 1),
+            "as_in_stack": "h pre-quantized by the FFN norm; route + gate/up and the down GEMV only, the combine "
+                           "riding with the next layer's norm and q/k/v GEMV (combine_rms_norm_gemv)"}
 
 
 def bench_attn_decode(hip, S, positions=(255, 1023, 4099), layers=48):
