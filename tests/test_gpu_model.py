@@ -104,6 +104,42 @@ def check_logits(got, want, tol=5e-2):
         assert int(np.argmax(got)) == O.argmax(want)
 
 
+def stage_check(c, L, x, p, mid, xout, kc, vc, tol=1e-5):
+    """One layer at position p, teacher-forced stage by stage on the device's own intermediate rows (mid: q after its
+    norm and rope, the attention output, the FFN norm's h, the routed ids and weights; kc / vc: the layer's f16 KV
+    cache rows as f32), each stage against the oracle within rel-L2 tol (ids exactly, weights within 1e-6): the
+    q projection with the q norm and rope (Model::attention's q), the attention over the device's cache
+    (src/model.rs:771-793), the o projection and the FFN norm, the route (Model::route on the F32 router's sequential
+    sums), and the expert FFN (cpu_moe::experts_multi) added to the layer's residual."""
+    H, nh, nkv, hd, k = c.n_embd, c.n_head, c.n_head_kv, c.head_dim, c.n_expert_used
+    h = O.rms_norm(x, L["attn_norm"], c.eps)[0]
+    q = O.matvec(c.ty_attn, L["q"], nh * hd, H, h)
+    qn = np.concatenate([O.rope_neox(O.rms_norm(q[i * hd:(i + 1) * hd], L["q_norm"], c.eps)[0], hd, p,
+                                     c.rope_base)[0] for i in range(nh)])
+    assert rel_l2(mid["q"], qn) <= tol, ("q", p, rel_l2(mid["q"], qn))
+    att = O.attention(mid["q"], kc[:p + 1], vc[:p + 1], 0, p + 1, nh, nkv, hd, float(1 / np.sqrt(hd)))
+    assert rel_l2(mid["att"], att) <= tol, ("attention", p, rel_l2(mid["att"], att))
+    x2 = x + O.matvec(c.ty_attn, L["o"], H, nh * hd, mid["att"])
+    h2 = O.rms_norm(x2, L["ffn_norm"], c.eps)[0]
+    assert rel_l2(mid["h"], h2) <= tol, ("ffn norm", p, rel_l2(mid["h"], h2))
+    lg = np.cumsum(L["router"] * mid["h"][None, :], axis=1, dtype=np.float32)[:, -1]
+    rid, rw = O.route(lg[None, :], k)
+    assert np.array_equal(mid["ids"], rid[0]), ("route", p)
+    assert np.abs(mid["wts"] - rw[0]).max() <= 1e-6, ("route weights", p)
+    y = O.experts_multi(c.ty_gate_up, c.ty_down, L["gate"], L["up"], L["down"], H, c.n_ff_exp, mid["h"][None, :],
+                        mid["ids"][None, :], mid["wts"][None, :])[0]
+    assert rel_l2(xout, x2 + y) <= tol, ("experts", p, rel_l2(xout, x2 + y))
+
+
+def mid_rows(hip, m, c, n):
+    """The prefill's intermediate rows of the layer just run (n chunk rows): q, attention, FFN-norm h, ids, weights."""
+    nh, hd, k, H = c.n_head, c.head_dim, c.n_expert_used, c.n_embd
+    return dict(q=hip.get(m.qb, np.float32, n * nh * hd).reshape(n, nh * hd),
+                att=hip.get(m.att, np.float32, n * nh * hd).reshape(n, nh * hd),
+                h=hip.get(m.h, np.float32, n * H).reshape(n, H),
+                ids=hip.get(m.ids, np.int32, n * k).reshape(n, k), wts=hip.get(m.wts, np.float32, n * k).reshape(n, k))
+
+
 CFGS = {
     "small": small_cfg,
     # the configs[4] head shape: head_dim 128, 8 query heads over each KV head
@@ -147,26 +183,35 @@ def test_layers_teacher_forced(hip):
     weights = Weights.from_host(hip, c, W["embd"], W["output"], W["output_norm"], W["layers"])
     m = Model(hip, weights, ctx=128, chunk=24)
     prompt = np.random.default_rng(4).integers(0, c.n_vocab, 40).tolist()
-    rows = {}
+    rows, mids = {}, {}
     chunk_no = [0]
 
     def hook(il, x):
         n = min(24, 40 - 24 * chunk_no[0])
         rows[(chunk_no[0], il)] = hip.get(x, np.float32, n * c.n_embd).reshape(n, c.n_embd)
+        if il >= 0:
+            mids[(chunk_no[0], il)] = mid_rows(hip, m, c, n)
         if il == c.n_layer - 1:
             chunk_no[0] += 1
 
     m.prefill(prompt, layer_hook=hook)
     ref = RefModel(c, W)
+    kv = c.n_head_kv * c.head_dim
     for il in range(c.n_layer):
         kc, vc, errs = [], [], []
+        kcd = hip.get(m.kc[il], np.float16, 40 * kv).astype(np.float32).reshape(40, kv)
+        vcd = hip.get(m.vc[il], np.float16, 40 * kv).astype(np.float32).reshape(40, kv)
         for ch in range(2):
             xin, xout = rows[(ch, il - 1)], rows[(ch, il)]
             for r in range(xin.shape[0]):
+                # every stage of every row from the device's own intermediate rows: within 1e-5
+                stage_check(c, W["layers"][il], xin[r], 24 * ch + r, {key: v[r] for key, v in mids[(ch, il)].items()},
+                            xout[r], kcd, vcd)
                 want = ref.layer(il, xin[r].copy(), 24 * ch + r, kc, vc)
                 errs.append(rel_l2(xout[r], want))
         errs = np.array(errs)
-        # the rows agree to f32 rounding; a row where one requantized int8 value lands one step over stays within 2e-2
+        # the whole layer from the same input row: a requantized int8 value (of the attention output, of h, of a
+        # SwiGLU row) that lands one step over moves a row by up to ~1e-2 of its scale, now and then
         assert np.mean(errs <= 1e-5) >= 0.9 and errs.max() <= 2e-2, (il, errs)
 
 
@@ -294,28 +339,7 @@ def test_config4_full_workload(hip):
         M = mid[il]
         for j, p in enumerate(pos):
             x = xin[il][j]
-            # q after the attention norm, q projection, q norm and rope
-            h = O.rms_norm(x, L["attn_norm"], c.eps)[0]
-            q = O.matvec(c.ty_attn, L["q"], nh * hd, H, h)
-            qn = np.concatenate([O.rope_neox(O.rms_norm(q[i * hd:(i + 1) * hd], L["q_norm"], c.eps)[0], hd, p,
-                                             c.rope_base)[0] for i in range(nh)])
-            assert rel_l2(M["q"][j], qn) <= 1e-5, (il, p, rel_l2(M["q"][j], qn))
-            # the attention output from the device's q and KV cache
-            att = O.attention(M["q"][j], kc[:p + 1], vc[:p + 1], 0, p + 1, nh, nkv, hd, float(1 / np.sqrt(hd)))
-            assert rel_l2(M["att"][j], att) <= 1e-5, (il, p, rel_l2(M["att"][j], att))
-            # o projection of the device's attention output, then the FFN norm
-            x2 = x + O.matvec(c.ty_attn, L["o"], H, nh * hd, M["att"][j])
-            h2 = O.rms_norm(x2, L["ffn_norm"], c.eps)[0]
-            assert rel_l2(M["h"][j], h2) <= 1e-5, (il, p, rel_l2(M["h"][j], h2))
-            # routing of the device's h (the F32 router's sequential sums)
-            lg = np.cumsum(L["router"] * M["h"][j][None, :], axis=1, dtype=np.float32)[:, -1]
-            rid, rw = O.route(lg[None, :], k)
-            assert np.array_equal(M["ids"][j], rid[0]), (il, p)
-            assert np.abs(M["wts"][j] - rw[0]).max() <= 1e-6, (il, p)
-            # the expert FFN of the device's h, ids and weights, added to x2
-            y = O.experts_multi(c.ty_gate_up, c.ty_down, L["gate"], L["up"], L["down"], H, c.n_ff_exp,
-                                M["h"][j][None, :], M["ids"][j][None, :], M["wts"][j][None, :])[0]
-            assert rel_l2(xout[il][j], x2 + y) <= 1e-5, (il, p, rel_l2(xout[il][j], x2 + y))
+            stage_check(c, L, x, p, {key: v[j] for key, v in M.items()}, xout[il][j], kc, vc)
             # the whole layer from the same input row (and its own key and value rows against the cache)
             kl, vl = list(kc[:p]), list(vc[:p])
             want = ref.layer(il, x.copy(), p, kl, vl)
