@@ -49,6 +49,91 @@ __device__ __forceinline__ void load_lds4_so(uint64_t base, uint32_t off, const 
 // __syncthreads() fence would also wait for every outstanding vector memory operation).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
 
+// Scale-after decode for the formats whose scales are per 32-value group (Q4_K, Q5_K, IQ3_S, IQ4_XS): the
+// weights enter the MFMA as their raw int8 codes q (|q| <= 127), one K=32 MFMA (v_mfma_i32_16x16x32_i8) per group
+// gives each group's exact sum d_g = q . x, and the close forms s = sum_g sc_g d_g in int32: the same integer as the
+// digit planes' 256 H.x + L.x, so the same bits, with a fraction of the decode work (no per-value scale product and
+// byte split). Group g's values 8 kl .. 8 kl + 7 (lane group kl) of the row at b go to q[0..1]; sc the group's integer
+// scale, m its min (formats with mins). Layouts: src/quant/mod.rs (Q4_K 209-221, Q5_K 223-237, IQ2_XXS 287-297,
+// IQ3_S 345-361, IQ4_XS 363-376). Measured on the 512-token GEMMs: Q5_K gate/up 172-177 -> 164 us, IQ3_S 0.112-0.116
+// -> 0.092 ms, IQ4_XS 0.089-0.097 -> 0.083 ms.
+template <int T> struct Dsa {
+    static constexpr bool ON = false;
+};
+template <bool Q5> struct DsaQ45 {
+    static constexpr bool ON = true, MIN = true;
+    struct Row { uint32_t sc_lo, sc_hi, m_lo, m_hi; uint2 qh; };
+    __device__ static Row row(const uint8_t* b, int kl) {
+        const uint4 h = *(const uint4*)b;  // d, dmin, 12 bytes of packed 6-bit scales / mins (scale_min_k4)
+        Row r;
+        r.sc_lo = h.y & 0x3F3F3F3Fu;
+        r.m_lo = h.z & 0x3F3F3F3Fu;
+        r.sc_hi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+        r.m_hi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+        if constexpr (Q5) r.qh = *(const uint2*)(b + 16 + 8 * kl);
+        return r;
+    }
+    __device__ static void run(const uint8_t* b, const Row& r, int g, int kl, const IqTables*, uint32_t* q, int& sc, int& m) {
+        const uint2 w = *(const uint2*)(b + (Q5 ? 48 : 16) + 32 * (g >> 1) + 8 * kl);
+        const uint32_t ws[2] = {w.x, w.y}, hs[2] = {r.qh.x, r.qh.y};
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            q[i] = (ws[i] >> (4 * (g & 1))) & 0x0F0F0F0Fu;
+            // bit g of each qh byte to bit 4: a rotate right by g - 4 (mod 32), masked
+            if constexpr (Q5) q[i] |= __builtin_amdgcn_alignbit(hs[i], hs[i], (uint32_t)(g + 28) & 31) & 0x10101010u;
+        }
+        sc = (int)(((g < 4 ? r.sc_lo : r.sc_hi) >> (8 * (g & 3))) & 0xFF);
+        m = (int)(((g < 4 ? r.m_lo : r.m_hi) >> (8 * (g & 3))) & 0xFF);
+    }
+};
+template <> struct Dsa<Q4_K> : DsaQ45<false> {};
+template <> struct Dsa<Q5_K> : DsaQ45<true> {};
+// (IQ2_XXS keeps the digit planes: its per-group header reads made this form slower, 0.105 -> 0.126 ms for the
+// configs[3] 512-token GEMM)
+template <> struct Dsa<IQ2_XXS> {
+    static constexpr bool ON = false, MIN = false;
+    struct Row {};
+    __device__ static Row row(const uint8_t*, int) { return Row{}; }
+    // group g: grid entry kl of the 4 (8 values with its 7-bit sign index); sc = 2 ls + 1
+    __device__ static void run(const uint8_t* b, const Row&, int g, int kl, const IqTables* tab, uint32_t* q, int& sc, int& m) {
+        const uint32_t gi = rd32<2>(b + 2 + 8 * g), aux = rd32<2>(b + 6 + 8 * g);
+        const uint64_t grid = tab->iq2xxs[(gi >> (8 * kl)) & 255];
+        const uint32_t sg = tab->ksigns[(aux >> (7 * kl)) & 127];
+        q[0] = (uint32_t)neg_bytes((uint32_t)grid, sg);
+        q[1] = (uint32_t)neg_bytes((uint32_t)(grid >> 32), sg >> 4);
+        sc = (int)(2 * (aux >> 28) + 1);
+        m = 0;
+    }
+};
+template <> struct Dsa<IQ3_S> {
+    static constexpr bool ON = true, MIN = false;
+    struct Row {};
+    __device__ static Row row(const uint8_t*, int) { return Row{}; }
+    // group g: grid pair kl (two 4-value entries, 9-bit indices with a qh bit), sign byte kl; sc = 1 + 2 nibble
+    __device__ static void run(const uint8_t* b, const Row&, int g, int kl, const IqTables* tab, uint32_t* q, int& sc, int& m) {
+        const uint32_t q2 = rd16(b + 2 + 8 * g + 2 * kl), hb = b[66 + g], sg = b[74 + 4 * g + kl];
+        const uint32_t g1 = tab->iq3s[(q2 & 255) | ((hb << (8 - 2 * kl)) & 256)];
+        const uint32_t g2 = tab->iq3s[((q2 >> 8) & 255) | ((hb << (7 - 2 * kl)) & 256)];
+        q[0] = (uint32_t)neg_bytes(g1, sg);
+        q[1] = (uint32_t)neg_bytes(g2, sg >> 4);
+        sc = (int)(1 + 2 * ((b[106 + (g >> 1)] >> (4 * (g & 1))) & 0xF));
+        m = 0;
+    }
+};
+template <> struct Dsa<IQ4_XS> {
+    static constexpr bool ON = true, MIN = false;
+    struct Row { uint32_t sh; };
+    __device__ static Row row(const uint8_t* b, int) { return Row{rd16(b + 2)}; }
+    // group g: values 0..15 are the low nibbles of its 16 bytes, 16..31 the high ones; sc = ls - 32
+    __device__ static void run(const uint8_t* b, const Row& r, int g, int kl, const IqTables*, uint32_t* q, int& sc, int& m) {
+        const uint2 w = *(const uint2*)(b + 8 + 16 * g + 8 * (kl & 1));
+        q[0] = (uint32_t)iq4nl_lut((w.x >> (4 * (kl >> 1))) & 0x0F0F0F0Fu);
+        q[1] = (uint32_t)iq4nl_lut((w.y >> (4 * (kl >> 1))) & 0x0F0F0F0Fu);
+        sc = (int)(((b[4 + (g >> 1)] >> (4 * (g & 1))) & 0xF) | (((r.sh >> (2 * g)) & 3) << 4)) - 32;
+        m = 0;
+    }
+};
+
 template <int T>
 __global__ __launch_bounds__(64 * SW, 1) void gemm_small_kernel(GemmArgs a) {
     using F = SmallFmt<T>;
@@ -173,10 +258,27 @@ __global__ __launch_bounds__(64 * SW, 1) void gemm_small_kernel(GemmArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; q++) acc[i][q] = 0.0f;
     const int kl = lane >> 4, aswz = lane & 15;
+    constexpr bool SA = Dsa<T>::ON;
     v4i B[4][NP];
+    // scale-after form: the 8 groups' codes (8 bytes a lane each), integer scales and min words
+    uint32_t Bq[8][2], Bm[8];
+    int scg[8];
     float D = 0.0f, M = 0.0f;
     auto decode = [&](uint32_t rbeg, int s, int wb, auto&& hook) __attribute__((always_inline)) {
         const uint8_t* b = raw + wb * WBUF + wave * WREG + (lane & 15) * RAWP + ((rbeg + (uint32_t)s * SBB) & 15);
+        if constexpr (SA) {
+            using DS = Dsa<T>;
+            const auto r = DS::row(b, kl);
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                int m;
+                DS::run(b, r, g, kl, tab, Bq[g], scg[g], m);
+                if constexpr (DS::MIN) Bm[g] = (uint32_t)m * 0x01010101u;
+                if (g & 1) hook(g >> 1);
+            }
+            Dec<T>::scales(b, D, M);
+            return;
+        }
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
             uint32_t hi[4], lo[4];
@@ -250,7 +352,44 @@ __global__ __launch_bounds__(64 * SW, 1) void gemm_small_kernel(GemmArgs a) {
             acc[i][q] = acc[i][q] + f0;
         }
     };
+    // scale-after tile i: group g's K=32 MFMA on the A fragment X[p][32 g + 8 kl .. + 7] (8 bytes), the min chain
+    // over the groups with B = the group's min (formats with mins), then s = sum_g sc_g d_g and the float close
+    auto tile_sa = [&](const int i, int xb) __attribute__((always_inline)) {
+        const int8_t* xp = xs + xb * SXB + (16 * i + aswz) * 256 + 8 * (kl & 1);
+        long af[8];
+#pragma unroll
+        for (int g = 0; g < 8; g++) af[g] = *(const long*)(xp + 16 * ((2 * g + (kl >> 1)) ^ aswz));
+        v4i d[8], mn = (v4i){0, 0, 0, 0};
+#pragma unroll
+        for (int g = 0; g < 8; g++) {
+            const long bq = (long)(((uint64_t)Bq[g][1] << 32) | Bq[g][0]);
+            d[g] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[g], bq, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            if constexpr (F::MIN) {
+                const long bm = (long)(((uint64_t)Bm[g] << 32) | Bm[g]);
+                mn = __builtin_amdgcn_mfma_i32_16x16x32_i8(af[g], bm, mn, 0, 0, 0);
+            }
+        }
+        const float4 d0 = *(const float4*)(dxs + xb * SDX + SM * wave + 16 * i + 4 * kl);
+        const float dq0[4] = {d0.x, d0.y, d0.z, d0.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            int sv = __mul24(scg[0], d[0][q]);
+#pragma unroll
+            for (int g = 1; g < 8; g++) sv += __mul24(scg[g], d[g][q]);
+            // the reference's float steps, rounded one by one (src/cpu_moe.rs:327-377): sum += (D dx) s - (M dx) m
+            float f0 = (D * dq0[q]) * (float)sv;
+            if constexpr (F::MIN) f0 = f0 - (M * dq0[q]) * (float)mn[q];
+            acc[i][q] = acc[i][q] + f0;
+        }
+    };
     auto tiles = [&](int xb, int ntt) __attribute__((always_inline)) {
+        if constexpr (SA) {
+            static_for<0, STT>([&](auto I) {
+                constexpr int i = decltype(I)::value;
+                if (i < ntt) tile_sa(i, xb);
+            });
+            return;
+        }
         static_for<0, STT / 2>([&](auto I) {
             constexpr int i = 2 * decltype(I)::value;
             if (i + 1 < ntt) {
