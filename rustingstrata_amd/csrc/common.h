@@ -90,6 +90,16 @@ __device__ __forceinline__ void load_lds16_so(uint64_t base, uint32_t off, const
                         (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(sb), "s"(m0) : "memory", "m0");
 }
+// 4 bytes per lane from a wave-uniform base plus a per-lane offset into LDS at lds + 4 * lane (global_load_lds_dword).
+__device__ __forceinline__ void load_lds4_so(uint64_t base, uint32_t off, const void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32)) << 32) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(sb), "s"(m0) : "memory", "m0");
+}
+// Block barrier after this wave's LDS operations complete, without waiting for its loads in flight (a
+// __syncthreads() fence would also wait for every outstanding vector memory operation).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
 // This wave's loads into LDS are complete (vmcnt 0; the barrier that follows publishes them to the block).
 __device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // Wait for this wave's LDS reads: before global_load_lds overwrites LDS bytes the wave has just read, since the

@@ -38,17 +38,6 @@ template <int T> struct SmallFmt : GemmPlanes<T> {
     static constexpr int NLOAD = SXI + WI + 1;                       // loads per wave and step
 };
 
-// 4 bytes per lane from a wave-uniform base plus a per-lane offset into LDS at lds + 4 * lane (global_load_lds_dword).
-__device__ __forceinline__ void load_lds4_so(uint64_t base, uint32_t off, const void* lds) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    const uint64_t sb = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(base >> 32)) << 32) |
-                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)base);
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(sb), "s"(m0) : "memory", "m0");
-}
-// Block barrier after this wave's LDS operations complete, without waiting for its loads in flight (a
-// __syncthreads() fence would also wait for every outstanding vector memory operation).
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
-
 // Scale-after decode for the formats whose scales are per 32-value group (Q4_K, Q5_K, IQ3_S, IQ4_XS): the
 // weights enter the MFMA as their raw int8 codes q (|q| <= 127), one K=32 MFMA (v_mfma_i32_16x16x32_i8) per group
 // gives each group's exact sum d_g = q . x, and the close forms s = sum_g sc_g d_g in int32: the same integer as the
