@@ -709,6 +709,33 @@ def test_gemm_tiles_match_cpu(hip, ty, fl):
 
 
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
+def test_gemm_small_tiles_same_bits_random_lists(hip, ty):
+    """The 64-position GEMM form against the 256-position one over seeded random tile lists (counts 1-256, so tiles
+    of more than 64 positions run as several chunks; experts in random order, gathered X rows, partial row blocks):
+    the same bits for every type (IQ4_XS included: both forms close its super-blocks from the same integer sum)."""
+    rng = np.random.default_rng(900 + ty)
+    rows, cols, E, n_x = 136, 768, 5, 60
+    rb = ggml.row_bytes(ty, cols)
+    w = random_blocks(ty, E * rows, cols, seed=901 + ty)
+    wb = up(hip, w)
+    x = normal((n_x, cols), seed=902 + ty)
+    spans, m0 = [], 0
+    for _ in range(9):
+        c = int(rng.integers(1, 257))
+        spans.append((int(rng.integers(0, E)), m0, c))
+        m0 += c
+    npos = m0
+    xrow = rng.integers(0, n_x, npos).astype(np.int32)
+    tiles, nt = tile_list(hip, int(wb), rows * rb, spans)
+    xb, xr = up(hip, x), up(hip, xrow)
+    ya, yb = hip.alloc(npos * rows * 4), hip.alloc(npos * rows * 4)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, ya, rows, S.ACT_STORE)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, yb, rows, S.ACT_STORE | S.SAME_X | S.SMALL_TILES)
+    a, b = down(hip, ya, np.uint32, npos * rows), down(hip, yb, np.uint32, npos * rows)
+    assert np.array_equal(a, b), int((a != b).sum())
+
+
+@pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
 @pytest.mark.parametrize("fl", [0, S.SMALL_TILES], ids=["blocks256", "small64"])
 def test_gemm_gate_up_fused_matches_two_calls(hip, ty, fl):
     """gemm_grouped_gate_up gives the bits of gemm (gate, act store) followed by gemm (up, act SwiGLU, same X) over the
