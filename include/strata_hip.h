@@ -239,9 +239,11 @@ int strata_moe_sort(strata_ctx* ctx, uint64_t ids, uint64_t t, uint64_t k, uint6
 /* Backend::gemm (src/backend.rs:187-191): for each tile [w, m0 | cnt << 32] of the device tile list, positions
  * m0 .. m0 + cnt get y[m, 0..rows] (op) W x[xrow[m]] (x row m when xrow is 0), W the rows x cols matrix of type ty
  * at w. act: STRATA_ACT_STORE, STRATA_ACT_SWIGLU (y = silu(y) * result), STRATA_ACT_ADD, | STRATA_SAME_X (x is
- * unchanged since the previous gemm that read it: its int8 copy is reused). n_x: rows of x the tiles read. cols
- * must be a multiple of 256 (the reference needs 64, src/cuda/mod.rs:584; every hot-path shape is a multiple of
- * 256). */
+ * unchanged since the previous gemm that read it: its int8 copy is reused) | STRATA_SMALL_TILES (the 64-position
+ * GEMM form, for tiles of a few dozen positions; the same bits). n_x: rows of x the tiles read. A tile holds at most
+ * strata_gemm_block_positions() (256) positions (the reference's host tiles hold at most GEMM_BM = 128,
+ * src/backend.rs:16, src/gpu_model/prefill.rs:618-642); positions past 256 of a tile are not computed. cols must be a multiple of 256 (the reference needs 64,
+ * src/cuda/mod.rs:584; every hot-path shape is a multiple of 256). */
 int strata_gemm(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t n_tiles, uint64_t x,
                 uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y, uint64_t y_stride, int act);
 /* strata_gemm with the tile count read on the device from n_tiles_dev (at most max_tiles), as strata_moe_sort
