@@ -181,7 +181,7 @@ int strata_combine_rms_norm_q(strata_ctx* ctx, uint64_t x, uint64_t x_stride, ui
  * ye[j] (slots j < k in order, rows of n = w->cols floats; res may be 0, k may be 0), then y = W h with h =
  * rms_norm(x_out) * nw quantized as Q8_K: the bits of strata_combine_rms_norm_q (strata_rms_norm_q with res when
  * k = 0) followed by strata_gemvq on its quantized output. x is only read (every block of the GEMV normalizes the row
- * itself), x_out (when not 0) is written, and must not be x. One row of at most 2048 values (a multiple of 8),
+ * itself), x_out (when not 0) is written, and must not overlap x, res or ye. One row of at most 2048 values (a multiple of 8),
  * k <= 8, 16-byte aligned rows, STRATA_NUM_Q8K; otherwise an error, and the caller makes the two calls. */
 int strata_combine_rms_norm_gemv(strata_ctx* ctx, uint64_t x, uint64_t res, uint64_t ye, uint64_t wh, uint64_t k,
                                  uint64_t nw, float eps, const strata_tensor* w, uint64_t x_out, uint64_t y);

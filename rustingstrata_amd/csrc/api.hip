@@ -414,11 +414,17 @@ int strata_combine_rms_norm_gemv(strata_ctx* c, uint64_t x, uint64_t res, uint64
     if (check_ctx(c) || check_tensor(w, "combine_rms_norm_gemv")) return -1;
     if (!x || !nw || !y || (k && (!ye || !wh))) return set_error("combine_rms_norm_gemv: null x, nw, y, ye or wh");
     const uint64_t n = w->cols;
-    if (k > 8 || n > 2048 || n % 8 || x_out == x || c->numerics != STRATA_NUM_Q8K ||
+    if (k > 8 || n > 2048 || n % 8 || c->numerics != STRATA_NUM_Q8K ||
         ((x | res | ye | nw | x_out) % 16))
         return set_error("combine_rms_norm_gemv: one row of at most 2048 values (a multiple of 8, 16-byte aligned), "
-                         "at most 8 slots, x_out not x, Q8_K numerics (" + std::to_string(n) + " values, " +
+                         "at most 8 slots, Q8_K numerics (" + std::to_string(n) + " values, " +
                          std::to_string(k) + " slots)");
+    // block 0 writes x_out while the other blocks still read x, res and ye: x_out may overlap none of them
+    if (x_out) {
+        auto overlaps = [&](uint64_t p, uint64_t bytes) { return p && x_out < p + bytes && p < x_out + 4 * n; };
+        if (overlaps(x, 4 * n) || overlaps(res, 4 * n) || overlaps(ye, 4 * n * k))
+            return set_error("combine_rms_norm_gemv: x_out overlaps x, res or ye");
+    }
     if (check_gemv_cols(w->ty, w->cols, false) || check_align(w->ty, w->ptr, "combine_rms_norm_gemv")) return -1;
     if (w->rows == 0 || w->rows > (1u << 30)) return set_error("combine_rms_norm_gemv: " + std::to_string(w->rows) + " rows");
     GemvLaunch g;

@@ -214,8 +214,11 @@ def test_combine_rms_norm_gemv_equals_two_calls(hip, ty, rows, n, k, res):
     assert np.array_equal(down(hip, xb, np.float32, n), x0)  # x is only read
     assert np.array_equal(down(hip, xo, np.uint32, n), down(hip, xa, np.uint32, n))
     assert np.array_equal(down(hip, yf, np.uint32, rows), down(hip, ya, np.uint32, rows))
-    with pytest.raises(S.StrataError, match="x_out not x"):
+    with pytest.raises(S.StrataError, match="x_out overlaps"):
         hip.combine_rms_norm_gemv(xb, rb, 0, 0, 0, nwb, 1e-6, t, xb, yf)
+    if k:
+        with pytest.raises(S.StrataError, match="x_out overlaps"):
+            hip.combine_rms_norm_gemv(xb, rb, yb, whb, k, nwb, 1e-6, t, int(yb) + 4 * n, yf)
 
 
 @pytest.mark.parametrize("numerics", [S.NUM_Q8K, S.NUM_Q8_32])
