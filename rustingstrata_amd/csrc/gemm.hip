@@ -41,6 +41,38 @@ template <int T> struct GemmFmt : GemmPlanes<T> {
     static constexpr int WBUF = GN * GemmPlanes<T>::RAWP;         // bytes of one raw weight buffer
 };
 
+// Items [first, last) of XCD x when the items are split by cost rather than by count. Item (tile t, row block r)
+// costs c_t = bal + ceil(cnt_t / 16) (its decode, then one unit per 16-position MFMA tile) and spans the cost
+// interval [nrb P_t + r c_t, + c_t), P_t the cost of the tiles before t; it goes to the XCD that holds its midpoint,
+// XCD x holding [x C / 8, (x + 1) C / 8) of the whole cost C = nrb sum c_t. The ranges stay contiguous (a tile's row
+// blocks and an expert's tiles share one L2) and every block finds them from the tile list alone: item r of tile t
+// lies before XCD x's range iff 8 (2 nrb P_t + 2 r c_t + c_t) < 2 x C.
+__device__ __forceinline__ int2 xcd_range(const uint64_t* tiles, int ntiles, int nrb, int bal, int x, int lane) {
+    const uint32_t* t32 = (const uint32_t*)tiles;
+    auto cost = [&](int t) __attribute__((always_inline)) {
+        return t < ntiles ? bal + ((min(GM, (int)t32[4 * t + 3]) + 15) >> 4) : 0;
+    };
+    long long csum = 0;
+    for (int c0 = 0; c0 < ntiles; c0 += 64) csum += wave_sum64(cost(c0 + lane));
+    const long long C = csum * nrb;
+    const long long R0 = 2LL * x * C, R1 = 2LL * (x + 1) * C;
+    long long carry = 0, n0 = 0, n1 = 0;
+    for (int c0 = 0; c0 < ntiles; c0 += 64) {
+        const int ct = cost(c0 + lane), inc = wave_scan(ct, lane);
+        long long b0 = 0, b1 = 0;
+        if (ct > 0) {
+            const long long base = 8LL * (2LL * nrb * (carry + inc - ct) + ct), u = 16LL * ct;
+            // the number of r in [0, nrb) with base + u r < R
+            b0 = R0 > base ? min((long long)nrb, (R0 - base + u - 1) / u) : 0;
+            b1 = R1 > base ? min((long long)nrb, (R1 - base + u - 1) / u) : 0;
+        }
+        n0 += wave_sum64(b0);
+        n1 += wave_sum64(b1);
+        carry += __shfl(inc, 63);
+    }
+    return make_int2(__builtin_amdgcn_readfirstlane((int)n0), __builtin_amdgcn_readfirstlane((int)n1));
+}
+
 template <int T>
 __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     using F = GemmFmt<T>;
@@ -59,16 +91,25 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     const int cols = a.cols, nsb = cols / 256;
 
     // Items are (tile, row block) pairs, item = tile * nrb + row block. XCD x (the hardware deals consecutive block
-    // ids to the 8 XCDs in turn) takes the items x * per .. (x + 1) * per - 1, so a tile's row blocks and an
-    // expert's tiles run on one XCD and share its L2 (X rows, expert weights); its a.gx blocks take every a.gx-th
-    // item from their index j.
+    // ids to the 8 XCDs in turn) takes a contiguous run of items, an eighth of the cost for tile lists (xcd_range)
+    // and of the count for dense matrices, so a tile's row blocks and an expert's tiles run on one XCD and share its
+    // L2 (X rows, expert weights); its a.gx blocks take every a.gx-th item from their index j.
     const int ntiles = a.n_tiles_dev ? min(sload(a.n_tiles_dev), a.max_tiles) : a.max_tiles;
     // pair mode: an item covers 64 output columns (64 rows of each of the two matrices)
     const bool pair = a.pair != 0;
     const int GNO = pair ? GN / 2 : GN;
     const int nrb = (a.rows + GNO - 1) / GNO, total = nrb * ntiles;
-    const int per = (total + NXCD - 1) / NXCD, xcd = blockIdx.x % NXCD, jb = blockIdx.x / NXCD;
-    const int ibeg = xcd * per + jb, iend = min((xcd + 1) * per, total);
+    const int xcd = blockIdx.x % NXCD, jb = blockIdx.x / NXCD;
+    int ibeg, iend;
+    if (a.tiles && a.bal >= 0) {
+        const int2 r = xcd_range(a.tiles, ntiles, nrb, a.bal, xcd, tid & 63);
+        ibeg = r.x + jb;
+        iend = r.y;
+    } else {
+        const int per = (total + NXCD - 1) / NXCD;
+        ibeg = xcd * per + jb;
+        iend = min((xcd + 1) * per, total);
+    }
     if (ibeg >= iend) return;
     const int nitems = (iend - ibeg + a.gx - 1) / a.gx;
 
@@ -470,6 +511,9 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
         while (a.dense_p > 64 && (long long)((g.dense_n + a.dense_p - 1) / a.dense_p) * nrb < ncu) a.dense_p /= 2;
         a.max_tiles = (g.dense_n + a.dense_p - 1) / a.dense_p;
     }
+    // tile lists split by cost over the XCDs; an item's decode costs about as much as 4 MFMA position tiles (3 to 5
+    // time the same on the 4096-token MoE layer, equal counts 3% slower)
+    a.bal = g.tiles ? 4 : -1;
     const long long total = nrb * a.max_tiles;
     const long long per = (total + NXCD - 1) / NXCD;
     const long long gx = std::min<long long>(per, std::max(ncu / NXCD, 1));
