@@ -39,25 +39,8 @@ struct GemmArgs {
     int pair;             // gate/up pair mode (GemmLaunch::pair)
     int64_t w2;           // pair: byte offset of the second matrix
     int dense_p;          // dense: positions per tile (GM, or less to give every CU an item)
-    int bal;              // tile lists: an item's fixed cost in 16-position tiles for the XCD split (< 0: equal counts)
+    int bal;              // tile lists: an item's fixed cost in 16-position tiles, 0..47 (< 0: split by count)
 };
-
-// Sum over the wave's 64 lanes (every lane gets it).
-__device__ __forceinline__ long long wave_sum64(long long v) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-// Inclusive prefix sum over the wave's lanes.
-__device__ __forceinline__ int wave_scan(int v, int lane) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(v, o);
-        if (lane >= o) v += u;
-    }
-    return v;
-}
 
 // silu(v) = v / (1 + e^-v) for the SwiGLU epilogues. e^-v = 2^t with t = -v log2(e) carried as th + tl (the
 // product's rounding error and the tail of log2(e) in tl): 2^th by v_exp_f32 and 2^tl as 1 + tl ln 2. Within a few ulp

@@ -738,6 +738,48 @@ def test_gemm_small_tiles_same_bits_random_lists(hip, ty):
     assert np.array_equal(a, b), int((a != b).sum())
 
 
+@pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q6_K])
+@pytest.mark.parametrize("case", ["plan_300", "count_600", "index_order"])
+def test_gemm_item_plans_cover_every_tile(hip, ty, case):
+    """The 256-position GEMM's three ways of dealing a tile list's items to its blocks, each against the CPU dots
+    (the same bits): plan_300, 300 tiles of 1-256 positions (the cost split over the XCDs and the larger-tiles-first
+    order); count_600, 600 tiles of 1-20 positions (past the 512 tiles a block plans: an eighth of the items an XCD);
+    index_order, 80 tiles over 32768 rows (256 row blocks a tile: past 64 items a block, the cost split dealt in
+    index order)."""
+    rng = np.random.default_rng(1300 + ty + len(case))
+    if case == "index_order":
+        rows, cols, E, n_tiles, cmax = 32768, 256, 2, 80, 3
+    else:
+        rows, cols, E = 200, 512, 6
+        n_tiles, cmax = (300, 256) if case == "plan_300" else (600, 20)
+    rb = ggml.row_bytes(ty, cols)
+    w = random_blocks(ty, E * rows, cols, seed=1301 + ty)
+    wb = up(hip, w)
+    n_x = 64
+    x = normal((n_x, cols), seed=1302 + ty)
+    spans, m0 = [], 0
+    for _ in range(n_tiles):
+        c = int(rng.integers(1, cmax + 1))
+        spans.append((int(rng.integers(0, E)), m0, c))
+        m0 += c
+    npos = m0
+    xrow = rng.integers(0, n_x, npos).astype(np.int32)
+    tiles, nt = tile_list(hip, int(wb), rows * rb, spans)
+    y = hip.alloc(npos * rows * 4)
+    hip.gemm(ty, rows, cols, tiles, nt, up(hip, x), cols, n_x, up(hip, xrow), y, rows, S.ACT_STORE)
+    got = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
+    # one CPU dot per (expert, X row) pair, shared by the positions that gather it
+    cache = {}
+    want = np.empty((npos, rows), dtype=np.float32)
+    for e, m0, c in spans:
+        for m in range(m0, m0 + c):
+            key = (e, int(xrow[m]))
+            if key not in cache:
+                cache[key] = O.matvec(ty, w[e * rows:(e + 1) * rows], rows, cols, x[xrow[m]])
+            want[m] = cache[key]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), int((got != want).sum())
+
+
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.IQ2_XXS, ggml.IQ3_S, ggml.IQ4_XS, ggml.Q2_K, ggml.Q3_K])
 @pytest.mark.parametrize("fl", [0, S.SMALL_TILES], ids=["blocks256", "small64"])
 def test_gemm_gate_up_fused_matches_two_calls(hip, ty, fl):
