@@ -42,6 +42,136 @@ struct GemmArgs {
     int bal;              // tile lists: an item's fixed cost in 16-position tiles, 0..47 (< 0: split by count)
 };
 
+// ---- the order of a tile list's items ----
+// Items are (tile, row block) pairs, item = tile * nrb + row block. Item (tile t, row block r) costs c_t = bal + b_t,
+// b_t = ceil(min(cnt_t, 256) / 16) the tile's MFMA position tiles (its bucket) and bal the weight decode in those
+// units. A block of NWV waves plans its items at the start, one thread a tile (lists of up to 64 NWV tiles), in `sh`
+// (PLAN_INTS ints of LDS that the block writes next only after a barrier).
+//   1. Range x of nx takes the items whose cost midpoint falls in [x C / nx, (x + 1) C / nx), C = nrb sum c_t: a
+//      contiguous range [ia, ib) (one a XCD: a tile's row blocks and an expert's tiles share its L2); item r of tile t
+//      lies before range x iff nx (2 nrb P_t + 2 r c_t + c_t) < 2 x C, P_t the cost of the tiles before t.
+//   2. The range's items are ordered by bucket, larger first (a bucket's tiles and a tile's row blocks in index
+//      order), and dealt to the range's gx blocks in a snake: block jb takes order positions q = k gx + jb for even k
+//      and k gx + gx - 1 - jb for odd k, so the last items the blocks run are the cheapest.
+// Returns the block's item count with item k in lane k of `mine`, or -1 (the caller then deals [ia, ib) in index
+// order) when a block would take more than 64 items. Every tile of the range has nrb items but the first and the last,
+// which the range may cut.
+constexpr int NBK = 17;  // buckets 0 .. 16
+constexpr int PLAN_INTS = 32 + 8 * NBK + NBK + 64;  // the plan's LDS ints (in `sh`)
+
+// The tile sizes go into `cnt` (thread t: tile t's count) before the list's length is known: `cap` slots are
+// readable, the first ntiles of them tiles.
+__device__ __forceinline__ int plan_load(const uint64_t* tiles, int cap) {
+    const int tid = threadIdx.x;
+    return tid < cap ? (int)((const uint32_t*)tiles)[4 * tid + 3] : 0;
+}
+template <int NWV>
+__device__ __forceinline__ int plan_items(int cnt, int ntiles, int nrb, int bal, int nx, int x, int jb, int gx, int* sh,
+                                          int& ia, int& ib, int& mine) {
+    static_assert(NWV == 8, "the plan's per-wave LDS slots are sized for 8 waves");
+    constexpr int NW = NWV;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const bool valid = tid < ntiles;
+    const int bkt = valid ? (min(256, cnt) + 15) >> 4 : -1;
+    const int ct = valid ? bal + bkt : 0;
+    int* wsum = sh;          // [NW] the waves' cost sums
+    int* full = sh + 8;      // [2][NW] the waves' tiles wholly before each boundary
+    int* part = sh + 24;     // [2] the items of the tile a boundary cuts, before it
+    int* tab = sh + 32;      // [NW][NBK] a wave's items of each bucket, then their prefix over the waves
+    int* tot = tab + 8 * NBK;  // [NBK] the range's items of each bucket
+    int* list = tot + NBK;   // [64] the block's items
+    // 1. block prefix of the costs (a wave scan, then the wave sums), and the XCD range
+    int inc = ct;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o);
+        if (lane >= o) inc += u;
+    }
+    if (lane == 63) wsum[w] = inc;
+    if (tid < 2) part[tid] = 0;
+    __syncthreads();
+    int P = inc - ct, csum = 0;
+#pragma unroll
+    for (int v = 0; v < NW; v++) {
+        const int s = wsum[v];
+        csum += s;
+        if (v < w) P += s;
+    }
+    const long long C = (long long)csum * nrb;
+    const long long base = (long long)nx * (2LL * nrb * P + ct), u = 2LL * nx * ct;
+    // the r in [0, nrb) with base + u r < R: none, all, or (the one tile the boundary cuts) a division
+    auto before = [&](long long R) __attribute__((always_inline)) {
+        if (!valid || R <= base) return 0;
+        if (R > base + u * (nrb - 1)) return nrb;
+        return (int)(((uint32_t)(R - base) + (uint32_t)u - 1u) / (uint32_t)u);
+    };
+    const int b0 = before(2LL * x * C), b1 = before(2LL * (x + 1) * C);  // (b1 = nrb throughout for the last range)
+    const uint64_t f0 = __ballot(b0 == nrb), f1 = __ballot(b1 == nrb);
+    if (lane == 0) {
+        full[w] = (int)__popcll(f0);
+        full[NW + w] = (int)__popcll(f1);
+    }
+    if (b0 > 0 && b0 < nrb) part[0] = b0;
+    if (b1 > 0 && b1 < nrb) part[1] = b1;
+    __syncthreads();
+    int n0 = 0, n1 = 0;
+#pragma unroll
+    for (int v = 0; v < NW; v++) {
+        n0 += full[v];
+        n1 += full[NW + v];
+    }
+    ia = n0 * nrb + part[0];
+    ib = n1 * nrb + part[1];
+    const int n = ib - ia;
+    if (n <= 0) return 0;
+    if ((n + gx - 1) / gx > 64) return -1;
+    // 2. each range tile's first order position: the buckets above its own, its bucket's items in earlier waves and
+    // in earlier lanes of its wave
+    const int ta = ia / nrb, tb = (ib - 1) / nrb;
+    const int na = min(ib, (ta + 1) * nrb) - ia, nb = ib - max(ia, tb * nrb);
+    const bool inr = valid && tid >= ta && tid <= tb;
+    const int bt = inr ? bkt : -1;
+    const int bta = __shfl(bt, ta & 63), btb = __shfl(bt, tb & 63);  // (meaningful in the waves of ta and tb)
+    const bool wa = w == (ta >> 6), wb = w == (tb >> 6) && tb != ta;
+    uint64_t mm = 0;
+    int wcnt = 0;
+#pragma unroll
+    for (int b = 0; b < NBK; b++) {
+        const uint64_t m = __ballot(bt == b);
+        if (bt == b) mm = m;
+        if (lane == b) wcnt = (int)__popcll(m) * nrb - (wa && bta == b ? nrb - na : 0) - (wb && btb == b ? nrb - nb : 0);
+    }
+    if (lane < NBK) tab[w * NBK + lane] = wcnt;
+    const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
+    const int pre = below * nrb - (wa && bta == bt && ta < tid ? nrb - na : 0);
+    __syncthreads();
+    if (tid < NBK) {
+        int s = 0;
+#pragma unroll
+        for (int v = 0; v < NW; v++) {
+            const int c = tab[v * NBK + tid];
+            tab[v * NBK + tid] = s;
+            s += c;
+        }
+        tot[tid] = s;
+    }
+    __syncthreads();
+    if (inr) {
+        int R = tab[w * NBK + bt] + pre;
+        for (int b = bt + 1; b < NBK; b++) R += tot[b];
+        const int nt = min(ib, (tid + 1) * nrb) - max(ia, tid * nrb), f = max(ia, tid * nrb);
+        // the block's order positions in [R, R + nt): q_k increases with k, q_k in [k gx, k gx + gx)
+        for (int k = max(R / gx - 1, 0); k < 64 && k * gx < R + nt; k++) {
+            const int q = k * gx + ((k & 1) ? gx - 1 - jb : jb);
+            if (q >= R && q < R + nt) list[k] = f + (q - R);
+        }
+    }
+    __syncthreads();
+    const int q = lane * gx + ((lane & 1) ? gx - 1 - jb : jb);
+    mine = q < n ? list[lane] : 0;
+    return (int)__popcll(__ballot(q < n));
+}
+
 // silu(v) = v / (1 + e^-v) for the SwiGLU epilogues. e^-v = 2^t with t = -v log2(e) carried as th + tl (the
 // product's rounding error and the tail of log2(e) in tl): 2^th by v_exp_f32 and 2^tl as 1 + tl ln 2. Within a few ulp
 // of the correctly rounded value over the whole range (e^-v overflowing to inf gives -0, as silu's limit); the 4K

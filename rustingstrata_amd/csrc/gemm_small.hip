@@ -143,17 +143,26 @@ __global__ __launch_bounds__(64 * SW, 1) void gemm_small_kernel(GemmArgs a) {
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int cols = a.cols, nsb = cols / 256;
 
-    // Items (tile, row block), item = tile * nrb + row block, dealt to the blocks in turn (block b takes items b,
-    // b + grid, ...: with tiles this small the items' costs vary with their expert's load, and dealing them round the
-    // whole grid balances the blocks better than giving each XCD a contiguous range; measured 0.285 -> 0.268 ms for
-    // a 512-token layer's grouped GEMMs). A tile of more than 64 positions runs as consecutive 64-position chunks of
-    // its item.
+    // Items (tile, row block), item = tile * nrb + row block, dealt round the whole grid: with tiles this small the
+    // items' costs vary with their expert's load, and one range for the grid balances the blocks better than giving
+    // each XCD a contiguous range (measured 0.285 -> 0.268 ms for a 512-token layer's grouped GEMMs). Tile lists of
+    // up to 512 tiles are planned (plan_items: larger tiles first, in a snake over the blocks; the slowest block of the
+    // 512-token gate/up GEMM ended at 1.26x the mean block's end time with the items in index order); longer ones
+    // deal block b the items b, b + grid, ... A tile of more than 64 positions runs as consecutive 64-position chunks
+    // of its item.
+    const int cnt0 = a.bal >= 0 ? plan_load(a.tiles, a.max_tiles) : 0;  // requested with the count
     const int ntiles = a.n_tiles_dev ? min(sload(a.n_tiles_dev), a.max_tiles) : a.max_tiles;
     const bool pair = a.pair != 0;
     const int GNO = pair ? SN / 2 : SN;
     const int nrb = (a.rows + GNO - 1) / GNO, total = nrb * ntiles;
     const int ibeg = blockIdx.x, gstep = gridDim.x;
-    const int nitems = ibeg < total ? (total - ibeg + gstep - 1) / gstep : 0;
+    int mine = 0, ns = -1;
+    if (a.bal >= 0 && ntiles <= 64 * SW) {
+        int ia, ib;
+        ns = plan_items<SW>(cnt0, ntiles, nrb, a.bal, 1, 0, ibeg, gstep, (int*)(xs + 2 * SXB), ia, ib, mine);
+    }
+    const bool mine_ok = ns >= 0;
+    const int nitems = mine_ok ? ns : ibeg < total ? (total - ibeg + gstep - 1) / gstep : 0;
 
     struct Item {
         uint64_t w;
@@ -163,7 +172,7 @@ __global__ __launch_bounds__(64 * SW, 1) void gemm_small_kernel(GemmArgs a) {
     // chunk pc of item k (k < nitems)
     auto item_at = [&](int k, int pc) __attribute__((always_inline)) {
         Item it;
-        const int id = ibeg + k * gstep, tile = id / nrb;
+        const int id = mine_ok ? __builtin_amdgcn_readlane(mine, k) : ibeg + k * gstep, tile = id / nrb;
         it.n0 = (id - tile * nrb) * GNO;
         const uint64_t t0 = sload(a.tiles + 2 * tile), t1 = sload(a.tiles + 2 * tile + 1);
         const int cnt = min(256, (int)(t1 >> 32)) - SM * pc;
@@ -537,6 +546,7 @@ static hipError_t gemm_small_t(const GemmLaunch& g, hipStream_t s) {
     a.w2 = g.w2;
     a.rb = row_bytes(T, g.cols);
     a.max_tiles = g.n_tiles;
+    a.bal = 4;  // the items' plan orders them by position tiles only (one range for the grid: no cost split)
     const size_t smem = gemm_small_smem<T>();
     static bool attr = false;
     if (!attr) {
