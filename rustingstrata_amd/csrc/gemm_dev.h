@@ -57,7 +57,15 @@ struct GemmArgs {
 // order) when a block would take more than 64 items. Every tile of the range has nrb items but the first and the last,
 // which the range may cut.
 constexpr int NBK = 17;  // buckets 0 .. 16
-constexpr int PLAN_INTS = 32 + 8 * NBK + NBK + 64;  // the plan's LDS ints (in `sh`)
+constexpr int PLAN_INTS = 32 + 2 * 8 * NBK + 2 * NBK + 64;  // the plan's LDS ints (in `sh`)
+
+// a / b for 0 <= a < 2^22, 0 < b < 2^10 through a float quotient and one correction step
+__device__ __forceinline__ int div_small(int a, int b) {
+    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
+    if (q * b > a) q--;
+    else if ((q + 1) * b <= a) q++;
+    return q;
+}
 
 // The tile sizes go into `cnt` (thread t: tile t's count) before the list's length is known: `cap` slots are
 // readable, the first ntiles of them tiles.
@@ -77,20 +85,23 @@ __device__ __forceinline__ int plan_items(int cnt, int ntiles, int nrb, int bal,
     int* wsum = sh;          // [NW] the waves' cost sums
     int* full = sh + 8;      // [2][NW] the waves' tiles wholly before each boundary
     int* part = sh + 24;     // [2] the items of the tile a boundary cuts, before it
-    int* tab = sh + 32;      // [NW][NBK] a wave's items of each bucket, then their prefix over the waves
-    int* tot = tab + 8 * NBK;  // [NBK] the range's items of each bucket
-    int* list = tot + NBK;   // [64] the block's items
-    // 1. block prefix of the costs (a wave scan, then the wave sums), and the XCD range
-    int inc = ct;
+    int* tab = sh + 32;      // [NW][NBK] a wave's items of each bucket
+    int* etab = tab + 8 * NBK;   // [NW][NBK] their sums over the earlier waves
+    int* tot = etab + 8 * NBK;   // [NBK] the range's items of each bucket
+    int* sbk = tot + NBK;        // [NBK] a bucket's first order position (the items of the larger buckets)
+    int* list = sbk + NBK;       // [64] the block's items
+    // 1. block prefix of the costs (c_t < 64: bit planes through ballots, the waves' sums through LDS), and the range
+    int P = 0, wt = 0;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(inc, o);
-        if (lane >= o) inc += u;
+    for (int j = 0; j < 6; j++) {
+        const uint64_t m = __ballot((ct >> j) & 1);
+        P += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << j;
+        wt += (int)__popcll(m) << j;
     }
-    if (lane == 63) wsum[w] = inc;
+    if (lane == 0) wsum[w] = wt;
     if (tid < 2) part[tid] = 0;
     __syncthreads();
-    int P = inc - ct, csum = 0;
+    int csum = 0;
 #pragma unroll
     for (int v = 0; v < NW; v++) {
         const int s = wsum[v];
@@ -145,23 +156,27 @@ __device__ __forceinline__ int plan_items(int cnt, int ntiles, int nrb, int bal,
     const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mm, 0u));
     const int pre = below * nrb - (wa && bta == bt && ta < tid ? nrb - na : 0);
     __syncthreads();
-    if (tid < NBK) {
-        int s = 0;
+    if (tid < NW * NBK) {
+        const int v0 = tid / NBK, b = tid - v0 * NBK;
+        int e = 0;
 #pragma unroll
-        for (int v = 0; v < NW; v++) {
-            const int c = tab[v * NBK + tid];
-            tab[v * NBK + tid] = s;
-            s += c;
-        }
-        tot[tid] = s;
+        for (int v = 0; v < NW - 1; v++) e += v < v0 ? tab[v * NBK + b] : 0;
+        etab[tid] = e;
+        if (v0 == NW - 1) tot[b] = e + tab[tid];
+    }
+    __syncthreads();
+    if (tid < NBK) {
+        int e = 0;
+#pragma unroll
+        for (int b = 1; b < NBK; b++) e += b > tid ? tot[b] : 0;
+        sbk[tid] = e;
     }
     __syncthreads();
     if (inr) {
-        int R = tab[w * NBK + bt] + pre;
-        for (int b = bt + 1; b < NBK; b++) R += tot[b];
+        const int R = sbk[bt] + etab[w * NBK + bt] + pre;
         const int nt = min(ib, (tid + 1) * nrb) - max(ia, tid * nrb), f = max(ia, tid * nrb);
         // the block's order positions in [R, R + nt): q_k increases with k, q_k in [k gx, k gx + gx)
-        for (int k = max(R / gx - 1, 0); k < 64 && k * gx < R + nt; k++) {
+        for (int k = max(div_small(R, gx) - 1, 0); k < 64 && k * gx < R + nt; k++) {
             const int q = k * gx + ((k & 1) ? gx - 1 - jb : jb);
             if (q >= R && q < R + nt) list[k] = f + (q - R);
         }
