@@ -586,6 +586,9 @@ def test_empty_inputs_are_no_ops(hip):
     assert np.array_equal(down(hip, off, np.int32, E + 1), np.zeros(E + 1, np.int32))
     assert down(hip, ntd, np.int32, 1)[0] == 0 and down(hip, err, np.int32, 1)[0] == 0
     hip.gemm_grouped(ty, 64, H, tiles, max_tiles, ntd, b, H, 0, xrow, y, 64, S.ACT_STORE)
+    hip.gemm_grouped(ty, 64, H, tiles, max_tiles, ntd, b, H, 0, xrow, y, 64, S.ACT_STORE | S.SMALL_TILES)
+    for fl in (0, S.SMALL_TILES):
+        hip.gemm_grouped_gate_up(ty, 64, H, tiles, max_tiles, ntd, b, H, 0, xrow, y, 64, 0, flags=fl)
     assert np.array_equal(down(hip, y, np.float32, 64), sentinel)
 
 
