@@ -247,15 +247,17 @@ int strata_moe_sort(strata_ctx* ctx, uint64_t ids, uint64_t t, uint64_t k, uint6
 int strata_gemm(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t n_tiles, uint64_t x,
                 uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y, uint64_t y_stride, int act);
 /* strata_gemm with the tile count read on the device from n_tiles_dev (at most max_tiles), as strata_moe_sort
- * leaves it: no host round trip between routing and the expert GEMMs. */
+ * leaves it: no host round trip between routing and the expert GEMMs. All max_tiles slots of the tile buffer must be
+ * readable (the GEMM reads the tiles' sizes with the count to plan its blocks' work); slots past the count are
+ * ignored. */
 int strata_gemm_grouped(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t tiles, uint64_t max_tiles,
                         uint64_t n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x, uint64_t xrow, uint64_t y,
                         uint64_t y_stride, int act);
 /* The gate and up projections of the prefill MoE block in one grouped GEMM (src/gpu_model/prefill.rs: gemm of the
  * gate experts with act store, then of the up experts with act SwiGLU over the same tiles and X): for each tile the
  * up matrix is the gate matrix's address + up_offset bytes, and y[m, 0..rows) = silu(W_gate x) * (W_up x), the same
- * bits as the two calls. rows must be a multiple of 64, y rows 16-byte aligned; not for Q8_0. flags: STRATA_SAME_X
- * or 0, as in strata_gemm. */
+ * bits as the two calls. rows must be a multiple of 64, y rows 16-byte aligned; not for Q8_0. flags: STRATA_SAME_X,
+ * STRATA_SMALL_TILES or 0, as in strata_gemm; max_tiles as in strata_gemm_grouped. */
 int strata_gemm_grouped_gate_up(strata_ctx* ctx, int ty, uint64_t rows, uint64_t cols, uint64_t tiles,
                                 uint64_t max_tiles, uint64_t n_tiles_dev, uint64_t x, uint64_t x_stride, uint64_t n_x,
                                 uint64_t xrow, uint64_t y, uint64_t y_stride, int64_t up_offset, int flags);
