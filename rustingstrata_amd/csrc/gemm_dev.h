@@ -53,7 +53,8 @@ struct GemmArgs {
 //   2. The range's items are ordered by bucket, larger first (a bucket's tiles and a tile's row blocks in index
 //      order), and dealt to the range's gx blocks in a snake: block jb takes order positions q = k gx + jb for even k
 //      and k gx + gx - 1 - jb for odd k, so the last items the blocks run are the cheapest.
-// Returns the block's item count with item k in lane k of `mine`, or -1 (the caller then deals [ia, ib) in index
+// Every block of a range derives the same order from the tile list alone (no atomics, no timing), so the blocks'
+// shares partition the range. Returns the block's item count with item k in lane k of `mine`, or -1 (the caller then deals [ia, ib) in index
 // order) when a block would take more than 64 items. Every tile of the range has nrb items but the first and the last,
 // which the range may cut.
 constexpr int NBK = 17;  // buckets 0 .. 16
