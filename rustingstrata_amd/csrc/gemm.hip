@@ -73,6 +73,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm_kernel(GemmArgs a) {
     // of the items and its a.gx blocks every a.gx-th item from their index jb
     int ibeg, iend, mine = 0, ns = -1;
     if (a.tiles && a.bal >= 0 && ntiles <= 64 * NW) {
+        static_assert(PLAN_INTS * 4 <= XBUF, "the plan fits the second X buffer, first written after the first barrier");
         ns = plan_items<NW>(cnt0, ntiles, nrb, a.bal, NXCD, xcd, jb, a.gx, (int*)(xs + XBUF), ibeg, iend, mine);
         ibeg += jb;
     } else {

@@ -48,15 +48,16 @@ struct GemmArgs {
 // units. A block of NWV waves plans its items at the start, one thread a tile (lists of up to 64 NWV tiles), in `sh`
 // (PLAN_INTS ints of LDS that the block writes next only after a barrier).
 //   1. Range x of nx takes the items whose cost midpoint falls in [x C / nx, (x + 1) C / nx), C = nrb sum c_t: a
-//      contiguous range [ia, ib) (one a XCD: a tile's row blocks and an expert's tiles share its L2); item r of tile t
-//      lies before range x iff nx (2 nrb P_t + 2 r c_t + c_t) < 2 x C, P_t the cost of the tiles before t.
+//      contiguous range [ia, ib) (with one range per XCD, a tile's row blocks and an expert's tiles share its L2);
+//      item r of tile t lies before range x iff nx (2 nrb P_t + 2 r c_t + c_t) < 2 x C, P_t the cost of the tiles
+//      before t.
 //   2. The range's items are ordered by bucket, larger first (a bucket's tiles and a tile's row blocks in index
 //      order), and dealt to the range's gx blocks in a snake: block jb takes order positions q = k gx + jb for even k
 //      and k gx + gx - 1 - jb for odd k, so the last items the blocks run are the cheapest.
 // Every block of a range derives the same order from the tile list alone (no atomics, no timing), so the blocks'
-// shares partition the range. Returns the block's item count with item k in lane k of `mine`, or -1 (the caller then deals [ia, ib) in index
-// order) when a block would take more than 64 items. Every tile of the range has nrb items but the first and the last,
-// which the range may cut.
+// shares partition the range. Returns the block's item count with item k in lane k of `mine`, or -1 (the caller then
+// deals [ia, ib) in index order) when a block would take more than 64 items. Every tile of the range has nrb items
+// but the first and the last, which the range may cut. The block has 64 NWV threads and every one of them calls.
 constexpr int NBK = 17;  // buckets 0 .. 16
 constexpr int PLAN_INTS = 32 + 2 * 8 * NBK + 2 * NBK + 64;  // the plan's LDS ints (in `sh`)
 

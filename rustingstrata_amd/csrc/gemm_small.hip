@@ -159,6 +159,7 @@ __global__ __launch_bounds__(64 * SW, 1) void gemm_small_kernel(GemmArgs a) {
     int mine = 0, ns = -1;
     if (a.bal >= 0 && ntiles <= 64 * SW) {
         int ia, ib;
+        static_assert(PLAN_INTS * 4 <= SXB, "the plan fits X slot 2, first written after the first barrier");
         ns = plan_items<SW>(cnt0, ntiles, nrb, a.bal, 1, 0, ibeg, gstep, (int*)(xs + 2 * SXB), ia, ib, mine);
     }
     const bool mine_ok = ns >= 0;
