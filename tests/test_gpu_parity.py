@@ -741,6 +741,43 @@ def test_gemm_small_tiles_same_bits_random_lists(hip, ty):
     assert np.array_equal(a, b), int((a != b).sum())
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_gemm_plans_over_random_lists(hip, seed):
+    """Both GEMM forms over seeded random tile lists of 1-500 tiles (1-256 positions each, experts in random order,
+    gathered X rows) and 64-2048 rows: the 256-position form (its items planned over the XCDs) and the 64-position form
+    (planned over the grid) give the same bits, and sampled positions carry the CPU dots' bits."""
+    rng = np.random.default_rng(1400 + seed)
+    ty = [ggml.Q4_K, ggml.Q5_K, ggml.Q6_K, ggml.Q2_K, ggml.Q3_K, ggml.IQ3_S][seed]
+    rows = int(rng.choice([64, 128, 200, 384, 1024, 2048]))
+    cols, E, n_x = 512, 7, 96
+    n_tiles = int(rng.integers(1, 501))
+    cmax = int(rng.choice([8, 64, 256]))
+    rb = ggml.row_bytes(ty, cols)
+    w = random_blocks(ty, E * rows, cols, seed=1401 + seed)
+    wb = up(hip, w)
+    x = normal((n_x, cols), seed=1402 + seed)
+    spans, m0 = [], 0
+    for _ in range(n_tiles):
+        c = int(rng.integers(1, cmax + 1))
+        spans.append((int(rng.integers(0, E)), m0, c))
+        m0 += c
+    npos = m0
+    xrow = rng.integers(0, n_x, npos).astype(np.int32)
+    tiles, nt = tile_list(hip, int(wb), rows * rb, spans)
+    xb, xr = up(hip, x), up(hip, xrow)
+    ya, yb = hip.alloc(npos * rows * 4), hip.alloc(npos * rows * 4)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, ya, rows, S.ACT_STORE)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, yb, rows, S.ACT_STORE | S.SAME_X | S.SMALL_TILES)
+    a, b = down(hip, ya, np.uint32, npos * rows), down(hip, yb, np.uint32, npos * rows)
+    assert np.array_equal(a, b), int((a != b).sum())
+    got = a.view(np.float32).reshape(npos, rows)
+    starts = np.array([m for _, m, _ in spans])
+    for m in rng.choice(npos, min(npos, 24), replace=False):
+        e = spans[int(np.searchsorted(starts, m, side="right")) - 1][0]
+        want = O.matvec(ty, w[e * rows:(e + 1) * rows], rows, cols, x[xrow[m]])
+        assert np.array_equal(got[m].view(np.uint32), want.view(np.uint32)), (int(m), e)
+
+
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q6_K])
 @pytest.mark.parametrize("case", ["plan_300", "count_600", "index_order"])
 def test_gemm_item_plans_cover_every_tile(hip, ty, case):
