@@ -239,17 +239,31 @@ __global__ __launch_bounds__(1024) void sort_scan_kernel(SortLaunch a, int W) {
     int* cnt = a.scratch;
     const uint64_t L = (uint64_t)E * W;
     // expert e's row of wave counts (coalesced, 64 waves at a time) into exclusive prefixes within the expert; the
-    // expert's total into offs[e]
-    for (int e = wave; e < E; e += 16) {
+    // expert's total into offs[e]. This wave's (expert, 64-count chunk) pairs p = ei nch + ch (expert wave + 16 ei)
+    // go 8 at a time: the 8 loads together, then their scans in order (one round trip per 8 chunks, not per chunk).
+    {
+        const int nch = (W + 63) / 64, nE = wave < E ? (E - wave + 15) / 16 : 0, P = nE * nch;
         int carry = 0;
-        for (int w0 = 0; w0 < W; w0 += 64) {
-            const int w = w0 + lane;
-            const int c = w < W ? cnt[(uint64_t)e * W + w] : 0;
-            const int inc = wave_incl_scan(c);
-            if (w < W) cnt[(uint64_t)e * W + w] = carry + inc - c;
-            carry += __builtin_amdgcn_readlane(inc, 63);
+        for (int p0 = 0; p0 < P; p0 += 8) {
+            int c[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int p = p0 + u, ei = p / nch, ch = p - ei * nch, w = 64 * ch + lane;
+                c[u] = p < P && w < W ? cnt[(uint64_t)(wave + 16 * ei) * W + w] : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int p = p0 + u;
+                if (p < P) {
+                    const int ei = p / nch, ch = p - ei * nch, e = wave + 16 * ei, w = 64 * ch + lane;
+                    if (ch == 0) carry = 0;
+                    const int inc = wave_incl_scan(c[u]);
+                    if (w < W) cnt[(uint64_t)e * W + w] = carry + inc - c[u];
+                    carry += __builtin_amdgcn_readlane(inc, 63);
+                    if (ch == nch - 1 && lane == 0) offs[e] = carry;
+                }
+            }
         }
-        if (lane == 0) offs[e] = carry;
     }
     // the bad-id count: each thread sums waves tid, tid + 1024, ..., then the block in order
     int bad = 0;
