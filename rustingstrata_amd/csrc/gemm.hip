@@ -483,8 +483,8 @@ static hipError_t gemm_t(const GemmLaunch& g, hipStream_t s) {
         while (a.dense_p > 64 && (long long)((g.dense_n + a.dense_p - 1) / a.dense_p) * nrb < ncu) a.dense_p /= 2;
         a.max_tiles = (g.dense_n + a.dense_p - 1) / a.dense_p;
     }
-    // tile lists split by cost over the XCDs; an item's decode costs about as much as 4 MFMA position tiles (3 to 5
-    // time the same on the 4096-token MoE layer, equal counts 3% slower)
+    // tile lists split by cost over the XCDs; an item's decode costs about as much as 4 MFMA position tiles (3, 4 and
+    // 5 measure the same on the 4096-token MoE layer; a split by count is 3% slower)
     a.bal = g.tiles ? 4 : -1;
     const long long total = nrb * a.max_tiles;
     const long long per = (total + NXCD - 1) / NXCD;
