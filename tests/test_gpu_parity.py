@@ -781,11 +781,11 @@ def test_gemm_plans_over_random_lists(hip, seed):
 @pytest.mark.parametrize("ty", [ggml.Q4_K, ggml.Q6_K])
 @pytest.mark.parametrize("case", ["plan_300", "count_600", "index_order"])
 def test_gemm_item_plans_cover_every_tile(hip, ty, case):
-    """The 256-position GEMM's three ways of dealing a tile list's items to its blocks, each against the CPU dots
-    (the same bits): plan_300, 300 tiles of 1-256 positions (the cost split over the XCDs and the larger-tiles-first
-    order); count_600, 600 tiles of 1-20 positions (past the 512 tiles a block plans: an eighth of the items an XCD);
-    index_order, 80 tiles over 32768 rows (256 row blocks a tile: past 64 items a block, the cost split dealt in
-    index order)."""
+    """The GEMMs' ways of dealing a tile list's items to their blocks, each against the CPU dots (the same bits), with
+    the 64-position form bit-equal to the 256-position one: plan_300, 300 tiles of 1-256 positions (the cost split over
+    the XCDs and the larger-tiles-first order); count_600, 600 tiles of 1-20 positions (past the 512 tiles a block
+    plans: an eighth of the items an XCD, and index order over the grid); index_order, 80 tiles over 32768 rows (256
+    row blocks a tile: past 64 items a block, the plan's range dealt in index order)."""
     rng = np.random.default_rng(1300 + ty + len(case))
     if case == "index_order":
         rows, cols, E, n_tiles, cmax = 32768, 256, 2, 80, 3
@@ -805,9 +805,14 @@ def test_gemm_item_plans_cover_every_tile(hip, ty, case):
     npos = m0
     xrow = rng.integers(0, n_x, npos).astype(np.int32)
     tiles, nt = tile_list(hip, int(wb), rows * rb, spans)
-    y = hip.alloc(npos * rows * 4)
-    hip.gemm(ty, rows, cols, tiles, nt, up(hip, x), cols, n_x, up(hip, xrow), y, rows, S.ACT_STORE)
+    y, y64 = hip.alloc(npos * rows * 4), hip.alloc(npos * rows * 4)
+    xb, xr = up(hip, x), up(hip, xrow)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y, rows, S.ACT_STORE)
+    # the 64-position form over the same list (index_order: past 64 items a block of its grid too)
+    hip.gemm(ty, rows, cols, tiles, nt, xb, cols, n_x, xr, y64, rows, S.ACT_STORE | S.SAME_X | S.SMALL_TILES)
     got = down(hip, y, np.float32, npos * rows).reshape(npos, rows)
+    got64 = down(hip, y64, np.float32, npos * rows).reshape(npos, rows)
+    assert np.array_equal(got.view(np.uint32), got64.view(np.uint32)), int((got != got64).sum())
     # one CPU dot per (expert, X row) pair, shared by the positions that gather it
     cache = {}
     want = np.empty((npos, rows), dtype=np.float32)
