@@ -60,3 +60,27 @@ def test_no_gpu_open_fails_cleanly():
         S.lib().strata_close(ctx)
         pytest.skip("a GPU is present")
     assert S.lib().strata_last_error()
+
+
+def test_size_helpers():
+    """The host-side size queries the bindings use: an f16 cache takes one u16 word a value (Backend::kv_words,
+    src/backend.rs:186), a GEMM block holds 256 positions, and the decode attention's partials take hd + 2 floats per
+    head and position split (128 splits)."""
+    from rustingstrata_amd import backend as B
+    lib = B.lib()
+    assert all(lib.strata_kv_words(n) == n for n in (0, 1, 128, 512, 4096))
+    assert lib.strata_gemm_block_positions() == 256
+    assert lib.strata_attn_part_floats(32, 128) == 32 * 128 * 130
+    assert lib.strata_attn_part_floats(8, 64) == 8 * 128 * 66
+
+
+def test_config4_shape():
+    """the Qwen3-30B-A3B-shaped stack (48 layers, hidden 2048, 32 query heads over 4 KV heads of 128,
+    128 experts top-8 of intermediate 768, vocabulary 151936) with the UD-Q2_K_XL-like mix (Q2_K/Q3_K experts, Q6_K
+    attention, Q8_0 embeddings and output)."""
+    from rustingstrata_amd.qwen3moe import Config
+    c = Config.qwen3_30b_a3b()
+    assert (c.n_layer, c.n_embd, c.n_head, c.n_head_kv, c.head_dim) == (48, 2048, 32, 4, 128)
+    assert (c.n_expert, c.n_expert_used, c.n_ff_exp, c.n_vocab) == (128, 8, 768, 151936)
+    assert (c.ty_gate_up, c.ty_down, c.ty_attn, c.ty_embd, c.ty_out) == (ggml.Q2_K, ggml.Q3_K, ggml.Q6_K, ggml.Q8_0,
+                                                                          ggml.Q8_0)
